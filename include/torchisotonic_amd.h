@@ -1,0 +1,123 @@
+/*
+ * torchisotonic_amd: batched weighted L2 isotonic regression on AMD MI355X (gfx950).
+ *
+ * The C ABI of libtorchisotonic_amd.so. Plain pointers and sizes only; every device pointer
+ * is memory of the current HIP device, every launch goes on the stream passed in (a
+ * hipStream_t, passed as void*), nothing synchronises the host, and the library never
+ * allocates device memory: the caller allocates outputs and the workspace whose size the
+ * *_workspace calls report. Functions return TI_OK (0) or a TI_E* code; ti_last_error()
+ * then holds a message for the calling thread.
+ *
+ * Layouts. A problem set is [batch, n] row-major and contiguous, dtype float32 or float64;
+ * weights, when given, have the same shape and dtype. The block partition ("starts") is a bit
+ * array: row b owns ti_starts_words(1, n) 32-bit words starting at word b * that count; bit i
+ * of the row (word i / 32, bit i % 32) is set where a block of the fit starts. Element 0 is
+ * always a start.
+ *
+ * Replaces the reference's operator library (reference src/torchisotonic/csrc/ops.cpp:45-51
+ * schemas, ops_tiles.cu:8-11 CUDA registrations).
+ */
+#ifndef TORCHISOTONIC_AMD_H
+#define TORCHISOTONIC_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TI_ABI_VERSION 1
+
+/* dtype codes */
+#define TI_F32 0
+#define TI_F64 1
+
+/* status codes */
+#define TI_OK 0
+#define TI_EINVAL 1     /* a null pointer, a negative size, an inconsistent argument */
+#define TI_EDTYPE 2     /* a dtype code other than TI_F32 / TI_F64 */
+#define TI_ESIZE 3      /* n >= 2^31 - 1, or a row count the grid cannot hold */
+#define TI_EWORKSPACE 4 /* workspace missing or smaller than *_workspace reported */
+#define TI_ELAUNCH 5    /* the HIP runtime rejected a launch */
+
+/* flag bits */
+#define TI_INCREASING 1u /* non-decreasing fit (else non-increasing: minus the fit of -y) */
+#define TI_EXACT 2u      /* reference's exact= flag; this library is always exact (see ti_fwd) */
+#define TI_CLIP_MIN 4u   /* clamp the fit from below at y_min */
+#define TI_CLIP_MAX 8u   /* clamp the fit from above at y_max */
+
+/* The ABI version this library was built with (TI_ABI_VERSION). */
+int ti_abi_version(void);
+
+/* The last error message of the calling thread ("" if none). */
+const char* ti_last_error(void);
+
+/* Number of 32-bit words of the starts bit array of a [batch, n] problem set. */
+int64_t ti_starts_words(int64_t batch, int64_t n);
+
+/* Bytes of device workspace ti_fwd needs for this problem set (0 when none). */
+int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes);
+
+/*
+ * The isotonic fit of every row of y, and optionally its block partition.
+ * Replaces torchisotonic::isotonic_tiles (reference ops.cpp:47-49, implementation
+ * tiles.cuh:1923-1959), with the clamp the reference applies afterwards in Python
+ * (reference _api.py:68-69) fused in.
+ *
+ *   y       [batch, n] input (dtype), no NaN handling needed by the caller: a row holding a
+ *           NaN comes back all NaN with starts [1, 0, ...] (reference pava.h:29-38).
+ *   w       [batch, n] positive weights, or NULL for weights of one.
+ *   out     [batch, n] the fit, clamped to [y_min, y_max] where TI_CLIP_* is set (a clamp
+ *           with y_min > y_max gives y_max, as torch.clamp does). May not alias y or w.
+ *   starts  ti_starts_words(batch, n) words, or NULL when the partition is not wanted.
+ *   bad_weight  one device word, or NULL: when w is given, the kernels set it to a nonzero
+ *           value (and never clear it) if some weight is not > 0, NaN included. This fuses
+ *           the reference's separate check bool((w > 0).all()) (reference _api.py:60-61)
+ *           into the one read of w; the caller zeroes the word first and reads it afterwards.
+ *   flags   TI_INCREASING | TI_EXACT | TI_CLIP_MIN | TI_CLIP_MAX.
+ *   workspace / workspace_bytes: at least ti_fwd_workspace() bytes, 256-byte aligned
+ *           (may be NULL when that is 0).
+ *   stream  hipStream_t.
+ * Sums and hull predicates run in float64 whatever the dtype; float32 fits are rounded once.
+ * TI_EXACT is accepted for API parity and changes nothing.
+ */
+int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+           int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace ti_bwd needs for this problem set (0 when none). */
+int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes);
+
+/*
+ * Gradients of a fit with respect to y and w, given the upstream gradient g and the fit's
+ * block partition. Replaces torchisotonic::isotonic_grad (reference ops.cpp:50, implementation
+ * grad.cuh:386-413) together with the clamp's backward (torch's, applied by autograd in the
+ * reference, _api.py:69).
+ *
+ * With G, W and M the sums of g, w and w*y over an element's block (W = count when w is
+ * NULL) and mask = [y_min <= M/W <= y_max] for the flags set (the unclamped fit, rounded to
+ * dtype, against the bounds rounded to dtype; torch.clamp's backward, equality passes):
+ *   gy_i = w_i * mask * G / W,          gw_i = (y_i - M / W) * mask * G / W.
+ * The block mean M/W is recomputed from y and w, so the forward's output is not read.
+ *
+ *   starts  the partition ti_fwd wrote for the same y, w.
+ *   g       [batch, n] upstream gradient.
+ *   w       weights or NULL (unweighted).
+ *   y       [batch, n] input of the fit; needed when gw is wanted or a TI_CLIP_* flag is set.
+ *   gy, gw  outputs, either may be NULL.
+ */
+int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy,
+           void* gw, int64_t batch, int64_t n, int dtype, unsigned flags, double y_min,
+           double y_max, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Test hook: the starts bit array of a [batch, n] set as bytes (0/1), row-major - the
+ * reference's bool starts tensor (reference tests/test_cuda.py:176 reads it). */
+int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHISOTONIC_AMD_H */

@@ -1,0 +1,111 @@
+"""The C ABI without a GPU: the library loads, exports every function include/*.h declares,
+reports its version, sizes its buffers, and turns bad arguments into status codes and
+messages before touching the device (the reference's preconditions, tiles.cuh:1926-1934 and
+grad.cuh:389-394, as TI_E* codes)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from torchisotonic_amd import _ext
+
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+
+
+def declared_functions() -> list[str]:
+    names = []
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(ti_\w+)\s*\(", text, flags=re.M)
+    return names
+
+
+def test_headers_declare_the_bound_symbols() -> None:
+    names = declared_functions()
+    assert len(names) >= 8
+    assert set(names) == set(_ext.SYMBOLS)
+
+
+def test_library_exports_every_declared_function() -> None:
+    lib = _ext.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version() -> None:
+    assert _ext.load().ti_abi_version() == _ext.ABI_VERSION
+
+
+def test_starts_words() -> None:
+    lib = _ext.load()
+    assert lib.ti_starts_words(1_000_000, 16) == 1_000_000
+    assert lib.ti_starts_words(3, 33) == 6
+    assert lib.ti_starts_words(1, 100_000_000) == 3_125_000
+    assert lib.ti_starts_words(0, 5) == 0
+
+
+def test_workspace_queries() -> None:
+    lib = _ext.load()
+    size = ctypes.c_size_t(123)
+    assert lib.ti_fwd_workspace(1000, 16, _ext.F32, 0, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert lib.ti_bwd_workspace(1000, 16, _ext.F64, 1, ctypes.byref(size)) == 0
+    assert lib.ti_fwd_workspace(10, 16, 7, 0, ctypes.byref(size)) == 2  # TI_EDTYPE
+    assert lib.ti_fwd_workspace(10, 16, 0, 0, None) == 1  # TI_EINVAL
+
+
+def call_fwd(y: int | None, out: int | None, batch: int, n: int, dtype: int = 0) -> int:
+    return _ext.load().ti_fwd(y, None, out, None, None, batch, n, dtype, 1, 0.0, 0.0, None, 0, None)
+
+
+@pytest.mark.parametrize(
+    ("args", "code", "words"),
+    [
+        ((1, 2, 4, 16, 5), 2, "dtype"),
+        ((1, 2, -1, 16), 1, "batch >= 0"),
+        ((1, 2, 4, 0), 1, "n >= 1"),
+        ((1, 2, 1, 2**31), 3, "2^31"),
+        ((None, 2, 4, 16), 1, "null"),
+        ((1, None, 4, 16), 1, "null"),
+        ((8, 8, 4, 16), 1, "alias"),
+    ],
+)
+def test_fwd_argument_errors(args: tuple, code: int, words: str) -> None:
+    assert call_fwd(*args) == code
+    assert words in _ext.load().ti_last_error().decode()
+
+
+def test_empty_batch_is_a_no_op() -> None:
+    assert call_fwd(None, None, 0, 16) == 0
+    assert _ext.load().ti_last_error() == b""
+
+
+def test_bwd_argument_errors() -> None:
+    lib = _ext.load()
+    bwd = lib.ti_bwd
+    # gw wanted without y
+    assert bwd(1, 2, None, None, None, 3, 4, 16, 0, 1, 0.0, 0.0, None, 0, None) == 1
+    assert b"y is needed" in lib.ti_last_error()
+    # clamp mask without y
+    assert bwd(1, 2, None, None, 3, None, 4, 16, 0, 1 | 4, 0.0, 0.0, None, 0, None) == 1
+    # starts missing
+    assert bwd(None, 2, None, None, 3, None, 4, 16, 0, 1, 0.0, 0.0, None, 0, None) == 1
+    # nothing wanted: fine, no launch
+    assert bwd(1, 2, None, None, None, None, 4, 16, 0, 1, 0.0, 0.0, None, 0, None) == 0
+
+
+def test_errors_are_per_thread() -> None:
+    import threading
+
+    lib = _ext.load()
+    assert call_fwd(1, 2, 4, 16, 9) == 2
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(lib.ti_last_error()))
+    t.start()
+    t.join()
+    assert seen == [b""]
+    assert b"dtype" in lib.ti_last_error()

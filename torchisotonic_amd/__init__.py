@@ -1,0 +1,10 @@
+"""Batched isotonic regression for PyTorch tensors on AMD MI355X: a drop-in for
+``torchisotonic.isotonic`` (reference src/torchisotonic/__init__.py:3-6) backed by hand-written
+HIP kernels for gfx950."""
+
+from torchisotonic_amd._api import isotonic
+
+__all__ = ["isotonic"]
+__version__ = "0.1.0"
+# The torchisotonic release whose API and semantics this package reproduces.
+REFERENCE_VERSION = "0.2.1"

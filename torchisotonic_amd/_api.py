@@ -1,0 +1,131 @@
+"""Batched isotonic regression with the semantics of ``sklearn.isotonic.isotonic_regression``,
+on the GPU through hand-written HIP kernels for MI355X.
+
+A drop-in for ``torchisotonic.isotonic`` (reference src/torchisotonic/_api.py:13-70): the same
+signature, argument checks and messages, dtype policy, ``dim`` handling, weight broadcasting
+and autograd behaviour. What differs inside: the clamp to ``[y_min, y_max]`` and its backward
+are fused into the kernels, the weights' positivity is checked by the forward kernel as it
+reads them (one read of ``w`` instead of two), and the backward recomputes the block means from
+``y`` and ``w`` instead of reading the fit. There is no CPU solver: tensors must be on a ROCm
+device (arguments are still validated first, so the reference's error messages hold
+everywhere).
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from torchisotonic_amd import _ext
+
+
+def isotonic(
+    y: Tensor,
+    weight: Tensor | None = None,
+    *,
+    increasing: bool = True,
+    y_min: float | None = None,
+    y_max: float | None = None,
+    dim: int = -1,
+    exact: bool = True,
+) -> Tensor:
+    """Isotonic regression of every 1-D slice of ``y`` along ``dim``.
+
+    For each slice, returns the non-decreasing (or, with ``increasing=False``,
+    non-increasing) sequence closest to it in weighted least squares, like
+    ``sklearn.isotonic.isotonic_regression``. ``weight`` must be positive and shaped like
+    ``y`` (or broadcast to it). Results are clipped to ``[y_min, y_max]`` if given. A slice
+    containing NaN comes back as NaN. Integer input becomes the default float dtype; float
+    input keeps its dtype, with float16/bfloat16 computed in float32.
+
+    Differentiable in ``y`` and ``weight``: the fit is constant on blocks of neighbouring
+    elements, each the weighted mean of ``y`` over its block, so a gradient is averaged over
+    the blocks.
+
+    ``exact`` is accepted for compatibility with torchisotonic; the kernels always form sums
+    and hull tests in float64 and round the float32 fit once, so it changes nothing.
+    """
+    # Argument checks and messages: reference _api.py:43-61.
+    if not isinstance(y, Tensor):
+        raise TypeError(f"y must be a torch.Tensor, got {type(y).__name__}")
+    if y.is_complex():
+        raise TypeError("complex tensors are not supported")
+    if y.ndim == 0:
+        raise ValueError("y must have at least one dimension")
+    out_dtype = y.dtype if y.is_floating_point() else torch.get_default_dtype()
+    acc = torch.float64 if out_dtype == torch.float64 else torch.float32
+    rows = y.movedim(dim, -1)
+    w: Tensor | None = None
+    if weight is not None:
+        if not isinstance(weight, Tensor):
+            raise TypeError(f"weight must be a torch.Tensor, got {type(weight).__name__}")
+        try:
+            w = weight.to(device=y.device, dtype=acc).broadcast_to(y.shape).movedim(dim, -1)
+        except RuntimeError as e:
+            raise ValueError(f"weight of shape {tuple(weight.shape)} does not fit y") from e
+        if y.device.type != "cuda" and not bool((w > 0).all()):
+            # On the GPU the forward kernel makes this check as it reads w.
+            raise ValueError("weight must be strictly positive")
+    shape = rows.shape
+    if rows.numel() == 0:
+        return y.to(out_dtype, copy=True)
+    flat_y = rows.reshape(-1, shape[-1]).to(acc)
+    flat_w = None if w is None else w.reshape(-1, shape[-1])
+    lo = None if y_min is None else float(y_min)
+    hi = None if y_max is None else float(y_max)
+    out: Tensor = _Isotonic.apply(flat_y, flat_w, increasing, exact, lo, hi)
+    return out.reshape(shape).movedim(-1, dim).to(out_dtype)
+
+
+class _Isotonic(torch.autograd.Function):
+    """The clamped fit, with its gradient: the upstream gradient masked where the clamp
+    binds, then averaged over the fit's blocks (reference _api.py:73-97 plus torch.clamp's
+    backward)."""
+
+    @staticmethod
+    def forward(
+        ctx: Any,
+        flat_y: Tensor,
+        flat_w: Tensor | None,
+        increasing: bool,
+        exact: bool,
+        y_min: float | None,
+        y_max: float | None,
+    ) -> Tensor:
+        want = any(ctx.needs_input_grad[:2])
+        out, starts = _solve(flat_y, flat_w, increasing, exact, want, y_min, y_max)
+        ctx.save_for_backward(flat_y, flat_w, starts)
+        ctx.bounds = (y_min, y_max)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, grad: Tensor) -> tuple[Tensor | None, Tensor | None, None, None, None, None]:
+        flat_y, flat_w, starts = ctx.saved_tensors
+        want_y, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        y_min, y_max = ctx.bounds
+        need_y = want_w or y_min is not None or y_max is not None
+        gy, gw = _ext.grad(
+            starts, grad, flat_w, flat_y if need_y else None, want_y, want_w, y_min, y_max
+        )
+        return gy, gw, None, None, None, None
+
+
+def _solve(
+    flat_y: Tensor,
+    flat_w: Tensor | None,
+    increasing: bool,
+    exact: bool = True,
+    with_starts: bool = False,
+    y_min: float | None = None,
+    y_max: float | None = None,
+) -> tuple[Tensor, Tensor]:
+    """The (clamped) fit of [batch, n] problems (n >= 1) in flat_y's dtype, by the HIP
+    kernels, and, if ``with_starts``, where its blocks start as a packed bit array (else an
+    empty tensor). Reference _api.py:118-134 without its CPU branch."""
+    _ext._on_gpu(flat_y, "y")
+    out, starts, bad = _ext.fit(flat_y, flat_w, increasing, exact, with_starts, y_min, y_max)
+    if bad is not None and bool(bad.item()):
+        raise ValueError("weight must be strictly positive")
+    return out, starts

@@ -1,0 +1,252 @@
+"""The boundary to the HIP kernels: a ctypes binding of libtorchisotonic_amd.so (C ABI in
+include/torchisotonic_amd.h) and the tensor-level calls the rest of the package makes.
+
+Takes the place of the reference's JIT-built operator library (reference
+src/torchisotonic/_ext.py:18-68): ``isotonic_tiles`` and ``isotonic_grad`` keep the
+reference's names and argument meaning; ``fit`` and ``grad`` are what ``_api`` calls, with the
+partition as a packed bit array instead of a bool tensor. Torch allocates every output and
+workspace and supplies the current stream; the library never allocates and never falls back
+to anything: a missing library, a tensor off the GPU or a failed launch raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from pathlib import Path
+
+import torch
+from torch import Tensor
+
+LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
+ABI_VERSION = 1
+
+F32, F64 = 0, 1
+INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
+
+_vp, _i64, _int, _uint, _dbl, _sz = (
+    ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint, ctypes.c_double, ctypes.c_size_t,
+)
+
+SYMBOLS = (
+    "ti_abi_version",
+    "ti_last_error",
+    "ti_starts_words",
+    "ti_fwd_workspace",
+    "ti_fwd",
+    "ti_bwd_workspace",
+    "ti_bwd",
+    "ti_starts_to_bool",
+)
+
+
+@functools.cache
+def load() -> ctypes.CDLL:
+    """The HIP library, bound. torch is imported first so that the process has one HIP runtime
+    (torch's; the library's libamdhip64.so.7 dependency resolves to it)."""
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"torchisotonic_amd: the HIP library {LIB_PATH} is not built "
+            "(run `python -m torchisotonic_amd.build`)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.ti_abi_version.restype = _int
+    lib.ti_abi_version.argtypes = []
+    lib.ti_last_error.restype = ctypes.c_char_p
+    lib.ti_last_error.argtypes = []
+    lib.ti_starts_words.restype = _i64
+    lib.ti_starts_words.argtypes = [_i64, _i64]
+    for name in ("ti_fwd_workspace", "ti_bwd_workspace"):
+        fn = getattr(lib, name)
+        fn.restype = _int
+        fn.argtypes = [_i64, _i64, _int, _int, ctypes.POINTER(_sz)]
+    lib.ti_fwd.restype = _int
+    lib.ti_fwd.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_bwd.restype = _int
+    lib.ti_bwd.argtypes = [_vp] * 6 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_starts_to_bool.restype = _int
+    lib.ti_starts_to_bool.argtypes = [_vp, _vp, _i64, _i64, _vp]
+    got = lib.ti_abi_version()
+    if got != ABI_VERSION:
+        raise RuntimeError(f"torchisotonic_amd: library ABI {got}, expected {ABI_VERSION}")
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().ti_last_error().decode(errors="replace")
+        raise RuntimeError(f"torchisotonic_amd.{what}: {msg} (status {rc})")
+
+
+def _on_gpu(t: Tensor, name: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"torchisotonic_amd runs on the GPU (HIP); {name} is on {t.device}. "
+            "Move the tensors to a ROCm device first."
+        )
+
+
+def _dtype_code(t: Tensor) -> int:
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.float64:
+        return F64
+    raise RuntimeError(f"torchisotonic_amd: kernels take float32 or float64, got {t.dtype}")
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def starts_words(batch: int, n: int) -> int:
+    return int(load().ti_starts_words(batch, n))
+
+
+def _workspace(kind: str, batch: int, n: int, dtype: int, weighted: bool, device: torch.device) -> Tensor | None:
+    size = _sz(0)
+    fn = load().ti_fwd_workspace if kind == "fwd" else load().ti_bwd_workspace
+    _check(fn(batch, n, dtype, int(weighted), ctypes.byref(size)), f"{kind}_workspace")
+    if size.value == 0:
+        return None
+    return torch.empty(size.value, dtype=torch.uint8, device=device)
+
+
+def _flags(increasing: bool, exact: bool, y_min: float | None, y_max: float | None) -> int:
+    f = (INCREASING if increasing else 0) | (EXACT if exact else 0)
+    f |= CLIP_MIN if y_min is not None else 0
+    f |= CLIP_MAX if y_max is not None else 0
+    return f
+
+
+def fit(
+    y: Tensor,
+    w: Tensor | None,
+    increasing: bool,
+    exact: bool = True,
+    with_starts: bool = False,
+    y_min: float | None = None,
+    y_max: float | None = None,
+) -> tuple[Tensor, Tensor, Tensor | None]:
+    """The fit of every row of ``y`` ([batch, n], float32/float64, on the GPU), clamped to
+    [y_min, y_max] where given; the packed partition (int32 words) if ``with_starts`` (else an
+    empty tensor); and, for weighted fits, a one-word device flag that is nonzero if some
+    weight was not positive (the caller checks it)."""
+    _on_gpu(y, "y")
+    dtype = _dtype_code(y)
+    if y.dim() != 2:
+        raise RuntimeError("torchisotonic_amd.fit: y must be [batch, n]")
+    y = y.contiguous()
+    batch, n = y.shape
+    if w is not None:
+        _on_gpu(w, "weight")
+        if w.shape != y.shape or w.dtype != y.dtype or w.device != y.device:
+            raise RuntimeError("torchisotonic_amd.fit: w must match y in shape, dtype and device")
+        w = w.contiguous()
+    out = torch.empty_like(y)
+    starts = torch.empty(
+        starts_words(batch, n) if with_starts else 0, dtype=torch.int32, device=y.device
+    )
+    bad = torch.zeros(1, dtype=torch.int32, device=y.device) if w is not None else None
+    with torch.cuda.device(y.device):
+        ws = _workspace("fwd", batch, n, dtype, w is not None, y.device)
+        rc = load().ti_fwd(
+            _ptr(y), _ptr(w), _ptr(out), _ptr(starts) if with_starts else None, _ptr(bad),
+            batch, n, dtype, _flags(increasing, exact, y_min, y_max),
+            float(y_min) if y_min is not None else 0.0,
+            float(y_max) if y_max is not None else 0.0,
+            _ptr(ws), 0 if ws is None else ws.numel(), _stream(y),
+        )
+    _check(rc, "fit")
+    return out, starts, bad
+
+
+def grad(
+    starts: Tensor,
+    g: Tensor,
+    w: Tensor | None,
+    y: Tensor | None,
+    want_y: bool,
+    want_w: bool,
+    y_min: float | None = None,
+    y_max: float | None = None,
+) -> tuple[Tensor | None, Tensor | None]:
+    """Gradients w.r.t. y and w of a fit whose packed partition is ``starts``, for the upstream
+    gradient ``g`` (the clamp's backward included where y_min / y_max are given)."""
+    _on_gpu(g, "grad")
+    dtype = _dtype_code(g)
+    batch, n = g.shape
+    g = g.contiguous()
+    if w is not None:
+        w = w.contiguous()
+    if y is not None:
+        y = y.contiguous()
+    gy = torch.empty_like(g) if want_y else None
+    gw = torch.empty_like(g) if want_w else None
+    if gy is None and gw is None:
+        return None, None
+    with torch.cuda.device(g.device):
+        ws = _workspace("bwd", batch, n, dtype, w is not None, g.device)
+        rc = load().ti_bwd(
+            _ptr(starts), _ptr(g), _ptr(w), _ptr(y), _ptr(gy), _ptr(gw), batch, n, dtype,
+            _flags(True, True, y_min, y_max),
+            float(y_min) if y_min is not None else 0.0,
+            float(y_max) if y_max is not None else 0.0,
+            _ptr(ws), 0 if ws is None else ws.numel(), _stream(g),
+        )
+    _check(rc, "grad")
+    return gy, gw
+
+
+def starts_to_bool(starts: Tensor, batch: int, n: int) -> Tensor:
+    """The packed partition as the reference's bool [batch, n] tensor (a test hook)."""
+    out = torch.empty(batch, n, dtype=torch.uint8, device=starts.device)
+    with torch.cuda.device(starts.device):
+        rc = load().ti_starts_to_bool(_ptr(starts), _ptr(out), batch, n, _stream(starts))
+    _check(rc, "starts_to_bool")
+    return out.bool()
+
+
+def bool_to_starts(starts: Tensor) -> Tensor:
+    """A bool [batch, n] partition packed into the kernels' layout (int32 words)."""
+    batch, n = starts.shape
+    words = (n + 31) // 32
+    bits = torch.zeros(batch, words * 32, dtype=torch.int64, device=starts.device)
+    bits[:, :n] = starts.to(torch.int64)
+    bits[:, 0] = 1
+    weights = torch.bitwise_left_shift(
+        torch.ones(32, dtype=torch.int64, device=starts.device),
+        torch.arange(32, dtype=torch.int64, device=starts.device),
+    )
+    packed = (bits.view(batch, words, 32) * weights).sum(-1)
+    packed = torch.where(packed >= 2**31, packed - 2**32, packed)
+    return packed.to(torch.int32).reshape(-1)
+
+
+def isotonic_tiles(
+    y: Tensor, w: Tensor | None, increasing: bool, exact: bool = True, with_starts: bool = False
+) -> tuple[Tensor, Tensor]:
+    """The reference's operator (reference _ext.py:25-31): the fit of every row of ``y``
+    ([batch, n], on the GPU) in y's dtype, and if ``with_starts`` a bool tensor marking where
+    its blocks start (else an empty one)."""
+    out, starts, bad = fit(y, w, increasing, exact, with_starts)
+    if bad is not None and bool(bad.item()):
+        raise ValueError("weight must be strictly positive")
+    if not with_starts:
+        return out, torch.empty(0, dtype=torch.bool, device=y.device)
+    return out, starts_to_bool(starts, *y.shape)
+
+
+def isotonic_grad(
+    out: Tensor, starts: Tensor, g: Tensor, w: Tensor | None, y: Tensor | None
+) -> list[Tensor | None]:
+    """The reference's gradient operator (reference _ext.py:34-40): the gradients of a fit
+    whose blocks start where the bool ``starts`` is set, w.r.t. y and, given y, the weights.
+    ``out`` is accepted for the signature's sake; the block means are recomputed from y."""
+    del out
+    packed = bool_to_starts(starts) if starts.dtype == torch.bool else starts
+    gy, gw = grad(packed, g, w, y, True, y is not None)
+    return [gy, gw]

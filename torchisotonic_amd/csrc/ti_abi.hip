@@ -1,0 +1,139 @@
+// The C ABI of libtorchisotonic_amd.so (declared in include/torchisotonic_amd.h): argument
+// checks, regime dispatch and launch-error reporting. Preconditions mirror the reference's
+// TORCH_CHECKs (reference src/torchisotonic/csrc/tiles.cuh:1926-1934, grad.cuh:389-394) as
+// status codes with a thread-local message instead of exceptions.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "ti_kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return TI_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(TI_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+// The largest row the kernels index with 32-bit element offsets within a row (the reference
+// limits n the same way, tiles.cuh:1933-1934).
+constexpr int64_t kMaxN = (int64_t(1) << 31) - 2;
+
+int check_shape(int64_t batch, int64_t n, int dtype) {
+  if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
+  if (batch < 0 || n < 1) return fail(TI_EINVAL, "need batch >= 0 and n >= 1, got batch=%lld n=%lld", (long long)batch, (long long)n);
+  if (n > kMaxN) return fail(TI_ESIZE, "rows of %lld elements exceed the limit of 2^31 - 2", (long long)n);
+  return TI_OK;
+}
+
+__global__ void starts_to_bool_kernel(const uint32_t* __restrict__ starts, uint8_t* __restrict__ out,
+                                      int64_t batch, int64_t n, int64_t wpr) {
+  const int64_t total = batch * n;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = e / n, i = e - b * n;
+    out[e] = (starts[b * wpr + (i >> 5)] >> (i & 31)) & 1u;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ti_abi_version(void) { return TI_ABI_VERSION; }
+
+const char* ti_last_error(void) { return g_error.c_str(); }
+
+int64_t ti_starts_words(int64_t batch, int64_t n) {
+  if (batch < 0 || n < 0) return 0;
+  return batch * ((n + 31) / 32);
+}
+
+int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes) {
+  (void)weighted;
+  if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  *bytes = 0;
+  if (n <= ti::kShortMax) return ok();
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+}
+
+int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+           int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+           void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  if (batch == 0) return ok();
+  if (y == nullptr || out == nullptr) return fail(TI_EINVAL, "y and out must not be null");
+  if (out == y || (w != nullptr && out == w)) return fail(TI_EINVAL, "out must not alias y or w");
+  if (n <= ti::kShortMax) {
+    if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
+    ti::ShortArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
+                    static_cast<hipStream_t>(stream)};
+    return launched(ti::short_fit(a), "short-row fit");
+  }
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+}
+
+int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes) {
+  (void)weighted;
+  if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  *bytes = 0;
+  if (n <= ti::kShortMax) return ok();
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+}
+
+int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy,
+           void* gw, int64_t batch, int64_t n, int dtype, unsigned flags, double y_min,
+           double y_max, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  if (batch == 0) return ok();
+  if (starts == nullptr || g == nullptr) return fail(TI_EINVAL, "starts and g must not be null");
+  const bool clipping = (flags & (TI_CLIP_MIN | TI_CLIP_MAX)) != 0;
+  if ((gw != nullptr || clipping) && y == nullptr)
+    return fail(TI_EINVAL, "y is needed for the weight gradient and for the clamp's mask");
+  if (gy == nullptr && gw == nullptr) return ok();
+  if (n <= ti::kShortMax) {
+    if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
+    ti::ShortGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
+                        static_cast<hipStream_t>(stream)};
+    return launched(ti::short_grad(a), "short-row gradient");
+  }
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+}
+
+int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n, void* stream) {
+  if (batch < 0 || n < 0) return fail(TI_EINVAL, "negative size");
+  if (batch == 0 || n == 0) return ok();
+  if (starts == nullptr || out == nullptr) return fail(TI_EINVAL, "null pointer");
+  const int64_t total = batch * n;
+  const int64_t blocks = (total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536;
+  starts_to_bool_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                          static_cast<hipStream_t>(stream)>>>(starts, out, batch, n, (n + 31) / 32);
+  return launched(hipGetLastError(), "starts_to_bool");
+}
+
+}  // extern "C"

@@ -1,0 +1,112 @@
+// Device helpers shared by the isotonic kernels (gfx950, wave64).
+//
+// The fit of a row is the slope of the greatest convex minorant (lower convex hull) of its
+// cumulative sum diagram P_k = (W_k, S_k), W_k = sum_{j<k} w_j, S_k = sum_{j<k} w_j y_j: element
+// i takes the slope of the hull edge over [W_i, W_{i+1}], and blocks start at hull vertices.
+// Pool-adjacent-violators (reference src/torchisotonic/csrc/pava.h:16-69) pools a block into its
+// predecessor while mean(prev) >= mean(cur); in the diagram that is: drop the vertex B between
+// A and C while slope(A, B) >= slope(B, C). Equal means pool, so collinear points are not
+// vertices.
+//
+// All sums and predicates run in float64 whatever the data's dtype: on CDNA3/4 a float64 add,
+// mul or fma issues at the float32 rate, and the path is bound by HBM bandwidth.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ti {
+
+constexpr int kWave = 64;
+
+// Sign of a*b - c*d, exact whenever a, b, c, d are exact: each product is split into its
+// rounded value and its exact rounding error with an fma (two-product, Dekker / Ogita-Rump-
+// Oishi). The rounded products' difference is exact when they are within a factor of two of
+// each other (Sterbenz), and otherwise too large for the errors to change its sign; the
+// errors' difference only decides when the rounded products tie.
+__device__ __forceinline__ int cross_sign(double a, double b, double c, double d) {
+  const double p = a * b;
+  const double q = c * d;
+  const double ep = __builtin_fma(a, b, -p);
+  const double eq = __builtin_fma(c, d, -q);
+  const double r = (p - q) + (ep - eq);
+  return (r > 0.0) - (r < 0.0);
+}
+
+// True when vertex B (between A and C) must leave a lower hull built for PAVA semantics:
+// slope(A,B) >= slope(B,C), i.e. dS1 * dW2 >= dS2 * dW1 with dS1 = S_B - S_A, dW1 = W_B - W_A,
+// dS2 = S_C - S_B, dW2 = W_C - W_B (weights positive). Mirrors reference pava.h:46-55:
+// merge unless total_a * weight_b < total_b * weight_a.
+//
+// EXACT: the decision is exact for the given (exact) differences. A single fma forms
+// dS1*dW2 - fl(dS2*dW1) with one rounding; its sign is right unless it is within
+// 2^-52 |dS2*dW1| of zero (the second product's rounding error plus its own), and only then
+// does the two-product test run. Without EXACT the products are compared as rounded, which
+// is exact whenever they fit 53 bits (unweighted float32 rows: sums of at most 32 float32
+// values times counts of at most 32).
+template <bool EXACT>
+__device__ __forceinline__ bool pools(double dS1, double dW1, double dS2, double dW2) {
+  if constexpr (EXACT) {
+    const double q = dS2 * dW1;
+    const double d = __builtin_fma(dS1, dW2, -q);
+    if (__builtin_fabs(d) > 0x1p-52 * __builtin_fabs(q)) return d > 0.0;
+    return cross_sign(dS1, dW2, dS2, dW1) >= 0;
+  } else {
+    return dS1 * dW2 >= dS2 * dW1;
+  }
+}
+
+// num / den for den > 0, within an ulp or so of the correctly rounded quotient: a hardware
+// reciprocal refined by two Newton steps, then one residual correction of the quotient
+// (Markstein). Used wherever a block's mean (a hull slope) is formed, so the forward and the
+// backward get bit-identical means from the same sums.
+__device__ __forceinline__ double slope_div(double num, double den) {
+  double r = __builtin_amdgcn_rcp(den);
+  r = __builtin_fma(__builtin_fma(-den, r, 1.0), r, r);
+  r = __builtin_fma(__builtin_fma(-den, r, 1.0), r, r);
+  const double q = num * r;
+  return __builtin_fma(__builtin_fma(-den, q, num), r, q);
+}
+
+template <typename T>
+__device__ __forceinline__ T quiet_nan();
+template <>
+__device__ __forceinline__ float quiet_nan<float>() {
+  return __builtin_nanf("");
+}
+template <>
+__device__ __forceinline__ double quiet_nan<double>() {
+  return __builtin_nan("");
+}
+
+// torch.clamp on the fit's dtype: NaN stays NaN (both comparisons are false), and with
+// lo > hi everything becomes hi (the upper bound is applied last).
+template <typename T>
+__device__ __forceinline__ T clip(T v, bool use_lo, T lo, bool use_hi, T hi) {
+  if (use_lo) v = v < lo ? lo : v;
+  if (use_hi) v = v > hi ? hi : v;
+  return v;
+}
+
+// torch.clamp's backward mask for the fit value v: passes where lo <= v <= hi (equality
+// included); a NaN fit passes nothing.
+template <typename T>
+__device__ __forceinline__ bool clip_passes(T v, bool use_lo, T lo, bool use_hi, T hi) {
+  bool ok = v == v;
+  if (use_lo) ok = ok && v >= lo;
+  if (use_hi) ok = ok && v <= hi;
+  return ok;
+}
+
+// floor(e / n) for 0 <= e < 2^20 and 1 <= n <= 2^10: the high word of e * ceil(2^32 / n)
+// (exact there, since e * (ceil(2^32/n) - 2^32/n) < 2^32 / n). n = 1 has no 32-bit
+// multiplier and is passed through.
+struct DivBy {
+  uint32_t n, magic;
+  __device__ __forceinline__ explicit DivBy(uint32_t d) : n(d), magic(d > 1 ? 0xFFFFFFFFu / d + 1u : 0u) {}
+  __device__ __forceinline__ uint32_t operator()(uint32_t e) const {
+    return n > 1 ? __umulhi(e, magic) : e;
+  }
+};
+
+}  // namespace ti

@@ -1,0 +1,45 @@
+// Internal interface between the C ABI (ti_abi.hip) and the kernel families.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/torchisotonic_amd.h"
+
+namespace ti {
+
+// Rows up to this length take the short-row kernels (one thread per row).
+constexpr int64_t kShortMax = 32;
+
+struct ShortArgs {
+  const void* y;
+  const void* w;  // null: unweighted
+  void* out;
+  uint32_t* starts;      // null: not wanted
+  uint32_t* bad_weight;  // null: not checked
+  int64_t batch, n;
+  int dtype;
+  unsigned flags;
+  double lo, hi;
+  hipStream_t stream;
+};
+
+struct ShortGradArgs {
+  const uint32_t* starts;
+  const void* g;
+  const void* w;  // null: unweighted
+  const void* y;  // needed for gw and for the clamp mask
+  void* gy;
+  void* gw;
+  int64_t batch, n;
+  int dtype;
+  unsigned flags;
+  double lo, hi;
+  hipStream_t stream;
+};
+
+int64_t short_grid(int64_t batch, int64_t n, bool weighted);
+hipError_t short_fit(const ShortArgs& a);
+hipError_t short_grad(const ShortGradArgs& a);
+
+}  // namespace ti

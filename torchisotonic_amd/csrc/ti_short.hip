@@ -1,0 +1,650 @@
+// Short rows (n <= 32): one thread per row, many rows per wavefront.
+//
+// Replaces the reference's packed regime (reference src/torchisotonic/csrc/tiles.cuh:920-1112,
+// packed_kernel; grad.cuh:200-290 with E=1 for the backward) with a design for wave64:
+//   - a workgroup owns THREADS consecutive rows, i.e. one contiguous span of THREADS * n
+//     elements. When a row is a whole number of 16-byte vectors (n * sizeof(T) % 16 == 0, the
+//     headline [1e6, 16] float32 case) each thread moves its own row with 16-byte loads and
+//     stores ("direct"); otherwise the workgroup moves its span with coalesced 16-byte
+//     accesses through LDS, rows padded to n + 1 entries ("staged");
+//   - each thread builds its row's cumulative sums in float64 registers and runs the monotone
+//     chain (Andrew) for the lower hull of the n + 1 points, keeping the hull as a bit mask
+//     and the points in a per-thread LDS column for the pops' random access (the third
+//     vertex is prefetched, so a pop does not wait on LDS before the next test);
+//   - the fit is one float64 slope per block, rounded once, with the clamp fused; the
+//     partition is one 32-bit word of start bits per row.
+// The backward moves g (and w, y) the same way; block sums of g (and w) and the block mean
+// for the clamp mask and the weight gradient are formed per thread, in registers.
+#include <type_traits>
+
+#include "ti_common.h"
+#include "ti_kernels.h"
+
+namespace ti {
+
+namespace {
+
+// Threads per workgroup: the pops' point columns take (NMAX + 1) * THREADS float64 values per
+// coordinate; keep them at or under 36 KB, four workgroups per CU.
+template <int NMAX, bool W>
+constexpr int short_threads() {
+  constexpr int per_thread = (NMAX + 1) * 8 * (W ? 2 : 1);
+  return per_thread * 256 <= 36 * 1024 ? 256 : per_thread * 128 <= 36 * 1024 ? 128 : 64;
+}
+
+template <int NMAX, bool W>
+constexpr int short_lds_doubles() {
+  return (NMAX + 1) * short_threads<NMAX, W>() * (W ? 2 : 1);
+}
+
+template <typename T>
+struct Vec16 {
+  static constexpr int kN = 16 / sizeof(T);
+  using type = T __attribute__((ext_vector_type(kN)));
+};
+
+// One row of NMAX values (n == NMAX, 16-byte aligned) straight into / out of registers.
+template <typename T, int NMAX>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, T (&v)[NMAX]) {
+  constexpr int V = Vec16<T>::kN;
+  using VT = typename Vec16<T>::type;
+  const VT* q = reinterpret_cast<const VT*>(p);
+  VT buf[NMAX / V];
+#pragma unroll
+  for (int j = 0; j < NMAX / V; ++j) buf[j] = q[j];
+#pragma unroll
+  for (int j = 0; j < NMAX / V; ++j) {
+#pragma unroll
+    for (int t = 0; t < V; ++t) v[j * V + t] = buf[j][t];
+  }
+}
+
+template <typename T, int NMAX>
+__device__ __forceinline__ void store_row(T* __restrict__ p, const T (&v)[NMAX]) {
+  constexpr int V = Vec16<T>::kN;
+  using VT = typename Vec16<T>::type;
+  VT* q = reinterpret_cast<VT*>(p);
+#pragma unroll
+  for (int j = 0; j < NMAX / V; ++j) {
+    VT x;
+#pragma unroll
+    for (int t = 0; t < V; ++t) x[t] = v[j * V + t];
+    q[j] = x;
+  }
+}
+
+// The staged path: this workgroup's span of `count` = rows * n elements, read with coalesced
+// 16-byte loads (all issued before any is used), into registers; then written to LDS row r at
+// stg[r * (n + 1) + c]. A span that does not start on a 16-byte boundary is read per element.
+template <typename T, int THREADS, int NMAX>
+struct Span {
+  static constexpr int V = Vec16<T>::kN;
+  static constexpr int kIters = (NMAX + V - 1) / V;
+  using VT = typename Vec16<T>::type;
+  VT buf[kIters];
+  T tailv;  // the span's last (count % V) elements, one per thread, in the vector path
+
+  __device__ __forceinline__ void load(const T* __restrict__ src, int count) {
+    const int tid = threadIdx.x;
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+      const VT* s = reinterpret_cast<const VT*>(src);
+      const int nvec = count / V;
+#pragma unroll
+      for (int j = 0; j < kIters; ++j) {
+        const int idx = tid + j * THREADS;
+        if (idx < nvec) buf[j] = s[idx];
+      }
+      const int tail = count - nvec * V;
+      if (tid < tail) tailv = src[nvec * V + tid];
+    } else {
+#pragma unroll
+      for (int j = 0; j < kIters; ++j) {
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+          const int e = (tid + j * THREADS) * V + t;
+          if (e < count) buf[j][t] = src[e];
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void to_lds(const T* __restrict__ src, T* stg, int count,
+                                         DivBy div) const {
+    const int tid = threadIdx.x;
+    const bool vec = (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+    const int nvec = vec ? count / V : (count + V - 1) / V;
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+      const int idx = tid + j * THREADS;
+      if (idx < nvec) {
+#pragma unroll
+        for (int t = 0; t < V; ++t) {
+          const int e = idx * V + t;
+          if (e < count) stg[e + div(e)] = buf[j][t];
+        }
+      }
+    }
+    if (vec) {
+      const int tail = count - (count / V) * V;
+      if (tid < tail) {
+        const int e = (count / V) * V + tid;
+        stg[e + div(e)] = tailv;
+      }
+    }
+  }
+};
+
+template <typename T, int THREADS>
+__device__ __forceinline__ void stage_out(T* __restrict__ dst, const T* stg, int count, DivBy div) {
+  constexpr int V = Vec16<T>::kN;
+  using VT = typename Vec16<T>::type;
+  const int tid = threadIdx.x;
+  if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+    const int nvec = count / V;
+    VT* d = reinterpret_cast<VT*>(dst);
+    for (int idx = tid; idx < nvec; idx += THREADS) {
+      VT x;
+#pragma unroll
+      for (int t = 0; t < V; ++t) {
+        const int e = idx * V + t;
+        x[t] = stg[e + div(e)];
+      }
+      d[idx] = x;
+    }
+    for (int e = nvec * V + tid; e < count; e += THREADS) dst[e] = stg[e + div(e)];
+  } else {
+    for (int e = tid; e < count; e += THREADS) dst[e] = stg[e + div(e)];
+  }
+}
+
+// Vertex masks over the n + 1 points of a row.
+template <int NMAX>
+struct MaskOf {
+  using type = typename std::conditional<(NMAX < 32), uint32_t, uint64_t>::type;
+};
+
+__device__ __forceinline__ int lowest_bit(uint32_t v) { return __builtin_ctz(v); }
+__device__ __forceinline__ int lowest_bit(uint64_t v) { return __builtin_ctzll(v); }
+__device__ __forceinline__ int highest_bit(uint32_t v) { return 31 - __builtin_clz(v); }
+__device__ __forceinline__ int highest_bit(uint64_t v) { return 63 - __builtin_clzll(v); }
+
+// sgn * a < sgn * b, exactly (a, b in the data's dtype; sgn = +-1).
+template <typename T>
+__device__ __forceinline__ bool tsgn_lt(double sgn, T a, T b) {
+  return sgn > 0.0 ? a < b : b < a;
+}
+
+template <typename T, int NMAX, bool W, bool DIRECT>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
+    const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
+    uint32_t* __restrict__ starts, uint32_t* __restrict__ bad_weight, int64_t batch, int n,
+    unsigned flags, T lo, T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  constexpr bool EXACT = W || sizeof(T) == 8;
+  __shared__ double lds[short_lds_doubles<NMAX, W>()];
+  T* stg = reinterpret_cast<T*>(lds);
+  double* colS = lds;                        // [NMAX + 1][THREADS]
+  double* colW = lds + (NMAX + 1) * THREADS;  // weighted only
+
+  const int tid = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
+  const int rows = static_cast<int>(min<int64_t>(THREADS, batch - row0));
+  const int count = rows * n;
+  const DivBy div(static_cast<uint32_t>(n));
+  const bool active = tid < rows;
+  const double sgn = (flags & TI_INCREASING) ? 1.0 : -1.0;
+
+  T yv[NMAX];
+  T wv[W ? NMAX : 1];
+  if constexpr (DIRECT) {
+    if (active) {
+      load_row<T, NMAX>(y + (row0 + tid) * NMAX, yv);
+      if constexpr (W) load_row<T, NMAX>(w + (row0 + tid) * NMAX, wv);
+    }
+  } else {
+    Span<T, THREADS, NMAX> sy;
+    Span<T, THREADS, NMAX> sw;
+    sy.load(y + row0 * n, count);
+    if constexpr (W) sw.load(w + row0 * n, count);
+    sy.to_lds(y + row0 * n, stg, count, div);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n) yv[c] = stg[tid * (n + 1) + c];
+    }
+    if constexpr (W) {
+      __syncthreads();
+      sw.to_lds(w + row0 * n, stg, count, div);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < n) wv[c] = stg[tid * (n + 1) + c];
+      }
+    }
+    __syncthreads();  // staging is dead from here: the area becomes the point columns
+  }
+
+  // The row length: a constant when each thread moves whole rows of NMAX.
+  const int nn = DIRECT ? NMAX : n;
+
+  // Cumulative sums in float64 (of sgn * y: a decreasing fit is minus the increasing fit of -y).
+  double S[NMAX + 1];
+  double P[W ? NMAX + 1 : 1];
+  bool bad = false;
+  bool wbad = false;
+  S[0] = 0.0;
+  if constexpr (W) P[0] = 0.0;
+#pragma unroll
+  for (int c = 0; c < NMAX; ++c) {
+    if (c < nn) {
+      const double yc = sgn * static_cast<double>(yv[c]);
+      bad |= yc != yc;
+      if constexpr (W) {
+        const double wc = static_cast<double>(wv[c]);
+        wbad |= !(wc > 0.0);
+        S[c + 1] = S[c] + wc * yc;
+        P[c + 1] = P[c] + wc;
+      } else {
+        S[c + 1] = S[c] + yc;
+      }
+    }
+  }
+  auto Wk = [&](int k) -> double {
+    if constexpr (W) return P[k];
+    else return static_cast<double>(k);
+  };
+  if constexpr (W) {
+    if (active && wbad && bad_weight != nullptr) *bad_weight = 1u;
+  }
+  if (active) {
+#pragma unroll
+    for (int k = 0; k <= NMAX; ++k) {
+      if (k <= nn) {
+        colS[k * THREADS + tid] = S[k];
+        if constexpr (W) colW[k * THREADS + tid] = P[k];
+      }
+    }
+  }
+
+  // Lower hull of P_0..P_n by the monotone chain, run as an event loop: every iteration either
+  // pops the last vertex or pushes the next candidate, so a wave iterates max over its lanes of
+  // (pushes + pops) rather than, step by step, the most pops any lane needs.
+  //
+  // Candidates: a point k (0 < k < n) with y_{k-1} >= y_k lies on or above the segment between
+  // its neighbours (the slopes into and out of it are y_{k-1} and y_k, weighted or not), so it
+  // is never a vertex of the hull with equal means pooled; dropping those first is exact and
+  // removes about half the work on noisy rows.
+  using Mask = typename MaskOf<NMAX>::type;
+  Mask m = 1;
+  if (active) {
+    Mask cand = Mask(1) | (Mask(1) << nn);
+#pragma unroll
+    for (int k = 1; k < NMAX; ++k) {
+      if (k < nn && tsgn_lt(sgn, yv[k - 1], yv[k])) cand |= Mask(1) << k;
+    }
+    // stack: t1 (last vertex), t2, t3 (< 0: none), with sums s* and weights w*
+    int t1 = 0, t2 = -1, t3 = -1;
+    double s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    double w1 = 0.0, w2 = 0.0, w3 = 0.0;
+    // the candidate being pushed (k) and the one after it (kn, prefetched)
+    Mask rest = cand & ~Mask(1);
+    int k = lowest_bit(rest);
+    rest &= rest - 1;
+    double sk = colS[k * THREADS + tid];
+    double wk = W ? colW[W ? k * THREADS + tid : 0] : static_cast<double>(k);
+    int kn = rest ? lowest_bit(rest) : -1;
+    double skn = 0.0, wkn = 0.0;
+    if (kn >= 0) {
+      skn = colS[kn * THREADS + tid];
+      if constexpr (W) wkn = colW[kn * THREADS + tid];
+      else wkn = static_cast<double>(kn);
+    }
+    while (k >= 0) {
+      bool pop = false;
+      if (t2 >= 0) {
+        if constexpr (W) pop = pools<EXACT>(s1 - s2, w1 - w2, sk - s1, wk - w1);
+        else pop = pools<EXACT>(s1 - s2, static_cast<double>(t1 - t2), sk - s1,
+                                static_cast<double>(k - t1));
+      }
+      if (pop) {
+        m &= ~(Mask(1) << t1);
+        t1 = t2;
+        s1 = s2;
+        w1 = w2;
+        t2 = t3;
+        s2 = s3;
+        w2 = w3;
+        if (t3 >= 0) {
+          const Mask below = m & ((Mask(1) << t3) - Mask(1));
+          t3 = below ? highest_bit(below) : -1;
+          if (t3 >= 0) {
+            s3 = colS[t3 * THREADS + tid];
+            if constexpr (W) w3 = colW[t3 * THREADS + tid];
+            else w3 = static_cast<double>(t3);
+          }
+        }
+      } else {
+        m |= Mask(1) << k;
+        t3 = t2;
+        s3 = s2;
+        w3 = w2;
+        t2 = t1;
+        s2 = s1;
+        w2 = w1;
+        t1 = k;
+        s1 = sk;
+        w1 = wk;
+        k = kn;
+        sk = skn;
+        wk = wkn;
+        if (kn >= 0) {
+          rest &= rest - 1;
+          kn = rest ? lowest_bit(rest) : -1;
+          if (kn >= 0) {
+            skn = colS[kn * THREADS + tid];
+            if constexpr (W) wkn = colW[kn * THREADS + tid];
+            else wkn = static_cast<double>(kn);
+          }
+        }
+      }
+    }
+  }
+
+  // Slopes: backwards, each vertex i takes the slope to the next vertex; then forwards, each
+  // element the slope of the last vertex at or before it.
+  T fit[NMAX];
+  {
+    double slope[NMAX];
+    double se = 0.0, we = 0.0;
+#pragma unroll
+    for (int i = NMAX - 1; i >= 0; --i) {
+      if (i < nn) {
+        if (i == nn - 1) {
+          se = S[i + 1];
+          we = Wk(i + 1);
+        }
+        if ((m >> i) & 1ull) {
+          slope[i] = slope_div(se - S[i], we - Wk(i));
+          se = S[i];
+          we = Wk(i);
+        }
+      }
+    }
+    const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
+    const T tsgn = static_cast<T>(sgn);
+    double cur = 0.0;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      if (i < nn) {
+        if ((m >> i) & 1ull) cur = slope[i];
+        const T v = bad ? quiet_nan<T>() : tsgn * static_cast<T>(cur);
+        fit[i] = clip(v, use_lo, lo, use_hi, hi);
+      }
+    }
+  }
+
+  if (starts != nullptr && active) {
+    const uint32_t low = nn >= 32 ? 0xFFFFFFFFu : ((1u << nn) - 1u);
+    starts[row0 + tid] = bad ? 1u : static_cast<uint32_t>(m) & low;
+  }
+
+  if constexpr (DIRECT) {
+    if (active) store_row<T, NMAX>(out + (row0 + tid) * NMAX, fit);
+  } else {
+    __syncthreads();  // every thread is done with the point columns
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n && active) stg[tid * (n + 1) + c] = fit[c];
+    }
+    __syncthreads();
+    stage_out<T, THREADS>(out + row0 * n, stg, count, div);
+  }
+}
+
+// Backward: gy = w * mask * G / W, gw = (y - fit) * mask * G / W over each block, the block's
+// fit recomputed from the same float64 cumulative sums and division the forward used (so
+// bit-identical to it).
+template <typename T, int NMAX, bool W, bool DIRECT>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_kernel(
+    const uint32_t* __restrict__ starts, const T* __restrict__ g, const T* __restrict__ w,
+    const T* __restrict__ y, T* __restrict__ gy, T* __restrict__ gw, int64_t batch, int n,
+    unsigned flags, T lo, T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  // staging only (no point columns), one array of T at a time
+  __shared__ T stg[DIRECT ? 1 : (NMAX + 1) * THREADS];
+
+  const int tid = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
+  const int rows = static_cast<int>(min<int64_t>(THREADS, batch - row0));
+  const int count = rows * n;
+  const DivBy div(static_cast<uint32_t>(n));
+  const bool active = tid < rows;
+  const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
+  const bool need_mean = (gw != nullptr) || use_lo || use_hi;
+
+  T gv[NMAX];
+  T wv[W ? NMAX : 1];
+  T yv[NMAX];
+  const uint32_t bits = (active ? starts[row0 + tid] : 0u) | 1u;
+  if constexpr (DIRECT) {
+    if (active) {
+      load_row<T, NMAX>(g + (row0 + tid) * NMAX, gv);
+      if constexpr (W) load_row<T, NMAX>(w + (row0 + tid) * NMAX, wv);
+      if (need_mean) load_row<T, NMAX>(y + (row0 + tid) * NMAX, yv);
+    }
+  } else {
+    Span<T, THREADS, NMAX> sg, sw, sy;
+    sg.load(g + row0 * n, count);
+    if constexpr (W) sw.load(w + row0 * n, count);
+    if (need_mean) sy.load(y + row0 * n, count);
+    sg.to_lds(g + row0 * n, stg, count, div);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n) gv[c] = stg[tid * (n + 1) + c];
+    }
+    if constexpr (W) {
+      __syncthreads();
+      sw.to_lds(w + row0 * n, stg, count, div);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < n) wv[c] = stg[tid * (n + 1) + c];
+      }
+    }
+    if (need_mean) {
+      __syncthreads();
+      sy.to_lds(y + row0 * n, stg, count, div);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < n) yv[c] = stg[tid * (n + 1) + c];
+      }
+    }
+  }
+
+  // Cumulative sums of w*y and w exactly as the forward forms them (increasing sign).
+  double S[NMAX + 1];
+  double P[W ? NMAX + 1 : 1];
+  S[0] = 0.0;
+  if constexpr (W) P[0] = 0.0;
+  if (need_mean) {
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n) {
+        const double yc = static_cast<double>(yv[c]);
+        if constexpr (W) {
+          const double wc = static_cast<double>(wv[c]);
+          S[c + 1] = S[c] + wc * yc;
+          P[c + 1] = P[c] + wc;
+        } else {
+          S[c + 1] = S[c] + yc;
+        }
+      }
+    }
+  }
+  auto Wk = [&](int k) -> double {
+    if constexpr (W) return P[k];
+    else return static_cast<double>(k);
+  };
+
+  // Backwards: per block start i, q[i] = mask * G / W and fitv[i] = the block's fit.
+  double q[NMAX];
+  T fitv[NMAX];
+  {
+    double ga = 0.0, wa = 0.0, se = 0.0, we = 0.0;
+    int end = n;
+#pragma unroll
+    for (int i = NMAX - 1; i >= 0; --i) {
+      if (i < n) {
+        if (i == n - 1 && need_mean) {
+          se = S[i + 1];
+          we = Wk(i + 1);
+        }
+        ga += static_cast<double>(gv[i]);
+        if constexpr (W) wa += static_cast<double>(wv[i]);
+        if ((bits >> i) & 1u) {
+          const double wsum = W ? wa : static_cast<double>(end - i);
+          bool pass = true;
+          if (need_mean) {
+            const T f = static_cast<T>(slope_div(se - S[i], we - Wk(i)));
+            fitv[i] = f;
+            pass = !(use_lo || use_hi) || clip_passes(f, use_lo, lo, use_hi, hi);
+            se = S[i];
+            we = Wk(i);
+          }
+          q[i] = pass ? ga / wsum : 0.0;
+          ga = 0.0;
+          wa = 0.0;
+          end = i;
+        }
+      }
+    }
+  }
+  T oy[NMAX], ow[NMAX];
+  {
+    double cq = 0.0;
+    T cf = T(0);
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      if (i < n) {
+        if ((bits >> i) & 1u) {
+          cq = q[i];
+          if (need_mean) cf = fitv[i];
+        }
+        const double wi = W ? static_cast<double>(wv[W ? i : 0]) : 1.0;
+        oy[i] = static_cast<T>(wi * cq);
+        if (need_mean) {
+          ow[i] = static_cast<T>((static_cast<double>(yv[i]) - static_cast<double>(cf)) * cq);
+        }
+      }
+    }
+  }
+  if constexpr (DIRECT) {
+    if (active) {
+      if (gy != nullptr) store_row<T, NMAX>(gy + (row0 + tid) * NMAX, oy);
+      if (gw != nullptr) store_row<T, NMAX>(gw + (row0 + tid) * NMAX, ow);
+    }
+  } else {
+    if (gy != nullptr) {
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < n && active) stg[tid * (n + 1) + c] = oy[c];
+      }
+      __syncthreads();
+      stage_out<T, THREADS>(gy + row0 * n, stg, count, div);
+    }
+    if (gw != nullptr) {
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < n && active) stg[tid * (n + 1) + c] = ow[c];
+      }
+      __syncthreads();
+      stage_out<T, THREADS>(gw + row0 * n, stg, count, div);
+    }
+  }
+}
+
+bool aligned16(const void* p) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+template <typename T, int NMAX, bool W>
+hipError_t launch_fit(const ShortArgs& a) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  const unsigned blocks = static_cast<unsigned>((a.batch + THREADS - 1) / THREADS);
+  auto run = [&](auto kernel) {
+    kernel<<<dim3(blocks), dim3(THREADS), 0, a.stream>>>(
+        static_cast<const T*>(a.y), static_cast<const T*>(a.w), static_cast<T*>(a.out),
+        a.starts, a.bad_weight, a.batch, static_cast<int>(a.n), a.flags, static_cast<T>(a.lo),
+        static_cast<T>(a.hi));
+    return hipGetLastError();
+  };
+  if constexpr ((NMAX * sizeof(T)) % 16 == 0) {
+    if (a.n == NMAX && aligned16(a.y) && aligned16(a.w) && aligned16(a.out))
+      return run(short_fit_kernel<T, NMAX, W, true>);
+  }
+  return run(short_fit_kernel<T, NMAX, W, false>);
+}
+
+template <typename T, int NMAX, bool W>
+hipError_t launch_grad(const ShortGradArgs& a) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  const unsigned blocks = static_cast<unsigned>((a.batch + THREADS - 1) / THREADS);
+  auto run = [&](auto kernel) {
+    kernel<<<dim3(blocks), dim3(THREADS), 0, a.stream>>>(
+        a.starts, static_cast<const T*>(a.g), static_cast<const T*>(a.w),
+        static_cast<const T*>(a.y), static_cast<T*>(a.gy), static_cast<T*>(a.gw), a.batch,
+        static_cast<int>(a.n), a.flags, static_cast<T>(a.lo), static_cast<T>(a.hi));
+    return hipGetLastError();
+  };
+  if constexpr ((NMAX * sizeof(T)) % 16 == 0) {
+    if (a.n == NMAX && aligned16(a.g) && aligned16(a.w) && aligned16(a.y) && aligned16(a.gy) &&
+        aligned16(a.gw))
+      return run(short_grad_kernel<T, NMAX, W, true>);
+  }
+  return run(short_grad_kernel<T, NMAX, W, false>);
+}
+
+template <typename T, bool W>
+hipError_t fit_by_n(const ShortArgs& a) {
+  if (a.n <= 4) return launch_fit<T, 4, W>(a);
+  if (a.n <= 8) return launch_fit<T, 8, W>(a);
+  if (a.n <= 16) return launch_fit<T, 16, W>(a);
+  return launch_fit<T, 32, W>(a);
+}
+
+template <typename T, bool W>
+hipError_t grad_by_n(const ShortGradArgs& a) {
+  if (a.n <= 4) return launch_grad<T, 4, W>(a);
+  if (a.n <= 8) return launch_grad<T, 8, W>(a);
+  if (a.n <= 16) return launch_grad<T, 16, W>(a);
+  return launch_grad<T, 32, W>(a);
+}
+
+}  // namespace
+
+int64_t short_grid(int64_t batch, int64_t n, bool weighted) {
+  int threads = 0;
+  if (n <= 4) threads = weighted ? short_threads<4, true>() : short_threads<4, false>();
+  else if (n <= 8) threads = weighted ? short_threads<8, true>() : short_threads<8, false>();
+  else if (n <= 16) threads = weighted ? short_threads<16, true>() : short_threads<16, false>();
+  else threads = weighted ? short_threads<32, true>() : short_threads<32, false>();
+  return (batch + threads - 1) / threads;
+}
+
+hipError_t short_fit(const ShortArgs& a) {
+  const bool weighted = a.w != nullptr;
+  if (a.dtype == TI_F32) return weighted ? fit_by_n<float, true>(a) : fit_by_n<float, false>(a);
+  return weighted ? fit_by_n<double, true>(a) : fit_by_n<double, false>(a);
+}
+
+hipError_t short_grad(const ShortGradArgs& a) {
+  const bool weighted = a.w != nullptr;
+  if (a.dtype == TI_F32) return weighted ? grad_by_n<float, true>(a) : grad_by_n<float, false>(a);
+  return weighted ? grad_by_n<double, true>(a) : grad_by_n<double, false>(a);
+}
+
+}  // namespace ti
