@@ -1,0 +1,148 @@
+"""Rows longer than 32 elements (the tile kernels) on the GPU against the oracle: the
+reference's lane/chunk edge shapes and adversarial patterns (reference
+tests/test_cuda.py:31-134, 224-265) restated for the HIP path."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import check_fit, gpu_fit, tolerance
+
+pytestmark = pytest.mark.gpu
+
+# Tile sizes: 4096 elements unweighted, 2048 weighted; longer rows are merged across tiles.
+SHAPES = [33, 63, 64, 65, 100, 255, 256, 511, 1000, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096]
+LONG_SHAPES = [4097, 8193, 20_000, 100_000]
+MULTI_TILE = False  # rows longer than one tile
+
+
+def fits(n: int, weighted: bool) -> bool:
+    return MULTI_TILE or n <= (2048 if weighted else 4096)
+
+
+def data(batch: int, n: int, dtype: type, seed: int) -> tuple[np.ndarray, np.ndarray]:
+    rng = np.random.default_rng(seed)
+    y = (np.linspace(0, 3, n) + rng.standard_normal((batch, n))).astype(dtype)
+    w = (rng.random((batch, n)) + 0.1).astype(dtype)
+    return y, w
+
+
+@pytest.mark.parametrize("n", SHAPES)
+@pytest.mark.parametrize("batch", [1, 3, 70])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_tile_shapes(n: int, batch: int, dtype: type) -> None:
+    print(f"tiles n={n} batch={batch} dtype={np.dtype(dtype).name}", flush=True)
+    y, w = data(batch, n, dtype, n + batch)
+    check_fit(y)
+    check_fit(y, None, increasing=False, y_min=-0.5, y_max=2.0)
+    if fits(n, True):
+        check_fit(y, w, increasing=False)
+        check_fit(y, w, increasing=True, y_min=0.0, y_max=2.5)
+
+
+PATTERNS = ["increasing", "decreasing", "saw", "cliff", "walk", "constant", "valley", "zeros_ones"]
+
+
+def pattern(name: str, n: int, rng: np.random.Generator) -> np.ndarray:
+    i = np.arange(n, dtype=np.float64)
+    if name == "increasing":  # every point is a vertex
+        return i
+    if name == "decreasing":  # one block
+        return -i
+    if name == "saw":  # convex runs with drops, not aligned to threads or tiles
+        return i % 7 + (i % 1500) * 0.1
+    if name == "cliff":  # one bridge across almost everything
+        return np.where(i == n - 1, -1e9, i)
+    if name == "walk":
+        return rng.standard_normal(n).cumsum()
+    if name == "constant":  # collinear points everywhere
+        return np.ones(n)
+    if name == "zeros_ones":  # exact ties in means
+        return (rng.random(n) < 1 / (1 + np.exp(-np.linspace(-3, 3, n)))).astype(np.float64)
+    return (i - n / 3) ** 2  # valley: falls, then rises
+
+
+@pytest.mark.parametrize("name", PATTERNS)
+@pytest.mark.parametrize("n", [700, 1025, 2048, 3000, 4096])
+def test_tile_patterns(name: str, n: int) -> None:
+    print(f"pattern {name} n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    y = pattern(name, n, rng)[None]
+    w = rng.random((1, n)) + 0.1
+    ties = name in ("constant", "zeros_ones", "saw")
+    check_fit(y, check_starts=not ties)
+    if fits(n, True):
+        check_fit(y, w, check_starts=not ties)
+        check_fit(y, w, increasing=False, check_starts=not ties)
+    check_fit(y.astype(np.float32), check_starts=False)
+
+
+@pytest.mark.parametrize("n", [40, 2048, 4096])
+def test_exact_ties_partition(n: int) -> None:
+    # 0/1 labels with integer weights: every sum is an exact integer, so the partition must be
+    # the exact one (long-double oracle), ties pooled.
+    rng = np.random.default_rng(n)
+    y = (rng.random((20, n)) < 1 / (1 + np.exp(-np.linspace(-3, 3, n)))).astype(np.float32)
+    w = rng.integers(1, 6, (20, n)).astype(np.float32)
+    for ww in (None, w):
+        if not fits(n, ww is not None):
+            continue
+        got, starts = gpu_fit(y, ww)
+        want, want_starts = oracle.pava(y, ww, acc="f64x")
+        assert np.abs(got - want).max() <= tolerance(y)
+        np.testing.assert_array_equal(starts, want_starts)
+
+
+def test_nan_rows_long() -> None:
+    rng = np.random.default_rng(1)
+    y = rng.standard_normal((40, 3000))
+    y[3, 17] = np.nan
+    y[39, 2999] = np.nan
+    y[20, 0] = np.nan
+    check_fit(y)
+    check_fit(y.astype(np.float32), increasing=False)
+
+
+@pytest.mark.parametrize("big", [1e3, 1e6, 1e12])
+@pytest.mark.parametrize("n", [500, 2048])
+def test_cancelling_sums(n: int, big: float) -> None:
+    # reference tests/test_cuda.py:243-265: per 64 elements, 32 of +big, one of -32 big, then
+    # small near-collinear values; coordinates are differences of far larger terms.
+    rng = np.random.default_rng(n)
+    k = np.arange(n) % 64
+    y = np.where(k < 32, big, 1.0)
+    y[k == 32] = -32 * big
+    y = y + 1e-3 * (-1.0) ** k * (k > 32) + 1e-6 * rng.standard_normal(n)
+    for w in (None, rng.random(n) + 0.1):
+        for dtype, step, dev in ((np.float64, 8 * 2.0**-52, 1e-14), (np.float32, 0, 1e-7)):
+            yy = y.astype(dtype)[None]
+            ww = None if w is None else w.astype(dtype)[None]
+            want, _ = oracle.pava(yy.astype(np.float64), None if ww is None else ww.astype(np.float64))
+            got, _ = gpu_fit(yy, ww, with_starts=False)
+            got = got.astype(np.float64)
+            scale = float(np.abs(yy.astype(np.float64)).max())
+            assert float((got[:, :-1] - got[:, 1:]).max()) <= step * scale
+            assert float(np.abs(got - want).max()) <= dev * scale
+
+
+@pytest.mark.parametrize("name", ["collinear", "offset", "consecutive"])
+def test_float32_fit_is_monotone_long(name: str) -> None:
+    rng = np.random.default_rng(2)
+    n = 4096
+    i = np.arange(n, dtype=np.float64)
+    one = np.float32(1.0).view(np.int32)
+    y = {
+        "collinear": 1e6 + 1e-3 * i + 1e-9 * rng.standard_normal(n),
+        "offset": 1e6 + rng.standard_normal(n),
+        "consecutive": (one + np.arange(n, dtype=np.int32)).view(np.float32).astype(np.float64),
+    }[name].astype(np.float32)[None]
+    u = rng.random((1, n))
+    for w in (None, (u + 0.1).astype(np.float32), np.exp(8 * u).astype(np.float32)):
+        if w is not None:
+            yy, ww = y[:, :2048], w[:, :2048]
+        else:
+            yy, ww = y, None
+        got, _ = gpu_fit(np.ascontiguousarray(yy), None if ww is None else np.ascontiguousarray(ww), with_starts=False)
+        assert (np.diff(got, axis=1) >= 0).all()

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "ti_kernels.h"
+#include "ti_tile.h"
 
 namespace {
 
@@ -73,8 +74,8 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
-  if (n <= ti::kShortMax) return ok();
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+  if (n <= ti::tile_elems(weighted != 0)) return ok();
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::tile_elems(weighted != 0));
 }
 
 int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
@@ -92,7 +93,14 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
                     static_cast<hipStream_t>(stream)};
     return launched(ti::short_fit(a), "short-row fit");
   }
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+  const int64_t tn = ti::tile_elems(w != nullptr);
+  if (n <= tn) {
+    if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
+    ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
+                   nullptr, 0, 0, static_cast<hipStream_t>(stream)};
+    return launched(ti::tile_run(a, ti::kTileSingle), "single-tile fit");
+  }
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)tn);
 }
 
 int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes) {

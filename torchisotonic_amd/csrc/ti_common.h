@@ -68,6 +68,39 @@ __device__ __forceinline__ double slope_div(double num, double den) {
   return __builtin_fma(__builtin_fma(-den, q, num), r, q);
 }
 
+// Double-double numbers (hi + lo, |lo| <= ulp(hi)/2): cumulative sums across threads, tiles and
+// rows, so that the difference of two nearby points keeps the precision of the difference
+// (Knuth's two-sum, Dekker's fast two-sum).
+struct DD {
+  double hi, lo;
+};
+
+__device__ __forceinline__ DD two_sum(double a, double b) {
+  const double s = a + b;
+  const double bb = s - a;
+  const double e = (a - (s - bb)) + (b - bb);
+  return {s, e};
+}
+
+__device__ __forceinline__ DD dd_add(DD a, DD b) {
+  DD s = two_sum(a.hi, b.hi);
+  const double e = s.lo + (a.lo + b.lo);
+  const double hi = s.hi + e;
+  return {hi, e - (hi - s.hi)};
+}
+
+__device__ __forceinline__ DD dd_add(DD a, double b) {
+  DD s = two_sum(a.hi, b);
+  const double e = s.lo + a.lo;
+  const double hi = s.hi + e;
+  return {hi, e - (hi - s.hi)};
+}
+
+// a - b, rounded once to a double.
+__device__ __forceinline__ double dd_diff(DD a, DD b) {
+  return (a.hi - b.hi) + (a.lo - b.lo);
+}
+
 template <typename T>
 __device__ __forceinline__ T quiet_nan();
 template <>

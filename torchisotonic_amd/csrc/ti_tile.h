@@ -1,0 +1,93 @@
+// Shared definitions of the long-row kernels: tile geometry, launch arguments and the layout of
+// the hull arrays that tiles and merged nodes leave in the workspace.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ti_kernels.h"
+
+namespace ti {
+
+constexpr int kWaves256 = 4;
+constexpr int kTileSingle = 0;  // the row is one tile: write the fit
+constexpr int kTileHull = 1;    // write the tile's hull for the cross-tile merge
+
+// 256 threads x E elements: E = 16 unweighted (4096-element tiles), 8 weighted (2048), so that
+// the LDS slots (E + 1 per thread) stay near 50 KB and three workgroups share a CU.
+template <bool W>
+struct TileCfg {
+  static constexpr int kThreads = 256;
+  static constexpr int kLogE = W ? 3 : 4;
+  static constexpr int kE = 1 << kLogE;
+  static constexpr int kN = kThreads * kE;
+  static constexpr int kSlots = kThreads * (kE + 1);
+};
+
+struct TileArgs {
+  const void* y;
+  const void* w;
+  void* out;
+  uint32_t* starts;
+  uint32_t* bad_weight;
+  int64_t batch, n;
+  int dtype;
+  unsigned flags;
+  double lo, hi;
+  void* scratch;       // hull arrays of all tiles (kTileHull)
+  int64_t tiles_total; // nodes in that array
+  int64_t cap;         // vertex capacity per node
+  hipStream_t stream;
+};
+
+// One node's hull array in a node array of K nodes with `cap` vertices each: vertex indices
+// relative to the node's first element, cumulative sums (double-double) relative to the node's
+// first point, the vertex count, a NaN flag and the node totals (W hi, W lo, S hi, S lo).
+struct NodeOut {
+  int* count;
+  int* bad;
+  double* tot;
+  int* idx;
+  double *shi, *slo, *whi, *wlo;
+};
+
+__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+__host__ __device__ inline size_t node_array_bytes(int64_t K, int64_t cap, bool weighted) {
+  const size_t k = static_cast<size_t>(K), c = static_cast<size_t>(cap);
+  size_t b = align256(k * 4) * 2 + align256(k * 32);
+  b += align256(k * c * 4) + align256(k * c * 8) * (weighted ? 4 : 2);
+  return b;
+}
+
+__host__ __device__ inline NodeOut node_out(void* base, int64_t K, int64_t cap, bool weighted, int64_t k) {
+  char* p = static_cast<char*>(base);
+  const size_t kk = static_cast<size_t>(K), c = static_cast<size_t>(cap);
+  NodeOut o;
+  o.count = reinterpret_cast<int*>(p) + k;
+  p += align256(kk * 4);
+  o.bad = reinterpret_cast<int*>(p) + k;
+  p += align256(kk * 4);
+  o.tot = reinterpret_cast<double*>(p) + 4 * k;
+  p += align256(kk * 32);
+  o.idx = reinterpret_cast<int*>(p) + k * cap;
+  p += align256(kk * c * 4);
+  o.shi = reinterpret_cast<double*>(p) + k * cap;
+  p += align256(kk * c * 8);
+  o.slo = reinterpret_cast<double*>(p) + k * cap;
+  p += align256(kk * c * 8);
+  if (weighted) {
+    o.whi = reinterpret_cast<double*>(p) + k * cap;
+    p += align256(kk * c * 8);
+    o.wlo = reinterpret_cast<double*>(p) + k * cap;
+  } else {
+    o.whi = o.wlo = nullptr;
+  }
+  return o;
+}
+
+int64_t tile_elems(bool weighted);
+hipError_t tile_run(const TileArgs& a, int mode);
+
+}  // namespace ti
