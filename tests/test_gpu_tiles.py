@@ -146,3 +146,115 @@ def test_float32_fit_is_monotone_long(name: str) -> None:
             yy, ww = y, None
         got, _ = gpu_fit(np.ascontiguousarray(yy), None if ww is None else np.ascontiguousarray(ww), with_starts=False)
         assert (np.diff(got, axis=1) >= 0).all()
+
+
+def grad_rows(batch: int, n: int, seed: int, dtype=np.float64):
+    rng = np.random.default_rng(seed)
+    y = (np.linspace(0, 3, n) + rng.standard_normal((batch, n))).astype(dtype)
+    w = (rng.random((batch, n)) + 0.1).astype(dtype)
+    c = rng.standard_normal((batch, n)).astype(dtype)
+    return y, w, c
+
+
+def gpu_grads(y, w, c, **kw):
+    import torch
+
+    import torchisotonic_amd
+
+    yy = torch.from_numpy(y).cuda().requires_grad_()
+    ww = None if w is None else torch.from_numpy(w).cuda().requires_grad_()
+    fit = torchisotonic_amd.isotonic(yy, ww, **kw)
+    inputs = (yy,) if ww is None else (yy, ww)
+    gs = torch.autograd.grad((fit * torch.from_numpy(c).cuda()).sum(), inputs)
+    return [x.cpu().numpy() for x in gs], fit.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize(("batch", "n"), [(70, 33), (9, 64), (9, 65), (7, 128), (5, 512), (5, 513),
+                                          (5, 1000), (5, 1024), (3, 1025), (3, 2048), (3, 4096)])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_tile_gradients_match_oracle(batch: int, n: int, dtype: type) -> None:
+    # reference tests/test_cuda.py:137-157: the gradient against the CPU's closed form on the
+    # oracle's partition (tie-free data), weighted (when one tile holds the row) and not.
+    print(f"tile grad batch={batch} n={n} dtype={np.dtype(dtype).name}", flush=True)
+    y, w, c = grad_rows(batch, n, n, dtype)
+    tol = 1e-12 if dtype == np.float64 else 2e-5
+    for inc in (True, False):
+        for weights in (w, None):
+            if weights is not None and not fits(n, True):
+                continue
+            gs, _ = gpu_grads(y, weights, c, increasing=inc)
+            fit, starts = oracle.pava(y, weights, increasing=inc, acc="f64")
+            ey, ew = oracle.block_grad(
+                starts, c.astype(np.float64), None if weights is None else weights.astype(np.float64),
+                y.astype(np.float64), fit, want_w=weights is not None,
+            )
+            np.testing.assert_allclose(gs[0], ey, rtol=tol, atol=tol)
+            if weights is not None:
+                scale = tol * (1 + float(np.abs(y).max()))
+                np.testing.assert_allclose(gs[1], ew, rtol=tol, atol=scale)
+
+
+@pytest.mark.parametrize("name", PATTERNS)
+@pytest.mark.parametrize("n", [1024, 1025, 2048, 3000])
+def test_tile_gradient_is_block_average(name: str, n: int) -> None:
+    # reference tests/test_cuda.py:160-183: whatever the data (ties included) the gradient is
+    # the block average over the blocks the GPU's fit reports.
+    import torch
+
+    from torchisotonic_amd import _ext
+
+    rng = np.random.default_rng(n)
+    y = np.broadcast_to(pattern(name, n, rng), (3, n)).copy()
+    w = rng.random((3, n)) + 0.1
+    c = rng.standard_normal((3, n))
+    for weights in (w, None):
+        if weights is not None and not fits(n, True):
+            continue
+        gs, fit = gpu_grads(y, weights, c)
+        _, starts = _ext.isotonic_tiles(
+            torch.from_numpy(y).cuda(), None if weights is None else torch.from_numpy(weights).cuda(),
+            True, True, True,
+        )
+        s = starts.cpu().numpy().astype(np.uint8)
+        ey, ew = oracle.block_grad(s, c, weights, y, fit, want_w=weights is not None)
+        np.testing.assert_allclose(gs[0], ey, rtol=1e-9, atol=1e-9)
+        if weights is not None:
+            np.testing.assert_allclose(gs[1], ew, rtol=1e-9, atol=1e-9 * (1 + np.abs(y).max()))
+
+
+@pytest.mark.parametrize("n", [100, 2048])
+def test_tile_clamp_gradient_matches_torch_clamp(n: int) -> None:
+    import torch
+
+    import torchisotonic_amd
+
+    rng = np.random.default_rng(n)
+    y = np.round(rng.standard_normal((20, n)) * 2) / 2
+    w = rng.random(y.shape) + 0.1
+    c = rng.standard_normal(y.shape)
+    for lo, hi in ((-0.5, 0.5), (0.0, None), (None, 1.0), (1.0, -1.0)):
+        yy = torch.from_numpy(y).cuda().requires_grad_()
+        ww = torch.from_numpy(w).cuda().requires_grad_()
+        out = torchisotonic_amd.isotonic(yy, ww, y_min=lo, y_max=hi)
+        gy, gw = torch.autograd.grad((out * torch.from_numpy(c).cuda()).sum(), (yy, ww))
+        yy2 = torch.from_numpy(y).cuda().requires_grad_()
+        ww2 = torch.from_numpy(w).cuda().requires_grad_()
+        out2 = torchisotonic_amd.isotonic(yy2, ww2).clamp(min=lo, max=hi)
+        gy2, gw2 = torch.autograd.grad((out2 * torch.from_numpy(c).cuda()).sum(), (yy2, ww2))
+        torch.testing.assert_close(out, out2, rtol=0, atol=0)
+        torch.testing.assert_close(gy, gy2, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(gw, gw2, rtol=1e-12, atol=1e-12)
+
+
+def test_tile_gradcheck() -> None:
+    import torch
+    from torch.autograd import gradcheck
+
+    import torchisotonic_amd
+
+    g = torch.Generator().manual_seed(0)
+    y = torch.randn(2, 40, generator=g, dtype=torch.float64).cuda().requires_grad_()
+    w = (torch.rand(2, 40, generator=g, dtype=torch.float64) + 0.1).cuda().requires_grad_()
+    for kw in ({}, {"increasing": False}, {"y_min": -0.3, "y_max": 0.5}):
+        assert gradcheck(lambda y, w: torchisotonic_amd.isotonic(y, w, **kw), (y, w))
+        assert gradcheck(lambda y: torchisotonic_amd.isotonic(y, **kw), (y,))

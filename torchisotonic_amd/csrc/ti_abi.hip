@@ -108,8 +108,8 @@ int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
-  if (n <= ti::kShortMax) return ok();
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+  if (n <= ti::tile_elems(weighted != 0)) return ok();
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::tile_elems(weighted != 0));
 }
 
 int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy,
@@ -130,7 +130,14 @@ int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, 
                         static_cast<hipStream_t>(stream)};
     return launched(ti::short_grad(a), "short-row gradient");
   }
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::kShortMax);
+  const int64_t tn = ti::tile_elems(w != nullptr);
+  if (n <= tn) {
+    if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
+    ti::TileGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
+                       static_cast<hipStream_t>(stream)};
+    return launched(ti::tile_grad_single(a), "single-tile gradient");
+  }
+  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)tn);
 }
 
 int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n, void* stream) {

@@ -87,7 +87,67 @@ __host__ __device__ inline NodeOut node_out(void* base, int64_t K, int64_t cap, 
   return o;
 }
 
+struct TileGradArgs {
+  const uint32_t* starts;
+  const void* g;
+  const void* w;
+  const void* y;
+  void* gy;
+  void* gw;
+  int64_t batch, n;
+  int dtype;
+  unsigned flags;
+  double lo, hi;
+  hipStream_t stream;
+};
+
+// E consecutive elements of one thread (count of them valid): 16-byte loads when whole and
+// aligned, element by element otherwise.
+template <typename T, int E>
+__device__ __forceinline__ void load_elems_any(const T* __restrict__ p, int count, T (&v)[E]) {
+  constexpr int V = 16 / sizeof(T);
+  using VT = T __attribute__((ext_vector_type(V)));
+  if (count == E && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    const VT* q = reinterpret_cast<const VT*>(p);
+    VT buf[E / V];
+#pragma unroll
+    for (int j = 0; j < E / V; ++j) buf[j] = q[j];
+#pragma unroll
+    for (int j = 0; j < E / V; ++j) {
+#pragma unroll
+      for (int t = 0; t < V; ++t) v[j * V + t] = buf[j][t];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if (k < count) v[k] = p[k];
+    }
+  }
+}
+
+template <typename T, int E>
+__device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, const T (&v)[E]) {
+  constexpr int V = 16 / sizeof(T);
+  using VT = T __attribute__((ext_vector_type(V)));
+  if (count == E && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    VT* q = reinterpret_cast<VT*>(p);
+#pragma unroll
+    for (int j = 0; j < E / V; ++j) {
+      VT x;
+#pragma unroll
+      for (int t = 0; t < V; ++t) x[t] = v[j * V + t];
+      q[j] = x;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if (k < count) p[k] = v[k];
+    }
+  }
+}
+
 int64_t tile_elems(bool weighted);
 hipError_t tile_run(const TileArgs& a, int mode);
+hipError_t tile_grad_single(const TileGradArgs& a);
 
 }  // namespace ti

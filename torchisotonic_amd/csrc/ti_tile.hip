@@ -34,8 +34,11 @@ namespace {
 template <typename T, bool W>
 struct TileShared {
   using C = TileCfg<W>;
+  static constexpr bool kPairs = sizeof(T) == 8;
   double ls[C::kSlots];              // cumulative w*y, relative to the point's owner thread
   double lw[W ? C::kSlots : 1];      // cumulative w, likewise (unweighted: the index)
+  float ls_lo[kPairs ? C::kSlots : 1];  // float64 data: the sums' rounding errors
+  float lw_lo[kPairs && W ? C::kSlots : 1];
   int16_t idx[C::kSlots];            // the point's index within the tile
   double off_s[2][C::kThreads + 1];  // owner offsets (hi, lo); [kThreads]: the tile total
   double off_w[2][W ? C::kThreads + 1 : 1];
@@ -49,10 +52,13 @@ struct TileShared {
   int wbad;
 };
 
-// A point of the tile: index, and sums relative to its owner thread (index >> kLogE).
+// A point of the tile: index, and sums relative to its owner thread (index >> kLogE); for
+// float64 data each sum is hi + lo (lo kept as float32 in LDS), so that the difference of
+// neighbouring points is the product w*y itself.
 struct Pt {
   int i;
   double w, s;
+  double wl, sl;
 };
 
 template <typename T, bool W>
@@ -60,11 +66,15 @@ struct TileOps {
   using C = TileCfg<W>;
   using Sh = TileShared<T, W>;
 
+  static constexpr bool kPairs = Sh::kPairs;
+
   __device__ static Pt load(const Sh& sh, int slot) {
     Pt p;
     p.i = sh.idx[slot];
     p.s = sh.ls[slot];
     p.w = W ? sh.lw[W ? slot : 0] : 0.0;
+    p.sl = kPairs ? static_cast<double>(sh.ls_lo[kPairs ? slot : 0]) : 0.0;
+    p.wl = (kPairs && W) ? static_cast<double>(sh.lw_lo[(kPairs && W) ? slot : 0]) : 0.0;
     return p;
   }
 
@@ -72,18 +82,28 @@ struct TileOps {
     sh.idx[slot] = static_cast<int16_t>(p.i);
     sh.ls[slot] = p.s;
     if constexpr (W) sh.lw[slot] = p.w;
+    if constexpr (kPairs) sh.ls_lo[slot] = static_cast<float>(p.sl);
+    if constexpr (kPairs && W) sh.lw_lo[slot] = static_cast<float>(p.wl);
   }
 
-  // b - a as (dW, dS).
+  // b - a as (dW, dS). Across owners the whole difference is formed in double-double and
+  // rounded once: the owners' offset difference, plus b's local sum, minus a's.
   __device__ static void diff(const Sh& sh, const Pt& a, const Pt& b, double& dW, double& dS) {
     const int oa = a.i >> C::kLogE, ob = b.i >> C::kLogE;
     if (oa == ob) {
-      dS = b.s - a.s;
-      if constexpr (W) dW = b.w - a.w;
+      dS = (b.s - a.s) + (b.sl - a.sl);
+      if constexpr (W) dW = (b.w - a.w) + (b.wl - a.wl);
     } else {
-      dS = ((sh.off_s[0][ob] - sh.off_s[0][oa]) + (sh.off_s[1][ob] - sh.off_s[1][oa])) + (b.s - a.s);
-      if constexpr (W)
-        dW = ((sh.off_w[0][ob] - sh.off_w[0][oa]) + (sh.off_w[1][ob] - sh.off_w[1][oa])) + (b.w - a.w);
+      DD d = dd_add(DD{sh.off_s[0][ob], sh.off_s[1][ob]}, DD{-sh.off_s[0][oa], -sh.off_s[1][oa]});
+      d = dd_add(dd_add(d, b.s), -a.s);
+      if constexpr (kPairs) d = dd_add(d, b.sl - a.sl);
+      dS = d.hi + d.lo;
+      if constexpr (W) {
+        DD e = dd_add(DD{sh.off_w[0][ob], sh.off_w[1][ob]}, DD{-sh.off_w[0][oa], -sh.off_w[1][oa]});
+        e = dd_add(dd_add(e, b.w), -a.w);
+        if constexpr (kPairs) e = dd_add(e, b.wl - a.wl);
+        dW = e.hi + e.lo;
+      }
     }
     if constexpr (!W) dW = static_cast<double>(b.i - a.i);
   }
@@ -203,49 +223,6 @@ __device__ __forceinline__ int wave_scan_int(int v, int lane) {
   return v;
 }
 
-template <typename T, int E>
-__device__ __forceinline__ void load_elems(const T* __restrict__ p, int count, T (&v)[E]) {
-  constexpr int V = 16 / sizeof(T);
-  using VT = T __attribute__((ext_vector_type(V)));
-  if (count == E && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-    const VT* q = reinterpret_cast<const VT*>(p);
-    VT buf[E / V];
-#pragma unroll
-    for (int j = 0; j < E / V; ++j) buf[j] = q[j];
-#pragma unroll
-    for (int j = 0; j < E / V; ++j) {
-#pragma unroll
-      for (int t = 0; t < V; ++t) v[j * V + t] = buf[j][t];
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < E; ++k) {
-      if (k < count) v[k] = p[k];
-    }
-  }
-}
-
-template <typename T, int E>
-__device__ __forceinline__ void store_elems(T* __restrict__ p, int count, const T (&v)[E]) {
-  constexpr int V = 16 / sizeof(T);
-  using VT = T __attribute__((ext_vector_type(V)));
-  if (count == E && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-    VT* q = reinterpret_cast<VT*>(p);
-#pragma unroll
-    for (int j = 0; j < E / V; ++j) {
-      VT x;
-#pragma unroll
-      for (int t = 0; t < V; ++t) x[t] = v[j * V + t];
-      q[j] = x;
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < E; ++k) {
-      if (k < count) p[k] = v[k];
-    }
-  }
-}
-
 template <int E>
 struct LocalMask {
   using type = typename std::conditional<(E < 32), uint32_t, uint64_t>::type;
@@ -284,38 +261,62 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
   // 1. Elements and local cumulative sums.
   T yv[E];
   T wv[W ? E : 1];
-  load_elems<T, E>(y + t0, ecount, yv);
-  if constexpr (W) load_elems<T, E>(w + t0, ecount, wv);
-  double S[E + 1];
-  double P[W ? E + 1 : 1];
+  load_elems_any<T, E>(y + t0, ecount, yv);
+  if constexpr (W) load_elems_any<T, E>(w + t0, ecount, wv);
+  // (float64 data: each sum also carries its rounding errors, SL / PL)
+  constexpr bool PAIRS = Sh::kPairs;
+  double S[E + 1], SL[PAIRS ? E + 1 : 1];
+  double P[W ? E + 1 : 1], PL[PAIRS && W ? E + 1 : 1];
   bool bad = false, wbad = false;
   S[0] = 0.0;
+  if constexpr (PAIRS) SL[0] = 0.0;
   if constexpr (W) P[0] = 0.0;
+  if constexpr (PAIRS && W) PL[0] = 0.0;
 #pragma unroll
   for (int k = 0; k < E; ++k) {
+    double term = 0.0, wk = 1.0;
     if (k < ecount) {
       const double yk = sgn * static_cast<double>(yv[k]);
       bad |= yk != yk;
       if constexpr (W) {
-        const double wk = static_cast<double>(wv[k]);
+        wk = static_cast<double>(wv[k]);
         wbad |= !(wk > 0.0);
-        S[k + 1] = S[k] + wk * yk;
-        P[k + 1] = P[k] + wk;
+        term = wk * yk;
       } else {
-        S[k + 1] = S[k] + yk;
+        term = yk;
       }
     } else {
-      S[k + 1] = S[k];
-      if constexpr (W) P[k + 1] = P[k];
+      wk = 0.0;
+    }
+    if constexpr (PAIRS) {
+      const DD t = two_sum(S[k], term);
+      S[k + 1] = t.hi;
+      SL[k + 1] = SL[k] + t.lo;
+    } else {
+      S[k + 1] = S[k] + term;
+    }
+    if constexpr (W) {
+      if constexpr (PAIRS) {
+        const DD t = two_sum(P[k], wk);
+        P[k + 1] = t.hi;
+        PL[k + 1] = PL[k] + t.lo;
+      } else {
+        P[k + 1] = P[k] + wk;
+      }
     }
   }
+  auto sum_s = [&](int k) -> DD { return DD{S[k], PAIRS ? SL[PAIRS ? k : 0] : 0.0}; };
+  auto sum_w = [&](int k) -> DD {
+    if constexpr (W) return DD{P[k], PAIRS ? PL[PAIRS ? k : 0] : 0.0};
+    else return DD{static_cast<double>(k), 0.0};
+  };
 
   // Thread offsets within the tile: exclusive double-double scans of the thread totals.
   {
-    DD vs{S[E], 0.0};
+    DD vs = sum_s(E);
     DD is = wave_scan_dd(vs, lane);
     DD iw{0.0, 0.0};
-    if constexpr (W) iw = wave_scan_dd(DD{P[E], 0.0}, lane);
+    if constexpr (W) iw = wave_scan_dd(sum_w(E), lane);
     __syncthreads();  // sh.bad initialised before anyone ORs into it
     if (bad) sh.bad = 1;
     if (wbad) sh.wbad = 1;
@@ -369,6 +370,8 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
         sh.idx[base + k] = static_cast<int16_t>(t0 + k);
         sh.ls[base + k] = S[k];
         if constexpr (W) sh.lw[base + k] = P[k];
+        if constexpr (PAIRS) sh.ls_lo[base + k] = static_cast<float>(SL[k]);
+        if constexpr (PAIRS && W) sh.lw_lo[base + k] = static_cast<float>(PL[k]);
       }
     }
     Mask m = 1;
@@ -379,59 +382,59 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
         const bool lt = sgn > 0.0 ? yv[k - 1] < yv[k] : yv[k] < yv[k - 1];
         if (k < ecount && lt) cand |= Mask(1) << k;
       }
+      // stack: t1 (last vertex), t2, t3 (< 0: none); their points p1, p2, p3 (local sums)
+      auto lpt = [&](int kk) -> Pt {
+        Pt p = Ops::load(sh, base + kk);
+        p.i = kk;
+        return p;
+      };
+      auto ldiff = [&](const Pt& a0, const Pt& b0, double& dW, double& dS) {
+        dS = (b0.s - a0.s) + (b0.sl - a0.sl);
+        if constexpr (W) dW = (b0.w - a0.w) + (b0.wl - a0.wl);
+        else dW = static_cast<double>(b0.i - a0.i);
+      };
       int t1 = 0, t2 = -1, t3 = -1;
-      double s1 = 0.0, s2 = 0.0, s3 = 0.0, w1 = 0.0, w2 = 0.0, w3 = 0.0;
+      Pt p1 = lpt(0), p2 = p1, p3 = p1;
       Mask rest = cand & ~Mask(1);
       int k = __builtin_ctz(static_cast<uint32_t>(rest));
       rest &= rest - 1;
-      double sk = sh.ls[base + k];
-      double wk = W ? sh.lw[W ? base + k : 0] : static_cast<double>(k);
+      Pt pk = lpt(k);
       int kn = rest ? static_cast<int>(__builtin_ctz(static_cast<uint32_t>(rest))) : -1;
-      double skn = 0.0, wkn = 0.0;
-      if (kn >= 0) {
-        skn = sh.ls[base + kn];
-        wkn = W ? sh.lw[W ? base + kn : 0] : static_cast<double>(kn);
-      }
+      Pt pkn = pk;
+      if (kn >= 0) pkn = lpt(kn);
       while (k >= 0) {
         bool pop = false;
-        if (t2 >= 0) pop = pools<EXACT_LOCAL>(s1 - s2, w1 - w2, sk - s1, wk - w1);
+        if (t2 >= 0) {
+          double dW1, dS1, dW2, dS2;
+          ldiff(p2, p1, dW1, dS1);
+          ldiff(p1, pk, dW2, dS2);
+          pop = pools<EXACT_LOCAL>(dS1, dW1, dS2, dW2);
+        }
         if (pop) {
           m &= ~(Mask(1) << t1);
           t1 = t2;
-          s1 = s2;
-          w1 = w2;
+          p1 = p2;
           t2 = t3;
-          s2 = s3;
-          w2 = w3;
+          p2 = p3;
           if (t3 >= 0) {
             const Mask below = m & ((Mask(1) << t3) - Mask(1));
             t3 = below ? 31 - __builtin_clz(static_cast<uint32_t>(below)) : -1;
-            if (t3 >= 0) {
-              s3 = sh.ls[base + t3];
-              w3 = W ? sh.lw[W ? base + t3 : 0] : static_cast<double>(t3);
-            }
+            if (t3 >= 0) p3 = lpt(t3);
           }
         } else {
           m |= Mask(1) << k;
           t3 = t2;
-          s3 = s2;
-          w3 = w2;
+          p3 = p2;
           t2 = t1;
-          s2 = s1;
-          w2 = w1;
+          p2 = p1;
           t1 = k;
-          s1 = sk;
-          w1 = wk;
+          p1 = pk;
           k = kn;
-          sk = skn;
-          wk = wkn;
+          pk = pkn;
           if (kn >= 0) {
             rest &= rest - 1;
             kn = rest ? static_cast<int>(__builtin_ctz(static_cast<uint32_t>(rest))) : -1;
-            if (kn >= 0) {
-              skn = sh.ls[base + kn];
-              wkn = W ? sh.lw[W ? base + kn : 0] : static_cast<double>(kn);
-            }
+            if (kn >= 0) pkn = lpt(kn);
           }
         }
       }
@@ -442,13 +445,11 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
     while (v) {
       const int kk = __builtin_ctz(static_cast<uint32_t>(v));
       v &= v - 1;
-      Pt p;
+      Pt p = Ops::load(sh, base + kk);
       p.i = t0 + kk;
-      p.s = sh.ls[base + kk];
-      p.w = W ? sh.lw[W ? base + kk : 0] : 0.0;
       if (kk == E) {
-        p.s = 0.0;
-        p.w = 0.0;
+        p.s = p.sl = 0.0;
+        p.w = p.wl = 0.0;
       }
       Ops::store(sh, base + count, p);
       ++count;
@@ -549,7 +550,7 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
       fit[k] = clip(v, use_lo, lo, use_hi, hi);
     }
     T* out = static_cast<T*>(a.out) + row * a.n + first;
-    store_elems<T, E>(out + t0, ecount, fit);
+    store_elems_any<T, E>(out + t0, ecount, fit);
     if (a.starts != nullptr && ecount > 0) {
       uint32_t sb = row_bad ? (t0 == 0 ? 1u : 0u) : mybits;
       if (ecount < E) sb &= (1u << ecount) - 1u;
@@ -578,11 +579,11 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
       const Pt p = Ops::load(sh, j);
       const int ow = p.i >> C::kLogE;
       o.idx[j] = p.i;
-      const DD s = dd_add(DD{sh.off_s[0][ow], sh.off_s[1][ow]}, p.s);
+      const DD s = dd_add(dd_add(DD{sh.off_s[0][ow], sh.off_s[1][ow]}, p.s), p.sl);
       o.shi[j] = s.hi;
       o.slo[j] = s.lo;
       if constexpr (W) {
-        const DD ww = dd_add(DD{sh.off_w[0][ow], sh.off_w[1][ow]}, p.w);
+        const DD ww = dd_add(dd_add(DD{sh.off_w[0][ow], sh.off_w[1][ow]}, p.w), p.wl);
         o.whi[j] = ww.hi;
         o.wlo[j] = ww.lo;
       }
