@@ -95,21 +95,28 @@ int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
  * grad.cuh:386-413) together with the clamp's backward (torch's, applied by autograd in the
  * reference, _api.py:69).
  *
- * With G, W and M the sums of g, w and w*y over an element's block (W = count when w is
- * NULL) and mask = [y_min <= M/W <= y_max] for the flags set (the unclamped fit, rounded to
- * dtype, against the bounds rounded to dtype; torch.clamp's backward, equality passes):
- *   gy_i = w_i * mask * G / W,          gw_i = (y_i - M / W) * mask * G / W.
- * The block mean M/W is recomputed from y and w, so the forward's output is not read.
+ * With G, W and F the sum of g, the sum of w (the count when w is NULL) and the fit (unclamped,
+ * rounded to dtype) over an element's block, and mask = [y_min <= F <= y_max] for the flags set
+ * (torch.clamp's backward: equality passes, a NaN fit passes nothing):
+ *   gy_i = w_i * mask * G / W,          gw_i = (y_i - F) * mask * G / W.
+ * A row holding a NaN is one block with F = NaN (the reference CPU path's convention).
  *
  *   starts  the partition ti_fwd wrote for the same y, w.
+ *   fwd_workspace / fwd_workspace_bytes: the workspace ti_fwd filled for the same call. Rows
+ *           longer than one tile (4096 elements unweighted, 2048 weighted) take their blocks'
+ *           weights and fits from the final hulls ti_fwd left there, so F and the mask are the
+ *           forward's bit for bit; shorter rows recompute them and may pass NULL, 0.
  *   g       [batch, n] upstream gradient.
  *   w       weights or NULL (unweighted).
  *   y       [batch, n] input of the fit; needed when gw is wanted or a TI_CLIP_* flag is set.
  *   gy, gw  outputs, either may be NULL.
+ *   flags   the forward's TI_INCREASING and TI_CLIP_* bits.
+ *   workspace / workspace_bytes: at least ti_bwd_workspace() bytes, 256-byte aligned.
  */
-int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy,
-           void* gw, int64_t batch, int64_t n, int dtype, unsigned flags, double y_min,
-           double y_max, void* workspace, size_t workspace_bytes, void* stream);
+int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspace_bytes,
+           const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
+           int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
+           size_t workspace_bytes, void* stream);
 
 /* Test hook: the starts bit array of a [batch, n] set as bytes (0/1), row-major - the
  * reference's bool starts tensor (reference tests/test_cuda.py:176 reads it). */

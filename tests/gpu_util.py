@@ -31,7 +31,7 @@ def gpu_fit(
     """The HIP fit of [batch, n] rows (through the tensor boundary), and its starts as uint8."""
     yt = torch.from_numpy(np.ascontiguousarray(y)).cuda()
     wt = None if w is None else torch.from_numpy(np.ascontiguousarray(w)).cuda()
-    out, starts, bad = _ext.fit(yt, wt, increasing, True, with_starts, y_min, y_max)
+    out, starts, bad, _ = _ext.fit(yt, wt, increasing, True, with_starts, y_min, y_max)
     if bad is not None:
         assert int(bad.item()) == 0
     s = None

@@ -53,7 +53,15 @@ def test_workspace_queries() -> None:
     size = ctypes.c_size_t(123)
     assert lib.ti_fwd_workspace(1000, 16, _ext.F32, 0, ctypes.byref(size)) == 0
     assert size.value == 0
+    assert lib.ti_fwd_workspace(1000, 4096, _ext.F32, 0, ctypes.byref(size)) == 0
+    assert size.value == 0  # one tile: no workspace
+    assert lib.ti_fwd_workspace(1, 100_000_000, _ext.F32, 1, ctypes.byref(size)) == 0
+    # two node arrays of about 36 bytes per element, and the tile ranks
+    assert 6e9 < size.value < 8e9
     assert lib.ti_bwd_workspace(1000, 16, _ext.F64, 1, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert lib.ti_bwd_workspace(1000, 65536, _ext.F32, 1, ctypes.byref(size)) == 0
+    assert size.value > 0
     assert lib.ti_fwd_workspace(10, 16, 7, 0, ctypes.byref(size)) == 2  # TI_EDTYPE
     assert lib.ti_fwd_workspace(10, 16, 0, 0, None) == 1  # TI_EINVAL
 
@@ -86,16 +94,21 @@ def test_empty_batch_is_a_no_op() -> None:
 
 def test_bwd_argument_errors() -> None:
     lib = _ext.load()
-    bwd = lib.ti_bwd
+    def bwd(starts, g, w, y, gy, gw, batch, n, flags, fws=None, fwsb=0, ws=None, wsb=0):
+        return lib.ti_bwd(starts, fws, fwsb, g, w, y, gy, gw, batch, n, 0, flags, 0.0, 0.0, ws, wsb, None)
+
     # gw wanted without y
-    assert bwd(1, 2, None, None, None, 3, 4, 16, 0, 1, 0.0, 0.0, None, 0, None) == 1
+    assert bwd(1, 2, None, None, None, 3, 4, 16, 1) == 1
     assert b"y is needed" in lib.ti_last_error()
     # clamp mask without y
-    assert bwd(1, 2, None, None, 3, None, 4, 16, 0, 1 | 4, 0.0, 0.0, None, 0, None) == 1
+    assert bwd(1, 2, None, None, 3, None, 4, 16, 1 | 4) == 1
     # starts missing
-    assert bwd(None, 2, None, None, 3, None, 4, 16, 0, 1, 0.0, 0.0, None, 0, None) == 1
+    assert bwd(None, 2, None, None, 3, None, 4, 16, 1) == 1
     # nothing wanted: fine, no launch
-    assert bwd(1, 2, None, None, None, None, 4, 16, 0, 1, 0.0, 0.0, None, 0, None) == 0
+    assert bwd(1, 2, None, None, None, None, 4, 16, 1) == 0
+    # a long row without the forward's workspace
+    assert bwd(1, 2, None, None, 3, None, 2, 100_000, 1) == 4
+    assert b"forward's workspace" in lib.ti_last_error()
 
 
 def test_errors_are_per_thread() -> None:

@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 # Tile sizes: 4096 elements unweighted, 2048 weighted; longer rows are merged across tiles.
 SHAPES = [33, 63, 64, 65, 100, 255, 256, 511, 1000, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096]
 LONG_SHAPES = [4097, 8193, 20_000, 100_000]
-MULTI_TILE = False  # rows longer than one tile
+MULTI_TILE = True  # rows longer than one tile
 
 
 def fits(n: int, weighted: bool) -> bool:
@@ -170,7 +170,8 @@ def gpu_grads(y, w, c, **kw):
 
 
 @pytest.mark.parametrize(("batch", "n"), [(70, 33), (9, 64), (9, 65), (7, 128), (5, 512), (5, 513),
-                                          (5, 1000), (5, 1024), (3, 1025), (3, 2048), (3, 4096)])
+                                          (5, 1000), (5, 1024), (3, 1025), (3, 2048), (3, 4096),
+                                          (3, 4097), (2, 9000), (2, 70_000)])
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_tile_gradients_match_oracle(batch: int, n: int, dtype: type) -> None:
     # reference tests/test_cuda.py:137-157: the gradient against the CPU's closed form on the
@@ -195,7 +196,7 @@ def test_tile_gradients_match_oracle(batch: int, n: int, dtype: type) -> None:
 
 
 @pytest.mark.parametrize("name", PATTERNS)
-@pytest.mark.parametrize("n", [1024, 1025, 2048, 3000])
+@pytest.mark.parametrize("n", [1024, 1025, 2048, 3000, 9000, 70_000])
 def test_tile_gradient_is_block_average(name: str, n: int) -> None:
     # reference tests/test_cuda.py:160-183: whatever the data (ties included) the gradient is
     # the block average over the blocks the GPU's fit reports.
@@ -214,7 +215,7 @@ def test_tile_gradient_is_block_average(name: str, n: int) -> None:
         _, starts = _ext.isotonic_tiles(
             torch.from_numpy(y).cuda(), None if weights is None else torch.from_numpy(weights).cuda(),
             True, True, True,
-        )
+        )  # the same fit again: its partition
         s = starts.cpu().numpy().astype(np.uint8)
         ey, ew = oracle.block_grad(s, c, weights, y, fit, want_w=weights is not None)
         np.testing.assert_allclose(gs[0], ey, rtol=1e-9, atol=1e-9)
@@ -222,7 +223,7 @@ def test_tile_gradient_is_block_average(name: str, n: int) -> None:
             np.testing.assert_allclose(gs[1], ew, rtol=1e-9, atol=1e-9 * (1 + np.abs(y).max()))
 
 
-@pytest.mark.parametrize("n", [100, 2048])
+@pytest.mark.parametrize("n", [100, 2048, 9000])
 def test_tile_clamp_gradient_matches_torch_clamp(n: int) -> None:
     import torch
 
@@ -258,3 +259,64 @@ def test_tile_gradcheck() -> None:
     for kw in ({}, {"increasing": False}, {"y_min": -0.3, "y_max": 0.5}):
         assert gradcheck(lambda y, w: torchisotonic_amd.isotonic(y, w, **kw), (y, w))
         assert gradcheck(lambda y: torchisotonic_amd.isotonic(y, **kw), (y,))
+
+
+@pytest.mark.parametrize("n", LONG_SHAPES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_long_rows(n: int, dtype: type) -> None:
+    # rows of several tiles: the cross-tile merge and the expansion
+    print(f"long rows n={n} dtype={np.dtype(dtype).name}", flush=True)
+    batch = 3
+    y, w = data(batch, n, dtype, n)
+    check_fit(y)
+    check_fit(y, w, increasing=False)
+    check_fit(y, None, increasing=False, y_min=-0.5, y_max=2.0)
+
+
+@pytest.mark.parametrize("name", PATTERNS)
+@pytest.mark.parametrize("n", [9000, 70_000, 300_000])
+def test_long_patterns(name: str, n: int) -> None:
+    print(f"long pattern {name} n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    y = pattern(name, n, rng)[None]
+    w = rng.random((1, n)) + 0.1
+    ties = name in ("constant", "zeros_ones", "saw")
+    check_fit(y, check_starts=not ties)
+    check_fit(y, w, check_starts=not ties)
+    check_fit(y, w, increasing=False, check_starts=not ties)
+    check_fit(y.astype(np.float32), check_starts=False)
+
+
+@pytest.mark.parametrize("n", [300_000, 5_000_000])
+def test_long_exact_ties(n: int) -> None:
+    # calibration-shaped rows (0/1 labels, integer counts): exact partitions across merges
+    rng = np.random.default_rng(n)
+    s = np.sort(rng.standard_normal(n) * 1.5)
+    y = (rng.random(n) < 1 / (1 + np.exp(-s))).astype(np.float32)[None]
+    w = rng.integers(1, 6, n).astype(np.float32)[None]
+    got, starts = gpu_fit(y, w)
+    want, want_starts = oracle.pava(y, w, acc="f64x")
+    assert np.abs(got - want).max() <= tolerance(y)
+    np.testing.assert_array_equal(starts, want_starts)
+
+
+def test_long_nan_row_gradients() -> None:
+    # a NaN row is one block: gy is the row's average gradient, gw NaN; through a clamp, zero
+    import torch
+
+    import torchisotonic_amd
+
+    rng = np.random.default_rng(5)
+    n = 9000
+    y = rng.standard_normal((2, n))
+    y[0, 4321] = np.nan
+    w = rng.random((2, n)) + 0.1
+    c = rng.standard_normal((2, n))
+    (gy, gw), _ = gpu_grads(y, w, c)
+    np.testing.assert_allclose(gy[0], w[0] * c[0].sum() / w[0].sum(), rtol=1e-10)
+    assert np.isnan(gw[0]).all()
+    fit, starts = oracle.pava(y[1:], w[1:])
+    ey, _ = oracle.block_grad(starts, c[1:], w[1:])
+    np.testing.assert_allclose(gy[1:], ey, rtol=1e-10, atol=1e-12)
+    (gy, gw), _ = gpu_grads(y, w, c, y_min=-0.5)
+    assert (gy[0] == 0).all() and np.isnan(gw[0]).all()

@@ -95,9 +95,11 @@ class _Isotonic(torch.autograd.Function):
         y_max: float | None,
     ) -> Tensor:
         want = any(ctx.needs_input_grad[:2])
-        out, starts = _solve(flat_y, flat_w, increasing, exact, want, y_min, y_max)
+        out, starts, ws = _solve(flat_y, flat_w, increasing, exact, want, y_min, y_max)
         ctx.save_for_backward(flat_y, flat_w, starts)
         ctx.bounds = (y_min, y_max)
+        ctx.increasing = increasing
+        ctx.fwd_ws = ws if want else None  # the final hulls of long rows, for the backward
         return out
 
     @staticmethod
@@ -107,7 +109,8 @@ class _Isotonic(torch.autograd.Function):
         y_min, y_max = ctx.bounds
         need_y = want_w or y_min is not None or y_max is not None
         gy, gw = _ext.grad(
-            starts, grad, flat_w, flat_y if need_y else None, want_y, want_w, y_min, y_max
+            starts, ctx.fwd_ws, grad, flat_w, flat_y if need_y else None, want_y, want_w,
+            y_min, y_max, ctx.increasing,
         )
         return gy, gw, None, None, None, None
 
@@ -120,12 +123,13 @@ def _solve(
     with_starts: bool = False,
     y_min: float | None = None,
     y_max: float | None = None,
-) -> tuple[Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor | None]:
     """The (clamped) fit of [batch, n] problems (n >= 1) in flat_y's dtype, by the HIP
-    kernels, and, if ``with_starts``, where its blocks start as a packed bit array (else an
-    empty tensor). Reference _api.py:118-134 without its CPU branch."""
+    kernels; if ``with_starts``, where its blocks start as a packed bit array (else an empty
+    tensor); and the fit's workspace (the final hulls of rows longer than one tile, which the
+    backward reads). Reference _api.py:118-134 without its CPU branch."""
     _ext._on_gpu(flat_y, "y")
-    out, starts, bad = _ext.fit(flat_y, flat_w, increasing, exact, with_starts, y_min, y_max)
+    out, starts, bad, ws = _ext.fit(flat_y, flat_w, increasing, exact, with_starts, y_min, y_max)
     if bad is not None and bool(bad.item()):
         raise ValueError("weight must be strictly positive")
-    return out, starts
+    return out, starts, ws

@@ -63,7 +63,7 @@ def load() -> ctypes.CDLL:
     lib.ti_fwd.restype = _int
     lib.ti_fwd.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_bwd.restype = _int
-    lib.ti_bwd.argtypes = [_vp] * 6 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_starts_to_bool.restype = _int
     lib.ti_starts_to_bool.argtypes = [_vp, _vp, _i64, _i64, _vp]
     got = lib.ti_abi_version()
@@ -130,11 +130,12 @@ def fit(
     with_starts: bool = False,
     y_min: float | None = None,
     y_max: float | None = None,
-) -> tuple[Tensor, Tensor, Tensor | None]:
+) -> tuple[Tensor, Tensor, Tensor | None, Tensor | None]:
     """The fit of every row of ``y`` ([batch, n], float32/float64, on the GPU), clamped to
     [y_min, y_max] where given; the packed partition (int32 words) if ``with_starts`` (else an
-    empty tensor); and, for weighted fits, a one-word device flag that is nonzero if some
-    weight was not positive (the caller checks it)."""
+    empty tensor); for weighted fits, a one-word device flag that is nonzero if some weight was
+    not positive (the caller checks it); and the workspace, which the backward of rows longer
+    than one tile reads (None when the fit needed none)."""
     _on_gpu(y, "y")
     dtype = _dtype_code(y)
     if y.dim() != 2:
@@ -161,11 +162,12 @@ def fit(
             _ptr(ws), 0 if ws is None else ws.numel(), _stream(y),
         )
     _check(rc, "fit")
-    return out, starts, bad
+    return out, starts, bad, ws
 
 
 def grad(
     starts: Tensor,
+    fwd_ws: Tensor | None,
     g: Tensor,
     w: Tensor | None,
     y: Tensor | None,
@@ -173,9 +175,11 @@ def grad(
     want_w: bool,
     y_min: float | None = None,
     y_max: float | None = None,
+    increasing: bool = True,
 ) -> tuple[Tensor | None, Tensor | None]:
     """Gradients w.r.t. y and w of a fit whose packed partition is ``starts``, for the upstream
-    gradient ``g`` (the clamp's backward included where y_min / y_max are given)."""
+    gradient ``g`` (the clamp's backward included where y_min / y_max are given); ``fwd_ws``
+    and ``increasing`` are the forward's."""
     _on_gpu(g, "grad")
     dtype = _dtype_code(g)
     batch, n = g.shape
@@ -191,8 +195,9 @@ def grad(
     with torch.cuda.device(g.device):
         ws = _workspace("bwd", batch, n, dtype, w is not None, g.device)
         rc = load().ti_bwd(
-            _ptr(starts), _ptr(g), _ptr(w), _ptr(y), _ptr(gy), _ptr(gw), batch, n, dtype,
-            _flags(True, True, y_min, y_max),
+            _ptr(starts), _ptr(fwd_ws), 0 if fwd_ws is None else fwd_ws.numel(),
+            _ptr(g), _ptr(w), _ptr(y), _ptr(gy), _ptr(gw), batch, n, dtype,
+            _flags(increasing, True, y_min, y_max),
             float(y_min) if y_min is not None else 0.0,
             float(y_max) if y_max is not None else 0.0,
             _ptr(ws), 0 if ws is None else ws.numel(), _stream(g),
@@ -232,7 +237,7 @@ def isotonic_tiles(
     """The reference's operator (reference _ext.py:25-31): the fit of every row of ``y``
     ([batch, n], on the GPU) in y's dtype, and if ``with_starts`` a bool tensor marking where
     its blocks start (else an empty one)."""
-    out, starts, bad = fit(y, w, increasing, exact, with_starts)
+    out, starts, bad, _ = fit(y, w, increasing, exact, with_starts)
     if bad is not None and bool(bad.item()):
         raise ValueError("weight must be strictly positive")
     if not with_starts:
@@ -245,8 +250,16 @@ def isotonic_grad(
 ) -> list[Tensor | None]:
     """The reference's gradient operator (reference _ext.py:34-40): the gradients of a fit
     whose blocks start where the bool ``starts`` is set, w.r.t. y and, given y, the weights.
-    ``out`` is accepted for the signature's sake; the block means are recomputed from y."""
+    ``out`` is accepted for the signature's sake. Rows longer than one tile (4096 elements
+    unweighted, 2048 weighted) take their blocks from the forward's final hulls, which this
+    signature cannot carry: for them it raises, and the autograd path (``isotonic``), which
+    keeps the forward's workspace, is the way in."""
     del out
+    if g.shape[-1] > (2048 if w is not None else 4096):
+        raise RuntimeError(
+            "torchisotonic_amd.isotonic_grad: rows longer than one tile need the forward's "
+            "workspace; use torchisotonic_amd.isotonic with autograd"
+        )
     packed = bool_to_starts(starts) if starts.dtype == torch.bool else starts
-    gy, gw = grad(packed, g, w, y, True, y is not None)
+    gy, gw = grad(packed, None, g, w, y, True, y is not None)
     return [gy, gw]

@@ -75,14 +75,13 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
   if (n <= ti::tile_elems(weighted != 0)) return ok();
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::tile_elems(weighted != 0));
+  *bytes = ti::long_plan(batch, n, weighted != 0).bytes;
+  return ok();
 }
 
 int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
            int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
            void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (int rc = check_shape(batch, n, dtype)) return rc;
   if (batch == 0) return ok();
   if (y == nullptr || out == nullptr) return fail(TI_EINVAL, "y and out must not be null");
@@ -100,23 +99,29 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
                    nullptr, 0, 0, static_cast<hipStream_t>(stream)};
     return launched(ti::tile_run(a, ti::kTileSingle), "single-tile fit");
   }
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)tn);
+  const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
+  if (workspace == nullptr || workspace_bytes < plan.bytes)
+    return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", plan.bytes, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspace must be 256-byte aligned");
+  if (batch * plan.tiles_per_row > 0x7FFFFFFF) return fail(TI_ESIZE, "too many tiles");
+  ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
+                 nullptr, 0, 0, static_cast<hipStream_t>(stream)};
+  return launched(ti::long_fit(a, plan, workspace), "multi-tile fit");
 }
 
 int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes) {
-  (void)weighted;
   if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
   if (n <= ti::tile_elems(weighted != 0)) return ok();
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)ti::tile_elems(weighted != 0));
+  *bytes = ti::long_grad_bytes(batch, n, weighted != 0);
+  return ok();
 }
 
-int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy,
-           void* gw, int64_t batch, int64_t n, int dtype, unsigned flags, double y_min,
-           double y_max, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
+int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspace_bytes,
+           const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
+           int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
+           size_t workspace_bytes, void* stream) {
   if (int rc = check_shape(batch, n, dtype)) return rc;
   if (batch == 0) return ok();
   if (starts == nullptr || g == nullptr) return fail(TI_EINVAL, "starts and g must not be null");
@@ -137,7 +142,18 @@ int ti_bwd(const uint32_t* starts, const void* g, const void* w, const void* y, 
                        static_cast<hipStream_t>(stream)};
     return launched(ti::tile_grad_single(a), "single-tile gradient");
   }
-  return fail(TI_ESIZE, "rows longer than %lld elements are not supported yet", (long long)tn);
+  const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
+  if (fwd_workspace == nullptr || fwd_workspace_bytes < plan.bytes)
+    return fail(TI_EWORKSPACE, "rows of %lld elements need the forward's workspace (%zu bytes), %zu given",
+                (long long)n, plan.bytes, fwd_workspace_bytes);
+  const size_t need = ti::long_grad_bytes(batch, n, w != nullptr);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0 || (reinterpret_cast<uintptr_t>(fwd_workspace) & 255) != 0)
+    return fail(TI_EINVAL, "workspaces must be 256-byte aligned");
+  ti::LongGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
+                     fwd_workspace, static_cast<hipStream_t>(stream)};
+  return launched(ti::long_grad(a, plan, workspace), "multi-tile gradient");
 }
 
 int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n, void* stream) {

@@ -1,0 +1,370 @@
+// Backward of rows longer than one tile.
+//
+// Replaces the reference's long-row gradient (reference src/torchisotonic/csrc/grad.cuh:
+// 165-195 tile summaries, 346-370 ATen tile scan, 200-290 fill), which reads starts, g and w
+// twice and runs about fifteen ATen kernels in between. Here the forward's final hulls (kept in
+// its workspace) give every block's weight and fit; only the block sums of g are new, and they
+// are differences of a prefix sum of g taken at the hull's vertices:
+//
+//   gsum_kernel    per tile: reads g once; the tile's total, and the prefix of g (within the
+//                  tile, double-double) at each hull vertex inside it, by the vertex's rank;
+//   gscan kernels  exclusive scans of the tile totals: within groups of 256 tiles, then over
+//                  the groups of a row;
+//   gfill_kernel   per tile: for each block overlapping the tile, G = difference of the row
+//                  prefix of g at its two vertices, W and the fit from the forward's vertices
+//                  (so the clamp mask is the forward's, bit for bit); then reads w (and y) once
+//                  and writes gy = w * mask * G / W and gw = (y - fit) * mask * G / W.
+// A row holding a NaN is one block (its fit is NaN), as in the reference's CPU path.
+#include "ti_common.h"
+#include "ti_kernels.h"
+#include "ti_tile.h"
+
+namespace ti {
+
+namespace {
+
+constexpr int kScanTiles = 256;
+
+struct GradPlan {
+  int64_t tpr, ngroups, cap_final;
+  size_t off_tg, off_lp, off_gt, off_gp, off_lv, bytes;
+};
+
+GradPlan grad_plan(int64_t batch, int64_t n, bool weighted) {
+  const LongPlan lp = long_plan(batch, n, weighted);
+  GradPlan g{};
+  g.tpr = lp.tiles_per_row;
+  g.ngroups = (g.tpr + kScanTiles - 1) / kScanTiles;
+  g.cap_final = lp.cap[lp.levels];
+  size_t off = 0;
+  g.off_tg = off;
+  off += align256(static_cast<size_t>(batch * g.tpr) * 16);
+  g.off_lp = off;
+  off += align256(static_cast<size_t>(batch * g.tpr) * 16);
+  g.off_gt = off;
+  off += align256(static_cast<size_t>(batch * g.ngroups) * 16);
+  g.off_gp = off;
+  off += align256(static_cast<size_t>(batch * (g.ngroups + 1)) * 16);
+  g.off_lv = off;
+  off += align256(static_cast<size_t>(batch * g.cap_final) * 16);
+  g.bytes = off;
+  return g;
+}
+
+struct GradKArgs {
+  const uint32_t* starts;
+  const void* g;
+  const void* w;
+  const void* y;
+  void* gy;
+  void* gw;
+  int64_t batch, n, tpr, ngroups, cap_final;
+  unsigned flags;
+  double lo, hi;
+  const void* hulls;     // the forward's final node array
+  const int* tile_rank;  // the forward's per-tile ranks (rA, rB)
+  double* tg;            // [batch * tpr][2]: tile totals of g
+  double* lp;            // [batch * tpr][2]: exclusive prefix within the tile's group
+  double* gt;            // [batch * ngroups][2]: group totals
+  double* gp;            // [batch * (ngroups + 1)][2]: exclusive prefix of groups, then total
+  double* lv;            // [batch * cap_final][2]: prefix of g within its tile at each vertex
+};
+
+__device__ __forceinline__ DD wave_scan_dd2(DD v, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    DD o{__shfl_up(v.hi, d, kWave), __shfl_up(v.lo, d, kWave)};
+    if (lane >= d) v = dd_add(o, v);
+  }
+  return v;
+}
+
+// Exclusive double-double scan over a 256-thread workgroup; returns the exclusive prefix and
+// sets `total`.
+__device__ DD block_scan_dd(DD v, DD* wave_tot, DD& total) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const DD inc = wave_scan_dd2(v, lane);
+  DD exc{__shfl_up(inc.hi, 1, kWave), __shfl_up(inc.lo, 1, kWave)};
+  if (lane == 0) exc = DD{0.0, 0.0};
+  if (lane == kWave - 1) wave_tot[wave] = inc;
+  __syncthreads();
+  DD pre{0.0, 0.0};
+  for (int w2 = 0; w2 < wave; ++w2) pre = dd_add(pre, wave_tot[w2]);
+  total = DD{0.0, 0.0};
+  for (int w2 = 0; w2 < kWaves256; ++w2) total = dd_add(total, wave_tot[w2]);
+  __syncthreads();
+  return dd_add(pre, exc);
+}
+
+__device__ __forceinline__ uint32_t tile_bits(const uint32_t* srow, int x, int E) {
+  const uint32_t mask = E == 32 ? 0xFFFFFFFFu : ((1u << E) - 1u);
+  return (srow[x >> 5] >> (x & 31)) & mask;
+}
+
+template <typename T, bool W>
+__global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
+  using C = TileCfg<W>;
+  constexpr int E = C::kE;
+  __shared__ DD wtot[kWaves256];
+  __shared__ int rank_scan[kWaves256];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int64_t row = blockIdx.x / a.tpr;
+  const int64_t tile = blockIdx.x - row * a.tpr;
+  const int64_t first = tile * C::kN;
+  const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
+  const int t0 = tid * E;
+  const int ecount = max(0, min(E, len - t0));
+  T gv[E];
+  load_elems_any<T, E>(static_cast<const T*>(a.g) + row * a.n + first + t0, ecount, gv);
+  // local exclusive prefixes (double-double) and the thread's total
+  DD lpre[E];
+  DD acc{0.0, 0.0};
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    lpre[k] = acc;
+    if (k < ecount) acc = dd_add(acc, static_cast<double>(gv[k]));
+  }
+  DD total;
+  const DD off = block_scan_dd(acc, wtot, total);
+  if (tid == 0) {
+    a.tg[2 * blockIdx.x] = total.hi;
+    a.tg[2 * blockIdx.x + 1] = total.lo;
+  }
+  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+  if (*fin.bad) return;  // a NaN row is one block: only its total is needed
+  // the hull vertices inside the tile, by rank: rA, less one if rA is the tile's first element
+  const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
+  uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
+  if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
+  if (first + t0 == 0) mybits |= 1u;
+  const int pc = __builtin_popcount(mybits);
+  int incl = pc;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == kWave - 1) rank_scan[wave] = incl;
+  __syncthreads();
+  int before = incl - pc;
+  for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
+  const int rA = a.tile_rank[2 * blockIdx.x];
+  const int at_start = (tile == 0) ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1));
+  double* lv = a.lv + 2 * row * a.cap_final;
+  int rank = rA - at_start + before;
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    if ((mybits >> k) & 1u) {
+      ++rank;
+      const DD p = dd_add(off, lpre[k]);
+      lv[2 * rank] = p.hi;
+      lv[2 * rank + 1] = p.lo;
+    }
+  }
+  if (tile == a.tpr - 1 && tid == 0) {  // the row's end point: the last vertex
+    const int last = *fin.count - 1;
+    lv[2 * last] = total.hi;
+    lv[2 * last + 1] = total.lo;
+  }
+}
+
+// Exclusive scan of tile totals within groups of 256 tiles; group totals.
+__global__ __launch_bounds__(256) void gscan_local_kernel(GradKArgs a) {
+  __shared__ DD wtot[kWaves256];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x / a.ngroups;
+  const int64_t grp = blockIdx.x - row * a.ngroups;
+  const int64_t tile = grp * kScanTiles + tid;
+  DD v{0.0, 0.0};
+  if (tile < a.tpr) v = DD{a.tg[2 * (row * a.tpr + tile)], a.tg[2 * (row * a.tpr + tile) + 1]};
+  DD total;
+  const DD ex = block_scan_dd(v, wtot, total);
+  if (tile < a.tpr) {
+    a.lp[2 * (row * a.tpr + tile)] = ex.hi;
+    a.lp[2 * (row * a.tpr + tile) + 1] = ex.lo;
+  }
+  if (tid == 0) {
+    a.gt[2 * blockIdx.x] = total.hi;
+    a.gt[2 * blockIdx.x + 1] = total.lo;
+  }
+}
+
+// Exclusive scan of group totals per row (chunks of 256 groups with a carry); [ngroups] = total.
+__global__ __launch_bounds__(256) void gscan_groups_kernel(GradKArgs a) {
+  __shared__ DD wtot[kWaves256];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  DD carry{0.0, 0.0};
+  for (int64_t g0 = 0; g0 < a.ngroups; g0 += 256) {
+    const int64_t gi = g0 + tid;
+    DD v{0.0, 0.0};
+    if (gi < a.ngroups) v = DD{a.gt[2 * (row * a.ngroups + gi)], a.gt[2 * (row * a.ngroups + gi) + 1]};
+    DD total;
+    const DD ex = dd_add(carry, block_scan_dd(v, wtot, total));
+    if (gi < a.ngroups) {
+      a.gp[2 * (row * (a.ngroups + 1) + gi)] = ex.hi;
+      a.gp[2 * (row * (a.ngroups + 1) + gi) + 1] = ex.lo;
+    }
+    carry = dd_add(carry, total);
+  }
+  if (tid == 0) {
+    a.gp[2 * (row * (a.ngroups + 1) + a.ngroups)] = carry.hi;
+    a.gp[2 * (row * (a.ngroups + 1) + a.ngroups) + 1] = carry.lo;
+  }
+}
+
+template <bool W>
+__device__ __forceinline__ DD vertex_w(const NodeOut& f, int r) {
+  if constexpr (W) return DD{f.whi[r], f.wlo[r]};
+  else return DD{static_cast<double>(f.idx[r]), 0.0};
+}
+
+template <typename T, bool W>
+__global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
+  using C = TileCfg<W>;
+  constexpr int E = C::kE;
+  constexpr int NT = C::kThreads;
+  __shared__ double qv[C::kN + 2];
+  __shared__ T mv[C::kN + 2];
+  __shared__ int rank_scan[kWaves256];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int64_t row = blockIdx.x / a.tpr;
+  const int64_t tile = blockIdx.x - row * a.tpr;
+  const int64_t first = tile * C::kN;
+  const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
+  const int t0 = tid * E;
+  const int ecount = max(0, min(E, len - t0));
+  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+  const bool bad = *fin.bad != 0;
+  const int count = *fin.count;
+  const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
+  const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
+  // the forward's hull is of sgn * y: its slopes are sgn * fit
+  const double sgn = (a.flags & TI_INCREASING) ? 1.0 : -1.0;
+  const double* lv = a.lv + 2 * row * a.cap_final;
+  const double* gp = a.gp + 2 * row * (a.ngroups + 1);
+  const double* lpr = a.lp + 2 * row * a.tpr;
+  // the row prefix of g at vertex r
+  auto pg = [&](int r) -> DD {
+    const int x = fin.idx[r];
+    const int64_t tl = min<int64_t>(x / C::kN, a.tpr - 1);
+    const int64_t grp = tl / kScanTiles;
+    DD p = dd_add(DD{gp[2 * grp], gp[2 * grp + 1]}, DD{lpr[2 * tl], lpr[2 * tl + 1]});
+    return dd_add(p, DD{lv[2 * r], lv[2 * r + 1]});
+  };
+  int rA = a.tile_rank[2 * blockIdx.x], rB = a.tile_rank[2 * blockIdx.x + 1];
+  if (bad) {  // one block over the whole row, fit NaN
+    if (tid == 0) {
+      const DD gtot{gp[2 * a.ngroups], gp[2 * a.ngroups + 1]};
+      const double wsum = dd_diff(vertex_w<W>(fin, count - 1), vertex_w<W>(fin, 0));
+      qv[0] = (use_lo || use_hi) ? 0.0 : (gtot.hi + gtot.lo) / wsum;
+      mv[0] = quiet_nan<T>();
+    }
+  } else {
+    for (int jb = rA + tid; jb < rB; jb += NT) {
+      const DD ga = pg(jb), gb = pg(jb + 1);
+      const double G = dd_diff(gb, ga);
+      double dW, dS;
+      dW = dd_diff(vertex_w<W>(fin, jb + 1), vertex_w<W>(fin, jb));
+      dS = dd_diff(DD{fin.shi[jb + 1], fin.slo[jb + 1]}, DD{fin.shi[jb], fin.slo[jb]});
+      const T mean = static_cast<T>(sgn * slope_div(dS, dW));
+      double q = G / dW;
+      if ((use_lo || use_hi) && !clip_passes(mean, use_lo, lo, use_hi, hi)) q = 0.0;
+      qv[jb - rA] = q;
+      mv[jb - rA] = mean;
+    }
+  }
+  // the block of each element: vertex bits of the tile, ranked
+  const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
+  uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
+  if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
+  if (first + t0 == 0) mybits |= 1u;
+  if (bad) mybits = 0u;
+  const int pc = __builtin_popcount(mybits);
+  int incl = pc;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += o;
+  }
+  if (lane == kWave - 1) rank_scan[wave] = incl;
+  __syncthreads();
+  int before = incl - pc;
+  for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
+  const int at_start = bad ? 0 : ((tile == 0) ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1)));
+  int jj = bad ? 0 : before + static_cast<int>(mybits & 1u) - at_start;
+  T wv[W ? E : 1], yv[E];
+  const bool need_y = a.gw != nullptr;
+  if constexpr (W) load_elems_any<T, E>(static_cast<const T*>(a.w) + row * a.n + first + t0, ecount, wv);
+  if (need_y) load_elems_any<T, E>(static_cast<const T*>(a.y) + row * a.n + first + t0, ecount, yv);
+  T oy[E], ow[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    if (k > 0) jj += (mybits >> k) & 1u;
+    const double q = qv[jj];
+    const double wk = W ? static_cast<double>(wv[W ? k : 0]) : 1.0;
+    oy[k] = static_cast<T>(wk * q);
+    if (need_y) ow[k] = static_cast<T>((static_cast<double>(yv[k]) - static_cast<double>(mv[jj])) * q);
+  }
+  if (a.gy != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gy) + row * a.n + first + t0, ecount, oy);
+  if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + row * a.n + first + t0, ecount, ow);
+}
+
+}  // namespace
+
+size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted) { return grad_plan(batch, n, weighted).bytes; }
+
+hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
+  const bool W = in.w != nullptr;
+  const GradPlan gpn = grad_plan(in.batch, in.n, W);
+  char* base = static_cast<char*>(ws);
+  const char* fbase = static_cast<const char*>(in.fwd_ws);
+  GradKArgs a;
+  a.starts = in.starts;
+  a.g = in.g;
+  a.w = in.w;
+  a.y = in.y;
+  a.gy = in.gy;
+  a.gw = in.gw;
+  a.batch = in.batch;
+  a.n = in.n;
+  a.tpr = gpn.tpr;
+  a.ngroups = gpn.ngroups;
+  a.cap_final = gpn.cap_final;
+  a.flags = in.flags;
+  a.lo = in.lo;
+  a.hi = in.hi;
+  a.hulls = fbase + p.off_buf[p.levels & 1];
+  a.tile_rank = reinterpret_cast<const int*>(fbase + p.off_rank);
+  a.tg = reinterpret_cast<double*>(base + gpn.off_tg);
+  a.lp = reinterpret_cast<double*>(base + gpn.off_lp);
+  a.gt = reinterpret_cast<double*>(base + gpn.off_gt);
+  a.gp = reinterpret_cast<double*>(base + gpn.off_gp);
+  a.lv = reinterpret_cast<double*>(base + gpn.off_lv);
+  const unsigned tiles = static_cast<unsigned>(in.batch * gpn.tpr);
+  if (in.dtype == TI_F32) {
+    if (W) gsum_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    else gsum_kernel<float, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+  } else {
+    if (W) gsum_kernel<double, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    else gsum_kernel<double, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  gscan_local_kernel<<<dim3(static_cast<unsigned>(in.batch * gpn.ngroups)), dim3(256), 0, in.stream>>>(a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  gscan_groups_kernel<<<dim3(static_cast<unsigned>(in.batch)), dim3(256), 0, in.stream>>>(a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (in.dtype == TI_F32) {
+    if (W) gfill_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    else gfill_kernel<float, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+  } else {
+    if (W) gfill_kernel<double, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    else gfill_kernel<double, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ti

@@ -146,6 +146,59 @@ __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, co
   }
 }
 
+// Cross-tile merge: G neighbouring hulls per workgroup.
+constexpr int kGroup = 64;
+constexpr int kMaxLevels = 8;
+
+struct MergeArgs {
+  const void* in;
+  int64_t k_in, cap_in, npr_in;  // child node array: nodes, capacity, nodes per row
+  void* out;
+  int64_t k_out, cap_out, npr_out;
+  int64_t child_elems;  // elements per child node
+};
+
+struct ExpandArgs {
+  const void* hulls;  // final node array: one node per row
+  int64_t batch, cap, n, tiles_per_row;
+  void* out;
+  uint32_t* starts;
+  int* tile_rank;  // per tile: the final hull's last vertex at or before the tile's first element,
+                   // and its first vertex at or after the tile's end
+  unsigned flags;
+  double lo, hi;
+};
+
+// Workspace of a long-row fit: two node arrays used in turn by the merge levels (the final
+// hulls end in buffer levels & 1), and the per-tile ranks.
+struct LongPlan {
+  int64_t tiles_per_row;
+  int levels;
+  int64_t npr[kMaxLevels + 1], cap[kMaxLevels + 1], span[kMaxLevels + 1];
+  size_t off_buf[2], off_rank, bytes;
+};
+
+LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
+hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
+
+// Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
+struct LongGradArgs {
+  const uint32_t* starts;
+  const void* g;
+  const void* w;
+  const void* y;
+  void* gy;
+  void* gw;
+  int64_t batch, n;
+  int dtype;
+  unsigned flags;
+  double lo, hi;
+  const void* fwd_ws;
+  hipStream_t stream;
+};
+size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted);
+hipError_t long_grad(const LongGradArgs& a, const LongPlan& p, void* ws);
+
 int64_t tile_elems(bool weighted);
 hipError_t tile_run(const TileArgs& a, int mode);
 hipError_t tile_grad_single(const TileGradArgs& a);
