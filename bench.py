@@ -1,23 +1,26 @@
 """Throughput of the isotonic hot path on one MI355X, against the HBM roofline, with the
 reference CPU solver timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3] [--no-cpu]
 
 Prints ONE JSON line. The headline ``value`` is BASELINE config C2: a forward
 ``torchisotonic_amd.isotonic`` of float32 y[1e6, 16] = -0.1 i + N(0, 1), unweighted,
 decreasing, inputs resident in HBM, K back-to-back calls of the public API between device
-synchronisations (Gelem/s = 1.6e7 K / seconds). ``extra`` holds the metric's other legs:
-C2 forward+backward (dy), and C4 (one row of 1e8, weighted) forward and forward+backward when
-the long-row path is built.
+synchronisations (Gelem/s = 1.6e7 K / seconds). ``extra`` holds the metric's other legs - C2
+forward+backward (dy), C4 (one row of 1e8, weighted 0/1 labels, integer counts) forward and
+forward+backward (dy, dw) - and the other BASELINE configs (C5 bootstrap, C1, C3).
+
+Bytes per element (algorithmic, float32, each API tensor moved once): forward 8 unweighted
+(y in, fit out), 12 weighted (+w); backward 8 for dy alone (g in, gy out), 24 for dy and dw
+(g, w, y, fit in; gy, gw out). ``%roofline`` = bytes * Gelem/s / 8000 GB/s.
 
 ``roofline`` is for the dominant kernel of the headline step, timed live with HIP events
-recorded on the launch stream around each launch (raw C-ABI calls on preallocated buffers):
-achieved = algorithmic bytes per launch / mean kernel time; peak = 8 TB/s. ``traffic`` is null
-unless --traffic-factor data from rocprofv3 PMC runs is supplied.
+recorded on the launch stream around each raw C-ABI launch on preallocated buffers: achieved =
+algorithmic bytes per launch / mean kernel time; peak = 8 TB/s.
 
 ``cpu_baseline`` times the reference's own pava.h (compiled from the reference checkout into
 oracle/_ref/libti_ref.so; kind "reference") or, if that library is absent, the C restatement
-(kind "port") on the host's cores over a bounded sample of C2 rows.
+(kind "port") on the host's cores over C2's rows.
 """
 
 from __future__ import annotations
@@ -46,29 +49,25 @@ def log(*a: object) -> None:
     print(*a, file=sys.stderr, flush=True)
 
 
-def c2_inputs(device: str) -> tuple[torch.Tensor, torch.Tensor]:
-    rng = np.random.default_rng(0)
-    b, n = 1_000_000, 16
-    y = (-0.1 * np.arange(n) + rng.standard_normal((b, n))).astype(np.float32)
-    g = np.random.default_rng(1).standard_normal((b, n)).astype(np.float32)
-    return torch.from_numpy(y).to(device), torch.from_numpy(g).to(device)
+def sync() -> None:
+    torch.cuda.synchronize()
 
 
 def timed_calls(fn, steps: int, warmup: int) -> float:
     """Seconds per call over `steps` back-to-back calls, bracketed by synchronisations."""
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
+    sync()
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
-    torch.cuda.synchronize()
+    sync()
     return (time.perf_counter() - t0) / steps
 
 
-def kernel_ms(launch, reps: int) -> float:
-    """Mean device time of one launch: HIP events recorded on the launch stream right before
-    and after each raw launch."""
+def event_ms(launch, reps: int) -> float:
+    """Mean device time of `launch`: HIP events recorded on the launch stream right before and
+    after each call."""
     stream = torch.cuda.current_stream()
     pairs = []
     for _ in range(reps):
@@ -78,64 +77,141 @@ def kernel_ms(launch, reps: int) -> float:
         launch()
         e1.record(stream)
         pairs.append((e0, e1))
-    torch.cuda.synchronize()
+    sync()
     return float(np.mean([a.elapsed_time(b) for a, b in pairs]))
 
 
 def warm_gpu() -> None:
-    # An idle GPU clocks down; keep it busy briefly first (the reference's method,
-    # bench/bench.py:51-55).
+    # An idle GPU clocks down; keep it busy first (the reference's method, bench/bench.py:51-55).
     x = torch.empty(1 << 26, device="cuda")
-    for _ in range(20):
+    for _ in range(30):
         x.mul_(1.0)
-    torch.cuda.synchronize()
+    sync()
+
+
+def rate(elems: int, seconds: float, bytes_per_elem: float) -> dict:
+    g = elems / seconds / 1e9
+    return {"ms": seconds * 1e3, "gelem_s": g, "pct_roofline": 100 * g * bytes_per_elem / PEAK_GBPS}
+
+
+def fwd_bwd_fn(y: torch.Tensor, w: torch.Tensor | None, g: torch.Tensor, want_w: bool, **kw):
+    yr = y.detach().requires_grad_()
+    wr = None if w is None else (w.detach().requires_grad_(want_w))
+    inputs = (yr, wr) if (wr is not None and want_w) else (yr,)
+
+    def f() -> None:
+        out = torchisotonic_amd.isotonic(yr, wr, **kw)
+        torch.autograd.grad(out, inputs, g)
+
+    return f
+
+
+# --- C2: [1e6, 16] ------------------------------------------------------------------------
 
 
 def bench_c2(steps: int, warmup: int) -> dict:
-    y, g = c2_inputs("cuda")
-    b, n = y.shape
+    rng = np.random.default_rng(0)
+    b, n = 1_000_000, 16
+    y = torch.from_numpy((-0.1 * np.arange(n) + rng.standard_normal((b, n))).astype(np.float32)).cuda()
+    g = torch.from_numpy(np.random.default_rng(1).standard_normal((b, n)).astype(np.float32)).cuda()
     elems = b * n
-    # forward through the public API
-    fwd = lambda: torchisotonic_amd.isotonic(y, increasing=False)  # noqa: E731
-    t_fwd = timed_calls(fwd, steps, warmup)
-    # forward + backward (dy) through the public API
-    yr = y.clone().requires_grad_()
-
-    def fwd_bwd() -> None:
-        out = torchisotonic_amd.isotonic(yr, increasing=False)
-        torch.autograd.grad(out, (yr,), g)
-
-    t_fb = timed_calls(fwd_bwd, steps, warmup)
-    # the raw kernels, for the roofline
+    t_fwd = timed_calls(lambda: torchisotonic_amd.isotonic(y, increasing=False), steps, warmup)
+    t_fb = timed_calls(fwd_bwd_fn(y, None, g, False, increasing=False), steps, warmup)
     lib = _ext.load()
     out = torch.empty_like(y)
     starts = torch.empty(_ext.starts_words(b, n), dtype=torch.int32, device="cuda")
     gy = torch.empty_like(y)
-    stream = torch.cuda.current_stream().cuda_stream
-
-    def launch_fwd() -> None:
-        lib.ti_fwd(y.data_ptr(), None, out.data_ptr(), None, None, b, n, _ext.F32, 0, 0.0, 0.0, None, 0, stream)
-
-    def launch_fwd_starts() -> None:
-        lib.ti_fwd(y.data_ptr(), None, out.data_ptr(), starts.data_ptr(), None, b, n, _ext.F32, 0, 0.0, 0.0, None, 0, stream)
-
-    def launch_bwd() -> None:
-        lib.ti_bwd(starts.data_ptr(), g.data_ptr(), None, None, gy.data_ptr(), None, b, n, _ext.F32, 1, 0.0, 0.0, None, 0, stream)
-
-    for f in (launch_fwd, launch_fwd_starts, launch_bwd):
-        f()
-    torch.cuda.synchronize()
-    k_fwd = kernel_ms(launch_fwd, 50)
-    k_fwd_s = kernel_ms(launch_fwd_starts, 50)
-    k_bwd = kernel_ms(launch_bwd, 50)
+    s = torch.cuda.current_stream().cuda_stream
+    fwd = lambda: lib.ti_fwd(y.data_ptr(), None, out.data_ptr(), None, None, b, n, 0, 0, 0.0, 0.0, None, 0, s)  # noqa: E731
+    fwd_s = lambda: lib.ti_fwd(y.data_ptr(), None, out.data_ptr(), starts.data_ptr(), None, b, n, 0, 0, 0.0, 0.0, None, 0, s)  # noqa: E731
+    bwd = lambda: lib.ti_bwd(starts.data_ptr(), None, 0, g.data_ptr(), None, None, gy.data_ptr(), None, b, n, 0, 0, 0.0, 0.0, None, 0, s)  # noqa: E731
+    for f in (fwd, fwd_s, bwd):
+        assert f() == 0
+    sync()
     return {
         "elems": elems,
-        "t_fwd": t_fwd,
-        "t_fb": t_fb,
-        "k_fwd_ms": k_fwd,
-        "k_fwd_starts_ms": k_fwd_s,
-        "k_bwd_ms": k_bwd,
+        "fwd": rate(elems, t_fwd, 8),
+        "fwd_bwd": rate(elems, t_fb, 16),
+        "kernel_ms": {
+            "short_fit_kernel<float,16,unweighted> (no starts)": event_ms(fwd, 50),
+            "short_fit_kernel<float,16,unweighted> (with starts)": event_ms(fwd_s, 50),
+            "short_grad_kernel<float,16,unweighted> (dy)": event_ms(bwd, 50),
+        },
     }
+
+
+# --- C4: one row of 1e8, weighted -------------------------------------------------------------
+
+
+def c4_inputs(n: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    rng = np.random.default_rng(0)
+    s = np.sort(rng.standard_normal(n) * 1.5)
+    y = (rng.random(n) < 1.0 / (1.0 + np.exp(-s))).astype(np.float32)
+    del s
+    w = rng.integers(1, 6, n).astype(np.float32)
+    g = np.random.default_rng(1).standard_normal(n).astype(np.float32)
+    return torch.from_numpy(y).cuda(), torch.from_numpy(w).cuda(), torch.from_numpy(g).cuda()
+
+
+def bench_c4(steps: int, warmup: int, n: int = 100_000_000) -> dict:
+    y, w, g = c4_inputs(n)
+    t_fwd = timed_calls(lambda: torchisotonic_amd.isotonic(y, w), steps, warmup)
+    t_fb = timed_calls(fwd_bwd_fn(y, w, g, True), steps, warmup)
+    t_fb_dy = timed_calls(fwd_bwd_fn(y, w, g, False), steps, warmup)
+    # raw forward pipeline on preallocated buffers (no API host work, no weight-flag sync)
+    lib = _ext.load()
+    yy, ww = y.view(1, n), w.view(1, n)
+    out = torch.empty_like(yy)
+    ws = _ext._workspace("fwd", 1, n, 0, True, y.device)
+    s = torch.cuda.current_stream().cuda_stream
+    fwd = lambda: lib.ti_fwd(yy.data_ptr(), ww.data_ptr(), out.data_ptr(), None, None, 1, n, 0, 1, 0.0, 0.0, ws.data_ptr(), ws.numel(), s)  # noqa: E731
+    assert fwd() == 0
+    sync()
+    return {
+        "elems": n,
+        "fwd": rate(n, t_fwd, 12),
+        "fwd_bwd": rate(n, t_fb, 36),
+        "fwd_bwd_dy_only": rate(n, t_fb_dy, 24),
+        "fwd_pipeline_ms": event_ms(fwd, 10),
+    }
+
+
+# --- C5: bootstrap [1000, 65536] ----------------------------------------------------------------
+
+
+def bench_c5(steps: int, warmup: int) -> dict:
+    b, n = 1000, 65536
+    rng = np.random.default_rng(0)
+    y0 = (rng.random(n) < 1 / (1 + np.exp(-np.linspace(-4, 4, n)))).astype(np.float32)
+    y = torch.from_numpy(y0).cuda().expand(b, n).contiguous()
+    w = torch.from_numpy(np.maximum(rng.exponential(1.0, (b, n)), 1e-6).astype(np.float32)).cuda()
+    g = torch.from_numpy(np.random.default_rng(1).standard_normal((b, n)).astype(np.float32)).cuda()
+    t_fwd = timed_calls(lambda: torchisotonic_amd.isotonic(y, w), steps, warmup)
+    t_fb = timed_calls(fwd_bwd_fn(y, w, g, True), steps, warmup)
+    return {"elems": b * n, "fwd": rate(b * n, t_fwd, 12), "fwd_bwd": rate(b * n, t_fb, 36)}
+
+
+# --- C1 and C3: [1000, 5000] ----------------------------------------------------------------
+
+
+def bench_c1_c3(steps: int, warmup: int) -> dict:
+    b, n = 1000, 5000
+    rng = np.random.default_rng(0)
+    y1 = torch.from_numpy((0.001 * np.arange(n) + rng.standard_normal((b, n))).astype(np.float32)).cuda()
+    res = {"c1_fwd": rate(b * n, timed_calls(lambda: torchisotonic_amd.isotonic(y1), steps, warmup), 8)}
+    base = 1 / (1 + np.exp(-(np.linspace(-4, 4, n) + 0.5 * rng.standard_normal((b, n)))))
+    wnp = rng.random((b, n)) + 0.1
+    gnp = np.random.default_rng(1).standard_normal((b, n))
+    kw = dict(increasing=False, y_min=0.0, y_max=1.0)
+    for name, dt in (("f32", np.float32), ("f64", np.float64)):
+        y, w, g = (torch.from_numpy(a.astype(dt)).cuda() for a in (base, wnp, gnp))
+        bpe = 12 if dt == np.float32 else 24
+        res[f"c3_{name}_fwd"] = rate(b * n, timed_calls(lambda: torchisotonic_amd.isotonic(y, w, **kw), steps, warmup), bpe)
+        res[f"c3_{name}_fwd_bwd"] = rate(b * n, timed_calls(fwd_bwd_fn(y, w, g, True, **kw), steps, warmup), 3 * bpe)
+    return res
+
+
+# --- CPU baseline ---------------------------------------------------------------------------
 
 
 def cpu_baseline(budget_s: float = 12.0) -> dict:
@@ -167,56 +243,71 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+def cpu_c4(n: int = 10_000_000) -> dict:
+    """The reference CPU solver on a 1e7-element prefix-shaped sample of C4 (one row: the
+    reference runs a row on one thread, ops.cpp:30)."""
+    import oracle
+
+    rng = np.random.default_rng(0)
+    s = np.sort(rng.standard_normal(n) * 1.5)
+    y = (rng.random(n) < 1.0 / (1.0 + np.exp(-s))).astype(np.float32)[None]
+    w = rng.integers(1, 6, n).astype(np.float32)[None]
+    impl = "reference" if oracle.ref_lib() is not None else "oracle"
+    t0 = time.perf_counter()
+    oracle.pava(y, w, threads=1, impl=impl, with_starts=False)
+    t = time.perf_counter() - t0
+    return {"gelem_s": n / t / 1e9, "cores": 1, "kind": "reference" if impl == "reference" else "port",
+            "sample": f"C4-shaped row of {n} elements, f32 weighted, one thread"}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="c2,c4,c5,c1,c3")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: rows are independent and this build runs on a single "
-            "MI355X; multi-GPU sharding is design-only (see DESIGN.md). Run with --gpus 1.",
+            "MI355X; multi-GPU sharding is design-only. Run with --gpus 1.",
             file=sys.stderr,
         )
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
+    configs = set(args.configs.split(","))
     warm_gpu()
+    log("C2 ...")
     c2 = bench_c2(args.steps, args.warmup)
+    extra: dict = {"c2": c2}
+    if "c4" in configs:
+        log("C4 ...")
+        extra["c4"] = bench_c4(max(3, args.steps // 5), 1)
+    if "c5" in configs:
+        log("C5 ...")
+        extra["c5"] = bench_c5(max(3, args.steps // 5), 1)
+    if "c1" in configs or "c3" in configs:
+        log("C1/C3 ...")
+        extra["c1_c3"] = bench_c1_c3(max(3, args.steps // 3), 2)
     elems = c2["elems"]
-    fwd_gelem = elems / c2["t_fwd"] / 1e9
-    fb_gelem = elems / c2["t_fb"] / 1e9
-    bytes_fwd = 8 * elems  # y in, fit out (f32)
-    achieved = bytes_fwd / (c2["k_fwd_ms"] * 1e-3) / 1e9
-    extra = {
-        "c2_fwd_gelem_s": fwd_gelem,
-        "c2_fwd_bwd_gelem_s": fb_gelem,
-        "c2_fwd_ms": c2["t_fwd"] * 1e3,
-        "c2_fwd_bwd_ms": c2["t_fb"] * 1e3,
-        "c2_fwd_pct_roofline": 100 * 8 * elems / c2["t_fwd"] / 1e9 / PEAK_GBPS,
-        "c2_fwd_bwd_pct_roofline": 100 * 16 * elems / c2["t_fb"] / 1e9 / PEAK_GBPS,
-        "kernel_ms": {
-            "short_fit (no starts)": c2["k_fwd_ms"],
-            "short_fit (with starts)": c2["k_fwd_starts_ms"],
-            "short_grad (dy)": c2["k_bwd_ms"],
-        },
-    }
+    k = c2["kernel_ms"]["short_fit_kernel<float,16,unweighted> (no starts)"]
+    achieved = 8 * elems / (k * 1e-3) / 1e9
     line = {
         "metric": METRIC,
-        "value": fwd_gelem,
+        "value": c2["fwd"]["gelem_s"],
         "unit": "Gelem/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": c2["t_fwd"] * 1e3,
+        "ms_per_step": c2["fwd"]["ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32 (f64 sums and hull tests)",
-        "data": "synthetic: y[b,i] = -0.1 i + N(0,1), seed 0",
+        "data": "synthetic: C2 y[b,i] = -0.1 i + N(0,1), seed 0",
         "config": {
             "workload": "C2: isotonic forward, y f32 [1000000, 16], unweighted, increasing=False",
             "batch": 1_000_000,
@@ -229,13 +320,16 @@ def main() -> None:
             "unit": "GB/s",
             "frac": achieved / PEAK_GBPS,
             "traffic": None,
-            "kernel": "short_fit_kernel<float,16,false>",
-            "algorithmic_bytes_per_launch": bytes_fwd,
+            "kernel": "short_fit_kernel<float,16,unweighted>",
+            "algorithmic_bytes_per_launch": 8 * elems,
         },
         "extra": extra,
     }
     if not args.no_cpu:
+        log("CPU baseline ...")
         line["cpu_baseline"] = cpu_baseline()
+        if "c4" in configs:
+            extra["c4_cpu"] = cpu_c4()
     print(json.dumps(line), flush=True)
 
 

@@ -1,10 +1,10 @@
-// Rows longer than one tile: the cross-tile merge and the expansion.
+// Rows longer than one tile: the cross-span merge and the expansion.
 //
 // Replaces the reference's chunk-start prefix, merge rounds and fit stages (reference
 // src/torchisotonic/csrc/tiles.cuh:1680-1725, 1524-1537 + 1728-1743, 1541-1667): instead of
 // one launch per pairwise round over segment lists, a workgroup merges G = 64 neighbouring
-// hulls at a time, six rounds in LDS, so a row of 1e8 elements (48,829 weighted tiles) needs
-// three merge launches.
+// hulls at a time, six rounds in LDS, so a row of 1e8 elements (390,625 span hulls of 256
+// elements) needs four merge launches.
 //
 //   merge_kernel   G child hulls (compact arrays, double-double coordinates relative to the
 //                  child) -> one parent hull relative to the parent. Children are laid end to
@@ -219,20 +219,23 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeArgs a) {
   else v = dvarr_of(pout);
 
   // Lay the children end to end (each child's first vertex is the previous child's last,
-  // stored once), in coordinates relative to the parent.
-  for (int c = 0; c < nch; ++c) {
-    const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + c);
-    const int cnt = sh.cnt[c];
-    const int o = sh.off[c];
-    const DD ow{sh.tot[0][c], sh.tot[1][c]}, os{sh.tot[2][c], sh.tot[3][c]};
-    const int ioff = static_cast<int>(c * a.child_elems);
-    for (int k = (c == 0 ? 0 : 1) + tid; k < cnt; k += kMergeThreads) {
-      VPt p;
-      p.i = ci.idx[k] + ioff;
-      p.s = dd_add(os, DD{ci.shi[k], ci.slo[k]});
-      if constexpr (W) p.w = dd_add(ow, DD{ci.whi[k], ci.wlo[k]});
-      vstore<W>(v, o + k, p);
+  // stored once), in coordinates relative to the parent: one thread per slot, its child found
+  // by a binary search over the children's first slots.
+  for (int s = tid; s < total; s += kMergeThreads) {
+    int lo = 0, hi = nch - 1;  // the last child whose first slot is below s (child 0 for s = 0)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sh.off[mid] < s) lo = mid;
+      else hi = mid - 1;
     }
+    const int c = lo, k = s - sh.off[c];
+    const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + c);
+    const DD ow{sh.tot[0][c], sh.tot[1][c]}, os{sh.tot[2][c], sh.tot[3][c]};
+    VPt p;
+    p.i = ci.idx[k] + static_cast<int>(c * a.child_elems);
+    p.s = dd_add(os, DD{ci.shi[k], ci.slo[k]});
+    if constexpr (W) p.w = dd_add(ow, DD{ci.whi[k], ci.wlo[k]});
+    vstore<W>(v, s, p);
   }
   __syncthreads();
 
@@ -451,8 +454,8 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
   LongPlan p{};
   const int64_t tn = tile_elems(weighted);
   p.tiles_per_row = (n + tn - 1) / tn;
-  int64_t npr = p.tiles_per_row;
-  int64_t span = tn;  // elements per node at this level
+  int64_t npr = (n + kSpan - 1) / kSpan;
+  int64_t span = kSpan;  // elements per node at this level
   size_t buf[2] = {0, 0};
   int level = 0;
   for (;;) {
@@ -478,12 +481,8 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   const bool W = t.w != nullptr;
   char* base = static_cast<char*>(ws);
-  // level 0: tile hulls
-  TileArgs a = t;
-  a.scratch = base + p.off_buf[0];
-  a.tiles_total = t.batch * p.tiles_per_row;
-  a.cap = p.cap[0];
-  hipError_t e = tile_run(a, kTileHull);
+  // level 0: span hulls
+  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0]);
   if (e != hipSuccess) return e;
   for (int l = 1; l <= p.levels; ++l) {
     MergeArgs m;

@@ -146,7 +146,9 @@ __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, co
   }
 }
 
-// Cross-tile merge: G neighbouring hulls per workgroup.
+// Rows longer than one tile: one lane builds the hull of each span of kSpan elements, then
+// workgroups merge G neighbouring hulls at a time until one hull per row remains.
+constexpr int kSpan = 256;
 constexpr int kGroup = 64;
 constexpr int kMaxLevels = 8;
 
@@ -169,10 +171,10 @@ struct ExpandArgs {
   double lo, hi;
 };
 
-// Workspace of a long-row fit: two node arrays used in turn by the merge levels (the final
-// hulls end in buffer levels & 1), and the per-tile ranks.
+// Workspace of a long-row fit: two node arrays used in turn by the span hulls and the merge
+// levels (the final hulls end in buffer levels & 1), and the per-tile ranks of the expansion.
 struct LongPlan {
-  int64_t tiles_per_row;
+  int64_t tiles_per_row;  // expansion (and backward) tiles
   int levels;
   int64_t npr[kMaxLevels + 1], cap[kMaxLevels + 1], span[kMaxLevels + 1];
   size_t off_buf[2], off_rank, bytes;
@@ -180,6 +182,7 @@ struct LongPlan {
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
+hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {

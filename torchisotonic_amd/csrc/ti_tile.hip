@@ -86,23 +86,21 @@ struct TileOps {
     if constexpr (kPairs && W) sh.lw_lo[slot] = static_cast<float>(p.wl);
   }
 
-  // b - a as (dW, dS). Across owners the whole difference is formed in double-double and
-  // rounded once: the owners' offset difference, plus b's local sum, minus a's.
+  // b - a as (dW, dS). Across owners the terms are taken in an order that keeps the
+  // cancellation exact: the owners' offset difference (exact for nearby owners), minus a's local
+  // sum (exact where the two nearly cancel, as for neighbouring points), then the small terms
+  // (offset and local rounding errors, b's local sum), so the result is rounded about once.
   __device__ static void diff(const Sh& sh, const Pt& a, const Pt& b, double& dW, double& dS) {
     const int oa = a.i >> C::kLogE, ob = b.i >> C::kLogE;
     if (oa == ob) {
       dS = (b.s - a.s) + (b.sl - a.sl);
       if constexpr (W) dW = (b.w - a.w) + (b.wl - a.wl);
     } else {
-      DD d = dd_add(DD{sh.off_s[0][ob], sh.off_s[1][ob]}, DD{-sh.off_s[0][oa], -sh.off_s[1][oa]});
-      d = dd_add(dd_add(d, b.s), -a.s);
-      if constexpr (kPairs) d = dd_add(d, b.sl - a.sl);
-      dS = d.hi + d.lo;
+      const double xs = (sh.off_s[0][ob] - sh.off_s[0][oa]) - a.s;
+      dS = xs + (((sh.off_s[1][ob] - sh.off_s[1][oa]) + (b.sl - a.sl)) + b.s);
       if constexpr (W) {
-        DD e = dd_add(DD{sh.off_w[0][ob], sh.off_w[1][ob]}, DD{-sh.off_w[0][oa], -sh.off_w[1][oa]});
-        e = dd_add(dd_add(e, b.w), -a.w);
-        if constexpr (kPairs) e = dd_add(e, b.wl - a.wl);
-        dW = e.hi + e.lo;
+        const double xw = (sh.off_w[0][ob] - sh.off_w[0][oa]) - a.w;
+        dW = xw + (((sh.off_w[1][ob] - sh.off_w[1][oa]) + (b.wl - a.wl)) + b.w);
       }
     }
     if constexpr (!W) dW = static_cast<double>(b.i - a.i);
@@ -479,17 +477,16 @@ __global__ __launch_bounds__(256) void tile_kernel(TileArgs a) {
     const int r = tid - leader;
     const int src = (leader + span) * (E + 1) + from;
     const int dst = leader * (E + 1) + keep;
+    const int mine = r < mlen ? (mlen - r + 2 * span - 1) / (2 * span) : 0;  // my entries
     Pt buf[kBuf];
 #pragma unroll
     for (int q = 0; q < kBuf; ++q) {
-      const int j = r + q * 2 * span;
-      if (j < mlen) buf[q] = Ops::load(sh, src + j);
+      if (q < mine) buf[q] = Ops::load(sh, src + r + q * 2 * span);
     }
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kBuf; ++q) {
-      const int j = r + q * 2 * span;
-      if (j < mlen) Ops::store(sh, dst + j, buf[q]);
+      if (q < mine) Ops::store(sh, dst + r + q * 2 * span, buf[q]);
     }
     __syncthreads();
   }
