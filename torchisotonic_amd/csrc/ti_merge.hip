@@ -23,8 +23,6 @@ namespace ti {
 
 namespace {
 
-constexpr int kMergeThreads = 256;
-constexpr int kLdsVerts = 2048;  // vertices a merge keeps in LDS
 
 // A vertex array: index (relative to the node's first element) and double-double sums.
 struct VArr {
@@ -143,140 +141,257 @@ __device__ void vbridge(const VArr& v, int ba, int cA, int bb, int cB, int& keep
 
 __device__ VArr dvarr_of(const NodeOut& o) { return VArr{o.idx, o.shi, o.slo, o.whi, o.wlo}; }
 
-template <bool W>
-struct MergeShared {
-  int idx[kLdsVerts];
-  double shi[kLdsVerts], slo[kLdsVerts];
-  double whi[W ? kLdsVerts : 1], wlo[W ? kLdsVerts : 1];
-  int cnt[kGroup], off[kGroup];       // per child: vertex count, first slot
-  double tot[4][kGroup + 1];          // per child offsets (W hi, lo, S hi, lo); [nch]: total
+// Per merge: the children (vertex counts, first slots, offsets within the parent) and the
+// fallback's pairwise-round bookkeeping.
+struct MergeSmall {
+  int cnt[kGroup], off[kGroup];
+  double tot[4][kGroup + 1];  // child offsets (W hi, lo, S hi, lo); [nch]: the parent's total
   int keep[kGroup / 2], from[kGroup / 2];
-  int maxlen;
-  int bad;
+  int total, bad, rounds_max;
 };
 
-template <bool W>
-__global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeArgs a) {
-  __shared__ MergeShared<W> sh;
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x / a.npr_out;
-  const int64_t j = blockIdx.x - row * a.npr_out;
-  const int64_t c0 = j * kGroup;  // first child within the row
-  const int nch = static_cast<int>(min<int64_t>(kGroup, a.npr_in - c0));
-  const NodeOut pout = node_out(a.out, a.k_out, a.cap_out, W, row * a.npr_out + j);
+// A merge's vertices in LDS (carved from dynamic LDS): coordinates, the doubly linked chain of
+// surviving vertices, and dead marks.
+template <bool W, bool PR>
+struct LdsVerts {
+  double *s, *sl, *w, *wl;
+  int* idx;
+  int16_t *prev, *next;
+  uint8_t* dead;
+};
 
-  // Children: counts, NaN flags, and offsets within the parent (double-double scan).
-  if (tid < kWave) {
-    int cnt = 0, bad = 0;
-    DD tw{0.0, 0.0}, ts{0.0, 0.0};
-    if (tid < nch) {
-      const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + tid);
-      cnt = *ci.count;
-      bad = *ci.bad;
-      tw = DD{ci.tot[0], ci.tot[1]};
-      ts = DD{ci.tot[2], ci.tot[3]};
-    }
-    // inclusive scans: totals (dd) and slots (count - 1, the shared point stored once)
-    DD iw = tw, is = ts;
-    int islot = max(cnt - 1, 0);
+template <bool W, bool PR>
+constexpr size_t lds_vertex_bytes() {
+  return 8 + (PR ? 8 : 0) + (W ? 8 : 0) + (W && PR ? 8 : 0) + 4 + 2 + 2 + 1;
+}
+
+// (cap is a multiple of 64, so every array stays 8-byte aligned)
+template <bool W, bool PR>
+__device__ LdsVerts<W, PR> lds_carve(char* p, int cap) {
+  LdsVerts<W, PR> v;
+  v.s = reinterpret_cast<double*>(p);
+  p += cap * 8;
+  v.sl = nullptr;
+  v.w = nullptr;
+  v.wl = nullptr;
+  if constexpr (PR) {
+    v.sl = reinterpret_cast<double*>(p);
+    p += cap * 8;
+  }
+  if constexpr (W) {
+    v.w = reinterpret_cast<double*>(p);
+    p += cap * 8;
+  }
+  if constexpr (W && PR) {
+    v.wl = reinterpret_cast<double*>(p);
+    p += cap * 8;
+  }
+  v.idx = reinterpret_cast<int*>(p);
+  p += cap * 4;
+  v.prev = reinterpret_cast<int16_t*>(p);
+  p += cap * 2;
+  v.next = reinterpret_cast<int16_t*>(p);
+  p += cap * 2;
+  v.dead = reinterpret_cast<uint8_t*>(p);
+  return v;
+}
+
+template <bool W, bool PR>
+__device__ __forceinline__ HPt lget(const LdsVerts<W, PR>& v, int k) {
+  HPt p;
+  p.i = v.idx[k];
+  p.s = v.s[k];
+  p.sl = PR ? v.sl[k] : 0.0;
+  p.w = W ? v.w[k] : 0.0;
+  p.wl = (W && PR) ? v.wl[k] : 0.0;
+  return p;
+}
+
+template <bool W, bool PR>
+__device__ __forceinline__ void lput(const LdsVerts<W, PR>& v, int k, const HPt& p) {
+  v.idx[k] = p.i;
+  v.s[k] = p.s;
+  if constexpr (PR) v.sl[k] = p.sl;
+  if constexpr (W) v.w[k] = p.w;
+  if constexpr (W && PR) v.wl[k] = p.wl;
+}
+
+// Slot s of the children laid end to end (each child's first vertex is the previous child's
+// last, stored once): the child holding it and the vertex within that child.
+__device__ __forceinline__ int child_of_slot(const MergeSmall& sm, int nch, int s) {
+  int lo = 0, hi = nch - 1;  // the last child whose first slot is below s (child 0 for s = 0)
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (sm.off[mid] < s) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Vertex k of child c in the parent's coordinates. Float32 data keeps float64 coordinates
+// (the double-double offset rounded once); float64 data keeps the rounding errors.
+template <bool W, bool PR>
+__device__ __forceinline__ HPt child_vertex(const MergeArgs& a, const MergeSmall& sm, int64_t row,
+                                            int64_t c0, int c, int k) {
+  const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + c);
+  HPt p;
+  p.i = ci.idx[k] + static_cast<int>(c * a.child_elems);
+  const DD S = dd_add(DD{sm.tot[2][c], sm.tot[3][c]}, DD{ci.shi[k], PR ? ci.slo[k] : 0.0});
+  p.s = S.hi;
+  p.sl = PR ? S.lo : 0.0;
+  p.w = 0.0;
+  p.wl = 0.0;
+  if constexpr (W) {
+    const DD Wd = dd_add(DD{sm.tot[0][c], sm.tot[1][c]}, DD{ci.whi[k], PR ? ci.wlo[k] : 0.0});
+    p.w = Wd.hi;
+    p.wl = PR ? Wd.lo : 0.0;
+  }
+  return p;
+}
+
+// The merge in LDS. Pairwise rounds over the children: the lane of each pair walks from their
+// shared point to the bridge (a step per removed vertex, marking it dead) and relinks the chain;
+// nothing moves. The survivors, in slot order, are the parent's hull.
+template <bool W, bool PR>
+__device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, const LdsVerts<W, PR>& v,
+                          int64_t row, int64_t c0, int nch, const NodeOut& pout) {
+  const int lane = threadIdx.x;
+  const int total = sm.total;
+  constexpr int B = 8;  // slots per lane with their loads in flight together
+  for (int s0 = 0; s0 < total; s0 += kWave * B) {
+    HPt p[B];
 #pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      DD ow{__shfl_up(iw.hi, d, kWave), __shfl_up(iw.lo, d, kWave)};
-      DD os{__shfl_up(is.hi, d, kWave), __shfl_up(is.lo, d, kWave)};
-      const int oslot = __shfl_up(islot, d, kWave);
-      if (tid >= d) {
-        iw = dd_add(ow, iw);
-        is = dd_add(os, is);
-        islot += oslot;
+    for (int u = 0; u < B; ++u) {
+      const int s = s0 + u * kWave + lane;
+      if (s < total) {
+        const int c = child_of_slot(sm, nch, s);
+        p[u] = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
       }
     }
-    const int anybad = __any(bad != 0);
-    DD ew{__shfl_up(iw.hi, 1, kWave), __shfl_up(iw.lo, 1, kWave)};
-    DD es{__shfl_up(is.hi, 1, kWave), __shfl_up(is.lo, 1, kWave)};
-    if (tid == 0) ew = es = DD{0.0, 0.0};
-    if (tid < nch) {
-      sh.cnt[tid] = cnt;
-      sh.off[tid] = islot - max(cnt - 1, 0);
-      sh.tot[0][tid] = ew.hi;
-      sh.tot[1][tid] = ew.lo;
-      sh.tot[2][tid] = es.hi;
-      sh.tot[3][tid] = es.lo;
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int s = s0 + u * kWave + lane;
+      if (s < total) {
+        lput<W, PR>(v, s, p[u]);
+        v.prev[s] = static_cast<int16_t>(s - 1);
+        v.next[s] = static_cast<int16_t>(s + 1);
+        v.dead[s] = 0;
+      }
     }
-    if (tid == nch - 1) {
-      sh.tot[0][nch] = iw.hi;
-      sh.tot[1][nch] = iw.lo;
-      sh.tot[2][nch] = is.hi;
-      sh.tot[3][nch] = is.lo;
-      sh.maxlen = islot + 1;  // total slots
-    }
-    if (tid == 0) sh.bad = anybad;
   }
   __syncthreads();
-  const int total = sh.maxlen;
-  const bool in_lds = total <= kLdsVerts;
-  VArr v;
-  if (in_lds) v = VArr{sh.idx, sh.shi, sh.slo, W ? sh.whi : nullptr, W ? sh.wlo : nullptr};
-  else v = dvarr_of(pout);
-
-  // Lay the children end to end (each child's first vertex is the previous child's last,
-  // stored once), in coordinates relative to the parent: one thread per slot, its child found
-  // by a binary search over the children's first slots.
-  for (int s = tid; s < total; s += kMergeThreads) {
-    int lo = 0, hi = nch - 1;  // the last child whose first slot is below s (child 0 for s = 0)
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (sh.off[mid] < s) lo = mid;
-      else hi = mid - 1;
+#pragma unroll 1
+  for (int span = 1; span < nch; span <<= 1) {
+    const int pa = lane * 2 * span, pb = pa + span;
+    if (pb < nch) {
+      const int x = sm.off[pb];
+      const int lhead = sm.off[pa];
+      const int rtail = pb + span < nch ? sm.off[pb + span] : total - 1;
+      int ia = v.prev[x], ib = v.next[x];
+      HPt A = lget<W, PR>(v, ia), B = lget<W, PR>(v, ib);
+      if (hpools<W, PR>(A, lget<W, PR>(v, x), B)) {
+        v.dead[x] = 1;
+        int iap = ia != lhead ? v.prev[ia] : -1;
+        int ibn = ib != rtail ? v.next[ib] : -1;
+        HPt AP = iap >= 0 ? lget<W, PR>(v, iap) : A;
+        HPt BN = ibn >= 0 ? lget<W, PR>(v, ibn) : B;
+        for (;;) {  // every step marks a vertex dead: at most `total` steps
+          if (iap >= 0 && hpools<W, PR>(AP, A, B)) {
+            v.dead[ia] = 1;
+            ia = iap;
+            A = AP;
+            iap = ia != lhead ? v.prev[ia] : -1;
+            if (iap >= 0) AP = lget<W, PR>(v, iap);
+          } else if (ibn >= 0 && hpools<W, PR>(A, B, BN)) {
+            v.dead[ib] = 1;
+            ib = ibn;
+            B = BN;
+            ibn = ib != rtail ? v.next[ib] : -1;
+            if (ibn >= 0) BN = lget<W, PR>(v, ibn);
+          } else {
+            break;
+          }
+        }
+        v.next[ia] = static_cast<int16_t>(ib);
+        v.prev[ib] = static_cast<int16_t>(ia);
+      }
     }
-    const int c = lo, k = s - sh.off[c];
-    const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + c);
-    const DD ow{sh.tot[0][c], sh.tot[1][c]}, os{sh.tot[2][c], sh.tot[3][c]};
+    __syncthreads();
+  }
+  // Compaction of the survivors into the parent's arrays.
+  int base = 0;
+  for (int s0 = 0; s0 < total; s0 += kWave) {
+    const int s = s0 + lane;
+    const bool alive = s < total && v.dead[s] == 0;
+    const uint64_t m = __ballot(alive);
+    if (alive) {
+      const int q = base + __popcll(m & ((uint64_t{1} << lane) - 1));
+      const HPt p = lget<W, PR>(v, s);
+      pout.idx[q] = p.i;
+      pout.shi[q] = p.s;
+      pout.slo[q] = p.sl;
+      if constexpr (W) {
+        pout.whi[q] = p.w;
+        pout.wlo[q] = p.wl;
+      }
+    }
+    base += __popcll(m);
+  }
+  if (lane == 0) *pout.count = base;
+}
+
+// The merge in the parent's global array, for children with more vertices than LDS holds
+// (hulls of trend-like data, where few vertices drop): children laid end to end, then pairwise
+// rounds of bridges (one lane per pair) and moves of each right part's surviving suffix.
+template <bool W, bool PR>
+__device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, int64_t c0, int nch,
+                             const NodeOut& pout) {
+  const int tid = threadIdx.x;
+  const int total = sm.total;
+  const VArr v = dvarr_of(pout);
+  for (int s = tid; s < total; s += kWave) {
+    const int c = child_of_slot(sm, nch, s);
+    const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
     VPt p;
-    p.i = ci.idx[k] + static_cast<int>(c * a.child_elems);
-    p.s = dd_add(os, DD{ci.shi[k], ci.slo[k]});
-    if constexpr (W) p.w = dd_add(ow, DD{ci.whi[k], ci.wlo[k]});
+    p.i = h.i;
+    p.s = DD{h.s, h.sl};
+    p.w = DD{h.w, h.wl};
     vstore<W>(v, s, p);
   }
   __syncthreads();
-
-  // Pairwise rounds.
 #pragma unroll 1
   for (int span = 1; span < nch; span <<= 1) {
     const int nm = (nch + 2 * span - 1) / (2 * span);  // merges this round
     if (tid < nm) {
       const int pa = tid * 2 * span, pb = pa + span;
-      int keep = sh.cnt[pa], from = 0;
-      if (pb < nch) {
-        vbridge<W>(v, sh.off[pa], sh.cnt[pa], sh.off[pb], sh.cnt[pb], keep, from);
-      }
-      sh.keep[tid] = keep;
-      sh.from[tid] = from;
+      int keep = sm.cnt[pa], from = 0;
+      if (pb < nch) vbridge<W>(v, sm.off[pa], sm.cnt[pa], sm.off[pb], sm.cnt[pb], keep, from);
+      sm.keep[tid] = keep;
+      sm.from[tid] = from;
     }
     __syncthreads();
     // Move each right part's kept suffix next to its left part's kept prefix.
-    const int gsz = kMergeThreads / nm >= 1 ? kMergeThreads / nm : 1;
+    const int gsz = kWave / nm >= 1 ? kWave / nm : 1;
     const int m = tid / gsz;
     const int r = tid - m * gsz;
     int len = 0, src = 0, dst = 0;
     if (m < nm) {
       const int pa = m * 2 * span, pb = pa + span;
       if (pb < nch) {
-        len = sh.cnt[pb] - sh.from[m];
-        src = sh.off[pb] + sh.from[m];
-        dst = sh.off[pa] + sh.keep[m];
+        len = sm.cnt[pb] - sm.from[m];
+        src = sm.off[pb] + sm.from[m];
+        dst = sm.off[pa] + sm.keep[m];
         if (src == dst) len = 0;
       }
     }
-    // rounds: every thread reads its share into registers, then writes (src is never below dst)
-    __shared__ int rounds_max;
-    if (tid == 0) rounds_max = 0;
+    if (tid == 0) sm.rounds_max = 0;
     __syncthreads();
     constexpr int R = 4;
     const int my_rounds = (len + gsz * R - 1) / (gsz * R);
-    if (my_rounds > 0) atomicMax(&rounds_max, my_rounds);
+    if (my_rounds > 0) atomicMax(&sm.rounds_max, my_rounds);
     __syncthreads();
-    const int rounds = rounds_max;
-    for (int rd = 0; rd < rounds; ++rd) {
+    const int rounds = sm.rounds_max;
+    for (int rd = 0; rd < rounds; ++rd) {  // reads, then writes: src is never below dst
       VPt buf[R];
 #pragma unroll
       for (int q = 0; q < R; ++q) {
@@ -293,24 +408,113 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(MergeArgs a) {
     }
     if (tid < nm) {
       const int pa = tid * 2 * span, pb = pa + span;
-      if (pb < nch) sh.cnt[pa] = sh.keep[tid] + (sh.cnt[pb] - sh.from[tid]);
+      if (pb < nch) sm.cnt[pa] = sm.keep[tid] + (sm.cnt[pb] - sm.from[tid]);
     }
     __syncthreads();
   }
+  if (tid == 0) *pout.count = sm.cnt[0];
+}
 
-  // The parent's hull.
-  const int hull = sh.cnt[0];
-  if (in_lds) {
-    for (int k = tid; k < hull; k += kMergeThreads) vstore<W>(dvarr_of(pout), k, vload<W>(v, k));
+// One wave per parent node: G = 64 children (fewer at a row's end) -> the parent's hull.
+template <bool W, bool PR>
+__global__ __launch_bounds__(kWave) void merge_kernel(MergeArgs a, int cap_lds) {
+  __shared__ MergeSmall sm;
+  extern __shared__ __align__(16) char lds_dyn[];
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x / a.npr_out;
+  const int64_t j = blockIdx.x - row * a.npr_out;
+  const int64_t c0 = j * kGroup;  // first child within the row
+  const int nch = static_cast<int>(min<int64_t>(kGroup, a.npr_in - c0));
+  const NodeOut pout = node_out(a.out, a.k_out, a.cap_out, W, row * a.npr_out + j);
+
+  // Children: counts, NaN flags, and offsets within the parent (double-double scan).
+  int cnt = 0, bad = 0;
+  DD tw{0.0, 0.0}, ts{0.0, 0.0};
+  if (lane < nch) {
+    const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + lane);
+    cnt = *ci.count;
+    bad = *ci.bad;
+    tw = DD{ci.tot[0], ci.tot[1]};
+    ts = DD{ci.tot[2], ci.tot[3]};
   }
-  if (tid == 0) {
-    *pout.count = hull;
-    *pout.bad = sh.bad;
-    pout.tot[0] = sh.tot[0][nch];
-    pout.tot[1] = sh.tot[1][nch];
-    pout.tot[2] = sh.tot[2][nch];
-    pout.tot[3] = sh.tot[3][nch];
+  // inclusive scans: totals (dd) and slots (count - 1, the shared point stored once)
+  DD iw = tw, is = ts;
+  int islot = max(cnt - 1, 0);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const DD ow{__shfl_up(iw.hi, d, kWave), __shfl_up(iw.lo, d, kWave)};
+    const DD os{__shfl_up(is.hi, d, kWave), __shfl_up(is.lo, d, kWave)};
+    const int oslot = __shfl_up(islot, d, kWave);
+    if (lane >= d) {
+      iw = dd_add(ow, iw);
+      is = dd_add(os, is);
+      islot += oslot;
+    }
   }
+  const int anybad = __any(bad != 0);
+  DD ew{__shfl_up(iw.hi, 1, kWave), __shfl_up(iw.lo, 1, kWave)};
+  DD es{__shfl_up(is.hi, 1, kWave), __shfl_up(is.lo, 1, kWave)};
+  if (lane == 0) ew = es = DD{0.0, 0.0};
+  if (lane < nch) {
+    sm.cnt[lane] = cnt;
+    sm.off[lane] = islot - max(cnt - 1, 0);
+    sm.tot[0][lane] = ew.hi;
+    sm.tot[1][lane] = ew.lo;
+    sm.tot[2][lane] = es.hi;
+    sm.tot[3][lane] = es.lo;
+  }
+  if (lane == nch - 1) {
+    sm.tot[0][nch] = iw.hi;
+    sm.tot[1][nch] = iw.lo;
+    sm.tot[2][nch] = is.hi;
+    sm.tot[3][nch] = is.lo;
+    sm.total = islot + 1;  // slots
+  }
+  if (lane == 0) sm.bad = anybad;
+  __syncthreads();
+
+  if (sm.total <= cap_lds) {
+    merge_lds<W, PR>(a, sm, lds_carve<W, PR>(lds_dyn, cap_lds), row, c0, nch, pout);
+  } else {
+    merge_global<W, PR>(a, sm, row, c0, nch, pout);
+  }
+  if (lane == 0) {
+    *pout.bad = sm.bad;
+    pout.tot[0] = sm.tot[0][nch];
+    pout.tot[1] = sm.tot[1][nch];
+    pout.tot[2] = sm.tot[2][nch];
+    pout.tot[3] = sm.tot[3][nch];
+  }
+}
+
+// Per expansion tile of tile_n elements (one thread each): the final hull's last vertex at or
+// before the tile's first element, and its first vertex at or after the tile's end, by binary
+// searches over the row's hull (which runs from index 0 to n). All tiles search at once, so the
+// expansion and the backward start from two loads.
+__global__ __launch_bounds__(256) void rank_kernel(const void* hulls, int64_t batch, int64_t cap, bool weighted,
+                                                   int64_t n, int64_t tile_n, int64_t tpr, int* rank) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= batch * tpr) return;
+  const int64_t row = g / tpr;
+  const int64_t ta = (g - row * tpr) * tile_n;
+  const int64_t tb = min(ta + tile_n, n);
+  const NodeOut fin = node_out(const_cast<void*>(hulls), batch, cap, weighted, row);
+  const int* idx = fin.idx;
+  const int count = *fin.count;
+  int lo = 0, hi = count - 1;  // idx[0] = 0 <= ta
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (idx[mid] <= ta) lo = mid;
+    else hi = mid - 1;
+  }
+  rank[2 * g] = lo;
+  hi = count - 1;  // idx[count - 1] = n >= tb
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (idx[mid] >= tb) hi = mid;
+    else lo = mid + 1;
+  }
+  rank[2 * g + 1] = lo;
 }
 
 // Per tile: the fit from the row's final hull.
@@ -321,7 +525,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   constexpr int NT = C::kThreads;
   __shared__ double sl[C::kN + 2];
   __shared__ uint32_t bits[C::kN / 32];
-  __shared__ int lo_s, hi_s, rank_scan[kWaves256];
+  __shared__ int rank_scan[kWaves256];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -333,65 +537,13 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   const VArr v = dvarr_of(fin);
   const int count = *fin.count;
   const bool row_bad = *fin.bad != 0;
-  const int ta = static_cast<int>(first), tb = static_cast<int>(first + len);
+  const int ta = static_cast<int>(first);
 
-  // rA: the last vertex at or before the tile's first element; rB: the first at or after its
-  // end. 256-ary search over the final hull's indices.
-  if (tid == 0) {
-    lo_s = 0;
-    hi_s = count - 1;
-  }
-  __syncthreads();
-  // (the indices strictly increase, so one sub-range always brackets ta; at most
-  // ceil(log_256(count)) rounds, bounded by 8 in any case)
-  for (int it = 0; it < 8; ++it) {
-    const int lo = lo_s, hi = hi_s;  // invariant: idx[lo] <= ta < idx[hi] (or lo == hi)
-    __syncthreads();
-    if (hi - lo <= 1) break;
-    const int64_t span = hi - lo;
-    const int p = lo + static_cast<int>((span * tid) / NT);
-    const int q = lo + static_cast<int>((span * (tid + 1)) / NT);
-    if (p < q) {
-      const int ip = v.idx[p];
-      const int iq = v.idx[q];
-      if (ip <= ta && ta < iq) {
-        lo_s = p;
-        hi_s = q;
-      }
-    }
-    __syncthreads();
-  }
-  const int rA = lo_s;
-  // rB: first vertex with idx >= tb, searching from rA
-  __syncthreads();
-  if (tid == 0) {
-    lo_s = rA;
-    hi_s = count - 1;
-  }
-  __syncthreads();
-  for (int it = 0; it < 8; ++it) {
-    const int lo = lo_s, hi = hi_s;  // invariant: idx[lo] < tb <= idx[hi] (or lo == hi)
-    __syncthreads();
-    if (hi - lo <= 1) break;
-    const int64_t span = hi - lo;
-    const int p = lo + static_cast<int>((span * tid) / NT);
-    const int q = lo + static_cast<int>((span * (tid + 1)) / NT);
-    if (p < q) {
-      const int ip = v.idx[p];
-      const int iq = v.idx[q];
-      if (ip < tb && tb <= iq) {
-        lo_s = p;
-        hi_s = q;
-      }
-    }
-    __syncthreads();
-  }
-  int rB = v.idx[lo_s] >= tb ? lo_s : hi_s;
-  rB = min(rB, rA + C::kN + 1);  // holds for any well-formed hull; keeps sl[] in bounds regardless
-  if (a.tile_rank != nullptr && tid == 0) {
-    a.tile_rank[2 * blockIdx.x] = rA;
-    a.tile_rank[2 * blockIdx.x + 1] = rB;
-  }
+  // the vertex ranks around the tile, written by the last merge
+  const int rA = a.tile_rank[2 * blockIdx.x];
+  int rB = a.tile_rank[2 * blockIdx.x + 1];
+  // (both hold for any well-formed hull; they keep sl[] and the vertex reads in bounds regardless)
+  rB = min(min(rB, rA + C::kN + 1), count - 1);
 
   // Edge slopes rA .. rB-1 and the vertex bits of the tile.
   for (int wd = tid; wd < C::kN / 32; wd += NT) bits[wd] = 0u;
@@ -496,8 +648,27 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     m.npr_out = p.npr[l];
     m.child_elems = p.span[l - 1];
     const unsigned grid = static_cast<unsigned>(t.batch * p.npr[l]);
-    if (W) merge_kernel<true><<<dim3(grid), dim3(kMergeThreads), 0, t.stream>>>(m);
-    else merge_kernel<false><<<dim3(grid), dim3(kMergeThreads), 0, t.stream>>>(m);
+    // LDS vertex capacity: 1024 where many merges share the GPU, else what 60 KB holds
+    auto launch = [&](auto kern, size_t vb) {
+      const int big = static_cast<int>((60 * 1024 / vb) & ~size_t(63));
+      const int cap = grid >= 1024 ? (big < 1024 ? big : 1024) : big;
+      kern<<<dim3(grid), dim3(kWave), cap * vb, t.stream>>>(m, cap);
+    };
+    if (t.dtype == TI_F32) {
+      if (W) launch(merge_kernel<true, false>, lds_vertex_bytes<true, false>());
+      else launch(merge_kernel<false, false>, lds_vertex_bytes<false, false>());
+    } else {
+      if (W) launch(merge_kernel<true, true>, lds_vertex_bytes<true, true>());
+      else launch(merge_kernel<false, true>, lds_vertex_bytes<false, true>());
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  {
+    const int64_t tiles = t.batch * p.tiles_per_row;
+    rank_kernel<<<dim3(static_cast<unsigned>((tiles + 255) / 256)), dim3(256), 0, t.stream>>>(
+        base + p.off_buf[p.levels & 1], t.batch, p.cap[p.levels], W, t.n, tile_elems(W), p.tiles_per_row,
+        reinterpret_cast<int*>(base + p.off_rank));
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -37,13 +37,6 @@ struct SpanArgs {
   int64_t cap;
 };
 
-// A point of the span: index, cumulative w*y and w relative to the span start (unweighted: w is
-// the index), and for float64 data their rounding errors.
-struct SPt {
-  int i;
-  double s, sl, w, wl;
-};
-
 template <typename T, bool W>
 struct SpanOps {
   static constexpr bool PR = sizeof(T) == 8;
@@ -57,7 +50,7 @@ struct SpanOps {
     double wl[W && PR ? kRing : 1][kSpanLanes];
   };
 
-  __device__ static void put(Ring& r, int slot, int lane, const SPt& p) {
+  __device__ static void put(Ring& r, int slot, int lane, const HPt& p) {
     r.idx[slot][lane] = p.i;
     r.s[slot][lane] = p.s;
     if constexpr (PR) r.sl[slot][lane] = p.sl;
@@ -65,8 +58,8 @@ struct SpanOps {
     if constexpr (W && PR) r.wl[slot][lane] = p.wl;
   }
 
-  __device__ static SPt get(const Ring& r, int slot, int lane) {
-    SPt p;
+  __device__ static HPt get(const Ring& r, int slot, int lane) {
+    HPt p;
     p.i = r.idx[slot][lane];
     p.s = r.s[slot][lane];
     p.sl = PR ? r.sl[PR ? slot : 0][lane] : 0.0;
@@ -76,7 +69,7 @@ struct SpanOps {
   }
 
   // Node arrays hold double-double sums; float32 data has no rounding errors to carry (lo = 0).
-  __device__ static void node_put(const NodeOut& o, int q, const SPt& p) {
+  __device__ static void node_put(const NodeOut& o, int q, const HPt& p) {
     o.idx[q] = p.i;
     o.shi[q] = p.s;
     o.slo[q] = p.sl;
@@ -86,8 +79,8 @@ struct SpanOps {
     }
   }
 
-  __device__ static SPt node_get(const NodeOut& o, int q) {
-    SPt p;
+  __device__ static HPt node_get(const NodeOut& o, int q) {
+    HPt p;
     p.i = o.idx[q];
     p.s = o.shi[q];
     p.sl = PR ? o.slo[q] : 0.0;
@@ -96,27 +89,6 @@ struct SpanOps {
     return p;
   }
 
-  // The vertex b leaves the hull through a, b, c (equal slopes pool).
-  __device__ static bool pools3(const SPt& a, const SPt& b, const SPt& c) {
-    double dS1 = b.s - a.s, dS2 = c.s - b.s;
-    if constexpr (PR) {
-      dS1 += b.sl - a.sl;
-      dS2 += c.sl - b.sl;
-    }
-    double dW1, dW2;
-    if constexpr (W) {
-      dW1 = b.w - a.w;
-      dW2 = c.w - b.w;
-      if constexpr (PR) {
-        dW1 += b.wl - a.wl;
-        dW2 += c.wl - b.wl;
-      }
-    } else {
-      dW1 = static_cast<double>(b.i - a.i);
-      dW2 = static_cast<double>(c.i - b.i);
-    }
-    return pools<true>(dS1, dW1, dS2, dW2);
-  }
 };
 
 template <typename T, int N>
@@ -159,7 +131,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // The stack holds positions [0, depth): [r0, depth) in the ring (position q in slot q % kRing),
   // [0, r0) in the node array. t1, t2, t3: positions depth-1, depth-2, depth-3.
   int depth = 1, r0 = 0;
-  SPt t1{0, 0.0, 0.0, 0.0, 0.0}, t2 = t1, t3 = t1;
+  HPt t1{0, 0.0, 0.0, 0.0, 0.0}, t2 = t1, t3 = t1;
   Ops::put(ring, 0, lane, t1);
 
   double S = 0.0, SL = 0.0, P = 0.0, PL = 0.0;
@@ -207,8 +179,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
           cand = inc ? yc[k] < ynext : ynext < yc[k];
         }
         if (cand) {
-          const SPt c{e + 1, S, SL, P, PL};
-          while (depth >= 2 && Ops::pools3(t2, t1, c)) {
+          const HPt c{e + 1, S, SL, P, PL};
+          while (depth >= 2 && hpools<W, PR>(t2, t1, c)) {
             --depth;
             t1 = t2;
             t2 = t3;

@@ -6,6 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "ti_common.h"
 #include "ti_kernels.h"
 
 namespace ti {
@@ -146,6 +147,38 @@ __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, co
   }
 }
 
+// A hull point of the long-row kernels: index (relative to its node's first element), and
+// cumulative w*y (s) and w (w; unweighted rows use the index) relative to the node's first point.
+// Float64 data also carries the sums' rounding errors (sl, wl), zero for float32 data.
+struct HPt {
+  int i;
+  double s, sl, w, wl;
+};
+
+// The vertex b leaves the hull through a, b, c (equal slopes pool); PR: the points carry
+// rounding errors.
+template <bool W, bool PR>
+__device__ __forceinline__ bool hpools(const HPt& a, const HPt& b, const HPt& c) {
+  double dS1 = b.s - a.s, dS2 = c.s - b.s;
+  if constexpr (PR) {
+    dS1 += b.sl - a.sl;
+    dS2 += c.sl - b.sl;
+  }
+  double dW1, dW2;
+  if constexpr (W) {
+    dW1 = b.w - a.w;
+    dW2 = c.w - b.w;
+    if constexpr (PR) {
+      dW1 += b.wl - a.wl;
+      dW2 += c.wl - b.wl;
+    }
+  } else {
+    dW1 = static_cast<double>(b.i - a.i);
+    dW2 = static_cast<double>(c.i - b.i);
+  }
+  return pools<true>(dS1, dW1, dS2, dW2);
+}
+
 // Rows longer than one tile: one lane builds the hull of each span of kSpan elements, then
 // workgroups merge G neighbouring hulls at a time until one hull per row remains.
 constexpr int kSpan = 256;
@@ -165,8 +198,7 @@ struct ExpandArgs {
   int64_t batch, cap, n, tiles_per_row;
   void* out;
   uint32_t* starts;
-  int* tile_rank;  // per tile: the final hull's last vertex at or before the tile's first element,
-                   // and its first vertex at or after the tile's end
+  const int* tile_rank;  // per tile: the final hull's vertex ranks around it (rank_kernel's)
   unsigned flags;
   double lo, hi;
 };
