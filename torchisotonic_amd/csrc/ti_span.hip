@@ -2,15 +2,22 @@
 //
 // Replaces the reference's chunk stage for long rows (reference src/torchisotonic/csrc/
 // tiles.cuh:665-913, chunk_kernel, which builds small lane hulls and merges them across the
-// block in rounds). A lane instead runs the monotone chain over its whole span by itself,
-// streaming the elements through registers kChunk at a time (the next chunk loading while the
-// current one is processed): no block-wide scans, no merge rounds, no barriers, every lane
-// busy. The lane's cumulative sums are float64 relative to the span start; float64 data also
-// carries their rounding errors (two-sum), so the difference of neighbouring points keeps the
-// precision of the difference. The hull stack keeps its top three vertices in registers and
-// its positions in a ring of kRing LDS slots per lane; positions that fall out of the ring go
-// to the span's hull array in global memory, where the finished hull ends anyway (noisy data
-// seldom gets that deep).
+// block in rounds). A lane instead runs the monotone chain over its whole span by itself: no
+// block-wide scans, no merge rounds, no barriers. The span streams through registers C elements
+// at a time (the next chunk loading meanwhile), in two phases per chunk:
+//
+//   1. uniform work: the cumulative sums (float64, relative to the span start; float64 data
+//      also carries their rounding errors, two-sum) at every point of the chunk go to the lane's
+//      LDS chunk buffer, and the candidate points to a bit mask;
+//   2. an event loop in which every lane does one stack operation per iteration on its own
+//      candidates - pop the top vertex, or push the next candidate - reading the top two
+//      vertices and the candidate from LDS. Lanes advance independently, so one lane's run of
+//      pops does not hold the others at a data-dependent loop (a loop per candidate would make
+//      the whole wave wait, at every point, for the lane with the most pops).
+//
+// The stack lives in a ring of R LDS slots per lane; positions that fall out of it go to the
+// span's hull array in global memory, where the finished hull ends anyway (noisy data seldom
+// gets that deep).
 //
 // A point is a candidate only where the data rises into it (y_{k-1} < y_k): elsewhere the slope
 // into it is at least the slope out of it, and equal slopes pool, so it is never a vertex.
@@ -25,7 +32,6 @@ namespace ti {
 namespace {
 
 constexpr int kSpanLanes = 64;
-constexpr int kChunk = 16;
 
 struct SpanArgs {
   const void* y;
@@ -37,58 +43,20 @@ struct SpanArgs {
   int64_t cap;
 };
 
-template <typename T, bool W>
-struct SpanOps {
+// Per lane (columns [slot][lane], so lanes never share a bank row): the chunk buffer (sums at
+// each point of the chunk) and the stack ring.
+template <typename T, bool W, int C, int R>
+struct SpanLds {
   static constexpr bool PR = sizeof(T) == 8;
-  static constexpr int kRing = W ? 8 : 16;
-
-  struct Ring {
-    int idx[kRing][kSpanLanes];
-    double s[kRing][kSpanLanes];
-    double sl[PR ? kRing : 1][kSpanLanes];
-    double w[W ? kRing : 1][kSpanLanes];
-    double wl[W && PR ? kRing : 1][kSpanLanes];
-  };
-
-  __device__ static void put(Ring& r, int slot, int lane, const HPt& p) {
-    r.idx[slot][lane] = p.i;
-    r.s[slot][lane] = p.s;
-    if constexpr (PR) r.sl[slot][lane] = p.sl;
-    if constexpr (W) r.w[slot][lane] = p.w;
-    if constexpr (W && PR) r.wl[slot][lane] = p.wl;
-  }
-
-  __device__ static HPt get(const Ring& r, int slot, int lane) {
-    HPt p;
-    p.i = r.idx[slot][lane];
-    p.s = r.s[slot][lane];
-    p.sl = PR ? r.sl[PR ? slot : 0][lane] : 0.0;
-    p.w = W ? r.w[W ? slot : 0][lane] : 0.0;
-    p.wl = (W && PR) ? r.wl[(W && PR) ? slot : 0][lane] : 0.0;
-    return p;
-  }
-
-  // Node arrays hold double-double sums; float32 data has no rounding errors to carry (lo = 0).
-  __device__ static void node_put(const NodeOut& o, int q, const HPt& p) {
-    o.idx[q] = p.i;
-    o.shi[q] = p.s;
-    o.slo[q] = p.sl;
-    if constexpr (W) {
-      o.whi[q] = p.w;
-      o.wlo[q] = p.wl;
-    }
-  }
-
-  __device__ static HPt node_get(const NodeOut& o, int q) {
-    HPt p;
-    p.i = o.idx[q];
-    p.s = o.shi[q];
-    p.sl = PR ? o.slo[q] : 0.0;
-    p.w = W ? o.whi[q] : 0.0;
-    p.wl = (W && PR) ? o.wlo[q] : 0.0;
-    return p;
-  }
-
+  double cs[C][kSpanLanes];
+  double csl[PR ? C : 1][kSpanLanes];
+  double cw[W ? C : 1][kSpanLanes];
+  double cwl[W && PR ? C : 1][kSpanLanes];
+  int ri[R][kSpanLanes];
+  double rs[R][kSpanLanes];
+  double rsl[PR ? R : 1][kSpanLanes];
+  double rw[W ? R : 1][kSpanLanes];
+  double rwl[W && PR ? R : 1][kSpanLanes];
 };
 
 template <typename T, int N>
@@ -99,7 +67,7 @@ __device__ __forceinline__ void load_chunk(const T* __restrict__ p, int count, T
     const VT* q = reinterpret_cast<const VT*>(p);
 #pragma unroll
     for (int j = 0; j < N / V; ++j) {
-      const VT x = __builtin_nontemporal_load(q + j);
+      const VT x = q[j];
 #pragma unroll
       for (int t = 0; t < V; ++t) v[j * V + t] = x[t];
     }
@@ -109,12 +77,11 @@ __device__ __forceinline__ void load_chunk(const T* __restrict__ p, int count, T
   }
 }
 
-template <typename T, bool W>
+template <typename T, bool W, int C, int R>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
-  using Ops = SpanOps<T, W>;
-  constexpr bool PR = Ops::PR;
-  constexpr int kRing = Ops::kRing;
-  __shared__ typename Ops::Ring ring;
+  static_assert((R & (R - 1)) == 0 && C <= 32, "ring slots: a power of two; chunk: a 32-bit mask");
+  constexpr bool PR = sizeof(T) == 8;
+  __shared__ SpanLds<T, W, C, R> L;
   const int lane = threadIdx.x;
   const int64_t node = static_cast<int64_t>(blockIdx.x) * kSpanLanes + lane;
   if (node >= a.nodes) return;  // no barriers below: the lanes are independent
@@ -128,90 +95,182 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   const T* w = W ? static_cast<const T*>(a.w) + row * a.n + first : nullptr;
   const NodeOut o = node_out(a.hulls, a.nodes, a.cap, W, node);
 
-  // The stack holds positions [0, depth): [r0, depth) in the ring (position q in slot q % kRing),
-  // [0, r0) in the node array. t1, t2, t3: positions depth-1, depth-2, depth-3.
+  auto ring_put = [&](int q, const HPt& p) {
+    const int r = q & (R - 1);
+    L.ri[r][lane] = p.i;
+    L.rs[r][lane] = p.s;
+    if constexpr (PR) L.rsl[r][lane] = p.sl;
+    if constexpr (W) L.rw[r][lane] = p.w;
+    if constexpr (W && PR) L.rwl[r][lane] = p.wl;
+  };
+  auto ring_get = [&](int q) -> HPt {
+    const int r = q & (R - 1);
+    HPt p;
+    p.i = L.ri[r][lane];
+    p.s = L.rs[r][lane];
+    p.sl = PR ? L.rsl[PR ? r : 0][lane] : 0.0;
+    p.w = W ? L.rw[W ? r : 0][lane] : 0.0;
+    p.wl = (W && PR) ? L.rwl[(W && PR) ? r : 0][lane] : 0.0;
+    return p;
+  };
+  // node arrays hold double-double sums; float32 data has no rounding errors to carry (lo = 0)
+  auto node_put = [&](int q, const HPt& p) {
+    o.idx[q] = p.i;
+    o.shi[q] = p.s;
+    o.slo[q] = p.sl;
+    if constexpr (W) {
+      o.whi[q] = p.w;
+      o.wlo[q] = p.wl;
+    }
+  };
+  auto node_get = [&](int q) -> HPt {
+    HPt p;
+    p.i = o.idx[q];
+    p.s = o.shi[q];
+    p.sl = PR ? o.slo[q] : 0.0;
+    p.w = W ? o.whi[q] : 0.0;
+    p.wl = (W && PR) ? o.wlo[q] : 0.0;
+    return p;
+  };
+
+  // The stack holds positions [0, depth): [r0, depth) in the ring (1 <= depth - r0 <= R), [0, r0)
+  // in the node array.
   int depth = 1, r0 = 0;
-  HPt t1{0, 0.0, 0.0, 0.0, 0.0}, t2 = t1, t3 = t1;
-  Ops::put(ring, 0, lane, t1);
+  ring_put(0, HPt{0, 0.0, 0.0, 0.0, 0.0});
 
   double S = 0.0, SL = 0.0, P = 0.0, PL = 0.0;
   bool bad = false, wbad = false;
-  T yc[kChunk], yn[kChunk];
-  T wc[W ? kChunk : 1], wn[W ? kChunk : 1];
-  load_chunk<T, kChunk>(y, len, yc);
-  if constexpr (W) load_chunk<T, kChunk>(w, len, wc);
-  for (int c0 = 0; c0 < len; c0 += kChunk) {
-    const int rest = len - (c0 + kChunk);
+  T yc[C], yn[C];
+  T wc[W ? C : 1], wn[W ? C : 1];
+  load_chunk<T, C>(y, len, yc);
+  if constexpr (W) load_chunk<T, C>(w, len, wc);
+  for (int c0 = 0; c0 < len; c0 += C) {
+    const int rest = len - (c0 + C);
     if (rest > 0) {
-      load_chunk<T, kChunk>(y + c0 + kChunk, rest, yn);
-      if constexpr (W) load_chunk<T, kChunk>(w + c0 + kChunk, rest, wn);
+      load_chunk<T, C>(y + c0 + C, rest, yn);
+      if constexpr (W) load_chunk<T, C>(w + c0 + C, rest, wn);
     }
-#pragma unroll
-    for (int k = 0; k < kChunk; ++k) {
-      const int e = c0 + k;  // the element; the point after it is e + 1
-      if (e < len) {
-        const double ye = sgn * static_cast<double>(yc[k]);
-        bad |= ye != ye;
-        double term = ye;
-        if constexpr (W) {
-          const double we = static_cast<double>(wc[k]);
-          wbad |= !(we > 0.0);
-          term = we * ye;
-          if constexpr (PR) {
-            const DD t = two_sum(P, we);
-            P = t.hi;
-            PL += t.lo;
-          } else {
-            P += we;
-          }
-        }
+    // 1. sums at every point of the chunk, and the candidates
+    uint32_t mask = 0;
+    auto element = [&](int k) {  // sums through element c0 + k, stored for the point after it
+      const double ye = sgn * static_cast<double>(yc[k]);
+      bad |= ye != ye;
+      double term = ye;
+      if constexpr (W) {
+        const double we = static_cast<double>(wc[k]);
+        wbad |= !(we > 0.0);
+        term = we * ye;
         if constexpr (PR) {
-          const DD t = two_sum(S, term);
-          S = t.hi;
-          SL += t.lo;
+          const DD t = two_sum(P, we);
+          P = t.hi;
+          PL += t.lo;
         } else {
-          S += term;
+          P += we;
         }
-        // the point after e is a candidate at the span's end or where y rises into e + 1
-        bool cand = e + 1 == len;
-        if (!cand) {
-          const T ynext = k + 1 < kChunk ? yc[k + 1 < kChunk ? k + 1 : 0] : yn[0];
-          cand = inc ? yc[k] < ynext : ynext < yc[k];
-        }
-        if (cand) {
-          const HPt c{e + 1, S, SL, P, PL};
-          while (depth >= 2 && hpools<W, PR>(t2, t1, c)) {
-            --depth;
-            t1 = t2;
-            t2 = t3;
-            if (depth >= 3) {
-              const int q = depth - 3;
-              t3 = q >= r0 ? Ops::get(ring, q % kRing, lane) : Ops::node_get(o, q);
-            }
-          }
-          const int q = depth;
-          if (q < r0) r0 = q;  // popped below the ring: it restarts at q
-          if (q >= r0 + kRing) {  // the ring's oldest position leaves for the node array
-            const int old = q - kRing;
-            Ops::node_put(o, old, Ops::get(ring, old % kRing, lane));
-            r0 = old + 1;
-          }
-          Ops::put(ring, q % kRing, lane, c);
-          ++depth;
-          t3 = t2;
-          t2 = t1;
-          t1 = c;
+      }
+      if constexpr (PR) {
+        const DD t = two_sum(S, term);
+        S = t.hi;
+        SL += t.lo;
+      } else {
+        S += term;
+      }
+      L.cs[k][lane] = S;
+      if constexpr (PR) L.csl[k][lane] = SL;
+      if constexpr (W) L.cw[k][lane] = P;
+      if constexpr (W && PR) L.cwl[k][lane] = PL;
+    };
+    // the point after element e is a candidate where y rises into e + 1, or at the span's end
+    auto rises = [&](T a, T b) { return inc ? a < b : b < a; };
+    if (__all(c0 + C <= len)) {
+      // whole chunks (all but a row's last span): no per-element bounds
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        element(k);
+        const bool cand = k + 1 < C ? rises(yc[k], yc[k + 1 < C ? k + 1 : 0]) : ((c0 + C == len) | rises(yc[k], yn[0]));
+        mask |= static_cast<uint32_t>(cand) << k;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        const int e = c0 + k;
+        if (e < len) {
+          element(k);
+          const T ynext = k + 1 < C ? yc[k + 1 < C ? k + 1 : 0] : yn[0];
+          const bool cand = (e + 1 == len) | (e + 1 < len && rises(yc[k], ynext));
+          mask |= static_cast<uint32_t>(cand) << k;
         }
       }
     }
+    // 2. one stack operation per lane and iteration until every lane has pushed its candidates.
+    // The loop touches LDS only (and stores spills), so the next chunk's loads stay in flight;
+    // a lane whose second vertex went to the node array makes the wave leave it, refill that
+    // lane's ring from the node array, and come back (rare).
+    for (;;) {
+      while (__any(mask != 0)) {
+        const bool act = mask != 0;
+        const bool two = act && depth >= 2;
+        if (__any(two && depth - 2 < r0)) break;
+        const int j = act ? __builtin_ctz(mask) : 0;
+        HPt c;
+        c.i = c0 + j + 1;
+        c.s = L.cs[j][lane];
+        c.sl = PR ? L.csl[PR ? j : 0][lane] : 0.0;
+        c.w = W ? L.cw[W ? j : 0][lane] : 0.0;
+        c.wl = (W && PR) ? L.cwl[(W && PR) ? j : 0][lane] : 0.0;
+        const HPt A = ring_get(depth - 2), B = ring_get(depth - 1);
+        // pools(A, B, c): a filtered fma test, exact where it cannot decide (see pools<true>)
+        double dS1 = B.s - A.s, dS2 = c.s - B.s, dW1, dW2;
+        if constexpr (PR) {
+          dS1 += B.sl - A.sl;
+          dS2 += c.sl - B.sl;
+        }
+        if constexpr (W) {
+          dW1 = B.w - A.w;
+          dW2 = c.w - B.w;
+          if constexpr (PR) {
+            dW1 += B.wl - A.wl;
+            dW2 += c.wl - B.wl;
+          }
+        } else {
+          dW1 = static_cast<double>(B.i - A.i);
+          dW2 = static_cast<double>(c.i - B.i);
+        }
+        const double qq = dS2 * dW1;
+        const double dd = __builtin_fma(dS1, dW2, -qq);
+        const bool close = !(__builtin_fabs(dd) > 0x1p-52 * __builtin_fabs(qq));
+        bool pop = two && dd > 0.0;
+        if (__any(two && close)) {
+          if (two && close) pop = cross_sign(dS1, dW2, dS2, dW1) >= 0;
+        }
+        const bool push = act && !pop;
+        if (push) {
+          const int q = depth;
+          if (q - r0 == R) {  // the ring is full: its oldest position leaves for the node array
+            node_put(r0, ring_get(r0));
+            ++r0;
+          }
+          ring_put(q, c);
+          mask &= mask - 1;
+        }
+        depth += push ? 1 : (pop ? -1 : 0);
+      }
+      if (!__any(mask != 0)) break;
+      if (mask != 0 && depth >= 2 && depth - 2 < r0) {
+        // only the top is in the ring (depth - 1 == r0): bring back up to R / 2 positions below
+        const int lo = r0 > R / 2 ? r0 - R / 2 : 0;
+        for (int q = lo; q < r0; ++q) ring_put(q, node_get(q));
+        r0 = lo;
+      }
+    }
 #pragma unroll
-    for (int k = 0; k < kChunk; ++k) {
+    for (int k = 0; k < C; ++k) {
       yc[k] = yn[k];
       if constexpr (W) wc[W ? k : 0] = wn[W ? k : 0];
     }
   }
   // the finished hull: positions [0, depth) of the span's array
-  for (int q = r0; q < depth; ++q) Ops::node_put(o, q, Ops::get(ring, q % kRing, lane));
+  for (int q = r0; q < depth; ++q) node_put(q, ring_get(q));
   *o.count = depth;
   *o.bad = bad ? 1 : 0;
   o.tot[0] = W ? P : static_cast<double>(len);
@@ -237,11 +296,11 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap) {
   const unsigned grid = static_cast<unsigned>((a.nodes + kSpanLanes - 1) / kSpanLanes);
   const bool W = t.w != nullptr;
   if (t.dtype == TI_F32) {
-    if (W) span_kernel<float, true><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<float, false><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) span_kernel<float, true, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    else span_kernel<float, false, 8, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   } else {
-    if (W) span_kernel<double, true><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<double, false><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) span_kernel<double, true, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    else span_kernel<double, false, 8, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   }
   return hipGetLastError();
 }
