@@ -16,7 +16,10 @@ Bytes per element (algorithmic, float32, each API tensor moved once): forward 8 
 
 ``roofline`` is for the dominant kernel of the headline step, timed live with HIP events
 recorded on the launch stream around each raw C-ABI launch on preallocated buffers: achieved =
-algorithmic bytes per launch / mean kernel time; peak = 8 TB/s.
+algorithmic bytes per launch / mean kernel time; peak = 8 TB/s. ``traffic`` is that kernel's
+HBM bytes per launch from the rocprofv3 FETCH_SIZE and WRITE_SIZE passes summarised in
+profiles/short_fit_kernel_c2_traffic.json (each counter scaled by what it reads for a copy-like
+kernel of known size), or null where that summary is absent.
 
 ``cpu_baseline`` times the reference's own pava.h (compiled from the reference checkout into
 oracle/_ref/libti_ref.so; kind "reference") or, if that library is absent, the C restatement
@@ -239,7 +242,8 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
         "cores": threads,
         "kind": kind,
         "sample": f"C2 [1e6,16] f32 decreasing unweighted, forward, median of {len(times)} calls "
-        f"({sum(times):.1f} s), rows over {threads} OpenMP threads",
+        f"({sum(times):.1f} s), rows over {threads} OpenMP threads of {os.cpu_count()} "
+        f"({cpu_model()})",
     }
 
 
@@ -258,6 +262,27 @@ def cpu_c4(n: int = 10_000_000) -> dict:
     t = time.perf_counter() - t0
     return {"gelem_s": n / t / 1e9, "cores": 1, "kind": "reference" if impl == "reference" else "port",
             "sample": f"C4-shaped row of {n} elements, f32 weighted, one thread"}
+
+
+def measured_traffic() -> float | None:
+    """HBM bytes per launch of the headline kernel, from the committed counter summary."""
+    f = ROOT / "profiles" / "short_fit_kernel_c2_traffic.json"
+    try:
+        t = json.loads(f.read_text())
+        kib = t["fetch_size_kib"] * t["fetch_scale"] + t["write_size_kib"] * t["write_scale"]
+        return kib * 1024.0
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main() -> None:
@@ -306,10 +331,11 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (f64 sums and hull tests)",
+        "dtype": "f64",
         "data": "synthetic: C2 y[b,i] = -0.1 i + N(0,1), seed 0",
         "config": {
-            "workload": "C2: isotonic forward, y f32 [1000000, 16], unweighted, increasing=False",
+            "workload": "C2: isotonic forward, y f32 [1000000, 16], unweighted, increasing=False "
+            "(float32 in and out; sums, hull tests and slopes in float64)",
             "batch": 1_000_000,
             "n": 16,
         },
@@ -319,7 +345,7 @@ def main() -> None:
             "peak": PEAK_GBPS,
             "unit": "GB/s",
             "frac": achieved / PEAK_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "short_fit_kernel<float,16,unweighted>",
             "algorithmic_bytes_per_launch": 8 * elems,
         },

@@ -5,10 +5,11 @@ A drop-in for ``torchisotonic.isotonic`` (reference src/torchisotonic/_api.py:13
 signature, argument checks and messages, dtype policy, ``dim`` handling, weight broadcasting
 and autograd behaviour. What differs inside: the clamp to ``[y_min, y_max]`` and its backward
 are fused into the kernels, the weights' positivity is checked by the forward kernel as it
-reads them (one read of ``w`` instead of two), and the backward recomputes the block means from
-``y`` and ``w`` instead of reading the fit. There is no CPU solver: tensors must be on a ROCm
-device (arguments are still validated first, so the reference's error messages hold
-everywhere).
+reads them (one read of ``w`` instead of two), and the backward does not read the fit: rows of
+up to one tile recompute their block means from ``y`` and ``w``, longer rows take them from the
+final hulls the forward left in its workspace (kept on the autograd context). There is no CPU
+solver: tensors must be on a ROCm device (arguments are still validated first, so the
+reference's error messages hold everywhere).
 """
 
 from __future__ import annotations
