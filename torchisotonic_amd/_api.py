@@ -57,13 +57,15 @@ def isotonic(
         raise ValueError("y must have at least one dimension")
     out_dtype = y.dtype if y.is_floating_point() else torch.get_default_dtype()
     acc = torch.float64 if out_dtype == torch.float64 else torch.float32
-    rows = y.movedim(dim, -1)
+    last = dim == -1 or dim == y.ndim - 1
+    rows = y if last else y.movedim(dim, -1)
     w: Tensor | None = None
     if weight is not None:
         if not isinstance(weight, Tensor):
             raise TypeError(f"weight must be a torch.Tensor, got {type(weight).__name__}")
         try:
-            w = weight.to(device=y.device, dtype=acc).broadcast_to(y.shape).movedim(dim, -1)
+            w = weight.to(device=y.device, dtype=acc).broadcast_to(y.shape)
+            w = w if last else w.movedim(dim, -1)
         except RuntimeError as e:
             raise ValueError(f"weight of shape {tuple(weight.shape)} does not fit y") from e
         if y.device.type != "cuda" and not bool((w > 0).all()):
@@ -77,7 +79,8 @@ def isotonic(
     lo = None if y_min is None else float(y_min)
     hi = None if y_max is None else float(y_max)
     out: Tensor = _Isotonic.apply(flat_y, flat_w, increasing, exact, lo, hi)
-    return out.reshape(shape).movedim(-1, dim).to(out_dtype)
+    out = out.reshape(shape)
+    return (out if last else out.movedim(-1, dim)).to(out_dtype)
 
 
 class _Isotonic(torch.autograd.Function):

@@ -98,21 +98,53 @@ def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: Tensor) -> int:
+    """The current stream of t's device, as the hipStream_t value the C ABI takes."""
+    if _raw_stream is not None:
+        return int(_raw_stream(t.device.index))
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+class _on_device:
+    """Makes t's device the current HIP device for the ABI calls (a no-op when it already is,
+    which is the common case and saves a device switch per call)."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.index = device.index
+        self.prev: int | None = None
+
+    def __enter__(self) -> None:
+        cur = torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            torch.cuda.set_device(self.index)
+
+    def __exit__(self, *exc: object) -> None:
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+@functools.lru_cache(maxsize=1024)
 def starts_words(batch: int, n: int) -> int:
     return int(load().ti_starts_words(batch, n))
 
 
-def _workspace(kind: str, batch: int, n: int, dtype: int, weighted: bool, device: torch.device) -> Tensor | None:
+@functools.lru_cache(maxsize=1024)
+def _workspace_bytes(kind: str, batch: int, n: int, dtype: int, weighted: bool) -> int:
     size = _sz(0)
     fn = load().ti_fwd_workspace if kind == "fwd" else load().ti_bwd_workspace
     _check(fn(batch, n, dtype, int(weighted), ctypes.byref(size)), f"{kind}_workspace")
-    if size.value == 0:
+    return int(size.value)
+
+
+def _workspace(kind: str, batch: int, n: int, dtype: int, weighted: bool, device: torch.device) -> Tensor | None:
+    size = _workspace_bytes(kind, batch, n, dtype, weighted)
+    if size == 0:
         return None
-    return torch.empty(size.value, dtype=torch.uint8, device=device)
+    return torch.empty(size, dtype=torch.uint8, device=device)
 
 
 def _flags(increasing: bool, exact: bool, y_min: float | None, y_max: float | None) -> int:
@@ -152,7 +184,7 @@ def fit(
         starts_words(batch, n) if with_starts else 0, dtype=torch.int32, device=y.device
     )
     bad = torch.zeros(1, dtype=torch.int32, device=y.device) if w is not None else None
-    with torch.cuda.device(y.device):
+    with _on_device(y.device):
         ws = _workspace("fwd", batch, n, dtype, w is not None, y.device)
         rc = load().ti_fwd(
             _ptr(y), _ptr(w), _ptr(out), _ptr(starts) if with_starts else None, _ptr(bad),
@@ -192,7 +224,7 @@ def grad(
     gw = torch.empty_like(g) if want_w else None
     if gy is None and gw is None:
         return None, None
-    with torch.cuda.device(g.device):
+    with _on_device(g.device):
         ws = _workspace("bwd", batch, n, dtype, w is not None, g.device)
         rc = load().ti_bwd(
             _ptr(starts), _ptr(fwd_ws), 0 if fwd_ws is None else fwd_ws.numel(),
@@ -209,7 +241,7 @@ def grad(
 def starts_to_bool(starts: Tensor, batch: int, n: int) -> Tensor:
     """The packed partition as the reference's bool [batch, n] tensor (a test hook)."""
     out = torch.empty(batch, n, dtype=torch.uint8, device=starts.device)
-    with torch.cuda.device(starts.device):
+    with _on_device(starts.device):
         rc = load().ti_starts_to_bool(_ptr(starts), _ptr(out), batch, n, _stream(starts))
     _check(rc, "starts_to_bool")
     return out.bool()

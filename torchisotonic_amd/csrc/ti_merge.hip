@@ -289,25 +289,42 @@ __device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, const LdsVer
       const int rtail = pb + span < nch ? sm.off[pb + span] : total - 1;
       int ia = v.prev[x], ib = v.next[x];
       HPt A = lget<W, PR>(v, ia), B = lget<W, PR>(v, ib);
+      // each point is read together with its link onward, so a walk step waits for one LDS
+      // round trip (the next point), not two (its index, then the point)
+      int pa_link = v.prev[ia], nb_link = v.next[ib];
       if (hpools<W, PR>(A, lget<W, PR>(v, x), B)) {
         v.dead[x] = 1;
-        int iap = ia != lhead ? v.prev[ia] : -1;
-        int ibn = ib != rtail ? v.next[ib] : -1;
-        HPt AP = iap >= 0 ? lget<W, PR>(v, iap) : A;
-        HPt BN = ibn >= 0 ? lget<W, PR>(v, ibn) : B;
+        int iap = ia != lhead ? pa_link : -1;
+        int ibn = ib != rtail ? nb_link : -1;
+        HPt AP = A, BN = B;
+        int ap_link = 0, bn_link = 0;
+        if (iap >= 0) {
+          AP = lget<W, PR>(v, iap);
+          ap_link = v.prev[iap];
+        }
+        if (ibn >= 0) {
+          BN = lget<W, PR>(v, ibn);
+          bn_link = v.next[ibn];
+        }
         for (;;) {  // every step marks a vertex dead: at most `total` steps
           if (iap >= 0 && hpools<W, PR>(AP, A, B)) {
             v.dead[ia] = 1;
             ia = iap;
             A = AP;
-            iap = ia != lhead ? v.prev[ia] : -1;
-            if (iap >= 0) AP = lget<W, PR>(v, iap);
+            iap = ia != lhead ? ap_link : -1;
+            if (iap >= 0) {
+              AP = lget<W, PR>(v, iap);
+              ap_link = v.prev[iap];
+            }
           } else if (ibn >= 0 && hpools<W, PR>(A, B, BN)) {
             v.dead[ib] = 1;
             ib = ibn;
             B = BN;
-            ibn = ib != rtail ? v.next[ib] : -1;
-            if (ibn >= 0) BN = lget<W, PR>(v, ibn);
+            ibn = ib != rtail ? bn_link : -1;
+            if (ibn >= 0) {
+              BN = lget<W, PR>(v, ibn);
+              bn_link = v.next[ibn];
+            }
           } else {
             break;
           }
@@ -648,10 +665,11 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     m.npr_out = p.npr[l];
     m.child_elems = p.span[l - 1];
     const unsigned grid = static_cast<unsigned>(t.batch * p.npr[l]);
-    // LDS vertex capacity: 1024 where many merges share the GPU, else what 60 KB holds
+    // LDS vertex capacity: 768 where many merges share the GPU (occupancy; 64 noisy span
+    // hulls take about 400-500 slots), else what 60 KB holds
     auto launch = [&](auto kern, size_t vb) {
       const int big = static_cast<int>((60 * 1024 / vb) & ~size_t(63));
-      const int cap = grid >= 1024 ? (big < 1024 ? big : 1024) : big;
+      const int cap = grid >= 1024 ? (big < 768 ? big : 768) : big;
       kern<<<dim3(grid), dim3(kWave), cap * vb, t.stream>>>(m, cap);
     };
     if (t.dtype == TI_F32) {
