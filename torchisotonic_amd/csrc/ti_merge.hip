@@ -623,8 +623,13 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
   LongPlan p{};
   const int64_t tn = tile_elems(weighted);
   p.tiles_per_row = (n + tn - 1) / tn;
-  int64_t npr = (n + kSpan - 1) / kSpan;
-  int64_t span = kSpan;  // elements per node at this level
+  // The longest span that still gives the span kernel about 2^17 lanes (two waves per SIMD),
+  // within [kSpanMin, kSpanMax]: long spans mean fewer hulls to merge, short ones more lanes.
+  int64_t span0 = kSpanMax;
+  while (span0 > kSpanMin && batch * ((n + span0 - 1) / span0) < (int64_t{1} << 17)) span0 >>= 1;
+  p.span0 = span0;
+  int64_t npr = (n + span0 - 1) / span0;
+  int64_t span = span0;  // elements per node at this level
   size_t buf[2] = {0, 0};
   int level = 0;
   for (;;) {
@@ -651,7 +656,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   const bool W = t.w != nullptr;
   char* base = static_cast<char*>(ws);
   // level 0: span hulls
-  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0]);
+  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0);
   if (e != hipSuccess) return e;
   for (int l = 1; l <= p.levels; ++l) {
     MergeArgs m;

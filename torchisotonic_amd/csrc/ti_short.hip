@@ -249,10 +249,6 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
       }
     }
   }
-  auto Wk = [&](int k) -> double {
-    if constexpr (W) return P[k];
-    else return static_cast<double>(k);
-  };
   if constexpr (W) {
     if (active && wbad && bad_weight != nullptr) *bad_weight = 1u;
   }
@@ -282,29 +278,37 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     for (int k = 1; k < NMAX; ++k) {
       if (k < nn && tsgn_lt(sgn, yv[k - 1], yv[k])) cand |= Mask(1) << k;
     }
-    // stack: t1 (last vertex), t2, t3 (< 0: none), with sums s* and weights w*
-    int t1 = 0, t2 = -1, t3 = -1;
-    double s1 = 0.0, s2 = 0.0, s3 = 0.0;
-    double w1 = 0.0, w2 = 0.0, w3 = 0.0;
-    // the candidate being pushed (k) and the one after it (kn, prefetched)
+    // stack: t1 (last vertex) and t2 (< 0: none) with their sums and weights; the stack itself
+    // is the mask m. The candidate being pushed is k; rest holds the candidates after it.
+    int t1 = 0, t2 = -1;
+    double s1 = 0.0, s2 = 0.0;
+    double w1 = 0.0, w2 = 0.0;
     Mask rest = cand & ~Mask(1);
-    int k = lowest_bit(rest);
+    int k = lowest_bit(rest);  // point nn is always a candidate
     rest &= rest - 1;
     double sk = colS[k * THREADS + tid];
     double wk = W ? colW[W ? k * THREADS + tid : 0] : static_cast<double>(k);
-    int kn = rest ? lowest_bit(rest) : -1;
-    double skn = 0.0, wkn = 0.0;
-    if (kn >= 0) {
-      skn = colS[kn * THREADS + tid];
-      if constexpr (W) wkn = colW[kn * THREADS + tid];
-      else wkn = static_cast<double>(kn);
-    }
     while (k >= 0) {
       bool pop = false;
-      if (t2 >= 0) {
-        if constexpr (W) pop = pools<EXACT>(s1 - s2, w1 - w2, sk - s1, wk - w1);
-        else pop = pools<EXACT>(s1 - s2, static_cast<double>(t1 - t2), sk - s1,
-                                static_cast<double>(k - t1));
+      if constexpr (W) {
+        pop = t2 >= 0 && pools<EXACT>(s1 - s2, w1 - w2, sk - s1, wk - w1);
+      } else {
+        pop = t2 >= 0 && pools<EXACT>(s1 - s2, static_cast<double>(t1 - t2), sk - s1,
+                                      static_cast<double>(k - t1));
+      }
+      // Both possible successors are read before the choice: the vertex below t2 (a pop makes
+      // it the second vertex) and the candidate after k (a push makes it the next candidate).
+      const Mask below = t2 > 0 ? (m & ((Mask(1) << t2) - Mask(1))) : Mask(0);
+      const int t3 = below ? highest_bit(below) : -1;
+      const int kn = rest ? lowest_bit(rest) : -1;
+      const double s3 = colS[(t3 > 0 ? t3 : 0) * THREADS + tid];
+      const double skn = colS[(kn > 0 ? kn : 0) * THREADS + tid];
+      double w3 = 0.0, wkn = 0.0;
+      if constexpr (W) {
+        w3 = colW[(t3 > 0 ? t3 : 0) * THREADS + tid];
+        wkn = colW[(kn > 0 ? kn : 0) * THREADS + tid];
+      } else {
+        wkn = static_cast<double>(kn);
       }
       if (pop) {
         m &= ~(Mask(1) << t1);
@@ -314,20 +318,8 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
         t2 = t3;
         s2 = s3;
         w2 = w3;
-        if (t3 >= 0) {
-          const Mask below = m & ((Mask(1) << t3) - Mask(1));
-          t3 = below ? highest_bit(below) : -1;
-          if (t3 >= 0) {
-            s3 = colS[t3 * THREADS + tid];
-            if constexpr (W) w3 = colW[t3 * THREADS + tid];
-            else w3 = static_cast<double>(t3);
-          }
-        }
       } else {
         m |= Mask(1) << k;
-        t3 = t2;
-        s3 = s2;
-        w3 = w2;
         t2 = t1;
         s2 = s1;
         w2 = w1;
@@ -337,38 +329,35 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
         k = kn;
         sk = skn;
         wk = wkn;
-        if (kn >= 0) {
-          rest &= rest - 1;
-          kn = rest ? lowest_bit(rest) : -1;
-          if (kn >= 0) {
-            skn = colS[kn * THREADS + tid];
-            if constexpr (W) wkn = colW[kn * THREADS + tid];
-            else wkn = static_cast<double>(kn);
-          }
-        }
+        rest &= rest - 1;
       }
     }
   }
 
-  // Slopes: backwards, each vertex i takes the slope to the next vertex; then forwards, each
-  // element the slope of the last vertex at or before it.
+  // Slopes, one per hull edge, from the last vertex down: each edge's slope replaces the sum
+  // at its first vertex in the point column (that sum is kept in a register for the next edge),
+  // then every element takes the slope of the last vertex at or before it.
   T fit[NMAX];
   {
-    double slope[NMAX];
-    double se = 0.0, we = 0.0;
-#pragma unroll
-    for (int i = NMAX - 1; i >= 0; --i) {
-      if (i < nn) {
-        if (i == nn - 1) {
-          se = S[i + 1];
-          we = Wk(i + 1);
-        }
-        if ((m >> i) & 1ull) {
-          slope[i] = slope_div(se - S[i], we - Wk(i));
-          se = S[i];
-          we = Wk(i);
-        }
+    if (active) {
+      int vh = nn;
+      double sh = colS[nn * THREADS + tid], wh;
+      if constexpr (W) wh = colW[nn * THREADS + tid];
+      else wh = static_cast<double>(nn);
+      Mask rem = m & ((Mask(1) << nn) - Mask(1));  // vertices below nn (point 0 among them)
+      while (rem) {
+        const int vl = highest_bit(rem);
+        rem &= ~(Mask(1) << vl);
+        const double sl = colS[vl * THREADS + tid];
+        double wl;
+        if constexpr (W) wl = colW[vl * THREADS + tid];
+        else wl = static_cast<double>(vl);
+        colS[vl * THREADS + tid] = slope_div(sh - sl, wh - wl);
+        vh = vl;
+        sh = sl;
+        wh = wl;
       }
+      (void)vh;
     }
     const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
     const T tsgn = static_cast<T>(sgn);
@@ -376,7 +365,7 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
 #pragma unroll
     for (int i = 0; i < NMAX; ++i) {
       if (i < nn) {
-        if ((m >> i) & 1ull) cur = slope[i];
+        if ((m >> i) & 1ull) cur = colS[i * THREADS + tid];
         const T v = bad ? quiet_nan<T>() : tsgn * static_cast<T>(cur);
         fit[i] = clip(v, use_lo, lo, use_hi, hi);
       }

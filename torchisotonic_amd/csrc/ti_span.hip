@@ -1,4 +1,4 @@
-// Rows longer than one tile, first stage: one lane per span of kSpan elements.
+// Rows longer than one tile, first stage: one lane per span of span0 elements.
 //
 // Replaces the reference's chunk stage for long rows (reference src/torchisotonic/csrc/
 // tiles.cuh:665-913, chunk_kernel, which builds small lane hulls and merges them across the
@@ -38,6 +38,7 @@ struct SpanArgs {
   const void* w;
   uint32_t* bad_weight;
   int64_t n, spr, nodes;  // row length, spans per row, spans in total
+  int64_t span0;          // elements per span
   unsigned flags;
   void* hulls;            // node array of the spans
   int64_t cap;
@@ -87,8 +88,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   if (node >= a.nodes) return;  // no barriers below: the lanes are independent
   const int64_t row = node / a.spr;
   const int64_t span = node - row * a.spr;
-  const int64_t first = span * kSpan;
-  const int len = static_cast<int>(min<int64_t>(kSpan, a.n - first));
+  const int64_t first = span * a.span0;
+  const int len = static_cast<int>(min<int64_t>(a.span0, a.n - first));
   const bool inc = (a.flags & TI_INCREASING) != 0;
   const double sgn = inc ? 1.0 : -1.0;
   const T* y = static_cast<const T*>(a.y) + row * a.n + first;
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 
 }  // namespace
 
-hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap) {
+hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, int64_t span0) {
   SpanArgs a;
   a.y = t.y;
   a.w = t.w;
@@ -293,6 +294,7 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap) {
   a.flags = t.flags;
   a.hulls = hulls;
   a.cap = cap;
+  a.span0 = span0;
   const unsigned grid = static_cast<unsigned>((a.nodes + kSpanLanes - 1) / kSpanLanes);
   const bool W = t.w != nullptr;
   if (t.dtype == TI_F32) {

@@ -179,9 +179,11 @@ __device__ __forceinline__ bool hpools(const HPt& a, const HPt& b, const HPt& c)
   return pools<true>(dS1, dW1, dS2, dW2);
 }
 
-// Rows longer than one tile: one lane builds the hull of each span of kSpan elements, then
+// Rows longer than one tile: one lane builds the hull of each span of span0 elements (a power
+// of two, kSpanMin..kSpanMax, chosen per call so that the span kernel has enough lanes), then
 // workgroups merge G neighbouring hulls at a time until one hull per row remains.
-constexpr int kSpan = 256;
+constexpr int kSpanMin = 32;
+constexpr int kSpanMax = 256;
 constexpr int kGroup = 64;
 constexpr int kMaxLevels = 8;
 
@@ -207,6 +209,7 @@ struct ExpandArgs {
 // levels (the final hulls end in buffer levels & 1), and the per-tile ranks of the expansion.
 struct LongPlan {
   int64_t tiles_per_row;  // expansion (and backward) tiles
+  int64_t span0;          // elements per span (the first node level)
   int levels;
   int64_t npr[kMaxLevels + 1], cap[kMaxLevels + 1], span[kMaxLevels + 1];
   size_t off_buf[2], off_rank, bytes;
@@ -214,7 +217,7 @@ struct LongPlan {
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
-hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap);
+hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap, int64_t span0);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {
