@@ -105,6 +105,9 @@ template <typename T, bool W>
 __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
+  // float32 g: a thread's prefix over E values is kept in float64 (its error is far below the
+  // data's); float64 g carries the rounding errors (double-double)
+  constexpr bool PR = sizeof(T) == 8;
   __shared__ DD wtot[kWaves256];
   __shared__ int rank_scan[kWaves256];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -114,15 +117,28 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
   const int t0 = tid * E;
   const int ecount = max(0, min(E, len - t0));
+  // every independent load first: g, the start bits, the tile's rank and the row's flags
   T gv[E];
   load_elems_any<T, E>(static_cast<const T*>(a.g) + row * a.n + first + t0, ecount, gv);
-  // local exclusive prefixes (double-double) and the thread's total
-  DD lpre[E];
+  const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
+  uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
+  const int at_start = (tile == 0) ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1));
+  const int rA = a.tile_rank[2 * blockIdx.x];
+  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+  const int bad = *fin.bad;
+  const int last = (tile == a.tpr - 1 && tid == 0) ? *fin.count - 1 : 0;
+
+  double lp[E];
+  double ll[PR ? E : 1];
   DD acc{0.0, 0.0};
 #pragma unroll
   for (int k = 0; k < E; ++k) {
-    lpre[k] = acc;
-    if (k < ecount) acc = dd_add(acc, static_cast<double>(gv[k]));
+    lp[k] = acc.hi;
+    if constexpr (PR) ll[k] = acc.lo;
+    if (k < ecount) {
+      if constexpr (PR) acc = dd_add(acc, static_cast<double>(gv[k]));
+      else acc.hi += static_cast<double>(gv[k]);
+    }
   }
   DD total;
   const DD off = block_scan_dd(acc, wtot, total);
@@ -130,11 +146,8 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     a.tg[2 * blockIdx.x] = total.hi;
     a.tg[2 * blockIdx.x + 1] = total.lo;
   }
-  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
-  if (*fin.bad) return;  // a NaN row is one block: only its total is needed
+  if (bad) return;  // a NaN row is one block: only its total is needed
   // the hull vertices inside the tile, by rank: rA, less one if rA is the tile's first element
-  const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
-  uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
   if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
   if (first + t0 == 0) mybits |= 1u;
   const int pc = __builtin_popcount(mybits);
@@ -148,21 +161,18 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   __syncthreads();
   int before = incl - pc;
   for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
-  const int rA = a.tile_rank[2 * blockIdx.x];
-  const int at_start = (tile == 0) ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1));
   double* lv = a.lv + 2 * row * a.cap_final;
   int rank = rA - at_start + before;
 #pragma unroll
   for (int k = 0; k < E; ++k) {
     if ((mybits >> k) & 1u) {
       ++rank;
-      const DD p = dd_add(off, lpre[k]);
+      const DD p = dd_add(off, DD{lp[k], PR ? ll[PR ? k : 0] : 0.0});
       lv[2 * rank] = p.hi;
       lv[2 * rank + 1] = p.lo;
     }
   }
   if (tile == a.tpr - 1 && tid == 0) {  // the row's end point: the last vertex
-    const int last = *fin.count - 1;
     lv[2 * last] = total.hi;
     lv[2 * last + 1] = total.lo;
   }
