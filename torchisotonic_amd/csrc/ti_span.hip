@@ -78,9 +78,10 @@ __device__ __forceinline__ void load_chunk(const T* __restrict__ p, int count, T
   }
 }
 
-template <typename T, bool W, int C, int R>
+template <typename T, bool W, int C, int R, int LC>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert((R & (R - 1)) == 0 && C <= 32, "ring slots: a power of two; chunk: a 32-bit mask");
+  static_assert(LC % C == 0, "a load block is a whole number of chunks");
   constexpr bool PR = sizeof(T) == 8;
   __shared__ SpanLds<T, W, C, R> L;
   const int lane = threadIdx.x;
@@ -141,24 +142,29 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 
   double S = 0.0, SL = 0.0, P = 0.0, PL = 0.0;
   bool bad = false, wbad = false;
-  T yc[C], yn[C];
-  T wc[W ? C : 1], wn[W ? C : 1];
-  load_chunk<T, C>(y, len, yc);
-  if constexpr (W) load_chunk<T, C>(w, len, wc);
-  for (int c0 = 0; c0 < len; c0 += C) {
-    const int rest = len - (c0 + C);
+  // loads come in blocks of LC elements (the next block in flight while this one is processed),
+  // processed in chunks of C
+  T yc[LC], yn[LC];
+  T wc[W ? LC : 1], wn[W ? LC : 1];
+  load_chunk<T, LC>(y, len, yc);
+  if constexpr (W) load_chunk<T, LC>(w, len, wc);
+  for (int b0 = 0; b0 < len; b0 += LC) {
+    const int rest = len - (b0 + LC);
     if (rest > 0) {
-      load_chunk<T, C>(y + c0 + C, rest, yn);
-      if constexpr (W) load_chunk<T, C>(w + c0 + C, rest, wn);
+      load_chunk<T, LC>(y + b0 + LC, rest, yn);
+      if constexpr (W) load_chunk<T, LC>(w + b0 + LC, rest, wn);
     }
+#pragma unroll
+    for (int sub = 0; sub < LC; sub += C) {
+    const int c0 = b0 + sub;
     // 1. sums at every point of the chunk, and the candidates
     uint32_t mask = 0;
     auto element = [&](int k) {  // sums through element c0 + k, stored for the point after it
-      const double ye = sgn * static_cast<double>(yc[k]);
+      const double ye = sgn * static_cast<double>(yc[sub + k]);
       bad |= ye != ye;
       double term = ye;
       if constexpr (W) {
-        const double we = static_cast<double>(wc[k]);
+        const double we = static_cast<double>(wc[W ? sub + k : 0]);
         wbad |= !(we > 0.0);
         term = we * ye;
         if constexpr (PR) {
@@ -188,7 +194,10 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 #pragma unroll
       for (int k = 0; k < C; ++k) {
         element(k);
-        const bool cand = k + 1 < C ? rises(yc[k], yc[k + 1 < C ? k + 1 : 0]) : ((c0 + C == len) | rises(yc[k], yn[0]));
+        const int kk = sub + k;
+        const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
+        // (the span can end only after a chunk's last element here)
+        const bool cand = k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext));
         mask |= static_cast<uint32_t>(cand) << k;
       }
     } else {
@@ -197,8 +206,9 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         const int e = c0 + k;
         if (e < len) {
           element(k);
-          const T ynext = k + 1 < C ? yc[k + 1 < C ? k + 1 : 0] : yn[0];
-          const bool cand = (e + 1 == len) | (e + 1 < len && rises(yc[k], ynext));
+          const int kk = sub + k;
+          const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
+          const bool cand = (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext));
           mask |= static_cast<uint32_t>(cand) << k;
         }
       }
@@ -264,8 +274,9 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         r0 = lo;
       }
     }
+    }  // chunks of the block
 #pragma unroll
-    for (int k = 0; k < C; ++k) {
+    for (int k = 0; k < LC; ++k) {
       yc[k] = yn[k];
       if constexpr (W) wc[W ? k : 0] = wn[W ? k : 0];
     }
@@ -298,11 +309,11 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   const unsigned grid = static_cast<unsigned>((a.nodes + kSpanLanes - 1) / kSpanLanes);
   const bool W = t.w != nullptr;
   if (t.dtype == TI_F32) {
-    if (W) span_kernel<float, true, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<float, false, 8, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) span_kernel<float, true, 8, 8, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    else span_kernel<float, false, 8, 16, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   } else {
-    if (W) span_kernel<double, true, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<double, false, 8, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) span_kernel<double, true, 8, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    else span_kernel<double, false, 8, 16, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   }
   return hipGetLastError();
 }
