@@ -309,8 +309,8 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   const unsigned grid = static_cast<unsigned>((a.nodes + kSpanLanes - 1) / kSpanLanes);
   const bool W = t.w != nullptr;
   if (t.dtype == TI_F32) {
-    if (W) span_kernel<float, true, 8, 8, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<float, false, 8, 16, 16><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) span_kernel<float, true, 8, 8, 32><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    else span_kernel<float, false, 8, 16, 32><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   } else {
     if (W) span_kernel<double, true, 8, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
     else span_kernel<double, false, 8, 16, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
