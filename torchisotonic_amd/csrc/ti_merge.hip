@@ -540,7 +540,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
   constexpr int NT = C::kThreads;
-  __shared__ double sl[C::kN + 2];
+  __shared__ T sl[C::kN + 2];  // sgn * slope per edge, rounded once to T
   __shared__ uint32_t bits[C::kN / 32];
   __shared__ int rank_scan[kWaves256];
   const int tid = threadIdx.x;
@@ -555,6 +555,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   const int count = *fin.count;
   const bool row_bad = *fin.bad != 0;
   const int ta = static_cast<int>(first);
+  const T tsgn = static_cast<T>((a.flags & TI_INCREASING) ? 1.0 : -1.0);
 
   // the vertex ranks around the tile, written by the last merge
   const int rA = a.tile_rank[2 * blockIdx.x];
@@ -569,7 +570,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     const VPt p = vload<W>(v, e), q = vload<W>(v, e + 1);
     double dW, dS;
     vdiff<W>(p, q, dW, dS);
-    sl[e - rA] = slope_div(dS, dW);
+    sl[e - rA] = tsgn * static_cast<T>(slope_div(dS, dW));
     if (p.i >= ta) atomicOr(&bits[(p.i - ta) >> 5], 1u << ((p.i - ta) & 31));
   }
   __syncthreads();
@@ -593,12 +594,11 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   int jj = before + static_cast<int>(mybits & 1u) - at_start;
   const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
   const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
-  const T tsgn = static_cast<T>((a.flags & TI_INCREASING) ? 1.0 : -1.0);
   T fit[E];
 #pragma unroll
   for (int k = 0; k < E; ++k) {
     if (k > 0) jj += (mybits >> k) & 1u;
-    const T val = row_bad ? quiet_nan<T>() : tsgn * static_cast<T>(sl[jj]);
+    const T val = row_bad ? quiet_nan<T>() : sl[jj];
     fit[k] = clip(val, use_lo, lo, use_hi, hi);
   }
   T* out = static_cast<T*>(a.out) + row * a.n + first;
