@@ -563,6 +563,42 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   // (both hold for any well-formed hull; they keep sl[] and the vertex reads in bounds regardless)
   rB = min(min(rB, rA + C::kN + 1), count - 1);
 
+  const int t0 = tid * E;
+  const int ecount = max(0, min(E, len - t0));
+  const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
+  const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
+  T* out = static_cast<T*>(a.out) + row * a.n + first;
+  const int64_t wpr = (a.n + 31) / 32;
+  auto write_starts = [&](uint32_t sb) {
+    if (a.starts == nullptr || ecount <= 0) return;
+    if (ecount < E) sb &= (1u << ecount) - 1u;
+    if constexpr (E == 16) {
+      uint16_t* s16 = reinterpret_cast<uint16_t*>(a.starts + row * wpr);
+      s16[(first + t0) >> 4] = static_cast<uint16_t>(sb);
+    } else {
+      uint8_t* s8 = reinterpret_cast<uint8_t*>(a.starts + row * wpr);
+      s8[(first + t0) >> 3] = static_cast<uint8_t>(sb);
+    }
+  };
+
+  if (rB == rA + 1) {
+    // One hull edge covers the whole tile (the common case on long rows, whose hulls have far
+    // fewer vertices than tiles): every thread forms its slope, no LDS, no barriers. The only
+    // possible start is the tile's first element, where vertex rA may sit.
+    const VPt p = vload<W>(v, rA), q = vload<W>(v, rA + 1);
+    double dW, dS;
+    vdiff<W>(p, q, dW, dS);
+    const T val = row_bad ? quiet_nan<T>() : tsgn * static_cast<T>(slope_div(dS, dW));
+    const T f = clip(val, use_lo, lo, use_hi, hi);
+    T fit[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) fit[k] = f;
+    store_elems_any<T, E>(out + t0, ecount, fit);
+    const bool head = row_bad ? (first + t0 == 0) : (t0 == 0 && p.i == ta);
+    write_starts(head ? 1u : 0u);
+    return;
+  }
+
   // Edge slopes rA .. rB-1 and the vertex bits of the tile.
   for (int wd = tid; wd < C::kN / 32; wd += NT) bits[wd] = 0u;
   __syncthreads();
@@ -574,8 +610,6 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     if (p.i >= ta) atomicOr(&bits[(p.i - ta) >> 5], 1u << ((p.i - ta) & 31));
   }
   __syncthreads();
-  const int t0 = tid * E;
-  const int ecount = max(0, min(E, len - t0));
   uint32_t mybits;
   if constexpr (E == 16) mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFFFu;
   else mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFu;
@@ -592,8 +626,6 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
   const int at_start = (v.idx[rA] == ta) ? 1 : 0;
   int jj = before + static_cast<int>(mybits & 1u) - at_start;
-  const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
-  const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
   T fit[E];
 #pragma unroll
   for (int k = 0; k < E; ++k) {
@@ -601,20 +633,8 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     const T val = row_bad ? quiet_nan<T>() : sl[jj];
     fit[k] = clip(val, use_lo, lo, use_hi, hi);
   }
-  T* out = static_cast<T*>(a.out) + row * a.n + first;
   store_elems_any<T, E>(out + t0, ecount, fit);
-  if (a.starts != nullptr && ecount > 0) {
-    uint32_t sb = row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits;
-    if (ecount < E) sb &= (1u << ecount) - 1u;
-    const int64_t wpr = (a.n + 31) / 32;
-    if constexpr (E == 16) {
-      uint16_t* s16 = reinterpret_cast<uint16_t*>(a.starts + row * wpr);
-      s16[(first + t0) >> 4] = static_cast<uint16_t>(sb);
-    } else {
-      uint8_t* s8 = reinterpret_cast<uint8_t*>(a.starts + row * wpr);
-      s8[(first + t0) >> 3] = static_cast<uint8_t>(sb);
-    }
-  }
+  write_starts(row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits);
 }
 
 }  // namespace
