@@ -60,22 +60,27 @@ struct SpanLds {
   double rwl[W && PR ? R : 1][kSpanLanes];
 };
 
+// N consecutive values at byte offset `off` of a buffer resource, 16 bytes per load. Reads past
+// the resource's end return zero and never fault, so a block is always loaded whole (its values
+// past the span's end are never used) and the loads stay straight-line code.
 template <typename T, int N>
-__device__ __forceinline__ void load_chunk(const T* __restrict__ p, int count, T (&v)[N]) {
+__device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t off, T (&v)[N]) {
   constexpr int V = 16 / sizeof(T);
   using VT = T __attribute__((ext_vector_type(V)));
-  if (count >= N && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-    const VT* q = reinterpret_cast<const VT*>(p);
 #pragma unroll
-    for (int j = 0; j < N / V; ++j) {
-      const VT x = q[j];
+  for (int j = 0; j < N / V; ++j) {
+    // (taken as a vector of T at once: element access on the builtin's integer-vector result
+    // is what this compiler narrows to a single-dword load)
+    const VT x = __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(r, off + j * 16, 0, 0));
 #pragma unroll
-      for (int t = 0; t < V; ++t) v[j * V + t] = x[t];
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < N; ++k) v[k] = k < count ? p[k] : T(0);
+    for (int t = 0; t < V; ++t) v[j * V + t] = x[t];
   }
+}
+
+// A buffer resource over [base, base + bytes) (bytes clamped to the 32-bit range field).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int nrec = static_cast<int>(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), nrec, 0x00020000);
 }
 
 template <typename T, bool W, int C, int R, int LC>
@@ -93,8 +98,15 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   const int len = static_cast<int>(min<int64_t>(a.span0, a.n - first));
   const bool inc = (a.flags & TI_INCREASING) != 0;
   const double sgn = inc ? 1.0 : -1.0;
-  const T* y = static_cast<const T*>(a.y) + row * a.n + first;
-  const T* w = W ? static_cast<const T*>(a.w) + row * a.n + first : nullptr;
+  // The wave's spans are consecutive elements of the [batch, n] array (rows follow each other),
+  // so one buffer resource based at the wave's first element serves every lane.
+  const int64_t node0 = static_cast<int64_t>(blockIdx.x) * kSpanLanes;
+  const int64_t row0 = node0 / a.spr;
+  const int64_t base = row0 * a.n + (node0 - row0 * a.spr) * a.span0;  // wave-uniform
+  const int64_t total = a.nodes / a.spr * a.n;                         // elements of the array
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + base, (total - base) * sizeof(T));
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(W ? static_cast<const T*>(a.w) + base : a.y, (total - base) * sizeof(T));
+  const uint32_t loff = static_cast<uint32_t>((row * a.n + first - base) * sizeof(T));  // this lane's span
   const NodeOut o = node_out(a.hulls, a.nodes, a.cap, W, node);
 
   auto ring_put = [&](int q, const HPt& p) {
@@ -146,14 +158,12 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // processed in chunks of C
   T yc[LC], yn[LC];
   T wc[W ? LC : 1], wn[W ? LC : 1];
-  load_chunk<T, LC>(y, len, yc);
-  if constexpr (W) load_chunk<T, LC>(w, len, wc);
+  load_block<T, LC>(ry, loff, yc);
+  if constexpr (W) load_block<T, LC>(rw, loff, wc);
   for (int b0 = 0; b0 < len; b0 += LC) {
-    const int rest = len - (b0 + LC);
-    if (rest > 0) {
-      load_chunk<T, LC>(y + b0 + LC, rest, yn);
-      if constexpr (W) load_chunk<T, LC>(w + b0 + LC, rest, wn);
-    }
+    // the next block, whole, whether or not the span reaches it
+    load_block<T, LC>(ry, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), yn);
+    if constexpr (W) load_block<T, LC>(rw, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), wn);
 #pragma unroll
     for (int sub = 0; sub < LC; sub += C) {
     const int c0 = b0 + sub;
