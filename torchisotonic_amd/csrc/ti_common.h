@@ -56,6 +56,16 @@ __device__ __forceinline__ bool pools(double dS1, double dW1, double dS2, double
   }
 }
 
+// pools<true> as straight-line code: both the filtered test and the exact one are formed and
+// one is selected, for loops that keep several tests in flight.
+__device__ __forceinline__ bool pools_nb(double dS1, double dW1, double dS2, double dW2) {
+  const double q = dS2 * dW1;
+  const double d = __builtin_fma(dS1, dW2, -q);
+  const bool sure = __builtin_fabs(d) > 0x1p-52 * __builtin_fabs(q);
+  const bool exact = cross_sign(dS1, dW2, dS2, dW1) >= 0;
+  return sure ? d > 0.0 : exact;
+}
+
 // num / den for den > 0, within an ulp or so of the correctly rounded quotient: a hardware
 // reciprocal refined by two Newton steps, then one residual correction of the quotient
 // (Markstein). Used wherever a block's mean (a hull slope) is formed, so the forward and the

@@ -17,6 +17,7 @@
 //                  edge with the clamp fused, and the start bits. y is not read again.
 #include "ti_common.h"
 #include "ti_kernels.h"
+#include "ti_slots.h"
 #include "ti_tile.h"
 
 namespace ti {
@@ -150,76 +151,11 @@ struct MergeSmall {
   int total, bad, rounds_max;
 };
 
-// A merge's vertices in LDS (carved from dynamic LDS): coordinates, the doubly linked chain of
-// surviving vertices, and dead marks.
-template <bool W, bool PR>
-struct LdsVerts {
-  double *s, *sl, *w, *wl;
-  int* idx;
-  int16_t *prev, *next;
-  uint8_t* dead;
-};
-
-template <bool W, bool PR>
-constexpr size_t lds_vertex_bytes() {
-  return 8 + (PR ? 8 : 0) + (W ? 8 : 0) + (W && PR ? 8 : 0) + 4 + 2 + 2 + 1;
-}
-
-// (cap is a multiple of 64, so every array stays 8-byte aligned)
-template <bool W, bool PR>
-__device__ LdsVerts<W, PR> lds_carve(char* p, int cap) {
-  LdsVerts<W, PR> v;
-  v.s = reinterpret_cast<double*>(p);
-  p += cap * 8;
-  v.sl = nullptr;
-  v.w = nullptr;
-  v.wl = nullptr;
-  if constexpr (PR) {
-    v.sl = reinterpret_cast<double*>(p);
-    p += cap * 8;
-  }
-  if constexpr (W) {
-    v.w = reinterpret_cast<double*>(p);
-    p += cap * 8;
-  }
-  if constexpr (W && PR) {
-    v.wl = reinterpret_cast<double*>(p);
-    p += cap * 8;
-  }
-  v.idx = reinterpret_cast<int*>(p);
-  p += cap * 4;
-  v.prev = reinterpret_cast<int16_t*>(p);
-  p += cap * 2;
-  v.next = reinterpret_cast<int16_t*>(p);
-  p += cap * 2;
-  v.dead = reinterpret_cast<uint8_t*>(p);
-  return v;
-}
-
-template <bool W, bool PR>
-__device__ __forceinline__ HPt lget(const LdsVerts<W, PR>& v, int k) {
-  HPt p;
-  p.i = v.idx[k];
-  p.s = v.s[k];
-  p.sl = PR ? v.sl[k] : 0.0;
-  p.w = W ? v.w[k] : 0.0;
-  p.wl = (W && PR) ? v.wl[k] : 0.0;
-  return p;
-}
-
-template <bool W, bool PR>
-__device__ __forceinline__ void lput(const LdsVerts<W, PR>& v, int k, const HPt& p) {
-  v.idx[k] = p.i;
-  v.s[k] = p.s;
-  if constexpr (PR) v.sl[k] = p.sl;
-  if constexpr (W) v.w[k] = p.w;
-  if constexpr (W && PR) v.wl[k] = p.wl;
-}
-
 // Slot s of the children laid end to end (each child's first vertex is the previous child's
-// last, stored once): the child holding it and the vertex within that child.
+// last, stored once): the child holding it, i.e. the last child whose first slot is below s
+// (child 0 for s = 0).
 __device__ __forceinline__ int child_of_slot(const MergeSmall& sm, int nch, int s) {
-  int lo = 0, hi = nch - 1;  // the last child whose first slot is below s (child 0 for s = 0)
+  int lo = 0, hi = nch - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (sm.off[mid] < s) lo = mid;
@@ -249,112 +185,49 @@ __device__ __forceinline__ HPt child_vertex(const MergeArgs& a, const MergeSmall
   return p;
 }
 
-// The merge in LDS. Pairwise rounds over the children: the lane of each pair walks from their
-// shared point to the bridge (a step per removed vertex, marking it dead) and relinks the chain;
-// nothing moves. The survivors, in slot order, are the parent's hull.
-template <bool W, bool PR>
-__device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, const LdsVerts<W, PR>& v,
+// The merge in LDS: the children's vertices into slots (every thread's loads in flight
+// together), the pairwise rounds, and the survivors out to the parent's arrays.
+template <bool W, bool PR, int NT, int G>
+__device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, MergeRounds& rs, const Slots<W, PR>& v,
                           int64_t row, int64_t c0, int nch, const NodeOut& pout) {
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
   const int total = sm.total;
-  constexpr int B = 8;  // slots per lane with their loads in flight together
-  for (int s0 = 0; s0 < total; s0 += kWave * B) {
+  // slots per thread with their loads in flight together (fewer in large workgroups, whose
+  // threads have fewer registers and fewer slots each)
+  constexpr int B = NT >= 1024 ? 2 : NT >= 256 ? 4 : 8;
+  for (int s0 = 0; s0 < total; s0 += NT * B) {
     HPt p[B];
+    int cs[B];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const int s = s0 + u * kWave + lane;
-      if (s < total) {
-        const int c = child_of_slot(sm, nch, s);
-        p[u] = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
-      }
+      // (slots past the end load the last slot again, so the loads need no branches)
+      const int s = min(s0 + u * NT + tid, total - 1);
+      cs[u] = child_of_slot(sm, nch, s);
+      p[u] = child_vertex<W, PR>(a, sm, row, c0, cs[u], s - sm.off[cs[u]]);
     }
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const int s = s0 + u * kWave + lane;
+      const int s = s0 + u * NT + tid;
       if (s < total) {
-        lput<W, PR>(v, s, p[u]);
-        v.prev[s] = static_cast<int16_t>(s - 1);
-        v.next[s] = static_cast<int16_t>(s + 1);
-        v.dead[s] = 0;
+        sput(v, s, p[u]);
+        v.cid[s] = static_cast<uint8_t>(cs[u]);
       }
     }
   }
+  for (int c = tid; c < nch; c += NT) rs.seg[0][c] = sm.off[c] + sm.cnt[c] - 1;
   __syncthreads();
-#pragma unroll 1
-  for (int span = 1; span < nch; span <<= 1) {
-    const int pa = lane * 2 * span, pb = pa + span;
-    if (pb < nch) {
-      const int x = sm.off[pb];
-      const int lhead = sm.off[pa];
-      const int rtail = pb + span < nch ? sm.off[pb + span] : total - 1;
-      int ia = v.prev[x], ib = v.next[x];
-      HPt A = lget<W, PR>(v, ia), B = lget<W, PR>(v, ib);
-      // each point is read together with its link onward, so a walk step waits for one LDS
-      // round trip (the next point), not two (its index, then the point)
-      int pa_link = v.prev[ia], nb_link = v.next[ib];
-      if (hpools<W, PR>(A, lget<W, PR>(v, x), B)) {
-        v.dead[x] = 1;
-        int iap = ia != lhead ? pa_link : -1;
-        int ibn = ib != rtail ? nb_link : -1;
-        HPt AP = A, BN = B;
-        int ap_link = 0, bn_link = 0;
-        if (iap >= 0) {
-          AP = lget<W, PR>(v, iap);
-          ap_link = v.prev[iap];
-        }
-        if (ibn >= 0) {
-          BN = lget<W, PR>(v, ibn);
-          bn_link = v.next[ibn];
-        }
-        for (;;) {  // every step marks a vertex dead: at most `total` steps
-          if (iap >= 0 && hpools<W, PR>(AP, A, B)) {
-            v.dead[ia] = 1;
-            ia = iap;
-            A = AP;
-            iap = ia != lhead ? ap_link : -1;
-            if (iap >= 0) {
-              AP = lget<W, PR>(v, iap);
-              ap_link = v.prev[iap];
-            }
-          } else if (ibn >= 0 && hpools<W, PR>(A, B, BN)) {
-            v.dead[ib] = 1;
-            ib = ibn;
-            B = BN;
-            ibn = ib != rtail ? bn_link : -1;
-            if (ibn >= 0) {
-              BN = lget<W, PR>(v, ibn);
-              bn_link = v.next[ibn];
-            }
-          } else {
-            break;
-          }
-        }
-        v.next[ia] = static_cast<int16_t>(ib);
-        v.prev[ib] = static_cast<int16_t>(ia);
-      }
+  const int count = merge_rounds<W, PR, NT, G>(v, rs, total, nch);
+  for (int s = tid; s < count; s += NT) {
+    const HPt x = sget(v, s);
+    pout.idx[s] = x.i;
+    pout.shi[s] = x.s;
+    pout.slo[s] = x.sl;
+    if constexpr (W) {
+      pout.whi[s] = x.w;
+      pout.wlo[s] = x.wl;
     }
-    __syncthreads();
   }
-  // Compaction of the survivors into the parent's arrays.
-  int base = 0;
-  for (int s0 = 0; s0 < total; s0 += kWave) {
-    const int s = s0 + lane;
-    const bool alive = s < total && v.dead[s] == 0;
-    const uint64_t m = __ballot(alive);
-    if (alive) {
-      const int q = base + __popcll(m & ((uint64_t{1} << lane) - 1));
-      const HPt p = lget<W, PR>(v, s);
-      pout.idx[q] = p.i;
-      pout.shi[q] = p.s;
-      pout.slo[q] = p.sl;
-      if constexpr (W) {
-        pout.whi[q] = p.w;
-        pout.wlo[q] = p.wl;
-      }
-    }
-    base += __popcll(m);
-  }
-  if (lane == 0) *pout.count = base;
+  if (tid == 0) *pout.count = count;
 }
 
 // The merge in the parent's global array, for children with more vertices than LDS holds
@@ -366,7 +239,8 @@ __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, in
   const int tid = threadIdx.x;
   const int total = sm.total;
   const VArr v = dvarr_of(pout);
-  for (int s = tid; s < total; s += kWave) {
+  // (the first wave does the work; every thread of a larger workgroup meets the barriers)
+  for (int s = tid < kWave ? tid : total; s < total; s += kWave) {
     const int c = child_of_slot(sm, nch, s);
     const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
     VPt p;
@@ -432,70 +306,76 @@ __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, in
   if (tid == 0) *pout.count = sm.cnt[0];
 }
 
-// One wave per parent node: G = 64 children (fewer at a row's end) -> the parent's hull.
-template <bool W, bool PR>
-__global__ __launch_bounds__(kWave) void merge_kernel(MergeArgs a, int cap_lds) {
+// One workgroup of NT threads per parent node: G = 64 children (fewer at a row's end) -> the
+// parent's hull. NT grows where few parents share the GPU (the upper levels), so that their
+// larger hulls still take few slots per thread.
+template <bool W, bool PR, int NT, int G>
+__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
   __shared__ MergeSmall sm;
+  __shared__ MergeRounds rs;
   extern __shared__ __align__(16) char lds_dyn[];
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
   const int64_t row = blockIdx.x / a.npr_out;
   const int64_t j = blockIdx.x - row * a.npr_out;
   const int64_t c0 = j * kGroup;  // first child within the row
   const int nch = static_cast<int>(min<int64_t>(kGroup, a.npr_in - c0));
   const NodeOut pout = node_out(a.out, a.k_out, a.cap_out, W, row * a.npr_out + j);
 
-  // Children: counts, NaN flags, and offsets within the parent (double-double scan).
-  int cnt = 0, bad = 0;
-  DD tw{0.0, 0.0}, ts{0.0, 0.0};
-  if (lane < nch) {
-    const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + lane);
-    cnt = *ci.count;
-    bad = *ci.bad;
-    tw = DD{ci.tot[0], ci.tot[1]};
-    ts = DD{ci.tot[2], ci.tot[3]};
-  }
-  // inclusive scans: totals (dd) and slots (count - 1, the shared point stored once)
-  DD iw = tw, is = ts;
-  int islot = max(cnt - 1, 0);
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const DD ow{__shfl_up(iw.hi, d, kWave), __shfl_up(iw.lo, d, kWave)};
-    const DD os{__shfl_up(is.hi, d, kWave), __shfl_up(is.lo, d, kWave)};
-    const int oslot = __shfl_up(islot, d, kWave);
-    if (lane >= d) {
-      iw = dd_add(ow, iw);
-      is = dd_add(os, is);
-      islot += oslot;
+  // Children (first wave): counts, NaN flags, and offsets within the parent (double-double scan).
+  if (tid < kWave) {
+    const int lane = tid;
+    int cnt = 0, bad = 0;
+    DD tw{0.0, 0.0}, ts{0.0, 0.0};
+    if (lane < nch) {
+      const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + lane);
+      cnt = *ci.count;
+      bad = *ci.bad;
+      tw = DD{ci.tot[0], ci.tot[1]};
+      ts = DD{ci.tot[2], ci.tot[3]};
     }
+    // inclusive scans: totals (dd) and slots (count - 1, the shared point stored once)
+    DD iw = tw, is = ts;
+    int islot = max(cnt - 1, 0);
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const DD ow{__shfl_up(iw.hi, d, kWave), __shfl_up(iw.lo, d, kWave)};
+      const DD os{__shfl_up(is.hi, d, kWave), __shfl_up(is.lo, d, kWave)};
+      const int oslot = __shfl_up(islot, d, kWave);
+      if (lane >= d) {
+        iw = dd_add(ow, iw);
+        is = dd_add(os, is);
+        islot += oslot;
+      }
+    }
+    const int anybad = __any(bad != 0);
+    DD ew{__shfl_up(iw.hi, 1, kWave), __shfl_up(iw.lo, 1, kWave)};
+    DD es{__shfl_up(is.hi, 1, kWave), __shfl_up(is.lo, 1, kWave)};
+    if (lane == 0) ew = es = DD{0.0, 0.0};
+    if (lane < nch) {
+      sm.cnt[lane] = cnt;
+      sm.off[lane] = islot - max(cnt - 1, 0);
+      sm.tot[0][lane] = ew.hi;
+      sm.tot[1][lane] = ew.lo;
+      sm.tot[2][lane] = es.hi;
+      sm.tot[3][lane] = es.lo;
+    }
+    if (lane == nch - 1) {
+      sm.tot[0][nch] = iw.hi;
+      sm.tot[1][nch] = iw.lo;
+      sm.tot[2][nch] = is.hi;
+      sm.tot[3][nch] = is.lo;
+      sm.total = islot + 1;  // slots
+    }
+    if (lane == 0) sm.bad = anybad;
   }
-  const int anybad = __any(bad != 0);
-  DD ew{__shfl_up(iw.hi, 1, kWave), __shfl_up(iw.lo, 1, kWave)};
-  DD es{__shfl_up(is.hi, 1, kWave), __shfl_up(is.lo, 1, kWave)};
-  if (lane == 0) ew = es = DD{0.0, 0.0};
-  if (lane < nch) {
-    sm.cnt[lane] = cnt;
-    sm.off[lane] = islot - max(cnt - 1, 0);
-    sm.tot[0][lane] = ew.hi;
-    sm.tot[1][lane] = ew.lo;
-    sm.tot[2][lane] = es.hi;
-    sm.tot[3][lane] = es.lo;
-  }
-  if (lane == nch - 1) {
-    sm.tot[0][nch] = iw.hi;
-    sm.tot[1][nch] = iw.lo;
-    sm.tot[2][nch] = is.hi;
-    sm.tot[3][nch] = is.lo;
-    sm.total = islot + 1;  // slots
-  }
-  if (lane == 0) sm.bad = anybad;
   __syncthreads();
 
   if (sm.total <= cap_lds) {
-    merge_lds<W, PR>(a, sm, lds_carve<W, PR>(lds_dyn, cap_lds), row, c0, nch, pout);
+    merge_lds<W, PR, NT, G>(a, sm, rs, slots_carve<W, PR>(lds_dyn, cap_lds), row, c0, nch, pout);
   } else {
     merge_global<W, PR>(a, sm, row, c0, nch, pout);
   }
-  if (lane == 0) {
+  if (tid == 0) {
     *pout.bad = sm.bad;
     pout.tot[0] = sm.tot[0][nch];
     pout.tot[1] = sm.tot[1][nch];
@@ -690,20 +570,30 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     m.npr_out = p.npr[l];
     m.child_elems = p.span[l - 1];
     const unsigned grid = static_cast<unsigned>(t.batch * p.npr[l]);
-    // LDS vertex capacity: 768 where many merges share the GPU (occupancy; 64 noisy span
-    // hulls take about 400-500 slots), else what 60 KB holds
-    auto launch = [&](auto kern, size_t vb) {
-      const int big = static_cast<int>((60 * 1024 / vb) & ~size_t(63));
-      const int cap = grid >= 1024 ? (big < 768 ? big : 768) : big;
-      kern<<<dim3(grid), dim3(kWave), cap * vb, t.stream>>>(m, cap);
+    // Workgroup size and LDS slots by how many merges share the GPU: one wave and 768 slots
+    // (64 noisy span hulls take 300-500) where there are thousands, else 256 or 1024 threads
+    // and up to 56 KB of slots for the fewer, larger hulls of the upper levels.
+    auto launch = [&](auto k64, auto k256, auto k1024, size_t vb) {
+      const int big = static_cast<int>((56 * 1024 / vb) & ~size_t(63));
+      if (grid >= 1024) {
+        k64<<<dim3(grid), dim3(64), 768 * vb, t.stream>>>(m, 768);
+      } else if (grid >= 64) {
+        k256<<<dim3(grid), dim3(256), big * vb, t.stream>>>(m, big);
+      } else {
+        k1024<<<dim3(grid), dim3(1024), big * vb, t.stream>>>(m, big);
+      }
     };
+#define TI_MERGE_LAUNCH(Wv, PRv)                                                                 \
+  launch(merge_kernel<Wv, PRv, 64, 4>, merge_kernel<Wv, PRv, 256, 2>, merge_kernel<Wv, PRv, 1024, 2>, \
+         slot_bytes<Wv, PRv>())
     if (t.dtype == TI_F32) {
-      if (W) launch(merge_kernel<true, false>, lds_vertex_bytes<true, false>());
-      else launch(merge_kernel<false, false>, lds_vertex_bytes<false, false>());
+      if (W) TI_MERGE_LAUNCH(true, false);
+      else TI_MERGE_LAUNCH(false, false);
     } else {
-      if (W) launch(merge_kernel<true, true>, lds_vertex_bytes<true, true>());
-      else launch(merge_kernel<false, true>, lds_vertex_bytes<false, true>());
+      if (W) TI_MERGE_LAUNCH(true, true);
+      else TI_MERGE_LAUNCH(false, true);
     }
+#undef TI_MERGE_LAUNCH
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
