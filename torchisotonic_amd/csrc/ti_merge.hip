@@ -320,6 +320,8 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
   const int64_t c0 = j * kGroup;  // first child within the row
   const int nch = static_cast<int>(min<int64_t>(kGroup, a.npr_in - c0));
   const NodeOut pout = node_out(a.out, a.k_out, a.cap_out, W, row * a.npr_out + j);
+  // (a first child's count of -1: the span kernel merged this group already)
+  if (*node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0).count < 0) return;
 
   // Children (first wave): counts, NaN flags, and offsets within the parent (double-double scan).
   if (tid < kWave) {
@@ -556,7 +558,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   const bool W = t.w != nullptr;
   char* base = static_cast<char*>(ws);
   // level 0: span hulls
-  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0);
+  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0, base + p.off_buf[1], p.cap[1]);
   if (e != hipSuccess) return e;
   for (int l = 1; l <= p.levels; ++l) {
     MergeArgs m;

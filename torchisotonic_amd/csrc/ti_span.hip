@@ -25,6 +25,7 @@
 // Output: the span hulls as the first node array of the cross-span merge (ti_merge.hip).
 #include "ti_common.h"
 #include "ti_kernels.h"
+#include "ti_slots.h"
 #include "ti_tile.h"
 
 namespace ti {
@@ -38,10 +39,13 @@ struct SpanArgs {
   const void* w;
   uint32_t* bad_weight;
   int64_t n, spr, nodes;  // row length, spans per row, spans in total
+  int64_t gpr;            // groups of kGroup spans per row (one wave each)
   int64_t span0;          // elements per span
   unsigned flags;
   void* hulls;            // node array of the spans
   int64_t cap;
+  void* hulls1;           // node array of the groups (the first merge level)
+  int64_t k1, cap1;
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the chunk buffer (sums at
@@ -88,25 +92,27 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert((R & (R - 1)) == 0 && C <= 32, "ring slots: a power of two; chunk: a 32-bit mask");
   static_assert(LC % C == 0, "a load block is a whole number of chunks");
   constexpr bool PR = sizeof(T) == 8;
+  static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
   __shared__ SpanLds<T, W, C, R> L;
   const int lane = threadIdx.x;
-  const int64_t node = static_cast<int64_t>(blockIdx.x) * kSpanLanes + lane;
-  if (node >= a.nodes) return;  // no barriers below: the lanes are independent
-  const int64_t row = node / a.spr;
-  const int64_t span = node - row * a.spr;
+  // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle).
+  const int64_t row = blockIdx.x / a.gpr;
+  const int64_t grp = blockIdx.x - row * a.gpr;
+  const int64_t span = grp * kSpanLanes + lane;
+  const bool active = span < a.spr;
+  const int nch = static_cast<int>(min<int64_t>(kSpanLanes, a.spr - grp * kSpanLanes));
+  const int64_t node = row * a.spr + (active ? span : 0);
   const int64_t first = span * a.span0;
-  const int len = static_cast<int>(min<int64_t>(a.span0, a.n - first));
+  const int len = active ? static_cast<int>(min<int64_t>(a.span0, a.n - first)) : 0;
   const bool inc = (a.flags & TI_INCREASING) != 0;
   const double sgn = inc ? 1.0 : -1.0;
-  // The wave's spans are consecutive elements of the [batch, n] array (rows follow each other),
-  // so one buffer resource based at the wave's first element serves every lane.
-  const int64_t node0 = static_cast<int64_t>(blockIdx.x) * kSpanLanes;
-  const int64_t row0 = node0 / a.spr;
-  const int64_t base = row0 * a.n + (node0 - row0 * a.spr) * a.span0;  // wave-uniform
-  const int64_t total = a.nodes / a.spr * a.n;                         // elements of the array
+  // The group's spans are consecutive elements of the row, so one buffer resource based at its
+  // first element serves every lane.
+  const int64_t base = row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
+  const int64_t total = a.nodes / a.spr * a.n;                 // elements of the array
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + base, (total - base) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(W ? static_cast<const T*>(a.w) + base : a.y, (total - base) * sizeof(T));
-  const uint32_t loff = static_cast<uint32_t>((row * a.n + first - base) * sizeof(T));  // this lane's span
+  const uint32_t loff = static_cast<uint32_t>(lane * a.span0 * static_cast<int64_t>(sizeof(T)));  // this lane's span
   const NodeOut o = node_out(a.hulls, a.nodes, a.cap, W, node);
 
   auto ring_put = [&](int q, const HPt& p) {
@@ -291,20 +297,117 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
       if constexpr (W) wc[W ? k : 0] = wn[W ? k : 0];
     }
   }
-  // the finished hull: positions [0, depth) of the span's array
-  for (int q = r0; q < depth; ++q) node_put(q, ring_get(q));
-  *o.count = depth;
-  *o.bad = bad ? 1 : 0;
-  o.tot[0] = W ? P : static_cast<double>(len);
-  o.tot[1] = W ? PL : 0.0;
-  o.tot[2] = S;
-  o.tot[3] = SL;
   if (W && wbad && a.bad_weight != nullptr) *a.bad_weight = 1u;
+
+  // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
+  // lane c's hull is child c, positions [0, depth), its first point shared with lane c - 1.
+  const int own = active ? (lane == 0 ? depth : depth - 1) : 0;
+  DD iw = active ? DD{W ? P : static_cast<double>(len), W ? PL : 0.0} : DD{0.0, 0.0};
+  DD is = active ? DD{S, SL} : DD{0.0, 0.0};
+  int islot = own;
+#pragma unroll
+  for (int d = 1; d < kSpanLanes; d <<= 1) {
+    const DD ow{__shfl_up(iw.hi, d, kSpanLanes), __shfl_up(iw.lo, d, kSpanLanes)};
+    const DD os{__shfl_up(is.hi, d, kSpanLanes), __shfl_up(is.lo, d, kSpanLanes)};
+    const int oslot = __shfl_up(islot, d, kSpanLanes);
+    if (lane >= d) {
+      iw = dd_add(ow, iw);
+      is = dd_add(os, is);
+      islot += oslot;
+    }
+  }
+  const int nslots = __shfl(islot, kSpanLanes - 1, kSpanLanes);
+  // (the round state first, then the slots, in the wave's LDS)
+  constexpr size_t kRoundBytes = (sizeof(MergeRounds) + 63) & ~size_t(63);
+  constexpr int kCap =
+      static_cast<int>(((sizeof(SpanLds<T, W, C, R>) - kRoundBytes) / slot_bytes<W, PR>()) & ~size_t(63));
+  static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
+  if (nslots > kCap) {
+    // too many vertices: the span's hull goes to the span array, for the merge kernel
+    if (active) {
+      for (int q = r0; q < depth; ++q) node_put(q, ring_get(q));
+      *o.count = depth;
+      *o.bad = bad ? 1 : 0;
+      o.tot[0] = W ? P : static_cast<double>(len);
+      o.tot[1] = W ? PL : 0.0;
+      o.tot[2] = S;
+      o.tot[3] = SL;
+    }
+    return;
+  }
+  // offsets of this lane's span within the group
+  DD ew{__shfl_up(iw.hi, 1, kSpanLanes), __shfl_up(iw.lo, 1, kSpanLanes)};
+  DD es{__shfl_up(is.hi, 1, kSpanLanes), __shfl_up(is.lo, 1, kSpanLanes)};
+  if (lane == 0) ew = es = DD{0.0, 0.0};
+  const int off = islot - own;
+  const int lidx = lane * static_cast<int>(a.span0);
+  const bool anybad = __any(active && bad);
+  auto to_group = [&](HPt p) {
+    p.i += lidx;
+    const DD Sd = dd_add(es, DD{p.s, p.sl});
+    p.s = Sd.hi;
+    p.sl = PR ? Sd.lo : 0.0;
+    if constexpr (W) {
+      const DD Wd = dd_add(ew, DD{p.w, p.wl});
+      p.w = Wd.hi;
+      p.wl = PR ? Wd.lo : 0.0;
+    }
+    return p;
+  };
+  // the ring into registers first: the slots take over the wave's LDS
+  HPt rv[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) rv[k] = ring_get(r0 + k);
+  char* const mem = reinterpret_cast<char*>(&L);
+  MergeRounds& rs = *reinterpret_cast<MergeRounds*>(mem);
+  const Slots<W, PR> v = slots_carve<W, PR>(mem + kRoundBytes, kCap);
+  const int q0 = lane == 0 ? 0 : 1;  // the first point of a later span is its left neighbour's last
+  if (active) {
+    for (int q = q0; q < r0; ++q) {
+      const int sl = off + q - q0;
+      sput(v, sl, to_group(node_get(q)));
+      v.cid[sl] = static_cast<uint8_t>(lane);
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int q = r0 + k;
+      if (q >= q0 && q < depth) {
+        const int sl = off + q - q0;
+        sput(v, sl, to_group(rv[k]));
+        v.cid[sl] = static_cast<uint8_t>(lane);
+      }
+    }
+    rs.seg[0][lane] = off + own - 1;
+  }
+  __syncthreads();
+  const int count = merge_rounds<W, PR, kSpanLanes, 2>(v, rs, nslots, nch);
+  const NodeOut pout = node_out(a.hulls1, a.k1, a.cap1, W, blockIdx.x);
+  for (int k = lane; k < count; k += kSpanLanes) {
+    const HPt x = sget(v, k);
+    pout.idx[k] = x.i;
+    pout.shi[k] = x.s;
+    pout.slo[k] = x.sl;
+    if constexpr (W) {
+      pout.whi[k] = x.w;
+      pout.wlo[k] = x.wl;
+    }
+  }
+  if (lane == nch - 1) {
+    *pout.count = count;
+    *pout.bad = anybad ? 1 : 0;
+    pout.tot[0] = iw.hi;
+    pout.tot[1] = iw.lo;
+    pout.tot[2] = is.hi;
+    pout.tot[3] = is.lo;
+  }
+  // the group is merged: its first span's count says so to the merge kernel
+  if (lane == 0) *o.count = -1;
 }
 
 }  // namespace
 
-hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, int64_t span0) {
+hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, int64_t span0, void* hulls1,
+                     int64_t cap1) {
   SpanArgs a;
   a.y = t.y;
   a.w = t.w;
@@ -316,7 +419,11 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.hulls = hulls;
   a.cap = cap;
   a.span0 = span0;
-  const unsigned grid = static_cast<unsigned>((a.nodes + kSpanLanes - 1) / kSpanLanes);
+  a.gpr = (spr + kSpanLanes - 1) / kSpanLanes;
+  a.hulls1 = hulls1;
+  a.k1 = t.batch * a.gpr;
+  a.cap1 = cap1;
+  const unsigned grid = static_cast<unsigned>(t.batch * a.gpr);
   const bool W = t.w != nullptr;
   if (t.dtype == TI_F32) {
     if (W) span_kernel<float, true, 8, 8, 32><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);

@@ -217,7 +217,10 @@ struct LongPlan {
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
-hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap, int64_t span0);
+// Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
+// place into `hulls1` (cap1 vertices per group) and its first span's count set to -1.
+hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap, int64_t span0,
+                    void* hulls1, int64_t cap1);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {
