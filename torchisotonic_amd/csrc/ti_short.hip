@@ -168,13 +168,11 @@ __device__ __forceinline__ int lowest_bit(uint64_t v) { return __builtin_ctzll(v
 __device__ __forceinline__ int highest_bit(uint32_t v) { return 31 - __builtin_clz(v); }
 __device__ __forceinline__ int highest_bit(uint64_t v) { return 63 - __builtin_clzll(v); }
 
-// sgn * a < sgn * b, exactly (a, b in the data's dtype; sgn = +-1).
-template <typename T>
-__device__ __forceinline__ bool tsgn_lt(double sgn, T a, T b) {
-  return sgn > 0.0 ? a < b : b < a;
-}
+// Unweighted rows (block weights are element counts, at most 32): a block's mean is its sum
+// times the correctly rounded reciprocal of its length, in the forward and the backward alike.
+constexpr int kRcpN = 33;
 
-template <typename T, int NMAX, bool W, bool DIRECT>
+template <typename T, int NMAX, bool W, bool DIRECT, bool INC>
 __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
     uint32_t* __restrict__ starts, uint32_t* __restrict__ bad_weight, int64_t batch, int n,
@@ -192,7 +190,11 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
   const int count = rows * n;
   const DivBy div(static_cast<uint32_t>(n));
   const bool active = tid < rows;
-  const double sgn = (flags & TI_INCREASING) ? 1.0 : -1.0;
+  constexpr double sgn = INC ? 1.0 : -1.0;
+  __shared__ double rcp[W ? 1 : kRcpN];
+  if constexpr (!W) {
+    if (tid < kRcpN) rcp[tid] = tid > 0 ? 1.0 / static_cast<double>(tid) : 0.0;
+  }
 
   T yv[NMAX];
   T wv[W ? NMAX : 1];
@@ -261,6 +263,7 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
       }
     }
   }
+  if constexpr (DIRECT && !W) __syncthreads();  // the reciprocals (staged rows met barriers already)
 
   // Lower hull of P_0..P_n by the monotone chain, run as an event loop: every iteration either
   // pops the last vertex or pushes the next candidate, so a wave iterates max over its lanes of
@@ -276,7 +279,7 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     Mask cand = Mask(1) | (Mask(1) << nn);
 #pragma unroll
     for (int k = 1; k < NMAX; ++k) {
-      if (k < nn && tsgn_lt(sgn, yv[k - 1], yv[k])) cand |= Mask(1) << k;
+      if (k < nn && (INC ? yv[k - 1] < yv[k] : yv[k] < yv[k - 1])) cand |= Mask(1) << k;
     }
     // stack: t1 (last vertex) and t2 (< 0: none) with their sums and weights; the stack itself
     // is the mask m. The candidate being pushed is k; rest holds the candidates after it.
@@ -310,64 +313,67 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
       } else {
         wkn = static_cast<double>(kn);
       }
-      if (pop) {
-        m &= ~(Mask(1) << t1);
-        t1 = t2;
-        s1 = s2;
-        w1 = w2;
-        t2 = t3;
-        s2 = s3;
-        w2 = w3;
-      } else {
-        m |= Mask(1) << k;
-        t2 = t1;
-        s2 = s1;
-        w2 = w1;
-        t1 = k;
-        s1 = sk;
-        w1 = wk;
-        k = kn;
-        sk = skn;
-        wk = wkn;
-        rest &= rest - 1;
-      }
+      // (selects, not branches: a wave whose lanes differ would run both)
+      m = pop ? (m & ~(Mask(1) << t1)) : (m | (Mask(1) << k));
+      const int nt1 = pop ? t2 : k, nt2 = pop ? t3 : t1;
+      const double ns1 = pop ? s2 : sk, ns2 = pop ? s3 : s1;
+      const double nw1 = pop ? w2 : wk, nw2 = pop ? w3 : w1;
+      t1 = nt1;
+      t2 = nt2;
+      s1 = ns1;
+      s2 = ns2;
+      w1 = nw1;
+      w2 = nw2;
+      k = pop ? k : kn;
+      sk = pop ? sk : skn;
+      wk = pop ? wk : wkn;
+      rest = pop ? rest : (rest & (rest - 1));
     }
   }
 
-  // Slopes, one per hull edge, from the last vertex down: each edge's slope replaces the sum
-  // at its first vertex in the point column (that sum is kept in a register for the next edge),
-  // then every element takes the slope of the last vertex at or before it.
   T fit[NMAX];
-  {
+  const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
+  if constexpr (!W) {
+    // Left to right: at a vertex i the block runs to the next vertex v (found from the mask, so
+    // every element's reads are independent), with mean (S_v - S_i) / (v - i); the others keep
+    // the mean of the block they are in.
+    const Mask mv = m | (Mask(1) << nn);  // (point nn is a vertex; idle threads set it here)
+    double cur = 0.0;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      if (i < nn) {
+        const int v = i + 1 + lowest_bit(static_cast<Mask>(mv >> (i + 1)));
+        const double mean = (colS[v * THREADS + tid] - colS[i * THREADS + tid]) * rcp[v - i];
+        cur = ((m >> i) & 1u) ? mean : cur;
+        const T val = bad ? quiet_nan<T>() : static_cast<T>(sgn * cur);
+        fit[i] = clip(val, use_lo, lo, use_hi, hi);
+      }
+    }
+  } else {
+    // Slopes, one per hull edge, from the last vertex down: each edge's slope replaces the sum
+    // at its first vertex in the point column (that sum is kept in a register for the next
+    // edge), then every element takes the slope of the last vertex at or before it.
     if (active) {
-      int vh = nn;
-      double sh = colS[nn * THREADS + tid], wh;
-      if constexpr (W) wh = colW[nn * THREADS + tid];
-      else wh = static_cast<double>(nn);
+      double sh = colS[nn * THREADS + tid];
+      double wh = colW[nn * THREADS + tid];
       Mask rem = m & ((Mask(1) << nn) - Mask(1));  // vertices below nn (point 0 among them)
       while (rem) {
         const int vl = highest_bit(rem);
         rem &= ~(Mask(1) << vl);
         const double sl = colS[vl * THREADS + tid];
-        double wl;
-        if constexpr (W) wl = colW[vl * THREADS + tid];
-        else wl = static_cast<double>(vl);
+        const double wl = colW[vl * THREADS + tid];
         colS[vl * THREADS + tid] = slope_div(sh - sl, wh - wl);
-        vh = vl;
         sh = sl;
         wh = wl;
       }
-      (void)vh;
     }
-    const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
-    const T tsgn = static_cast<T>(sgn);
     double cur = 0.0;
 #pragma unroll
     for (int i = 0; i < NMAX; ++i) {
       if (i < nn) {
         if ((m >> i) & 1ull) cur = colS[i * THREADS + tid];
-        const T v = bad ? quiet_nan<T>() : tsgn * static_cast<T>(cur);
-        fit[i] = clip(v, use_lo, lo, use_hi, hi);
+        const T val = bad ? quiet_nan<T>() : static_cast<T>(sgn * cur);
+        fit[i] = clip(val, use_lo, lo, use_hi, hi);
       }
     }
   }
@@ -496,7 +502,9 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_kernel(
           const double wsum = W ? wa : static_cast<double>(end - i);
           bool pass = true;
           if (need_mean) {
-            const T f = static_cast<T>(slope_div(se - S[i], we - Wk(i)));
+            // the forward's block mean, bit for bit
+            const T f = W ? static_cast<T>(slope_div(se - S[i], we - Wk(i)))
+                          : static_cast<T>((se - S[i]) * (1.0 / static_cast<double>(end - i)));
             fitv[i] = f;
             pass = !(use_lo || use_hi) || clip_passes(f, use_lo, lo, use_hi, hi);
             se = S[i];
@@ -571,11 +579,12 @@ hipError_t launch_fit(const ShortArgs& a) {
         static_cast<T>(a.hi));
     return hipGetLastError();
   };
+  const bool inc = (a.flags & TI_INCREASING) != 0;
   if constexpr ((NMAX * sizeof(T)) % 16 == 0) {
     if (a.n == NMAX && aligned16(a.y) && aligned16(a.w) && aligned16(a.out))
-      return run(short_fit_kernel<T, NMAX, W, true>);
+      return inc ? run(short_fit_kernel<T, NMAX, W, true, true>) : run(short_fit_kernel<T, NMAX, W, true, false>);
   }
-  return run(short_fit_kernel<T, NMAX, W, false>);
+  return inc ? run(short_fit_kernel<T, NMAX, W, false, true>) : run(short_fit_kernel<T, NMAX, W, false, false>);
 }
 
 template <typename T, int NMAX, bool W>
