@@ -345,8 +345,7 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
         const int v = i + 1 + lowest_bit(static_cast<Mask>(mv >> (i + 1)));
         const double mean = (colS[v * THREADS + tid] - colS[i * THREADS + tid]) * rcp[v - i];
         cur = ((m >> i) & 1u) ? mean : cur;
-        const T val = bad ? quiet_nan<T>() : static_cast<T>(sgn * cur);
-        fit[i] = clip(val, use_lo, lo, use_hi, hi);
+        fit[i] = static_cast<T>(sgn * cur);
       }
     }
   } else {
@@ -372,10 +371,18 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     for (int i = 0; i < NMAX; ++i) {
       if (i < nn) {
         if ((m >> i) & 1ull) cur = colS[i * THREADS + tid];
-        const T val = bad ? quiet_nan<T>() : static_cast<T>(sgn * cur);
-        fit[i] = clip(val, use_lo, lo, use_hi, hi);
+        fit[i] = static_cast<T>(sgn * cur);
       }
     }
+  }
+  // NaN rows and the clamp, each behind a test of the whole wave (most waves skip both)
+  if (__any(bad)) {
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) fit[i] = bad ? quiet_nan<T>() : fit[i];
+  }
+  if (use_lo || use_hi) {
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) fit[i] = clip(fit[i], use_lo, lo, use_hi, hi);
   }
 
   if (starts != nullptr && active) {
