@@ -87,13 +87,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), nrec, 0x00020000);
 }
 
-template <typename T, bool W, int C, int R, int LC>
+template <typename T, bool W, int C, int R, int LC, bool INC>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
-  static_assert((R & (R - 1)) == 0 && C <= 32, "ring slots: a power of two; chunk: a 32-bit mask");
-  static_assert(LC % C == 0, "a load block is a whole number of chunks");
+  static_assert((R & (R - 1)) == 0 && 2 * C <= 32, "ring slots: a power of two; two chunks: a 32-bit mask");
+  static_assert(LC % (2 * C) == 0, "a load block is a whole number of chunk pairs");
   constexpr bool PR = sizeof(T) == 8;
   static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
-  __shared__ SpanLds<T, W, C, R> L;
+  __shared__ SpanLds<T, W, 2 * C, R> L;  // the chunk buffer holds two chunks
   const int lane = threadIdx.x;
   // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle).
   const int64_t row = blockIdx.x / a.gpr;
@@ -104,8 +104,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   const int64_t node = row * a.spr + (active ? span : 0);
   const int64_t first = span * a.span0;
   const int len = active ? static_cast<int>(min<int64_t>(a.span0, a.n - first)) : 0;
-  const bool inc = (a.flags & TI_INCREASING) != 0;
-  const double sgn = inc ? 1.0 : -1.0;
+  constexpr double sgn = INC ? 1.0 : -1.0;
   // The group's spans are consecutive elements of the row, so one buffer resource based at its
   // first element serves every lane.
   const int64_t base = row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
@@ -160,91 +159,28 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 
   double S = 0.0, SL = 0.0, P = 0.0, PL = 0.0;
   bool bad = false, wbad = false;
-  // loads come in blocks of LC elements (the next block in flight while this one is processed),
-  // processed in chunks of C
-  T yc[LC], yn[LC];
-  T wc[W ? LC : 1], wn[W ? LC : 1];
-  load_block<T, LC>(ry, loff, yc);
-  if constexpr (W) load_block<T, LC>(rw, loff, wc);
-  for (int b0 = 0; b0 < len; b0 += LC) {
-    // the next block, whole, whether or not the span reaches it
-    load_block<T, LC>(ry, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), yn);
-    if constexpr (W) load_block<T, LC>(rw, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), wn);
-#pragma unroll
-    for (int sub = 0; sub < LC; sub += C) {
-    const int c0 = b0 + sub;
-    // 1. sums at every point of the chunk, and the candidates
-    uint32_t mask = 0;
-    auto element = [&](int k) {  // sums through element c0 + k, stored for the point after it
-      const double ye = sgn * static_cast<double>(yc[sub + k]);
-      bad |= ye != ye;
-      double term = ye;
-      if constexpr (W) {
-        const double we = static_cast<double>(wc[W ? sub + k : 0]);
-        wbad |= !(we > 0.0);
-        term = we * ye;
-        if constexpr (PR) {
-          const DD t = two_sum(P, we);
-          P = t.hi;
-          PL += t.lo;
-        } else {
-          P += we;
-        }
-      }
-      if constexpr (PR) {
-        const DD t = two_sum(S, term);
-        S = t.hi;
-        SL += t.lo;
-      } else {
-        S += term;
-      }
-      L.cs[k][lane] = S;
-      if constexpr (PR) L.csl[k][lane] = SL;
-      if constexpr (W) L.cw[k][lane] = P;
-      if constexpr (W && PR) L.cwl[k][lane] = PL;
-    };
-    // the point after element e is a candidate where y rises into e + 1, or at the span's end
-    auto rises = [&](T a, T b) { return inc ? a < b : b < a; };
-    if (__all(c0 + C <= len)) {
-      // whole chunks (all but a row's last span): no per-element bounds
-#pragma unroll
-      for (int k = 0; k < C; ++k) {
-        element(k);
-        const int kk = sub + k;
-        const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
-        // (the span can end only after a chunk's last element here)
-        const bool cand = k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext));
-        mask |= static_cast<uint32_t>(cand) << k;
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < C; ++k) {
-        const int e = c0 + k;
-        if (e < len) {
-          element(k);
-          const int kk = sub + k;
-          const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
-          const bool cand = (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext));
-          mask |= static_cast<uint32_t>(cand) << k;
-        }
-      }
-    }
-    // 2. one stack operation per lane and iteration until every lane has pushed its candidates.
-    // The loop touches LDS only (and stores spills), so the next chunk's loads stay in flight;
-    // a lane whose second vertex went to the node array makes the wave leave it, refill that
-    // lane's ring from the node array, and come back (rare).
+  // Candidates pending in the two chunks in LDS: bits [0, C) the older chunk, [C, 2C) the newer.
+  uint32_t pend = 0;
+  // 2. one stack operation per lane and iteration, until no lane has a candidate left among
+  // `need`; a lane done with those goes on with its later candidates. hk: the ring half (of the
+  // chunk buffer) of the older chunk, ck0 its first element. The loop touches LDS only (and
+  // stores spills), so the next loads stay in flight; a lane whose second vertex went to the
+  // node array makes the wave leave it, refill that lane's ring from the node array, and come
+  // back (rare).
+  auto run = [&](int hk, int ck0, uint32_t need) {
     for (;;) {
-      while (__any(mask != 0)) {
-        const bool act = mask != 0;
+      while (__any((pend & need) != 0)) {
+        const bool act = pend != 0;
         const bool two = act && depth >= 2;
         if (__any(two && depth - 2 < r0)) break;
-        const int j = act ? __builtin_ctz(mask) : 0;
+        const int j = act ? __builtin_ctz(pend) : 0;
+        const int slot = (hk * C + j) & (2 * C - 1);
         HPt c;
-        c.i = c0 + j + 1;
-        c.s = L.cs[j][lane];
-        c.sl = PR ? L.csl[PR ? j : 0][lane] : 0.0;
-        c.w = W ? L.cw[W ? j : 0][lane] : 0.0;
-        c.wl = (W && PR) ? L.cwl[(W && PR) ? j : 0][lane] : 0.0;
+        c.i = ck0 + j + 1;
+        c.s = L.cs[slot][lane];
+        c.sl = PR ? L.csl[PR ? slot : 0][lane] : 0.0;
+        c.w = W ? L.cw[W ? slot : 0][lane] : 0.0;
+        c.wl = (W && PR) ? L.cwl[(W && PR) ? slot : 0][lane] : 0.0;
         const HPt A = ring_get(depth - 2), B = ring_get(depth - 1);
         // pools(A, B, c): a filtered fma test, exact where it cannot decide (see pools<true>)
         double dS1 = B.s - A.s, dS2 = c.s - B.s, dW1, dW2;
@@ -278,25 +214,110 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
             ++r0;
           }
           ring_put(q, c);
-          mask &= mask - 1;
+          pend &= pend - 1;
         }
         depth += push ? 1 : (pop ? -1 : 0);
       }
-      if (!__any(mask != 0)) break;
-      if (mask != 0 && depth >= 2 && depth - 2 < r0) {
+      if (!__any((pend & need) != 0)) break;
+      if (pend != 0 && depth >= 2 && depth - 2 < r0) {
         // only the top is in the ring (depth - 1 == r0): bring back up to R / 2 positions below
         const int lo = r0 > R / 2 ? r0 - R / 2 : 0;
         for (int q = lo; q < r0; ++q) ring_put(q, node_get(q));
         r0 = lo;
       }
     }
-    }  // chunks of the block
+  };
+
+  // loads come in blocks of LC elements (the next block in flight while this one is processed),
+  // processed in chunks of C: the sums of chunk k + 1 go to LDS while chunk k's candidates
+  // remain, so lanes with few candidates in chunk k do not wait idle for the others
+  T yc[LC], yn[LC];
+  T wc[W ? LC : 1], wn[W ? LC : 1];
+  int ck_last = 0;  // the chunk whose candidates stay pending after the loop
+  load_block<T, LC>(ry, loff, yc);
+  if constexpr (W) load_block<T, LC>(rw, loff, wc);
+  for (int b0 = 0; b0 < len; b0 += LC) {
+    // the next block, whole, whether or not the span reaches it
+    load_block<T, LC>(ry, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), yn);
+    if constexpr (W) load_block<T, LC>(rw, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), wn);
+#pragma unroll
+    for (int sub = 0; sub < LC; sub += C) {
+      const int c0 = b0 + sub;
+      const int h = (sub / C) & 1;  // this chunk's half of the chunk buffer
+      // 1. sums at every point of the chunk, and the candidates
+      uint32_t mask = 0;
+      auto element = [&](int k) {  // sums through element c0 + k, stored for the point after it
+        const double ye = sgn * static_cast<double>(yc[sub + k]);
+        bad |= ye != ye;
+        double term = ye;
+        if constexpr (W) {
+          const double we = static_cast<double>(wc[W ? sub + k : 0]);
+          wbad |= !(we > 0.0);
+          term = we * ye;
+          if constexpr (PR) {
+            const DD t = two_sum(P, we);
+            P = t.hi;
+            PL += t.lo;
+          } else {
+            P += we;
+          }
+        }
+        if constexpr (PR) {
+          const DD t = two_sum(S, term);
+          S = t.hi;
+          SL += t.lo;
+        } else {
+          S += term;
+        }
+        L.cs[h * C + k][lane] = S;
+        if constexpr (PR) L.csl[h * C + k][lane] = SL;
+        if constexpr (W) L.cw[h * C + k][lane] = P;
+        if constexpr (W && PR) L.cwl[h * C + k][lane] = PL;
+      };
+      // the point after element e is a candidate where y rises into e + 1, or at the span's end
+      auto rises = [&](T u, T v) { return INC ? u < v : v < u; };
+      if (__all(c0 + C <= len)) {
+        // whole chunks (all but a row's last span): no per-element bounds
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          element(k);
+          const int kk = sub + k;
+          const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
+          // (the span can end only after a chunk's last element here)
+          const bool cand = k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext));
+          mask |= static_cast<uint32_t>(cand) << k;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          const int e = c0 + k;
+          if (e < len) {
+            element(k);
+            const int kk = sub + k;
+            const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
+            const bool cand = (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext));
+            mask |= static_cast<uint32_t>(cand) << k;
+          }
+        }
+      }
+      // 2. the previous chunk's candidates (with this one's to go on with)
+      if (c0 == 0) {
+        pend = mask;
+      } else {
+        pend |= mask << C;
+        run(h ^ 1, c0 - C, (1u << C) - 1u);
+        pend >>= C;
+      }
+      ck_last = c0;
+    }
 #pragma unroll
     for (int k = 0; k < LC; ++k) {
       yc[k] = yn[k];
       if constexpr (W) wc[W ? k : 0] = wn[W ? k : 0];
     }
   }
+  // the last chunk's candidates
+  run((ck_last / C) & 1, ck_last, ~0u);
   if (W && wbad && a.bad_weight != nullptr) *a.bad_weight = 1u;
 
   // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
@@ -320,7 +341,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // (the round state first, then the slots, in the wave's LDS)
   constexpr size_t kRoundBytes = (sizeof(MergeRounds) + 63) & ~size_t(63);
   constexpr int kCap =
-      static_cast<int>(((sizeof(SpanLds<T, W, C, R>) - kRoundBytes) / slot_bytes<W, PR>()) & ~size_t(63));
+      static_cast<int>(((sizeof(SpanLds<T, W, 2 * C, R>) - kRoundBytes) / slot_bytes<W, PR>()) & ~size_t(63));
   static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
   if (nslots > kCap) {
     // too many vertices: the span's hull goes to the span array, for the merge kernel
@@ -425,12 +446,17 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.cap1 = cap1;
   const unsigned grid = static_cast<unsigned>(t.batch * a.gpr);
   const bool W = t.w != nullptr;
+  const bool inc = (t.flags & TI_INCREASING) != 0;
+  auto go = [&](auto k_inc, auto k_dec) {
+    if (inc) k_inc<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    else k_dec<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+  };
   if (t.dtype == TI_F32) {
-    if (W) span_kernel<float, true, 8, 8, 32><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<float, false, 8, 16, 32><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) go(span_kernel<float, true, 4, 8, 32, true>, span_kernel<float, true, 4, 8, 32, false>);
+    else go(span_kernel<float, false, 4, 16, 32, true>, span_kernel<float, false, 4, 16, 32, false>);
   } else {
-    if (W) span_kernel<double, true, 8, 8, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
-    else span_kernel<double, false, 8, 16, 8><<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
+    if (W) go(span_kernel<double, true, 4, 8, 8, true>, span_kernel<double, true, 4, 8, 8, false>);
+    else go(span_kernel<double, false, 4, 16, 8, true>, span_kernel<double, false, 4, 16, 8, false>);
   }
   return hipGetLastError();
 }
