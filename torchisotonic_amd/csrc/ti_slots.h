@@ -261,8 +261,8 @@ __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, i
           const bool act = need[u] & (lo[u] < hi[u]);
           const bool lf = left[u];
           const bool t = hpools_nb<W, PR>(hsel(lf, P[u], A[u]), hsel(lf, A[u], B[u]), hsel(lf, B[u], P[u])) == lf;
-          lo[u] = act & t ? mid[u] + 1 : lo[u];
-          hi[u] = act & !t ? mid[u] : hi[u];
+          lo[u] = (act && t) ? mid[u] + 1 : lo[u];
+          hi[u] = (act && !t) ? mid[u] : hi[u];
         }
       }
       bool dies[G];
