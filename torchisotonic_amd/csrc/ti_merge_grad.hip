@@ -6,8 +6,10 @@
 // its workspace) give every block's weight and fit; only the block sums of g are new, and they
 // are differences of a prefix sum of g taken at the hull's vertices:
 //
-//   gsum_kernel    per tile: reads g once; the tile's total, and the prefix of g (within the
-//                  tile, double-double) at each hull vertex inside it, by the vertex's rank;
+//   gsum_kernel    per tile (two to a workgroup, their loads in flight together): reads g
+//                  once; the tile's total, and the prefix of g (within the tile, double-double)
+//                  at each hull vertex inside it, by the vertex's rank (a tile inside one block,
+//                  the common case, needs only its total);
 //   gscan kernels  exclusive scans of the tile totals: within groups of 256 tiles, then over
 //                  the groups of a row;
 //   gfill_kernel   per tile: for each block overlapping the tile, G = difference of the row
@@ -101,6 +103,22 @@ __device__ __forceinline__ uint32_t tile_bits(const uint32_t* srow, int x, int E
   return (srow[x >> 5] >> (x & 31)) & mask;
 }
 
+// Sum over a 256-thread workgroup (double-double), for every thread.
+__device__ DD block_sum_dd(DD v, DD* wave_tot) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) v = dd_add(v, DD{__shfl_xor(v.hi, d, kWave), __shfl_xor(v.lo, d, kWave)});
+  if (lane == 0) wave_tot[wave] = v;
+  __syncthreads();
+  DD t = wave_tot[0];
+  for (int w2 = 1; w2 < kWaves256; ++w2) t = dd_add(t, wave_tot[w2]);
+  __syncthreads();  // wave_tot is reused
+  return t;
+}
+
+// Tiles per gsum workgroup: their loads are all in flight before the first tile is summed.
+constexpr int kGsumTiles = 2;
+
 template <typename T, bool W>
 __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   using C = TileCfg<W>;
@@ -111,70 +129,112 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   __shared__ DD wtot[kWaves256];
   __shared__ int rank_scan[kWaves256];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int64_t row = blockIdx.x / a.tpr;
-  const int64_t tile = blockIdx.x - row * a.tpr;
-  const int64_t first = tile * C::kN;
-  const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
+  const int64_t ntiles = a.batch * a.tpr;
+  const int64_t gt0 = static_cast<int64_t>(blockIdx.x) * kGsumTiles;
   const int t0 = tid * E;
-  const int ecount = max(0, min(E, len - t0));
-  // every independent load first: g, the start bits, the tile's rank and the row's flags
-  T gv[E];
-  load_elems_any<T, E>(static_cast<const T*>(a.g) + row * a.n + first + t0, ecount, gv);
-  const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
-  uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
-  const int at_start = (tile == 0) ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1));
-  const int rA = a.tile_rank[2 * blockIdx.x];
-  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
-  const int bad = *fin.bad;
-  const int last = (tile == a.tpr - 1 && tid == 0) ? *fin.count - 1 : 0;
-
-  double lp[E];
-  double ll[PR ? E : 1];
-  DD acc{0.0, 0.0};
+  // every tile's loads first (a tile's own small reads would each cost a memory round trip):
+  // g, the tile's ranks, its row's NaN flag and vertex count, and whether a vertex starts it
+  T gv[kGsumTiles][E];
+  int rA[kGsumTiles], rB[kGsumTiles], badu[kGsumTiles], cntu[kGsumTiles], head[kGsumTiles];
 #pragma unroll
-  for (int k = 0; k < E; ++k) {
-    lp[k] = acc.hi;
-    if constexpr (PR) ll[k] = acc.lo;
-    if (k < ecount) {
-      if constexpr (PR) acc = dd_add(acc, static_cast<double>(gv[k]));
-      else acc.hi += static_cast<double>(gv[k]);
+  for (int u = 0; u < kGsumTiles; ++u) {
+    const int64_t gt = min(gt0 + u, ntiles - 1);
+    const int64_t row = gt / a.tpr;
+    const int64_t tile = gt - row * a.tpr;
+    const int64_t first = tile * C::kN;
+    const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
+    load_elems_any<T, E>(static_cast<const T*>(a.g) + row * a.n + first + t0, max(0, min(E, len - t0)), gv[u]);
+    rA[u] = a.tile_rank[2 * gt];
+    rB[u] = a.tile_rank[2 * gt + 1];
+    const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+    badu[u] = *fin.bad;
+    cntu[u] = *fin.count;
+    const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
+    head[u] = tile == 0 ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1));
+  }
+#pragma unroll
+  for (int u = 0; u < kGsumTiles; ++u) {
+    const int64_t gt = gt0 + u;
+    if (gt >= ntiles) break;
+    const int64_t row = gt / a.tpr;
+    const int64_t tile = gt - row * a.tpr;
+    const int64_t first = tile * C::kN;
+    const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
+    const int ecount = max(0, min(E, len - t0));
+    const int bad = badu[u];
+    double* lv = a.lv + 2 * row * a.cap_final;
+    double lp[E];
+    double ll[PR ? E : 1];
+    DD acc{0.0, 0.0};
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      lp[k] = acc.hi;
+      if constexpr (PR) ll[k] = acc.lo;
+      if (k < ecount) {
+        if constexpr (PR) acc = dd_add(acc, static_cast<double>(gv[u][k]));
+        else acc.hi += static_cast<double>(gv[u][k]);
+      }
     }
-  }
-  DD total;
-  const DD off = block_scan_dd(acc, wtot, total);
-  if (tid == 0) {
-    a.tg[2 * blockIdx.x] = total.hi;
-    a.tg[2 * blockIdx.x + 1] = total.lo;
-  }
-  if (bad) return;  // a NaN row is one block: only its total is needed
-  // the hull vertices inside the tile, by rank: rA, less one if rA is the tile's first element
-  if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
-  if (first + t0 == 0) mybits |= 1u;
-  const int pc = __builtin_popcount(mybits);
-  int incl = pc;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-  if (lane == kWave - 1) rank_scan[wave] = incl;
-  __syncthreads();
-  int before = incl - pc;
-  for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
-  double* lv = a.lv + 2 * row * a.cap_final;
-  int rank = rA - at_start + before;
-#pragma unroll
-  for (int k = 0; k < E; ++k) {
-    if ((mybits >> k) & 1u) {
-      ++rank;
-      const DD p = dd_add(off, DD{lp[k], PR ? ll[PR ? k : 0] : 0.0});
-      lv[2 * rank] = p.hi;
-      lv[2 * rank + 1] = p.lo;
+    if (bad || rB[u] == rA[u] + 1) {
+      // no vertex inside the tile (the common case on long rows): its total, a zero prefix for
+      // a vertex at its first element, and on the row's last tile the row's end point
+      const DD total = block_sum_dd(acc, wtot);
+      if (tid == 0) {
+        a.tg[2 * gt] = total.hi;
+        a.tg[2 * gt + 1] = total.lo;
+        if (!bad) {
+          if (head[u]) {  // vertex rA is the tile's first element
+            lv[2 * rA[u]] = 0.0;
+            lv[2 * rA[u] + 1] = 0.0;
+          }
+          if (tile == a.tpr - 1) {
+            const int last = cntu[u] - 1;
+            lv[2 * last] = total.hi;
+            lv[2 * last + 1] = total.lo;
+          }
+        }
+      }
+      continue;
     }
-  }
-  if (tile == a.tpr - 1 && tid == 0) {  // the row's end point: the last vertex
-    lv[2 * last] = total.hi;
-    lv[2 * last + 1] = total.lo;
+    DD total;
+    const DD off = block_scan_dd(acc, wtot, total);
+    if (tid == 0) {
+      a.tg[2 * gt] = total.hi;
+      a.tg[2 * gt + 1] = total.lo;
+    }
+    // the hull vertices inside the tile, by rank: rA, less one if rA is the tile's first element
+    const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
+    uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
+    const int at_start = head[u];
+    if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
+    if (first + t0 == 0) mybits |= 1u;
+    const int pc = __builtin_popcount(mybits);
+    int incl = pc;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) rank_scan[wave] = incl;
+    __syncthreads();
+    int before = incl - pc;
+    for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
+    __syncthreads();  // rank_scan is reused by the next tile
+    int rank = rA[u] - at_start + before;
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if ((mybits >> k) & 1u) {
+        ++rank;
+        const DD p = dd_add(off, DD{lp[k], PR ? ll[PR ? k : 0] : 0.0});
+        lv[2 * rank] = p.hi;
+        lv[2 * rank + 1] = p.lo;
+      }
+    }
+    if (tile == a.tpr - 1 && tid == 0) {  // the row's end point: the last vertex
+      const int last = cntu[u] - 1;
+      lv[2 * last] = total.hi;
+      lv[2 * last + 1] = total.lo;
+    }
   }
 }
 
@@ -352,12 +412,13 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.gp = reinterpret_cast<double*>(base + gpn.off_gp);
   a.lv = reinterpret_cast<double*>(base + gpn.off_lv);
   const unsigned tiles = static_cast<unsigned>(in.batch * gpn.tpr);
+  const unsigned gsum_blocks = (tiles + kGsumTiles - 1) / kGsumTiles;
   if (in.dtype == TI_F32) {
-    if (W) gsum_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
-    else gsum_kernel<float, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    if (W) gsum_kernel<float, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+    else gsum_kernel<float, false><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
   } else {
-    if (W) gsum_kernel<double, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
-    else gsum_kernel<double, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    if (W) gsum_kernel<double, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+    else gsum_kernel<double, false><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
