@@ -70,16 +70,18 @@ def timed_calls(fn, steps: int, warmup: int) -> float:
 
 def event_ms(launch, reps: int) -> float:
     """Mean device time of `launch`: HIP events recorded on the launch stream right before and
-    after each call."""
+    after each call. The calls queue behind a few hundred microseconds of other device work, so
+    they run back to back and an interval does not take in the host's time between calls."""
     stream = torch.cuda.current_stream()
-    pairs = []
-    for _ in range(reps):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    busy = torch.empty(1 << 26, device="cuda")
+    sync()
+    for _ in range(6):
+        busy.mul_(1.0)
+    for e0, e1 in pairs:
         e0.record(stream)
         launch()
         e1.record(stream)
-        pairs.append((e0, e1))
     sync()
     return float(np.mean([a.elapsed_time(b) for a, b in pairs]))
 
