@@ -12,9 +12,10 @@
 //                  is already convex moves nothing; a bridge moves the right part's surviving
 //                  suffix down. Works in LDS when the children's vertices fit (the case for
 //                  noisy data, where hulls are small), else in the parent's own global array.
-//   expand_kernel  per tile of the row: the final hull's vertices around the tile (a 256-ary
-//                  search), edge slopes in float64 rounded once, every element the slope of its
-//                  edge with the clamp fused, and the start bits. y is not read again.
+//   expand_kernel  per tile of the row (four to a workgroup): the final hull's vertices around
+//                  the tile (ranks from rank_kernel), edge slopes in float64 rounded once, every
+//                  element the slope of its edge with the clamp fused, and the start bits. y is
+//                  not read again.
 #include "ti_common.h"
 #include "ti_kernels.h"
 #include "ti_slots.h"
@@ -388,33 +389,53 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
 
 // Per expansion tile of tile_n elements (one thread each): the final hull's last vertex at or
 // before the tile's first element, and its first vertex at or after the tile's end, by binary
-// searches over the row's hull (which runs from index 0 to n). All tiles search at once, so the
-// expansion and the backward start from two loads.
-__global__ __launch_bounds__(256) void rank_kernel(const void* hulls, int64_t batch, int64_t cap, bool weighted,
-                                                   int64_t n, int64_t tile_n, int64_t tpr, int* rank) {
+// searches over the row's hull (which runs from index 0 to n), with the row's flags and, where
+// one edge covers the tile, its slope. All tiles search at once, so the expansion and the
+// backward start from one read per tile.
+template <bool W>
+__global__ __launch_bounds__(256) void rank_kernel(const void* hulls, int64_t batch, int64_t cap, int64_t n,
+                                                   int64_t tile_n, int64_t tpr, TileRec* tiles) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (g >= batch * tpr) return;
   const int64_t row = g / tpr;
   const int64_t ta = (g - row * tpr) * tile_n;
   const int64_t tb = min(ta + tile_n, n);
-  const NodeOut fin = node_out(const_cast<void*>(hulls), batch, cap, weighted, row);
+  const NodeOut fin = node_out(const_cast<void*>(hulls), batch, cap, W, row);
   const int* idx = fin.idx;
   const int count = *fin.count;
+  const bool bad = *fin.bad != 0;
+  TileRec r;
   int lo = 0, hi = count - 1;  // idx[0] = 0 <= ta
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (idx[mid] <= ta) lo = mid;
     else hi = mid - 1;
   }
-  rank[2 * g] = lo;
+  r.ra = lo;
   hi = count - 1;  // idx[count - 1] = n >= tb
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     if (idx[mid] >= tb) hi = mid;
     else lo = mid + 1;
   }
-  rank[2 * g + 1] = lo;
+  r.rb = lo;
+  r.last = count - 1;
+  const bool head = bad ? ta == 0 : idx[r.ra] == ta;
+  r.flags = (bad ? kTileBad : 0) | (head ? kTileHead : 0);
+  r.slope = 0.0;
+  r.unused = 0.0;
+  if (!bad && r.rb == r.ra + 1) {
+    const VArr v = dvarr_of(fin);
+    double dW, dS;
+    vdiff<W>(vload<W>(v, r.ra), vload<W>(v, r.ra + 1), dW, dS);
+    r.slope = slope_div(dS, dW);
+  }
+  tiles[g] = r;
 }
+
+// Tiles per expansion workgroup: their records are read together, so a workgroup waits for one
+// memory round trip, not one per tile.
+constexpr int kExpandTiles = 4;
 
 // Per tile: the fit from the row's final hull.
 template <typename T, bool W>
@@ -422,101 +443,117 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
   constexpr int NT = C::kThreads;
+  constexpr int K = kExpandTiles;
   __shared__ T sl[C::kN + 2];  // sgn * slope per edge, rounded once to T
   __shared__ uint32_t bits[C::kN / 32];
   __shared__ int rank_scan[kWaves256];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const int64_t row = blockIdx.x / a.tiles_per_row;
-  const int64_t tile = blockIdx.x - row * a.tiles_per_row;
-  const int64_t first = tile * C::kN;
-  const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
-  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row);
-  const VArr v = dvarr_of(fin);
-  const int count = *fin.count;
-  const bool row_bad = *fin.bad != 0;
-  const int ta = static_cast<int>(first);
+  const int64_t ntiles = a.batch * a.tiles_per_row;
+  const int64_t blk0 = static_cast<int64_t>(blockIdx.x) * K;
   const T tsgn = static_cast<T>((a.flags & TI_INCREASING) ? 1.0 : -1.0);
-
-  // the vertex ranks around the tile, written by the last merge
-  const int rA = a.tile_rank[2 * blockIdx.x];
-  int rB = a.tile_rank[2 * blockIdx.x + 1];
-  // (both hold for any well-formed hull; they keep sl[] and the vertex reads in bounds regardless)
-  rB = min(min(rB, rA + C::kN + 1), count - 1);
-
-  const int t0 = tid * E;
-  const int ecount = max(0, min(E, len - t0));
   const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
   const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
-  T* out = static_cast<T*>(a.out) + row * a.n + first;
+  const int t0 = tid * E;
   const int64_t wpr = (a.n + 31) / 32;
-  auto write_starts = [&](uint32_t sb) {
-    if (a.starts == nullptr || ecount <= 0) return;
-    if (ecount < E) sb &= (1u << ecount) - 1u;
-    if constexpr (E == 16) {
-      uint16_t* s16 = reinterpret_cast<uint16_t*>(a.starts + row * wpr);
-      s16[(first + t0) >> 4] = static_cast<uint16_t>(sb);
-    } else {
-      uint8_t* s8 = reinterpret_cast<uint8_t*>(a.starts + row * wpr);
-      s8[(first + t0) >> 3] = static_cast<uint8_t>(sb);
-    }
-  };
 
-  if (rB == rA + 1) {
-    // One hull edge covers the whole tile (the common case on long rows, whose hulls have far
-    // fewer vertices than tiles): every thread forms its slope, no LDS, no barriers. The only
-    // possible start is the tile's first element, where vertex rA may sit.
-    const VPt p = vload<W>(v, rA), q = vload<W>(v, rA + 1);
-    double dW, dS;
-    vdiff<W>(p, q, dW, dS);
-    const T val = row_bad ? quiet_nan<T>() : tsgn * static_cast<T>(slope_div(dS, dW));
-    const T f = clip(val, use_lo, lo, use_hi, hi);
+  // each tile's row and place in it: one division, then steps (a 64-bit division by a runtime
+  // value is a long scalar sequence)
+  int64_t rowu[K], tileu[K];
+  {
+    int64_t row = blk0 / a.tiles_per_row, tile = blk0 - row * a.tiles_per_row;
+#pragma unroll
+    for (int u = 0; u < K; ++u) {
+      rowu[u] = row;
+      tileu[u] = tile;
+      if (++tile == a.tiles_per_row && row + 1 < a.batch) {
+        tile = 0;
+        ++row;
+      }
+    }
+  }
+  // every tile's record first: one memory round trip for the workgroup
+  TileRec rec[K];
+#pragma unroll
+  for (int u = 0; u < K; ++u) rec[u] = a.tiles[min(blk0 + u, ntiles - 1)];
+
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+    const int64_t blk = blk0 + u;
+    if (blk >= ntiles) break;
+    const int64_t row = rowu[u];
+    const int64_t tile = tileu[u];
+    const int64_t first = tile * C::kN;
+    const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
+    const bool row_bad = (rec[u].flags & kTileBad) != 0;
+    const int ta = static_cast<int>(first);
+    const int rA = rec[u].ra;
+    const int ecount = max(0, min(E, len - t0));
+    T* out = static_cast<T*>(a.out) + row * a.n + first;
+    auto write_starts = [&](uint32_t sb) {
+      if (a.starts == nullptr || ecount <= 0) return;
+      if (ecount < E) sb &= (1u << ecount) - 1u;
+      if constexpr (E == 16) {
+        uint16_t* s16 = reinterpret_cast<uint16_t*>(a.starts + row * wpr);
+        s16[(first + t0) >> 4] = static_cast<uint16_t>(sb);
+      } else {
+        uint8_t* s8 = reinterpret_cast<uint8_t*>(a.starts + row * wpr);
+        s8[(first + t0) >> 3] = static_cast<uint8_t>(sb);
+      }
+    };
+
+    if (rec[u].rb == rA + 1) {
+      // One hull edge covers the whole tile (the common case on long rows, whose hulls have far
+      // fewer vertices than tiles): the edge's slope from the record, no LDS, no barriers. The
+      // only possible start is the tile's first element.
+      const T val = row_bad ? quiet_nan<T>() : tsgn * static_cast<T>(rec[u].slope);
+      fill_elems<T, E, NT>(out, len, tid, clip(val, use_lo, lo, use_hi, hi));
+      write_starts((t0 == 0 && (rec[u].flags & kTileHead)) ? 1u : 0u);
+      continue;
+    }
+    const VArr v = dvarr_of(node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row));
+    // (holds for any well-formed hull; it keeps the reads in bounds regardless)
+    const int rB = min(min(rec[u].rb, rA + C::kN + 1), rec[u].last);
+
+    // Edge slopes rA .. rB-1 and the vertex bits of the tile.
+    for (int wd = tid; wd < C::kN / 32; wd += NT) bits[wd] = 0u;
+    __syncthreads();
+    for (int e = rA + tid; e < rB; e += NT) {
+      const VPt p = vload<W>(v, e), q = vload<W>(v, e + 1);
+      double dW, dS;
+      vdiff<W>(p, q, dW, dS);
+      sl[e - rA] = tsgn * static_cast<T>(slope_div(dS, dW));
+      if (p.i >= ta) atomicOr(&bits[(p.i - ta) >> 5], 1u << ((p.i - ta) & 31));
+    }
+    __syncthreads();
+    uint32_t mybits;
+    if constexpr (E == 16) mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFFFu;
+    else mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFu;
+    const int pc = __builtin_popcount(mybits);
+    int incl = pc;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) rank_scan[wave] = incl;
+    __syncthreads();
+    int before = incl - pc;
+    for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
+    const int at_start = (v.idx[rA] == ta) ? 1 : 0;
+    int jj = before + static_cast<int>(mybits & 1u) - at_start;
     T fit[E];
 #pragma unroll
-    for (int k = 0; k < E; ++k) fit[k] = f;
+    for (int k = 0; k < E; ++k) {
+      if (k > 0) jj += (mybits >> k) & 1u;
+      const T val = row_bad ? quiet_nan<T>() : sl[jj];
+      fit[k] = clip(val, use_lo, lo, use_hi, hi);
+    }
     store_elems_any<T, E>(out + t0, ecount, fit);
-    const bool head = row_bad ? (first + t0 == 0) : (t0 == 0 && p.i == ta);
-    write_starts(head ? 1u : 0u);
-    return;
+    write_starts(row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits);
+    __syncthreads();  // sl, bits and rank_scan are reused by the next tile
   }
-
-  // Edge slopes rA .. rB-1 and the vertex bits of the tile.
-  for (int wd = tid; wd < C::kN / 32; wd += NT) bits[wd] = 0u;
-  __syncthreads();
-  for (int e = rA + tid; e < rB; e += NT) {
-    const VPt p = vload<W>(v, e), q = vload<W>(v, e + 1);
-    double dW, dS;
-    vdiff<W>(p, q, dW, dS);
-    sl[e - rA] = tsgn * static_cast<T>(slope_div(dS, dW));
-    if (p.i >= ta) atomicOr(&bits[(p.i - ta) >> 5], 1u << ((p.i - ta) & 31));
-  }
-  __syncthreads();
-  uint32_t mybits;
-  if constexpr (E == 16) mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFFFu;
-  else mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFu;
-  const int pc = __builtin_popcount(mybits);
-  int incl = pc;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
-  if (lane == kWave - 1) rank_scan[wave] = incl;
-  __syncthreads();
-  int before = incl - pc;
-  for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
-  const int at_start = (v.idx[rA] == ta) ? 1 : 0;
-  int jj = before + static_cast<int>(mybits & 1u) - at_start;
-  T fit[E];
-#pragma unroll
-  for (int k = 0; k < E; ++k) {
-    if (k > 0) jj += (mybits >> k) & 1u;
-    const T val = row_bad ? quiet_nan<T>() : sl[jj];
-    fit[k] = clip(val, use_lo, lo, use_hi, hi);
-  }
-  store_elems_any<T, E>(out + t0, ecount, fit);
-  write_starts(row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits);
 }
 
 }  // namespace
@@ -550,7 +587,7 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
   p.off_buf[0] = 0;
   p.off_buf[1] = align256(buf[0]);
   p.off_rank = p.off_buf[1] + align256(buf[1]);
-  p.bytes = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * 8);
+  p.bytes = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
   return p;
 }
 
@@ -601,9 +638,15 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   }
   {
     const int64_t tiles = t.batch * p.tiles_per_row;
-    rank_kernel<<<dim3(static_cast<unsigned>((tiles + 255) / 256)), dim3(256), 0, t.stream>>>(
-        base + p.off_buf[p.levels & 1], t.batch, p.cap[p.levels], W, t.n, tile_elems(W), p.tiles_per_row,
-        reinterpret_cast<int*>(base + p.off_rank));
+    const dim3 grid(static_cast<unsigned>((tiles + 255) / 256));
+    TileRec* recs = reinterpret_cast<TileRec*>(base + p.off_rank);
+    if (W) {
+      rank_kernel<true><<<grid, dim3(256), 0, t.stream>>>(base + p.off_buf[p.levels & 1], t.batch,
+                                                         p.cap[p.levels], t.n, tile_elems(W), p.tiles_per_row, recs);
+    } else {
+      rank_kernel<false><<<grid, dim3(256), 0, t.stream>>>(base + p.off_buf[p.levels & 1], t.batch,
+                                                          p.cap[p.levels], t.n, tile_elems(W), p.tiles_per_row, recs);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -615,11 +658,11 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   x.tiles_per_row = p.tiles_per_row;
   x.out = t.out;
   x.starts = t.starts;
-  x.tile_rank = reinterpret_cast<int*>(base + p.off_rank);
+  x.tiles = reinterpret_cast<const TileRec*>(base + p.off_rank);
   x.flags = t.flags;
   x.lo = t.lo;
   x.hi = t.hi;
-  const unsigned grid = static_cast<unsigned>(t.batch * p.tiles_per_row);
+  const unsigned grid = static_cast<unsigned>((t.batch * p.tiles_per_row + kExpandTiles - 1) / kExpandTiles);
   if (t.dtype == TI_F32) {
     if (W) expand_kernel<float, true><<<dim3(grid), dim3(256), 0, t.stream>>>(x);
     else expand_kernel<float, false><<<dim3(grid), dim3(256), 0, t.stream>>>(x);

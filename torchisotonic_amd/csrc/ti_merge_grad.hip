@@ -64,7 +64,7 @@ struct GradKArgs {
   unsigned flags;
   double lo, hi;
   const void* hulls;     // the forward's final node array
-  const int* tile_rank;  // the forward's per-tile ranks (rA, rB)
+  const TileRec* tiles;  // the forward's per-tile records
   double* tg;            // [batch * tpr][2]: tile totals of g
   double* lp;            // [batch * tpr][2]: exclusive prefix within the tile's group
   double* gt;            // [batch * ngroups][2]: group totals
@@ -133,31 +133,46 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   const int64_t gt0 = static_cast<int64_t>(blockIdx.x) * kGsumTiles;
   const int t0 = tid * E;
   // every tile's loads first (a tile's own small reads would each cost a memory round trip):
-  // g, the tile's ranks, its row's NaN flag and vertex count, and whether a vertex starts it
+  // g and the tile's record (the hull's ranks around it, the row's NaN flag and last vertex,
+  // whether a vertex starts it)
   T gv[kGsumTiles][E];
-  int rA[kGsumTiles], rB[kGsumTiles], badu[kGsumTiles], cntu[kGsumTiles], head[kGsumTiles];
+  int rA[kGsumTiles], rB[kGsumTiles], badu[kGsumTiles], lastu[kGsumTiles], head[kGsumTiles];
+  // each tile's row and place in it: one division, then steps (a 64-bit division by a runtime
+  // value is a long scalar sequence)
+  int64_t rowu[kGsumTiles], tileu[kGsumTiles];
+  {
+    int64_t row = gt0 / a.tpr, tile = gt0 - row * a.tpr;
+#pragma unroll
+    for (int u = 0; u < kGsumTiles; ++u) {
+      rowu[u] = row;
+      tileu[u] = tile;
+      if (++tile == a.tpr && row + 1 < a.batch) {
+        tile = 0;
+        ++row;
+      }
+    }
+  }
 #pragma unroll
   for (int u = 0; u < kGsumTiles; ++u) {
     const int64_t gt = min(gt0 + u, ntiles - 1);
-    const int64_t row = gt / a.tpr;
-    const int64_t tile = gt - row * a.tpr;
+    const int64_t row = rowu[u];
+    const int64_t tile = tileu[u];
     const int64_t first = tile * C::kN;
     const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
     load_elems_any<T, E>(static_cast<const T*>(a.g) + row * a.n + first + t0, max(0, min(E, len - t0)), gv[u]);
-    rA[u] = a.tile_rank[2 * gt];
-    rB[u] = a.tile_rank[2 * gt + 1];
-    const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
-    badu[u] = *fin.bad;
-    cntu[u] = *fin.count;
-    const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
-    head[u] = tile == 0 ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1));
+    const TileRec rec = a.tiles[gt];
+    rA[u] = rec.ra;
+    rB[u] = rec.rb;
+    badu[u] = rec.flags & kTileBad;
+    lastu[u] = rec.last;
+    head[u] = (rec.flags & kTileHead) ? 1 : 0;
   }
 #pragma unroll
   for (int u = 0; u < kGsumTiles; ++u) {
     const int64_t gt = gt0 + u;
     if (gt >= ntiles) break;
-    const int64_t row = gt / a.tpr;
-    const int64_t tile = gt - row * a.tpr;
+    const int64_t row = rowu[u];
+    const int64_t tile = tileu[u];
     const int64_t first = tile * C::kN;
     const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
     const int ecount = max(0, min(E, len - t0));
@@ -188,7 +203,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
             lv[2 * rA[u] + 1] = 0.0;
           }
           if (tile == a.tpr - 1) {
-            const int last = cntu[u] - 1;
+            const int last = lastu[u];
             lv[2 * last] = total.hi;
             lv[2 * last + 1] = total.lo;
           }
@@ -231,7 +246,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
       }
     }
     if (tile == a.tpr - 1 && tid == 0) {  // the row's end point: the last vertex
-      const int last = cntu[u] - 1;
+      const int last = lastu[u];
       lv[2 * last] = total.hi;
       lv[2 * last + 1] = total.lo;
     }
@@ -305,8 +320,9 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   const int t0 = tid * E;
   const int ecount = max(0, min(E, len - t0));
   const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
-  const bool bad = *fin.bad != 0;
-  const int count = *fin.count;
+  const TileRec rec = a.tiles[blockIdx.x];
+  const bool bad = (rec.flags & kTileBad) != 0;
+  const int count = rec.last + 1;
   const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
   const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
   // the forward's hull is of sgn * y: its slopes are sgn * fit
@@ -322,7 +338,7 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
     DD p = dd_add(DD{gp[2 * grp], gp[2 * grp + 1]}, DD{lpr[2 * tl], lpr[2 * tl + 1]});
     return dd_add(p, DD{lv[2 * r], lv[2 * r + 1]});
   };
-  int rA = a.tile_rank[2 * blockIdx.x], rB = a.tile_rank[2 * blockIdx.x + 1];
+  const int rA = rec.ra, rB = rec.rb;
   if (bad) {  // one block over the whole row, fit NaN
     if (tid == 0) {
       const DD gtot{gp[2 * a.ngroups], gp[2 * a.ngroups + 1]};
@@ -361,7 +377,7 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   __syncthreads();
   int before = incl - pc;
   for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
-  const int at_start = bad ? 0 : ((tile == 0) ? 1 : static_cast<int>(tile_bits(srow, static_cast<int>(first), 1)));
+  const int at_start = bad ? 0 : ((rec.flags & kTileHead) ? 1 : 0);
   int jj = bad ? 0 : before + static_cast<int>(mybits & 1u) - at_start;
   T wv[W ? E : 1], yv[E];
   const bool need_y = a.gw != nullptr;
@@ -405,7 +421,7 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.lo = in.lo;
   a.hi = in.hi;
   a.hulls = fbase + p.off_buf[p.levels & 1];
-  a.tile_rank = reinterpret_cast<const int*>(fbase + p.off_rank);
+  a.tiles = reinterpret_cast<const TileRec*>(fbase + p.off_rank);
   a.tg = reinterpret_cast<double*>(base + gpn.off_tg);
   a.lp = reinterpret_cast<double*>(base + gpn.off_lp);
   a.gt = reinterpret_cast<double*>(base + gpn.off_gt);

@@ -147,6 +147,33 @@ __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, co
   }
 }
 
+// Fills p[0, len) with f from the NT threads of a workgroup, each store instruction of a wave on
+// one contiguous run of 16-byte pieces (len <= NT * E). The elements before the first 16-byte
+// boundary are written singly.
+template <typename T, int E, int NT>
+__device__ __forceinline__ void fill_elems(T* __restrict__ p, int len, int tid, T f) {
+  constexpr int V = 16 / sizeof(T);
+  using VT = T __attribute__((ext_vector_type(V)));
+  const int head = min(len, static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / sizeof(T)));
+  if (tid < head) p[tid] = f;
+  T* __restrict__ q = p + head;
+  const int rest = len - head;
+  VT x;
+#pragma unroll
+  for (int t = 0; t < V; ++t) x[t] = f;
+#pragma unroll
+  for (int j = 0; j < E / V; ++j) {
+    const int k = (j * NT + tid) * V;
+    if (k + V <= rest) {
+      *reinterpret_cast<VT*>(q + k) = x;
+    } else {
+#pragma unroll
+      for (int t = 0; t < V; ++t)
+        if (k + t < rest) q[k + t] = f;
+    }
+  }
+}
+
 // A hull point of the long-row kernels: index (relative to its node's first element), and
 // cumulative w*y (s) and w (w; unweighted rows use the index) relative to the node's first point.
 // Float64 data also carries the sums' rounding errors (sl, wl), zero for float32 data.
@@ -195,18 +222,34 @@ struct MergeArgs {
   int64_t child_elems;  // elements per child node
 };
 
+// Per tile of a long row, written by rank_kernel once the row's final hull is known: the hull's
+// vertex ranks around the tile and, for the common case of one hull edge over the whole tile
+// (rb == ra + 1 on a row without NaN), that edge's slope, so that the expansion and the
+// backward start from one 32-byte read per tile.
+struct alignas(32) TileRec {
+  int ra;        // the last vertex at or before the tile's first element
+  int rb;        // the first vertex at or after the tile's end
+  int flags;     // kTileBad | kTileHead
+  int last;      // the row's last vertex (vertex count - 1)
+  double slope;  // dS / dW of the edge ra -> ra + 1, float64 from the double-double sums
+  double unused;
+};
+constexpr int kTileBad = 1;   // the row holds a NaN (its fit is NaN throughout)
+constexpr int kTileHead = 2;  // a block starts at the tile's first element: a vertex sits there
+                              // (on a NaN row: the tile is the row's first)
+
 struct ExpandArgs {
   const void* hulls;  // final node array: one node per row
   int64_t batch, cap, n, tiles_per_row;
   void* out;
   uint32_t* starts;
-  const int* tile_rank;  // per tile: the final hull's vertex ranks around it (rank_kernel's)
+  const TileRec* tiles;  // per tile (rank_kernel's)
   unsigned flags;
   double lo, hi;
 };
 
 // Workspace of a long-row fit: two node arrays used in turn by the span hulls and the merge
-// levels (the final hulls end in buffer levels & 1), and the per-tile ranks of the expansion.
+// levels (the final hulls end in buffer levels & 1), and the per-tile records of the expansion.
 struct LongPlan {
   int64_t tiles_per_row;  // expansion (and backward) tiles
   int64_t span0;          // elements per span (the first node level)
