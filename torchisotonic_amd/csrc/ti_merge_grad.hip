@@ -178,18 +178,17 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     const int ecount = max(0, min(E, len - t0));
     const int bad = badu[u];
     double* lv = a.lv + 2 * row * a.cap_final;
-    double lp[E];
-    double ll[PR ? E : 1];
-    DD acc{0.0, 0.0};
-#pragma unroll
-    for (int k = 0; k < E; ++k) {
-      lp[k] = acc.hi;
-      if constexpr (PR) ll[k] = acc.lo;
+    // the thread's sum; its prefixes are formed again, in the same order, where a vertex needs
+    // one (keeping them would hold E more float64 registers through the tile)
+    auto add = [&](DD& acc, int k) {
       if (k < ecount) {
         if constexpr (PR) acc = dd_add(acc, static_cast<double>(gv[u][k]));
         else acc.hi += static_cast<double>(gv[u][k]);
       }
-    }
+    };
+    DD acc{0.0, 0.0};
+#pragma unroll
+    for (int k = 0; k < E; ++k) add(acc, k);
     if (bad || rB[u] == rA[u] + 1) {
       // no vertex inside the tile (the common case on long rows): its total, a zero prefix for
       // a vertex at its first element, and on the row's last tile the row's end point
@@ -236,14 +235,16 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
     __syncthreads();  // rank_scan is reused by the next tile
     int rank = rA[u] - at_start + before;
+    DD run{0.0, 0.0};
 #pragma unroll
     for (int k = 0; k < E; ++k) {
       if ((mybits >> k) & 1u) {
         ++rank;
-        const DD p = dd_add(off, DD{lp[k], PR ? ll[PR ? k : 0] : 0.0});
+        const DD p = dd_add(off, DD{run.hi, PR ? run.lo : 0.0});
         lv[2 * rank] = p.hi;
         lv[2 * rank + 1] = p.lo;
       }
+      add(run, k);
     }
     if (tile == a.tpr - 1 && tid == 0) {  // the row's end point: the last vertex
       const int last = lastu[u];

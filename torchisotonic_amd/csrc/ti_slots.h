@@ -3,15 +3,17 @@
 // the span kernel (its lanes' own hulls).
 //
 // A round merges hull pairs (L, R) that share their boundary point q, L's last vertex and R's
-// first; the parent keeps a prefix of L and a suffix of R (the bridge). Per pair, one thread
-// tests q and, if it dies, walks outwards from it: drop L's end vertex while the hull does not
-// turn left there, else R's first, until both ends are convex (reference src/torchisotonic/csrc/
-// tiles.cuh:1524-1537 merges segment pairs through the same bridge). The arrays are compact, so
-// a step is two reads at known addresses. Noisy hulls lose a few vertices a merge; a walk still
-// going after kWalk steps hands over to every thread at once: each remaining vertex of L decides
-// whether it stays (its slope in below its lowest slope out to R, whose contact point a binary
-// search over R finds), likewise R's, and the pair's first dying slot of L and last of R fix the
-// bridge. The survivors then move down in one ordered compaction.
+// first; the parent keeps a prefix of L and a suffix of R (the bridge). Per pair, a group of S
+// lanes tests q and, if it dies, walks outwards from it (reference src/torchisotonic/csrc/
+// tiles.cuh:1524-1537 merges segment pairs through the same bridge): with L's end vertex a and
+// R's first b, lane k tests L's k-th vertex from the end against b and R's k-th from the start
+// against a, and each side drops its vertices up to the first that stays (along a convex chain
+// the test holds for a run from the end and then fails), until a step drops nothing: then both
+// ends are convex, the bridge. The arrays are compact, so a step is one round of reads at known
+// addresses. A walk still going after kWalk steps hands over to every thread at once: each
+// remaining vertex of L decides whether it stays (its slope in below its lowest slope out to R,
+// whose contact point a binary search over R finds), likewise R's, and the pair's first dying
+// slot of L and last of R fix the bridge. The survivors then move down in one ordered compaction.
 #pragma once
 
 #include "ti_tile.h"
@@ -89,7 +91,7 @@ struct MergeRounds {
   int jdead[kGroup / 2];
   double edge[kGroup / 2][4];
   int walk[kGroup / 2][2];  // where a pair's walk stopped: L's and R's current end vertices
-  int flag[2];              // some junction died; some walk did not finish
+  int wflag[16];            // per wave: bit 0 some junction died, bit 1 some walk did not finish
   int wsum[4][16];
 };
 
@@ -133,7 +135,13 @@ __device__ __forceinline__ bool hpools_nb(const HPt& a, const HPt& b, const HPt&
 // above that edge's line, so no slope from the vertex to R is lower), R every vertex whose slope
 // out is above L's last edge. By convexity those are all but a suffix of L and a prefix of R,
 // the only vertices that search.
-constexpr int kWalk = 16;
+constexpr int kWalk = 8;
+
+// The number of leading ones of the S-bit group g.
+__device__ __forceinline__ int lead_ones(uint64_t g, uint64_t gmask, int S) {
+  const uint64_t z = ~g & gmask;
+  return z ? __builtin_ctzll(z) : S;
+}
 
 template <bool W, bool PR, int NT, int G>
 __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, int nch) {
@@ -148,36 +156,49 @@ __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, i
     const int npair = nseg >> 1;
     const int* se = rs.seg[cur];
     int* sn = rs.seg[cur ^ 1];
-    // 1. per pair (a thread each: there are at most 32): the junction, and from a dying
-    // junction the two-sided walk outwards (drop L's end while the hull does not turn left there,
-    // else R's, until both ends are convex: the bridge), one removed vertex a step, for at most
-    // kWalk steps
-    if (tid < kWave) {
-      const bool has = tid < npair;
-      const int p = has ? tid : 0;
+    // 1. per pair (a group of S lanes each, the at most 32 pairs spread over the waves): the
+    // junction, and from a dying junction the walk outwards, for at most kWalk steps
+    {
+      const int per_wave = (npair + NW - 1) / NW;
+      int lg_ppw = 0;
+      while ((1 << lg_ppw) < per_wave) ++lg_ppw;
+      const int lg_s = 6 - lg_ppw;  // S = 64 / (pairs per wave), at least 2
+      const int S = 1 << lg_s;
+      const int sub = lane >> lg_s, k = lane & (S - 1);
+      const int p_raw = (wave << lg_ppw) + sub;
+      const bool has = p_raw < npair;
+      const int p = has ? p_raw : 0;
+      const uint64_t gmask = S == 64 ? ~uint64_t{0} : ((uint64_t{1} << S) - 1);
+      const int gshift = sub << lg_s;
       const int q = se[2 * p];
       const int lo_l = p > 0 ? se[max(2 * p - 1, 0)] : 0;
       const int hi_r = se[2 * p + 1];
-      HPt A = sget(v, q - 1), B = sget(v, q + 1);
-      const HPt Q = sget(v, q);
       double dSl, dWl, dSr, dWr;
-      hdiff<W, PR>(A, Q, dSl, dWl);
-      hdiff<W, PR>(Q, B, dSr, dWr);
+      {
+        const HPt A = sget(v, q - 1), Q = sget(v, q), B = sget(v, q + 1);
+        hdiff<W, PR>(A, Q, dSl, dWl);
+        hdiff<W, PR>(Q, B, dSr, dWr);
+      }
       const bool dead = has & pools_nb(dSl, dWl, dSr, dWr);
       int ia = q - 1, ib = q + 1;
       bool walking = dead;
-      for (int k = 0; k < kWalk; ++k) {
+      for (int it = 0; it < kWalk; ++it) {
         if (!__any(walking)) break;
-        const HPt AP = sget(v, max(ia - 1, lo_l)), BN = sget(v, min(ib + 1, hi_r));
-        const bool popL = walking & (ia > lo_l) & hpools_nb<W, PR>(AP, A, B);
-        const bool popR = walking & !popL & (ib < hi_r) & hpools_nb<W, PR>(A, B, BN);
-        walking = popL | popR;
-        ia -= popL ? 1 : 0;
-        ib += popR ? 1 : 0;
-        A = hsel(popL, AP, A);
-        B = hsel(popR, BN, B);
+        // every read of the step first: both ends, lane k's L vertex (and the one before it)
+        // and R vertex (and the one after it), indices clamped into the pair
+        const int xl = ia - k, xr = ib + k;
+        const HPt A = sget(v, ia), B = sget(v, ib);
+        const HPt XL = sget(v, max(xl, lo_l)), XLP = sget(v, max(xl - 1, lo_l));
+        const HPt XR = sget(v, min(xr, hi_r)), XRN = sget(v, min(xr + 1, hi_r));
+        const bool dl = walking & (xl > lo_l) & hpools_nb<W, PR>(XLP, XL, B);
+        const bool dr = walking & (xr < hi_r) & hpools_nb<W, PR>(A, XR, XRN);
+        const int ml = lead_ones(__ballot(dl) >> gshift, gmask, S);
+        const int mr = lead_ones(__ballot(dr) >> gshift, gmask, S);
+        ia -= ml;
+        ib += mr;
+        walking = walking & ((ml | mr) != 0);
       }
-      if (has) {
+      if (has && k == 0) {
         rs.jdead[p] = dead ? (walking ? 2 : 1) : 0;
         rs.fdl[p] = dead ? ia + 1 : 0x7FFFFFFF;
         rs.ldr[p] = dead ? ib - 1 : -1;
@@ -189,18 +210,18 @@ __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, i
         rs.edge[p][3] = dWr;
       }
       const bool anydead = __any(dead), more = __any(walking);
-      if (tid == 0) {
-        rs.flag[0] = anydead ? 1 : 0;
-        rs.flag[1] = more ? 1 : 0;
-      }
+      if (lane == 0) rs.wflag[wave] = (anydead ? 1 : 0) | (more ? 2 : 0);
     }
     __syncthreads();
+    int flags = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) flags |= rs.wflag[w2];
     // 2. the vertices near a dying junction. Straight-line code: every read has a valid
     // (clamped) index and results are selected, so the G slots' LDS reads overlap instead of each
     // waiting behind its own branch.
     static_assert(G >= 1 && G <= 4, "lockstep group of 1..4 slots");
 #pragma unroll 1
-    for (int g0 = 0; rs.flag[1] != 0 && g0 < total; g0 += NT * G) {
+    for (int g0 = 0; (flags & 2) != 0 && g0 < total; g0 += NT * G) {
       int sk[G], lo[G], hi[G], pk[G];
       bool left[G], need[G];
       HPt P[G], N[G];
@@ -285,7 +306,7 @@ __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, i
       }
     }
     __syncthreads();
-    if (rs.flag[0] == 0) {
+    if ((flags & 1) == 0) {
       // nothing died: nothing moves, and a merged pair ends where its right part did
       for (int k = tid; k < (nseg + 1) / 2; k += NT) sn[k] = se[min(2 * k + 1, nseg - 1)];
       __syncthreads();
