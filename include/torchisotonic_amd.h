@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 1
+#define TI_ABI_VERSION 2
 
 /* dtype codes */
 #define TI_F32 0
@@ -85,6 +85,18 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
 int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
            int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * ti_fwd, plus weights_read: a hipEvent_t (or NULL) that the call records on the stream as soon
+ * as every weight has been read, i.e. once *bad_weight is final. For rows longer than one tile
+ * that is after the first of the fit's several kernels, so a caller that must refuse
+ * non-positive weights before it returns (the reference checks them with a synchronous read of
+ * w before fitting, reference _api.py:60-61) waits on the event and reads bad_weight from
+ * another stream while the rest of the fit still runs. No other counterpart in the reference.
+ */
+int ti_fwd_ev(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+              int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+              void* workspace, size_t workspace_bytes, void* stream, void* weights_read);
 
 /* Bytes of device workspace ti_bwd needs for this problem set (0 when none). */
 int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes);

@@ -33,7 +33,7 @@ def gpu_fit(
     wt = None if w is None else torch.from_numpy(np.ascontiguousarray(w)).cuda()
     out, starts, bad, _ = _ext.fit(yt, wt, increasing, True, with_starts, y_min, y_max)
     if bad is not None:
-        assert int(bad.item()) == 0
+        assert bad is False
     s = None
     if with_starts:
         s = _ext.starts_to_bool(starts, *y.shape).cpu().numpy().astype(np.uint8)

@@ -134,6 +134,6 @@ def _solve(
     backward reads). Reference _api.py:118-134 without its CPU branch."""
     _ext._on_gpu(flat_y, "y")
     out, starts, bad, ws = _ext.fit(flat_y, flat_w, increasing, exact, with_starts, y_min, y_max)
-    if bad is not None and bool(bad.item()):
+    if bad:
         raise ValueError("weight must be strictly positive")
     return out, starts, ws

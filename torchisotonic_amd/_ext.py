@@ -13,13 +13,14 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import threading
 from pathlib import Path
 
 import torch
 from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -34,6 +35,7 @@ SYMBOLS = (
     "ti_starts_words",
     "ti_fwd_workspace",
     "ti_fwd",
+    "ti_fwd_ev",
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_starts_to_bool",
@@ -62,6 +64,8 @@ def load() -> ctypes.CDLL:
         fn.argtypes = [_i64, _i64, _int, _int, ctypes.POINTER(_sz)]
     lib.ti_fwd.restype = _int
     lib.ti_fwd.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_fwd_ev.restype = _int
+    lib.ti_fwd_ev.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp]
     lib.ti_bwd.restype = _int
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_starts_to_bool.restype = _int
@@ -154,6 +158,26 @@ def _flags(increasing: bool, exact: bool, y_min: float | None, y_max: float | No
     return f
 
 
+_local = threading.local()
+
+
+def _weight_check(device: torch.device) -> tuple[torch.cuda.Event, torch.cuda.Stream, Tensor]:
+    """Per thread and device: the event a weighted fit records once it has read every weight,
+    a side stream that copies the weight flag out after that event, and a pinned host word to
+    copy it into. The caller learns whether the weights were valid while the rest of its fit
+    still runs on the current stream."""
+    cache = getattr(_local, "weight_check", None)
+    if cache is None:
+        cache = _local.weight_check = {}
+    entry = cache.get(device.index)
+    if entry is None:
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(device))  # (torch creates the HIP event here)
+        entry = (event, torch.cuda.Stream(device), torch.zeros(1, dtype=torch.int32, pin_memory=True))
+        cache[device.index] = entry
+    return entry
+
+
 def fit(
     y: Tensor,
     w: Tensor | None,
@@ -165,9 +189,10 @@ def fit(
 ) -> tuple[Tensor, Tensor, Tensor | None, Tensor | None]:
     """The fit of every row of ``y`` ([batch, n], float32/float64, on the GPU), clamped to
     [y_min, y_max] where given; the packed partition (int32 words) if ``with_starts`` (else an
-    empty tensor); for weighted fits, a one-word device flag that is nonzero if some weight was
-    not positive (the caller checks it); and the workspace, which the backward of rows longer
-    than one tile reads (None when the fit needed none)."""
+    empty tensor); for weighted fits, whether some weight was not positive (the caller raises;
+    known once the kernels have read w, which for long rows is before the fit has finished),
+    else None; and the workspace, which the backward of rows longer than one tile reads (None
+    when the fit needed none)."""
     _on_gpu(y, "y")
     dtype = _dtype_code(y)
     if y.dim() != 2:
@@ -184,17 +209,25 @@ def fit(
         starts_words(batch, n) if with_starts else 0, dtype=torch.int32, device=y.device
     )
     bad = torch.zeros(1, dtype=torch.int32, device=y.device) if w is not None else None
+    args = (
+        batch, n, dtype, _flags(increasing, exact, y_min, y_max),
+        float(y_min) if y_min is not None else 0.0,
+        float(y_max) if y_max is not None else 0.0,
+    )
     with _on_device(y.device):
         ws = _workspace("fwd", batch, n, dtype, w is not None, y.device)
-        rc = load().ti_fwd(
-            _ptr(y), _ptr(w), _ptr(out), _ptr(starts) if with_starts else None, _ptr(bad),
-            batch, n, dtype, _flags(increasing, exact, y_min, y_max),
-            float(y_min) if y_min is not None else 0.0,
-            float(y_max) if y_max is not None else 0.0,
-            _ptr(ws), 0 if ws is None else ws.numel(), _stream(y),
-        )
-    _check(rc, "fit")
-    return out, starts, bad, ws
+        ws_args = (_ptr(ws), 0 if ws is None else ws.numel(), _stream(y))
+        ptrs = (_ptr(y), _ptr(w), _ptr(out), _ptr(starts) if with_starts else None, _ptr(bad))
+        if bad is None:
+            _check(load().ti_fwd(*ptrs, *args, *ws_args), "fit")
+            return out, starts, None, ws
+        event, side, host = _weight_check(y.device)
+        _check(load().ti_fwd_ev(*ptrs, *args, *ws_args, event.cuda_event), "fit")
+        side.wait_event(event)
+        with torch.cuda.stream(side):
+            host.copy_(bad, non_blocking=True)
+        side.synchronize()
+    return out, starts, bool(host.item()), ws
 
 
 def grad(
@@ -270,7 +303,7 @@ def isotonic_tiles(
     ([batch, n], on the GPU) in y's dtype, and if ``with_starts`` a bool tensor marking where
     its blocks start (else an empty one)."""
     out, starts, bad, _ = fit(y, w, increasing, exact, with_starts)
-    if bad is not None and bool(bad.item()):
+    if bad:
         raise ValueError("weight must be strictly positive")
     if not with_starts:
         return out, torch.empty(0, dtype=torch.bool, device=y.device)

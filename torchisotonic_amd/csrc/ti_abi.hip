@@ -79,25 +79,35 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   return ok();
 }
 
-int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
-           int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
-           void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// ti_fwd, recording weights_read (when given) on the stream once every weight has been read.
+int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+             int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+             void* workspace, size_t workspace_bytes, void* stream, hipEvent_t weights_read) {
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  // the one-kernel paths read the weights in their only kernel
+  auto then_record = [&](int rc) -> int {
+    if (rc != TI_OK || weights_read == nullptr) return rc;
+    return launched(hipEventRecord(weights_read, hs), "weights-read event");
+  };
   if (int rc = check_shape(batch, n, dtype)) return rc;
-  if (batch == 0) return ok();
+  if (batch == 0) return then_record(ok());
   if (y == nullptr || out == nullptr) return fail(TI_EINVAL, "y and out must not be null");
   if (out == y || (w != nullptr && out == w)) return fail(TI_EINVAL, "out must not alias y or w");
   if (n <= ti::kShortMax) {
     if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
-    ti::ShortArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
-                    static_cast<hipStream_t>(stream)};
-    return launched(ti::short_fit(a), "short-row fit");
+    ti::ShortArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
+    return then_record(launched(ti::short_fit(a), "short-row fit"));
   }
   const int64_t tn = ti::tile_elems(w != nullptr);
   if (n <= tn) {
     if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
     ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
-                   nullptr, 0, 0, static_cast<hipStream_t>(stream)};
-    return launched(ti::tile_run(a, ti::kTileSingle), "single-tile fit");
+                   nullptr, 0, 0, hs};
+    return then_record(launched(ti::tile_run(a, ti::kTileSingle), "single-tile fit"));
   }
   const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
   if (workspace == nullptr || workspace_bytes < plan.bytes)
@@ -105,8 +115,27 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspace must be 256-byte aligned");
   if (batch * plan.tiles_per_row > 0x7FFFFFFF) return fail(TI_ESIZE, "too many tiles");
   ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
-                 nullptr, 0, 0, static_cast<hipStream_t>(stream)};
+                 nullptr, 0, 0, hs};
+  a.weights_read = weights_read;  // after the span kernel, the first of several
   return launched(ti::long_fit(a, plan, workspace), "multi-tile fit");
+}
+
+}  // namespace
+
+extern "C" {
+
+int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+           int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+           void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, workspace,
+                  workspace_bytes, stream, nullptr);
+}
+
+int ti_fwd_ev(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+              int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+              void* workspace, size_t workspace_bytes, void* stream, void* weights_read) {
+  return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, workspace,
+                  workspace_bytes, stream, static_cast<hipEvent_t>(weights_read));
 }
 
 int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes) {

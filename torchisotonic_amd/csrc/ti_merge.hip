@@ -597,6 +597,8 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   // level 0: span hulls
   hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0, base + p.off_buf[1], p.cap[1]);
   if (e != hipSuccess) return e;
+  // the span kernel has read every weight (and set the flag if one is not positive)
+  if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
   for (int l = 1; l <= p.levels; ++l) {
     MergeArgs m;
     m.in = base + p.off_buf[(l - 1) & 1];

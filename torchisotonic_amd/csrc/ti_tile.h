@@ -40,6 +40,7 @@ struct TileArgs {
   int64_t tiles_total; // nodes in that array
   int64_t cap;         // vertex capacity per node
   hipStream_t stream;
+  hipEvent_t weights_read = nullptr;  // recorded once every weight has been read, if given
 };
 
 // One node's hull array in a node array of K nodes with `cap` vertices each: vertex indices
