@@ -49,19 +49,20 @@ struct SpanArgs {
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the chunk buffer (sums at
-// each point of the chunk) and the stack ring.
+// each point of the chunk) and the stack ring. Arrays a configuration does not use have no rows
+// (a zero-length array, which only code under a false `if constexpr` or condition names).
 template <typename T, bool W, int C, int R>
 struct SpanLds {
   static constexpr bool PR = sizeof(T) == 8;
   double cs[C][kSpanLanes];
-  double csl[PR ? C : 1][kSpanLanes];
-  double cw[W ? C : 1][kSpanLanes];
-  double cwl[W && PR ? C : 1][kSpanLanes];
+  double csl[PR ? C : 0][kSpanLanes];
+  double cw[W ? C : 0][kSpanLanes];
+  double cwl[W && PR ? C : 0][kSpanLanes];
   int ri[R][kSpanLanes];
   double rs[R][kSpanLanes];
-  double rsl[PR ? R : 1][kSpanLanes];
-  double rw[W ? R : 1][kSpanLanes];
-  double rwl[W && PR ? R : 1][kSpanLanes];
+  double rsl[PR ? R : 0][kSpanLanes];
+  double rw[W ? R : 0][kSpanLanes];
+  double rwl[W && PR ? R : 0][kSpanLanes];
 };
 
 // N consecutive values at byte offset `off` of a buffer resource, 16 bytes per load. Reads past
