@@ -283,14 +283,19 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     }
     // stack: t1 (last vertex) and t2 (< 0: none) with their sums and weights; the stack itself
     // is the mask m. The candidate being pushed is k; rest holds the candidates after it.
-    int t1 = 0, t2 = -1;
-    double s1 = 0.0, s2 = 0.0;
-    double w1 = 0.0, w2 = 0.0;
+    // The first candidate goes on the stack at once (with only point 0 below it there is
+    // nothing to test), which spares every lane the loop's first iteration.
     Mask rest = cand & ~Mask(1);
-    int k = lowest_bit(rest);  // point nn is always a candidate
+    int t1 = lowest_bit(rest);  // point nn is always a candidate
     rest &= rest - 1;
-    double sk = colS[k * THREADS + tid];
-    double wk = W ? colW[W ? k * THREADS + tid : 0] : static_cast<double>(k);
+    int t2 = 0;
+    double s1 = colS[t1 * THREADS + tid], s2 = 0.0;
+    double w1 = W ? colW[W ? t1 * THREADS + tid : 0] : static_cast<double>(t1), w2 = 0.0;
+    m |= Mask(1) << t1;
+    int k = rest ? lowest_bit(rest) : -1;
+    rest &= rest - 1;
+    double sk = colS[(k > 0 ? k : 0) * THREADS + tid];
+    double wk = W ? colW[W ? (k > 0 ? k : 0) * THREADS + tid : 0] : static_cast<double>(k);
     while (k >= 0) {
       bool pop = false;
       if constexpr (W) {
