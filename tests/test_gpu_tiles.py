@@ -320,3 +320,28 @@ def test_long_nan_row_gradients() -> None:
     np.testing.assert_allclose(gy[1:], ey, rtol=1e-10, atol=1e-12)
     (gy, gw), _ = gpu_grads(y, w, c, y_min=-0.5)
     assert (gy[0] == 0).all() and np.isnan(gw[0]).all()
+
+
+@pytest.mark.parametrize("n", [1000, 5000, 70_000])
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+def test_weight_check_every_path(n: int, dtype: str) -> None:
+    # a non-positive or NaN weight anywhere in a row of one tile or of several raises (the
+    # long-row forward returns once its first kernel has read w, before the fit is done), and a
+    # valid call right after is unaffected by the failed one
+    import torch
+
+    import torchisotonic_amd
+
+    print(f"weight check n={n} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(n)
+    y = torch.from_numpy(rng.standard_normal((2, n))).to(getattr(torch, dtype)).cuda()
+    good = torch.from_numpy(rng.random((2, n)) + 0.1).to(y.dtype).cuda()
+    for bad_value in (0.0, -2.0, float("nan")):
+        for row, col in ((0, 0), (1, n // 2), (1, n - 1)):
+            w = good.clone()
+            w[row, col] = bad_value
+            with pytest.raises(ValueError, match="strictly positive"):
+                torchisotonic_amd.isotonic(y, w)
+    got = torchisotonic_amd.isotonic(y, good).cpu().numpy()
+    want, _ = oracle.pava(y.cpu().double().numpy(), good.cpu().double().numpy())
+    assert np.abs(got - want).max() <= tolerance(y.cpu().numpy())
