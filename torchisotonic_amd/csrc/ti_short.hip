@@ -172,6 +172,19 @@ __device__ __forceinline__ int highest_bit(uint64_t v) { return 63 - __builtin_c
 // times the correctly rounded reciprocal of its length, in the forward and the backward alike.
 constexpr int kRcpN = 33;
 
+// 1/d for d = 1 .. kRcpN - 1, rounded once (by the compiler), so no kernel divides to build it.
+struct RcpTable {
+  double v[kRcpN];
+};
+
+constexpr RcpTable make_rcp_table() {
+  RcpTable t{};
+  for (int d = 1; d < kRcpN; ++d) t.v[d] = 1.0 / static_cast<double>(d);
+  return t;
+}
+
+__constant__ RcpTable kRcp = make_rcp_table();
+
 template <typename T, int NMAX, bool W, bool DIRECT, bool INC>
 __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
@@ -193,7 +206,7 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
   constexpr double sgn = INC ? 1.0 : -1.0;
   __shared__ double rcp[W ? 1 : kRcpN];
   if constexpr (!W) {
-    if (tid < kRcpN) rcp[tid] = tid > 0 ? 1.0 / static_cast<double>(tid) : 0.0;
+    if (tid < kRcpN) rcp[tid] = kRcp.v[tid];
   }
 
   T yv[NMAX];
@@ -343,14 +356,14 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     // every element's reads are independent), with mean (S_v - S_i) / (v - i); the others keep
     // the mean of the block they are in.
     const Mask mv = m | (Mask(1) << nn);  // (point nn is a vertex; idle threads set it here)
-    double cur = 0.0;
+    T cur = T(0);  // (rounded before the select: one register to carry, not two)
 #pragma unroll
     for (int i = 0; i < NMAX; ++i) {
       if (i < nn) {
         const int v = i + 1 + lowest_bit(static_cast<Mask>(mv >> (i + 1)));
         const double mean = (colS[v * THREADS + tid] - colS[i * THREADS + tid]) * rcp[v - i];
-        cur = ((m >> i) & 1u) ? mean : cur;
-        fit[i] = static_cast<T>(sgn * cur);
+        cur = ((m >> i) & 1u) ? static_cast<T>(sgn * mean) : cur;
+        fit[i] = cur;
       }
     }
   } else {
