@@ -123,3 +123,11 @@ def test_errors_are_per_thread() -> None:
     t.join()
     assert seen == [b""]
     assert b"dtype" in lib.ti_last_error()
+
+
+def test_operator_library_registers_the_fit() -> None:
+    # the torch operator over the C ABI loads without a GPU and has the documented schema
+    ops = _ext.ops()
+    schema = str(ops.isotonic_fit.default._schema)
+    assert schema.startswith("torchisotonic_amd::isotonic_fit(Tensor y, Tensor? w, bool increasing")
+    assert "float? y_min" in schema and "float? y_max" in schema and schema.endswith("-> Tensor")

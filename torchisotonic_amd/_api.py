@@ -5,7 +5,8 @@ A drop-in for ``torchisotonic.isotonic`` (reference src/torchisotonic/_api.py:13
 signature, argument checks and messages, dtype policy, ``dim`` handling, weight broadcasting
 and autograd behaviour. What differs inside: the clamp to ``[y_min, y_max]`` and its backward
 are fused into the kernels, the weights' positivity is checked by the forward kernel as it
-reads them (one read of ``w`` instead of two), and the backward does not read the fit: rows of
+reads them (one read of ``w`` instead of two), the autograd node is C++ (no Python, and no
+interpreter lock, in the backward), and the backward does not read the fit: rows of
 up to one tile recompute their block means from ``y`` and ``w``, longer rows take them from the
 final hulls the forward left in its workspace (kept on the autograd context). There is no CPU
 solver: tensors must be on a ROCm device (arguments are still validated first, so the
@@ -14,7 +15,6 @@ reference's error messages hold everywhere).
 
 from __future__ import annotations
 
-from typing import Any
 
 import torch
 from torch import Tensor
@@ -78,62 +78,9 @@ def isotonic(
     flat_w = None if w is None else w.reshape(-1, shape[-1])
     lo = None if y_min is None else float(y_min)
     hi = None if y_max is None else float(y_max)
-    out: Tensor = _Isotonic.apply(flat_y, flat_w, increasing, exact, lo, hi)
+    _ext._on_gpu(flat_y, "y")
+    # the clamped fit with its autograd node in C++ (csrc/ti_torch.cpp; the reference's Python
+    # autograd.Function, _api.py:73-97, plus torch.clamp's backward)
+    out: Tensor = _ext.ops().isotonic_fit(flat_y, flat_w, increasing, lo, hi)
     out = out.reshape(shape)
     return (out if last else out.movedim(-1, dim)).to(out_dtype)
-
-
-class _Isotonic(torch.autograd.Function):
-    """The clamped fit, with its gradient: the upstream gradient masked where the clamp
-    binds, then averaged over the fit's blocks (reference _api.py:73-97 plus torch.clamp's
-    backward)."""
-
-    @staticmethod
-    def forward(
-        ctx: Any,
-        flat_y: Tensor,
-        flat_w: Tensor | None,
-        increasing: bool,
-        exact: bool,
-        y_min: float | None,
-        y_max: float | None,
-    ) -> Tensor:
-        want = any(ctx.needs_input_grad[:2])
-        out, starts, ws = _solve(flat_y, flat_w, increasing, exact, want, y_min, y_max)
-        ctx.save_for_backward(flat_y, flat_w, starts)
-        ctx.bounds = (y_min, y_max)
-        ctx.increasing = increasing
-        ctx.fwd_ws = ws if want else None  # the final hulls of long rows, for the backward
-        return out
-
-    @staticmethod
-    def backward(ctx: Any, grad: Tensor) -> tuple[Tensor | None, Tensor | None, None, None, None, None]:
-        flat_y, flat_w, starts = ctx.saved_tensors
-        want_y, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        y_min, y_max = ctx.bounds
-        need_y = want_w or y_min is not None or y_max is not None
-        gy, gw = _ext.grad(
-            starts, ctx.fwd_ws, grad, flat_w, flat_y if need_y else None, want_y, want_w,
-            y_min, y_max, ctx.increasing,
-        )
-        return gy, gw, None, None, None, None
-
-
-def _solve(
-    flat_y: Tensor,
-    flat_w: Tensor | None,
-    increasing: bool,
-    exact: bool = True,
-    with_starts: bool = False,
-    y_min: float | None = None,
-    y_max: float | None = None,
-) -> tuple[Tensor, Tensor, Tensor | None]:
-    """The (clamped) fit of [batch, n] problems (n >= 1) in flat_y's dtype, by the HIP
-    kernels; if ``with_starts``, where its blocks start as a packed bit array (else an empty
-    tensor); and the fit's workspace (the final hulls of rows longer than one tile, which the
-    backward reads). Reference _api.py:118-134 without its CPU branch."""
-    _ext._on_gpu(flat_y, "y")
-    out, starts, bad, ws = _ext.fit(flat_y, flat_w, increasing, exact, with_starts, y_min, y_max)
-    if bad:
-        raise ValueError("weight must be strictly positive")
-    return out, starts, ws

@@ -1,5 +1,7 @@
 """The boundary to the HIP kernels: a ctypes binding of libtorchisotonic_amd.so (C ABI in
-include/torchisotonic_amd.h) and the tensor-level calls the rest of the package makes.
+include/torchisotonic_amd.h), the torch operator library over it (libtorchisotonic_amd_ops.so:
+the fit with its autograd node in C++, which ``isotonic`` calls), and the tensor-level calls
+the tests and the reference-named operators make.
 
 Takes the place of the reference's JIT-built operator library (reference
 src/torchisotonic/_ext.py:18-68): ``isotonic_tiles`` and ``isotonic_grad`` keep the
@@ -20,6 +22,7 @@ import torch
 from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
+OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
 ABI_VERSION = 2
 
 F32, F64 = 0, 1
@@ -74,6 +77,20 @@ def load() -> ctypes.CDLL:
     if got != ABI_VERSION:
         raise RuntimeError(f"torchisotonic_amd: library ABI {got}, expected {ABI_VERSION}")
     return lib
+
+
+@functools.cache
+def ops():
+    """``torch.ops.torchisotonic_amd``, loaded: ``isotonic_fit(y, w, increasing, y_min, y_max)``,
+    the clamped fit of [batch, n] rows with its backward in C++ (csrc/ti_torch.cpp)."""
+    load()  # the C ABI library first, its version checked
+    if not OPS_LIB_PATH.exists():
+        raise RuntimeError(
+            f"torchisotonic_amd: the operator library {OPS_LIB_PATH} is not built "
+            "(run `python -m torchisotonic_amd.build`)"
+        )
+    torch.ops.load_library(str(OPS_LIB_PATH))
+    return torch.ops.torchisotonic_amd
 
 
 def _check(rc: int, what: str) -> None:

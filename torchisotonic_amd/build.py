@@ -1,10 +1,14 @@
-"""Builds libtorchisotonic_amd.so in place, for gfx950, with hipcc.
+"""Builds the package's two libraries in place.
 
     python -m torchisotonic_amd.build
 
-Every ``csrc/*.hip`` file is compiled to an object (in parallel) and linked into
-``torchisotonic_amd/libtorchisotonic_amd.so``. Packed float32 instructions are switched off
-(``-packed-fp32-ops``) for all device code.
+``libtorchisotonic_amd.so``: every ``csrc/*.hip`` file compiled for gfx950 with hipcc (in
+parallel) and linked; packed float32 instructions are switched off (``-packed-fp32-ops``) for
+all device code. This is the C ABI of ``include/torchisotonic_amd.h``.
+
+``libtorchisotonic_amd_ops.so``: ``csrc/ti_torch.cpp`` (host code only) compiled with g++
+against torch's headers and linked to the first library: the ``torchisotonic_amd.isotonic_fit``
+operator with its autograd node in C++.
 """
 
 from __future__ import annotations
@@ -18,6 +22,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libtorchisotonic_amd.so"
+OPS_LIB = PKG / "libtorchisotonic_amd_ops.so"
+INCLUDE = PKG.parent / "include"
 OBJ = PKG / "_build"
 ARCH = os.environ.get("TI_OFFLOAD_ARCH", "gfx950")
 
@@ -42,6 +48,30 @@ def _run(cmd: list[str]) -> None:
         print(err, file=sys.stderr)
 
 
+def build_ops(verbose: bool = True) -> Path:
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = cpp_extension.library_paths()[0]
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *(f"-I{p}" for p in cpp_extension.include_paths()),
+        "-I/opt/rocm/include", f"-I{INCLUDE}",
+        str(CSRC / "ti_torch.cpp"),
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lamdhip64",
+        f"-L{PKG}", "-ltorchisotonic_amd",
+        f"-Wl,-rpath,{torch_lib}", "-Wl,-rpath,$ORIGIN",
+    ]
+    tmp = OPS_LIB.with_suffix(".so.tmp")
+    _run([*cmd, "-o", str(tmp)])
+    tmp.replace(OPS_LIB)
+    if verbose:
+        print(f"built {OPS_LIB}")
+    return OPS_LIB
+
+
 def build(verbose: bool = True) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     OBJ.mkdir(exist_ok=True)
@@ -54,6 +84,7 @@ def build(verbose: bool = True) -> Path:
     tmp.replace(LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")
+    build_ops(verbose)
     return LIB
 
 
