@@ -57,14 +57,14 @@ at::Tensor workspace(bool fwd, int64_t batch, int64_t n, int dtype, bool weighte
   return at::empty({static_cast<int64_t>(bytes)}, at::TensorOptions().dtype(at::kByte).device(dev));
 }
 
-// Per thread and device: the event a weighted fit records once it has read every weight, a side
-// stream that copies the weight flag out after that event, and a pinned host word to copy it
-// into, so the flag is known while the rest of the fit still runs on the current stream. (Kept
-// until the process ends.)
+// Per thread and device: the event a weighted fit records once it has read every weight, and
+// the weight flag itself in pinned host memory, which the kernels write through the fabric. The
+// host waits for that event only (the first of a long row's kernels) and reads the flag while
+// the rest of the fit still runs on the stream. (Kept until the process ends.)
 struct WeightCheck {
   hipEvent_t event = nullptr;
-  hipStream_t side = nullptr;
-  int32_t* host = nullptr;
+  uint32_t* host = nullptr;  // the host's view of the flag
+  uint32_t* dev = nullptr;   // the kernels' view
 };
 
 WeightCheck& weight_check(c10::DeviceIndex dev) {
@@ -73,10 +73,12 @@ WeightCheck& weight_check(c10::DeviceIndex dev) {
   WeightCheck& wc = per_device[dev];
   if (wc.event == nullptr) {
     check_hip(hipEventCreateWithFlags(&wc.event, hipEventDisableTiming), "hipEventCreateWithFlags");
-    wc.side = c10::hip::getStreamFromPool(false, dev).stream();  // default priority
     void* p = nullptr;
-    check_hip(hipHostMalloc(&p, sizeof(int32_t), hipHostMallocDefault), "hipHostMalloc");
-    wc.host = static_cast<int32_t*>(p);
+    check_hip(hipHostMalloc(&p, sizeof(uint32_t), hipHostMallocDefault), "hipHostMalloc");
+    wc.host = static_cast<uint32_t*>(p);
+    void* d = nullptr;
+    check_hip(hipHostGetDevicePointer(&d, p, 0), "hipHostGetDevicePointer");
+    wc.dev = static_cast<uint32_t*>(d);
   }
   return wc;
 }
@@ -110,17 +112,15 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
                    flags, lo, hi, ptr(ws), ws_bytes, stream),
             "fit");
     } else {
-      at::Tensor bad = at::zeros({1}, yc.options().dtype(at::kInt));
       WeightCheck& wc = weight_check(yc.device().index());
-      check(ti_fwd_ev(ptr(yc), ptr(w), ptr(out), static_cast<uint32_t*>(ptr(starts)),
-                      static_cast<uint32_t*>(ptr(bad)), batch, n, dtype, flags, lo, hi, ptr(ws), ws_bytes,
-                      stream, wc.event),
+      // (the previous call on this thread had read every weight before it returned, so nothing
+      // still running writes the word)
+      *static_cast<volatile uint32_t*>(wc.host) = 0u;
+      check(ti_fwd_ev(ptr(yc), ptr(w), ptr(out), static_cast<uint32_t*>(ptr(starts)), wc.dev, batch, n, dtype,
+                      flags, lo, hi, ptr(ws), ws_bytes, stream, wc.event),
             "fit");
-      check_hip(hipStreamWaitEvent(wc.side, wc.event, 0), "hipStreamWaitEvent");
-      check_hip(hipMemcpyAsync(wc.host, bad.data_ptr(), sizeof(int32_t), hipMemcpyDeviceToHost, wc.side),
-                "hipMemcpyAsync");
-      check_hip(hipStreamSynchronize(wc.side), "hipStreamSynchronize");
-      TORCH_CHECK_VALUE(*wc.host == 0, "weight must be strictly positive");
+      check_hip(hipEventSynchronize(wc.event), "hipEventSynchronize");
+      TORCH_CHECK_VALUE(*static_cast<volatile uint32_t*>(wc.host) == 0u, "weight must be strictly positive");
     }
     if (want) {
       ctx->save_for_backward({yc, w, starts});
