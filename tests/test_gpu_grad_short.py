@@ -141,3 +141,29 @@ def test_dtype_and_no_grad() -> None:
     (grad,) = torch.autograd.grad(torchisotonic_amd.isotonic(y).sum(), (y,))
     assert grad.dtype == torch.float32
     assert not torchisotonic_amd.isotonic(torch.randn(2, 5, device="cuda")).requires_grad
+
+
+@pytest.mark.parametrize("n", [12, 700, 9000])
+def test_partial_requires_grad_and_broadcast_weights(n: int) -> None:
+    # the C++ autograd node: only w differentiable, only y differentiable (w given), a weight
+    # broadcast from one row (its gradient summed over the rows by autograd), and two backward
+    # passes through one graph, on short, single-tile and multi-tile rows
+    print(f"partial grads n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    y = rng.standard_normal((3, n))
+    wrow = rng.random(n) + 0.1
+    c = rng.standard_normal((3, n))
+    fit, starts = oracle.pava(y, np.broadcast_to(wrow, (3, n)))
+    ey, ew = oracle.block_grad(starts, c, np.broadcast_to(wrow, (3, n)), y, fit, want_w=True)
+    yt, ct = torch.from_numpy(y).cuda(), torch.from_numpy(c).cuda()
+    wt = torch.from_numpy(wrow).cuda().requires_grad_()
+    (gw,) = torch.autograd.grad((torchisotonic_amd.isotonic(yt, wt) * ct).sum(), (wt,))
+    np.testing.assert_allclose(gw.cpu().numpy(), ew.sum(0), rtol=1e-9, atol=1e-9)
+    yy = yt.clone().requires_grad_()
+    out = torchisotonic_amd.isotonic(yy, wt.detach())
+    assert out.requires_grad
+    loss = (out * ct).sum()
+    (g1,) = torch.autograd.grad(loss, (yy,), retain_graph=True)
+    (g2,) = torch.autograd.grad(loss, (yy,))
+    np.testing.assert_allclose(g1.cpu().numpy(), ey, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(g1, g2, rtol=0, atol=0)
