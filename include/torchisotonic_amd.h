@@ -88,7 +88,7 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
 
 /*
  * ti_fwd, plus weights_read: a hipEvent_t (or NULL) that the call records on the stream as soon
- * as every weight has been read, i.e. once *bad_weight is final. For rows longer than one tile
+ * as every weight has been read, i.e. once *bad_weight is final. For rows longer than 32 elements
  * that is after the first of the fit's several kernels, so a caller that must refuse
  * non-positive weights before it returns (the reference checks them with a synchronous read of
  * w before fitting, reference _api.py:60-61) waits on the event and reads bad_weight from
@@ -114,10 +114,12 @@ int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
  * A row holding a NaN is one block with F = NaN (the reference CPU path's convention).
  *
  *   starts  the partition ti_fwd wrote for the same y, w.
- *   fwd_workspace / fwd_workspace_bytes: the workspace ti_fwd filled for the same call. Rows
- *           longer than one tile (4096 elements unweighted, 2048 weighted) take their blocks'
+ *   fwd_workspace / fwd_workspace_bytes: the workspace ti_fwd filled for the same call (none
+ *           for rows of up to 32 elements). Rows longer than 32 elements take their blocks'
  *           weights and fits from the final hulls ti_fwd left there, so F and the mask are the
- *           forward's bit for bit; shorter rows recompute them and may pass NULL, 0.
+ *           forward's bit for bit. A caller without it may pass NULL, 0 for rows of up to 4096
+ *           elements (2048 weighted): their blocks' weights and fits are then recomputed from y
+ *           and w (the same partition; a fit may differ from the forward's in its last bit).
  *   g       [batch, n] upstream gradient.
  *   w       weights or NULL (unweighted).
  *   y       [batch, n] input of the fit; needed when gw is wanted or a TI_CLIP_* flag is set.

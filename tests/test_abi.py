@@ -53,8 +53,10 @@ def test_workspace_queries() -> None:
     size = ctypes.c_size_t(123)
     assert lib.ti_fwd_workspace(1000, 16, _ext.F32, 0, ctypes.byref(size)) == 0
     assert size.value == 0
-    assert lib.ti_fwd_workspace(1000, 4096, _ext.F32, 0, ctypes.byref(size)) == 0
-    assert size.value == 0  # one tile: no workspace
+    assert lib.ti_fwd_workspace(1000, 32, _ext.F32, 0, ctypes.byref(size)) == 0
+    assert size.value == 0  # short rows: no workspace
+    assert lib.ti_fwd_workspace(1000, 33, _ext.F32, 0, ctypes.byref(size)) == 0
+    assert size.value > 0  # longer rows: span hulls, merges and tile records
     assert lib.ti_fwd_workspace(1, 100_000_000, _ext.F32, 1, ctypes.byref(size)) == 0
     # two node arrays of 36 bytes per vertex slot (one slot per element, rounded up to whole
     # nodes of the level), and the tile ranks

@@ -1,5 +1,5 @@
-"""Rows longer than 32 elements (the tile kernels) on the GPU against the oracle: the
-reference's lane/chunk edge shapes and adversarial patterns (reference
+"""Rows longer than 32 elements (the span kernel, merges and tiled expansion) on the GPU against
+the oracle: the reference's lane/chunk edge shapes and adversarial patterns (reference
 tests/test_cuda.py:31-134, 224-265) restated for the HIP path."""
 
 from __future__ import annotations
@@ -12,7 +12,8 @@ from gpu_util import check_fit, gpu_fit, tolerance
 
 pytestmark = pytest.mark.gpu
 
-# Tile sizes: 4096 elements unweighted, 2048 weighted; longer rows are merged across tiles.
+# Rows over 32 elements take the span kernel and the merges; the expansion and the backward work
+# in tiles of 4096 elements unweighted, 2048 weighted, so these shapes cross their edges.
 SHAPES = [33, 63, 64, 65, 100, 255, 256, 511, 1000, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096]
 LONG_SHAPES = [4097, 8193, 20_000, 100_000]
 MULTI_TILE = True  # rows longer than one tile

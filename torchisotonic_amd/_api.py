@@ -6,9 +6,9 @@ signature, argument checks and messages, dtype policy, ``dim`` handling, weight 
 and autograd behaviour. What differs inside: the clamp to ``[y_min, y_max]`` and its backward
 are fused into the kernels, the weights' positivity is checked by the forward kernel as it
 reads them (one read of ``w`` instead of two), the autograd node is C++ (no Python, and no
-interpreter lock, in the backward), and the backward does not read the fit: rows of
-up to one tile recompute their block means from ``y`` and ``w``, longer rows take them from the
-final hulls the forward left in its workspace (kept on the autograd context). There is no CPU
+interpreter lock, in the backward), and the backward does not read the fit: rows of up to 32
+elements recompute their block means from ``y`` and ``w``, longer rows take them from the final
+hulls the forward left in its workspace (kept on the autograd context). There is no CPU
 solver: tensors must be on a ROCm device (arguments are still validated first, so the
 reference's error messages hold everywhere).
 """

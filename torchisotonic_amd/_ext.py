@@ -208,7 +208,7 @@ def fit(
     [y_min, y_max] where given; the packed partition (int32 words) if ``with_starts`` (else an
     empty tensor); for weighted fits, whether some weight was not positive (the caller raises;
     known once the kernels have read w, which for long rows is before the fit has finished),
-    else None; and the workspace, which the backward of rows longer than one tile reads (None
+    else None; and the workspace, which the backward of rows longer than 32 elements reads (None
     when the fit needed none)."""
     _on_gpu(y, "y")
     dtype = _dtype_code(y)

@@ -74,7 +74,7 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
-  if (n <= ti::tile_elems(weighted != 0)) return ok();
+  if (n <= ti::kShortMax) return ok();
   *bytes = ti::long_plan(batch, n, weighted != 0).bytes;
   return ok();
 }
@@ -102,20 +102,12 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
     ti::ShortArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
     return then_record(launched(ti::short_fit(a), "short-row fit"));
   }
-  const int64_t tn = ti::tile_elems(w != nullptr);
-  if (n <= tn) {
-    if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
-    ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
-                   nullptr, 0, 0, hs};
-    return then_record(launched(ti::tile_run(a, ti::kTileSingle), "single-tile fit"));
-  }
   const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
   if (workspace == nullptr || workspace_bytes < plan.bytes)
     return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", plan.bytes, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspace must be 256-byte aligned");
   if (batch * plan.tiles_per_row > 0x7FFFFFFF) return fail(TI_ESIZE, "too many tiles");
-  ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max,
-                 nullptr, 0, 0, hs};
+  ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
   a.weights_read = weights_read;  // after the span kernel, the first of several
   return launched(ti::long_fit(a, plan, workspace), "multi-tile fit");
 }
@@ -142,7 +134,7 @@ int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
-  if (n <= ti::tile_elems(weighted != 0)) return ok();
+  if (n <= ti::kShortMax) return ok();
   *bytes = ti::long_grad_bytes(batch, n, weighted != 0);
   return ok();
 }
@@ -165,7 +157,9 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
     return launched(ti::short_grad(a), "short-row gradient");
   }
   const int64_t tn = ti::tile_elems(w != nullptr);
-  if (n <= tn) {
+  if (fwd_workspace == nullptr && n <= tn) {
+    // a caller holding only the partition: each block's weight and fit are recomputed from y
+    // and w, one workgroup per row
     if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
     ti::TileGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
                        static_cast<hipStream_t>(stream)};
@@ -173,8 +167,8 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
   }
   const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
   if (fwd_workspace == nullptr || fwd_workspace_bytes < plan.bytes)
-    return fail(TI_EWORKSPACE, "rows of %lld elements need the forward's workspace (%zu bytes), %zu given",
-                (long long)n, plan.bytes, fwd_workspace_bytes);
+    return fail(TI_EWORKSPACE, "the forward's workspace (%zu bytes, rows of %lld elements) is needed, %zu given",
+                plan.bytes, (long long)n, fwd_workspace_bytes);
   const size_t need = ti::long_grad_bytes(batch, n, w != nullptr);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);

@@ -1,4 +1,4 @@
-// Rows longer than one tile: the cross-span merge and the expansion.
+// Rows longer than 32 elements: the cross-span merge and the expansion.
 //
 // Replaces the reference's chunk-start prefix, merge rounds and fit stages (reference
 // src/torchisotonic/csrc/tiles.cuh:1680-1725, 1524-1537 + 1728-1743, 1541-1667): instead of

@@ -1,4 +1,4 @@
-// Backward of rows longer than one tile.
+// Backward of rows longer than 32 elements, from the forward's final hulls.
 //
 // Replaces the reference's long-row gradient (reference src/torchisotonic/csrc/grad.cuh:
 // 165-195 tile summaries, 346-370 ATen tile scan, 200-290 fill), which reads starts, g and w

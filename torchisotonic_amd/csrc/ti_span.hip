@@ -1,4 +1,4 @@
-// Rows longer than one tile, first stage: one lane per span of span0 elements.
+// Rows longer than 32 elements, first stage: one lane per span of span0 elements.
 //
 // Replaces the reference's chunk stage for long rows (reference src/torchisotonic/csrc/
 // tiles.cuh:665-913, chunk_kernel, which builds small lane hulls and merges them across the

@@ -12,18 +12,16 @@
 namespace ti {
 
 constexpr int kWaves256 = 4;
-constexpr int kTileSingle = 0;  // the row is one tile: write the fit
-constexpr int kTileHull = 1;    // write the tile's hull for the cross-tile merge
 
-// 256 threads x E elements: E = 16 unweighted (4096-element tiles), 8 weighted (2048), so that
-// the LDS slots (E + 1 per thread) stay near 50 KB and three workgroups share a CU.
+// The tiles of the expansion and of the long-row backward (and of the backward that recomputes
+// its blocks): 256 threads x E elements, E = 16 unweighted (4096-element tiles), 8 weighted
+// (2048).
 template <bool W>
 struct TileCfg {
   static constexpr int kThreads = 256;
   static constexpr int kLogE = W ? 3 : 4;
   static constexpr int kE = 1 << kLogE;
   static constexpr int kN = kThreads * kE;
-  static constexpr int kSlots = kThreads * (kE + 1);
 };
 
 struct TileArgs {
@@ -36,9 +34,6 @@ struct TileArgs {
   int dtype;
   unsigned flags;
   double lo, hi;
-  void* scratch;       // hull arrays of all tiles (kTileHull)
-  int64_t tiles_total; // nodes in that array
-  int64_t cap;         // vertex capacity per node
   hipStream_t stream;
   hipEvent_t weights_read = nullptr;  // recorded once every weight has been read, if given
 };
@@ -207,7 +202,7 @@ __device__ __forceinline__ bool hpools(const HPt& a, const HPt& b, const HPt& c)
   return pools<true>(dS1, dW1, dS2, dW2);
 }
 
-// Rows longer than one tile: one lane builds the hull of each span of span0 elements (a power
+// Rows longer than 32 elements: one lane builds the hull of each span of span0 elements (a power
 // of two, kSpanMin..kSpanMax, chosen per call so that the span kernel has enough lanes), then
 // workgroups merge G neighbouring hulls at a time until one hull per row remains.
 constexpr int kSpanMin = 32;
@@ -284,8 +279,7 @@ struct LongGradArgs {
 size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted);
 hipError_t long_grad(const LongGradArgs& a, const LongPlan& p, void* ws);
 
-int64_t tile_elems(bool weighted);
-hipError_t tile_run(const TileArgs& a, int mode);
+inline int64_t tile_elems(bool weighted) { return weighted ? TileCfg<true>::kN : TileCfg<false>::kN; }
 hipError_t tile_grad_single(const TileGradArgs& a);
 
 }  // namespace ti

@@ -1,5 +1,6 @@
-// Backward of rows that fit one tile (33 .. 4096 elements unweighted, .. 2048 weighted): one
-// workgroup per row, no workspace.
+// Backward of rows that fit one tile (33 .. 4096 elements unweighted, .. 2048 weighted) for a
+// caller without the forward's workspace (the reference-named isotonic_grad, which gets only the
+// partition): one workgroup per row, the blocks' sums recomputed from y and w.
 //
 // Replaces the reference's short-row gradient (reference src/torchisotonic/csrc/
 // grad.cuh:200-290, grad_fill_kernel with SINGLE) for these lengths. Every element needs the
