@@ -346,3 +346,23 @@ def test_weight_check_every_path(n: int, dtype: str) -> None:
     got = torchisotonic_amd.isotonic(y, good).cpu().numpy()
     want, _ = oracle.pava(y.cpu().double().numpy(), good.cpu().double().numpy())
     assert np.abs(got - want).max() <= tolerance(y.cpu().numpy())
+
+
+@pytest.mark.parametrize(("batch", "n"), [(10_000, 33), (9_000, 100), (8_192, 256), (140_000, 40)])
+def test_many_rows_of_one_span(batch: int, n: int) -> None:
+    # batches of thousands of rows of at most 256 elements: one span per row, one row per lane
+    # and 64 rows a wave, the span hulls the final hulls (no merge level)
+    print(f"one span a row batch={batch} n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    y = (np.linspace(0, 2, n) + rng.standard_normal((batch, n))).astype(np.float32)
+    w = (rng.random((batch, n)) + 0.1).astype(np.float32)
+    check_fit(y)
+    check_fit(y, w, increasing=False)
+    check_fit(y.astype(np.float64), w.astype(np.float64), y_min=-0.2, y_max=1.5)
+    if batch <= 10_000:
+        c = rng.standard_normal((batch, n))
+        (gy, gw), fit = gpu_grads(y.astype(np.float64), w.astype(np.float64), c)
+        want, starts = oracle.pava(y.astype(np.float64), w.astype(np.float64))
+        ey, ew = oracle.block_grad(starts, c, w.astype(np.float64), y.astype(np.float64), want, want_w=True)
+        np.testing.assert_allclose(gy, ey, rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(gw, ew, rtol=1e-9, atol=1e-9)

@@ -96,23 +96,29 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
   __shared__ SpanLds<T, W, 2 * C, R> L;  // the chunk buffer holds two chunks
   const int lane = threadIdx.x;
-  // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle).
-  const int64_t row = blockIdx.x / a.gpr;
-  const int64_t grp = blockIdx.x - row * a.gpr;
-  const int64_t span = grp * kSpanLanes + lane;
-  const bool active = span < a.spr;
+  // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle),
+  // or, where a row is one span (spr == 1), one row per lane and 64 rows a wave ("packed"): each
+  // span's hull is then its row's final hull, and there is nothing to merge.
+  const bool packed = a.spr == 1;
+  const int64_t batch = a.nodes / a.spr;
+  const int64_t row = packed ? static_cast<int64_t>(blockIdx.x) * kSpanLanes + lane : blockIdx.x / a.gpr;
+  const int64_t grp = packed ? 0 : blockIdx.x - row * a.gpr;
+  const int64_t span = packed ? 0 : grp * kSpanLanes + lane;
+  const bool active = packed ? row < batch : span < a.spr;
   const int nch = static_cast<int>(min<int64_t>(kSpanLanes, a.spr - grp * kSpanLanes));
-  const int64_t node = row * a.spr + (active ? span : 0);
+  const int64_t node = packed ? (active ? row : 0) : row * a.spr + (active ? span : 0);
   const int64_t first = span * a.span0;
   const int len = active ? static_cast<int>(min<int64_t>(a.span0, a.n - first)) : 0;
   constexpr double sgn = INC ? 1.0 : -1.0;
-  // The group's spans are consecutive elements of the row, so one buffer resource based at its
-  // first element serves every lane.
-  const int64_t base = row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
-  const int64_t total = a.nodes / a.spr * a.n;                 // elements of the array
+  // The wave's spans are consecutive elements (of one row, or of its 64 rows), so one buffer
+  // resource based at the first of them serves every lane.
+  const int64_t base = packed ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
+                              : row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
+  const int64_t total = batch * a.n;                                     // elements of the array
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + base, (total - base) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(W ? static_cast<const T*>(a.w) + base : a.y, (total - base) * sizeof(T));
-  const uint32_t loff = static_cast<uint32_t>(lane * a.span0 * static_cast<int64_t>(sizeof(T)));  // this lane's span
+  // this lane's span (packed: its row)
+  const uint32_t loff = static_cast<uint32_t>(lane * (packed ? a.n : a.span0) * static_cast<int64_t>(sizeof(T)));
   const NodeOut o = node_out(a.hulls, a.nodes, a.cap, W, node);
 
   auto ring_put = [&](int q, const HPt& p) {
@@ -321,6 +327,23 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   run((ck_last / C) & 1, ck_last, ~0u);
   if (W && wbad && a.bad_weight != nullptr) *a.bad_weight = 1u;
 
+  // The span's hull, whole, to the span array (for the merge kernel, or as the row's final hull)
+  auto write_span_hull = [&]() {
+    if (active) {
+      for (int q = r0; q < depth; ++q) node_put(q, ring_get(q));
+      *o.count = depth;
+      *o.bad = bad ? 1 : 0;
+      o.tot[0] = W ? P : static_cast<double>(len);
+      o.tot[1] = W ? PL : 0.0;
+      o.tot[2] = S;
+      o.tot[3] = SL;
+    }
+  };
+  if (packed) {
+    write_span_hull();
+    return;
+  }
+
   // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
   // lane c's hull is child c, positions [0, depth), its first point shared with lane c - 1.
   const int own = active ? (lane == 0 ? depth : depth - 1) : 0;
@@ -346,15 +369,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
   if (nslots > kCap) {
     // too many vertices: the span's hull goes to the span array, for the merge kernel
-    if (active) {
-      for (int q = r0; q < depth; ++q) node_put(q, ring_get(q));
-      *o.count = depth;
-      *o.bad = bad ? 1 : 0;
-      o.tot[0] = W ? P : static_cast<double>(len);
-      o.tot[1] = W ? PL : 0.0;
-      o.tot[2] = S;
-      o.tot[3] = SL;
-    }
+    write_span_hull();
     return;
   }
   // offsets of this lane's span within the group
@@ -445,7 +460,8 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.hulls1 = hulls1;
   a.k1 = t.batch * a.gpr;
   a.cap1 = cap1;
-  const unsigned grid = static_cast<unsigned>(t.batch * a.gpr);
+  // (rows of one span: one row per lane, and no first merge level to write)
+  const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes : t.batch * a.gpr);
   const bool W = t.w != nullptr;
   const bool inc = (t.flags & TI_INCREASING) != 0;
   auto go = [&](auto k_inc, auto k_dec) {
