@@ -667,6 +667,9 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  // rows of one span in large batches: the span kernel has written the fit and the start bits
+  // already (the tile records above serve the backward)
+  if (p.levels == 0 && p.npr[0] == 1 && expand_here(t.batch)) return hipSuccess;
   ExpandArgs x;
   x.hulls = base + p.off_buf[p.levels & 1];
   x.batch = t.batch;
