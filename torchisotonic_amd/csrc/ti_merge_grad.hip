@@ -116,6 +116,22 @@ __device__ DD block_sum_dd(DD v, DD* wave_tot) {
   return t;
 }
 
+// A tile's total of g; for rows of one tile also the scans' results (no scan kernel runs then):
+// the tile's prefix within its group and the group's within the row are 0, the row total is
+// the tile's.
+__device__ __forceinline__ void put_tile_total(const GradKArgs& a, int64_t gt, DD total) {
+  a.tg[2 * gt] = total.hi;
+  a.tg[2 * gt + 1] = total.lo;
+  if (a.tpr == 1) {
+    a.lp[2 * gt] = 0.0;
+    a.lp[2 * gt + 1] = 0.0;
+    a.gp[4 * gt] = 0.0;
+    a.gp[4 * gt + 1] = 0.0;
+    a.gp[4 * gt + 2] = total.hi;
+    a.gp[4 * gt + 3] = total.lo;
+  }
+}
+
 // Tiles per gsum workgroup: their loads are all in flight before the first tile is summed.
 constexpr int kGsumTiles = 2;
 
@@ -194,8 +210,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
       // a vertex at its first element, and on the row's last tile the row's end point
       const DD total = block_sum_dd(acc, wtot);
       if (tid == 0) {
-        a.tg[2 * gt] = total.hi;
-        a.tg[2 * gt + 1] = total.lo;
+        put_tile_total(a, gt, total);
         if (!bad) {
           if (head[u]) {  // vertex rA is the tile's first element
             lv[2 * rA[u]] = 0.0;
@@ -212,10 +227,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     }
     DD total;
     const DD off = block_scan_dd(acc, wtot, total);
-    if (tid == 0) {
-      a.tg[2 * gt] = total.hi;
-      a.tg[2 * gt + 1] = total.lo;
-    }
+    if (tid == 0) put_tile_total(a, gt, total);
     // the hull vertices inside the tile, by rank: rA, less one if rA is the tile's first element
     const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
     uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
@@ -439,12 +451,14 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  gscan_local_kernel<<<dim3(static_cast<unsigned>(in.batch * gpn.ngroups)), dim3(256), 0, in.stream>>>(a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  gscan_groups_kernel<<<dim3(static_cast<unsigned>(in.batch)), dim3(256), 0, in.stream>>>(a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (gpn.tpr > 1) {  // (rows of one tile: gsum wrote the scans' results)
+    gscan_local_kernel<<<dim3(static_cast<unsigned>(in.batch * gpn.ngroups)), dim3(256), 0, in.stream>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    gscan_groups_kernel<<<dim3(static_cast<unsigned>(in.batch)), dim3(256), 0, in.stream>>>(a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (in.dtype == TI_F32) {
     if (W) gfill_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
     else gfill_kernel<float, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
