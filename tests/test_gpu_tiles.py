@@ -197,7 +197,7 @@ def test_tile_gradients_match_oracle(batch: int, n: int, dtype: type) -> None:
 
 
 @pytest.mark.parametrize("name", PATTERNS)
-@pytest.mark.parametrize("n", [1024, 1025, 2048, 3000, 9000, 70_000])
+@pytest.mark.parametrize("n", [100, 333, 1024, 1025, 2048, 3000, 9000, 70_000])
 def test_tile_gradient_is_block_average(name: str, n: int) -> None:
     # reference tests/test_cuda.py:160-183: whatever the data (ties included) the gradient is
     # the block average over the blocks the GPU's fit reports.
@@ -301,16 +301,13 @@ def test_long_exact_ties(n: int) -> None:
     np.testing.assert_array_equal(starts, want_starts)
 
 
-def test_long_nan_row_gradients() -> None:
+@pytest.mark.parametrize("n", [100, 9000])
+def test_long_nan_row_gradients(n: int) -> None:
     # a NaN row is one block: gy is the row's average gradient, gw NaN; through a clamp, zero
-    import torch
-
-    import torchisotonic_amd
-
+    # (rows of 100: both rows in one workgroup of the packed backward)
     rng = np.random.default_rng(5)
-    n = 9000
     y = rng.standard_normal((2, n))
-    y[0, 4321] = np.nan
+    y[0, n // 2 - 1] = np.nan
     w = rng.random((2, n)) + 0.1
     c = rng.standard_normal((2, n))
     (gy, gw), _ = gpu_grads(y, w, c)
@@ -366,3 +363,12 @@ def test_many_rows_of_one_span(batch: int, n: int) -> None:
         ey, ew = oracle.block_grad(starts, c, w.astype(np.float64), y.astype(np.float64), want, want_w=True)
         np.testing.assert_allclose(gy, ey, rtol=1e-10, atol=1e-12)
         np.testing.assert_allclose(gw, ew, rtol=1e-9, atol=1e-9)
+        # float32, unweighted, decreasing, through a clamp: the clamp's mask from the GPU's fit
+        cf = c.astype(np.float32)
+        (gy,), _ = gpu_grads(y, None, cf, increasing=False, y_min=0.0, y_max=1.2)
+        (_,), raw = gpu_grads(y, None, cf, increasing=False)  # the fit before the clamp
+        want, starts = oracle.pava(y.astype(np.float64), None, increasing=False)
+        inside = ((raw >= 0.0) & (raw <= 1.2)).astype(np.float64)
+        ey, _ = oracle.block_grad(starts, cf.astype(np.float64), None)
+        # the mask is constant over a block (one fit value a block)
+        np.testing.assert_allclose(gy, ey * inside, rtol=2e-5, atol=2e-5)

@@ -409,6 +409,179 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + row * a.n + first + t0, ecount, ow);
 }
 
+// Rows of at most kPackMaxN elements: whole rows packed into a workgroup's kPackElems elements,
+// kPackE consecutive elements a thread.
+constexpr int kPackE = 4;
+constexpr int kPackElems = 256 * kPackE;
+constexpr int kPackMaxN = 512;
+constexpr int kPackRows = kPackElems / (static_cast<int>(kShortMax) + 1);  // rows a workgroup, n > 32
+static_assert(kPackMaxN <= TileCfg<true>::kN && kPackMaxN <= TileCfg<false>::kN, "rows of one tile");
+static_assert(kPackRows < 256, "row indices in uint8_t");
+
+// segmented sum: b's value unless b holds a block start, else a's plus b's
+__device__ __forceinline__ void seg_combine(double as, int ac, double& bs, int& bc) {
+  bs = bc > 0 ? bs : as + bs;
+  bc += ac;
+}
+
+// One kernel for the backward of such rows (no per-tile pass, no scan kernels): one segmented
+// scan of g over the workgroup's elements, reset at every block start, leaves each block's sum
+// G at its last element; a pass over the workgroup's blocks then takes each block's weight and
+// fit from the forward's hull vertices (as gfill_kernel does) and forms q = mask * G / W; each
+// element writes gy = w * q and gw = (y - fit) * q. A NaN row is one block (fit NaN).
+template <typename T, bool W>
+__global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg) {
+  constexpr int E = kPackE;
+  __shared__ double qv[kPackElems];       // per block of the workgroup: G, then mask * G / W
+  __shared__ T mv[kPackElems];            // per block: its fit
+  __shared__ uint8_t brow[kPackElems];    // per block: its row within the workgroup
+  __shared__ int rowbase[kPackRows];      // per row: its first block's index in the workgroup
+  __shared__ uint8_t rowbad[kPackRows];   // per row: NaN row (one block)
+  __shared__ double wave_s[kWaves256];
+  __shared__ int wave_c[kWaves256];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int n = static_cast<int>(a.n);
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
+  const int rows = static_cast<int>(min<int64_t>(rows_per_wg, a.batch - row0));
+  const int count = rows * n;
+  const int64_t base = row0 * a.n;
+  const int e0 = tid * E;
+  const int ecount = max(0, min(E, count - e0));
+  const DivBy div(static_cast<uint32_t>(n));
+  const int64_t wpr = (a.n + 31) / 32;
+  const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
+  const bool need_y = a.gw != nullptr;
+
+  T gv[E], wv[W ? E : 1], yv[E];
+  load_elems_any<T, E>(static_cast<const T*>(a.g) + base + e0, ecount, gv);
+  if constexpr (W) load_elems_any<T, E>(static_cast<const T*>(a.w) + base + e0, ecount, wv);
+  if (need_y) load_elems_any<T, E>(static_cast<const T*>(a.y) + base + e0, ecount, yv);
+  if (tid < rows) rowbad[tid] = (a.tiles[row0 + tid].flags & kTileBad) ? 1 : 0;
+  __syncthreads();
+
+  // block starts of elements e0 .. e0 + E (past the workgroup's last element: an end)
+  bool f[E + 1];
+  int er[E];  // each element's row within the workgroup
+#pragma unroll
+  for (int k = 0; k <= E; ++k) {
+    const int e = e0 + k;
+    if (e < count) {
+      const int r = static_cast<int>(div(static_cast<uint32_t>(e)));
+      const int i = e - r * n;
+      if (k < E) er[k] = r;
+      f[k] = i == 0 || (!rowbad[r] && ((a.starts[(row0 + r) * wpr + (i >> 5)] >> (i & 31)) & 1u));
+    } else {
+      f[k] = true;
+      if (k < E) er[k] = 0;
+    }
+  }
+
+  // the thread's segmented aggregate, then the workgroup's exclusive scan of them
+  double s = 0.0;
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    if (k < ecount) {
+      if (f[k]) {
+        s = 0.0;
+        ++c;
+      }
+      s += static_cast<double>(gv[k]);
+    }
+  }
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const double os = __shfl_up(s, d, kWave);
+    const int oc = __shfl_up(c, d, kWave);
+    if (lane >= d) seg_combine(os, oc, s, c);
+  }
+  if (lane == kWave - 1) {
+    wave_s[wave] = s;
+    wave_c[wave] = c;
+  }
+  double xs = __shfl_up(s, 1, kWave);
+  int xc = __shfl_up(c, 1, kWave);
+  if (lane == 0) {
+    xs = 0.0;
+    xc = 0;
+  }
+  __syncthreads();
+  double ps = 0.0;
+  int pc = 0, nb = 0;
+  for (int v = 0; v < kWaves256; ++v) {
+    if (v < wave) {
+      double ts = wave_s[v];
+      int tc = wave_c[v];
+      seg_combine(ps, pc, ts, tc);
+      ps = ts;
+      pc = tc;
+    }
+    nb += wave_c[v];
+  }
+  seg_combine(ps, pc, xs, xc);
+
+  // each block's sum at its last element; each row's first block
+  int eb[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    eb[k] = 0;
+    if (k < ecount) {
+      if (f[k]) {
+        xs = 0.0;
+        ++xc;
+        const int i = e0 + k - er[k] * n;
+        if (i == 0) rowbase[er[k]] = xc - 1;
+      }
+      xs += static_cast<double>(gv[k]);
+      eb[k] = xc - 1;
+      if (f[k + 1]) {
+        qv[xc - 1] = xs;
+        brow[xc - 1] = static_cast<uint8_t>(er[k]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // per block: q and the fit, from the forward's hull of its row
+  const double sgn = (a.flags & TI_INCREASING) ? 1.0 : -1.0;
+  const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
+  for (int b = tid; b < nb; b += 256) {
+    const int r = brow[b];
+    const int64_t row = row0 + r;
+    const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+    const double G = qv[b];
+    double q;
+    T mean;
+    if (rowbad[r]) {
+      const int last = a.tiles[row].last;
+      const double wsum = dd_diff(vertex_w<W>(fin, last), vertex_w<W>(fin, 0));
+      q = (use_lo || use_hi) ? 0.0 : G / wsum;
+      mean = quiet_nan<T>();
+    } else {
+      const int j = b - rowbase[r];
+      const double dW = dd_diff(vertex_w<W>(fin, j + 1), vertex_w<W>(fin, j));
+      const double dS = dd_diff(DD{fin.shi[j + 1], fin.slo[j + 1]}, DD{fin.shi[j], fin.slo[j]});
+      mean = static_cast<T>(sgn * slope_div(dS, dW));
+      q = G / dW;
+      if ((use_lo || use_hi) && !clip_passes(mean, use_lo, lo, use_hi, hi)) q = 0.0;
+    }
+    qv[b] = q;
+    mv[b] = mean;
+  }
+  __syncthreads();
+
+  T oy[E], ow[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    const double q = qv[eb[k]];
+    const double wk = W ? static_cast<double>(wv[W ? k : 0]) : 1.0;
+    oy[k] = static_cast<T>(wk * q);
+    if (need_y) ow[k] = static_cast<T>((static_cast<double>(yv[k]) - static_cast<double>(mv[eb[k]])) * q);
+  }
+  if (a.gy != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gy) + base + e0, ecount, oy);
+  if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + base + e0, ecount, ow);
+}
+
 }  // namespace
 
 size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted) { return grad_plan(batch, n, weighted).bytes; }
@@ -440,6 +613,18 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.gt = reinterpret_cast<double*>(base + gpn.off_gt);
   a.gp = reinterpret_cast<double*>(base + gpn.off_gp);
   a.lv = reinterpret_cast<double*>(base + gpn.off_lv);
+  if (in.n <= kPackMaxN) {  // (then one tile a row)
+    const int rpw = kPackElems / static_cast<int>(in.n);
+    const unsigned blocks = static_cast<unsigned>((in.batch + rpw - 1) / rpw);
+    if (in.dtype == TI_F32) {
+      if (W) gpack_kernel<float, true><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+      else gpack_kernel<float, false><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+    } else {
+      if (W) gpack_kernel<double, true><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+      else gpack_kernel<double, false><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+    }
+    return hipGetLastError();
+  }
   const unsigned tiles = static_cast<unsigned>(in.batch * gpn.tpr);
   const unsigned gsum_blocks = (tiles + kGsumTiles - 1) / kGsumTiles;
   if (in.dtype == TI_F32) {
