@@ -301,7 +301,7 @@ def test_long_exact_ties(n: int) -> None:
     np.testing.assert_array_equal(starts, want_starts)
 
 
-@pytest.mark.parametrize("n", [100, 9000])
+@pytest.mark.parametrize("n", [100, 1500, 9000])
 def test_long_nan_row_gradients(n: int) -> None:
     # a NaN row is one block: gy is the row's average gradient, gw NaN; through a clamp, zero
     # (rows of 100: both rows in one workgroup of the packed backward)

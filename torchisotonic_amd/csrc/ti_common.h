@@ -141,9 +141,9 @@ __device__ __forceinline__ bool clip_passes(T v, bool use_lo, T lo, bool use_hi,
   return ok;
 }
 
-// floor(e / n) for 0 <= e < 2^20 and 1 <= n <= 2^10: the high word of e * ceil(2^32 / n)
-// (exact there, since e * (ceil(2^32/n) - 2^32/n) < 2^32 / n). n = 1 has no 32-bit
-// multiplier and is passed through.
+// floor(e / n) for e * n < 2^32 (e >= 0, n >= 1): the high word of e * ceil(2^32 / n), exact
+// there since e * (ceil(2^32/n) - 2^32/n) < e < 2^32 / n. n = 1 has no 32-bit multiplier and is
+// passed through.
 struct DivBy {
   uint32_t n, magic;
   __device__ __forceinline__ explicit DivBy(uint32_t d) : n(d), magic(d > 1 ? 0xFFFFFFFFu / d + 1u : 0u) {}

@@ -16,7 +16,14 @@
 //                  prefix of g at its two vertices, W and the fit from the forward's vertices
 //                  (so the clamp mask is the forward's, bit for bit); then reads w (and y) once
 //                  and writes gy = w * mask * G / W and gw = (y - fit) * mask * G / W.
+// Rows of at most 2048 elements (one tile) take one kernel instead:
+//
+//   gpack_kernel   whole rows packed into a workgroup; a segmented scan of g over its elements
+//                  (reset at each block start) leaves every block's sum at its last element,
+//                  then as gfill_kernel, per block and per element.
 // A row holding a NaN is one block (its fit is NaN), as in the reference's CPU path.
+#include <type_traits>
+
 #include "ti_common.h"
 #include "ti_kernels.h"
 #include "ti_tile.h"
@@ -409,14 +416,17 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + row * a.n + first + t0, ecount, ow);
 }
 
-// Rows of at most kPackMaxN elements: whole rows packed into a workgroup's kPackElems elements,
-// kPackE consecutive elements a thread.
-constexpr int kPackE = 4;
-constexpr int kPackElems = 256 * kPackE;
-constexpr int kPackMaxN = 512;
-constexpr int kPackRows = kPackElems / (static_cast<int>(kShortMax) + 1);  // rows a workgroup, n > 32
-static_assert(kPackMaxN <= TileCfg<true>::kN && kPackMaxN <= TileCfg<false>::kN, "rows of one tile");
-static_assert(kPackRows < 256, "row indices in uint8_t");
+// Rows of at most 2048 elements: whole rows packed into a workgroup of 256 threads, E
+// consecutive elements a thread (E = 4 for rows up to 1024 elements, 8 up to 2048; the larger
+// E is slower for short rows, the smaller leaves half a workgroup idle above 1024).
+template <int E>
+struct PackCfg {
+  static constexpr int kElems = 256 * E;                                   // elements a workgroup
+  static constexpr int kRows = kElems / (static_cast<int>(kShortMax) + 1);  // rows a workgroup, n > 32
+  static_assert(kRows < 256, "row indices in uint8_t");
+  static_assert(kElems <= TileCfg<true>::kN && kElems <= TileCfg<false>::kN, "rows of one tile");
+};
+constexpr int kPackMaxN = PackCfg<8>::kElems;
 
 // segmented sum: b's value unless b holds a block start, else a's plus b's
 __device__ __forceinline__ void seg_combine(double as, int ac, double& bs, int& bc) {
@@ -429,14 +439,14 @@ __device__ __forceinline__ void seg_combine(double as, int ac, double& bs, int& 
 // G at its last element; a pass over the workgroup's blocks then takes each block's weight and
 // fit from the forward's hull vertices (as gfill_kernel does) and forms q = mask * G / W; each
 // element writes gy = w * q and gw = (y - fit) * q. A NaN row is one block (fit NaN).
-template <typename T, bool W>
+template <typename T, bool W, int E>
 __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg) {
-  constexpr int E = kPackE;
-  __shared__ double qv[kPackElems];       // per block of the workgroup: G, then mask * G / W
-  __shared__ T mv[kPackElems];            // per block: its fit
-  __shared__ uint8_t brow[kPackElems];    // per block: its row within the workgroup
-  __shared__ int rowbase[kPackRows];      // per row: its first block's index in the workgroup
-  __shared__ uint8_t rowbad[kPackRows];   // per row: NaN row (one block)
+  using C = PackCfg<E>;
+  __shared__ double qv[C::kElems];       // per block of the workgroup: G, then mask * G / W
+  __shared__ T mv[C::kElems];            // per block: its fit
+  __shared__ uint8_t brow[C::kElems];    // per block: its row within the workgroup
+  __shared__ int rowbase[C::kRows];      // per row: its first block's index in the workgroup
+  __shared__ uint8_t rowbad[C::kRows];   // per row: NaN row (one block)
   __shared__ double wave_s[kWaves256];
   __shared__ int wave_c[kWaves256];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -447,7 +457,7 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
   const int64_t base = row0 * a.n;
   const int e0 = tid * E;
   const int ecount = max(0, min(E, count - e0));
-  const DivBy div(static_cast<uint32_t>(n));
+  const DivBy div(static_cast<uint32_t>(n));  // (e, n <= 2048: e * n < 2^32)
   const int64_t wpr = (a.n + 31) / 32;
   const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
   const bool need_y = a.gw != nullptr;
@@ -614,16 +624,21 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.gp = reinterpret_cast<double*>(base + gpn.off_gp);
   a.lv = reinterpret_cast<double*>(base + gpn.off_lv);
   if (in.n <= kPackMaxN) {  // (then one tile a row)
-    const int rpw = kPackElems / static_cast<int>(in.n);
-    const unsigned blocks = static_cast<unsigned>((in.batch + rpw - 1) / rpw);
-    if (in.dtype == TI_F32) {
-      if (W) gpack_kernel<float, true><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
-      else gpack_kernel<float, false><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
-    } else {
-      if (W) gpack_kernel<double, true><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
-      else gpack_kernel<double, false><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
-    }
-    return hipGetLastError();
+    auto launch = [&](auto E_) -> hipError_t {
+      constexpr int E = decltype(E_)::value;
+      const int rpw = PackCfg<E>::kElems / static_cast<int>(in.n);
+      const unsigned blocks = static_cast<unsigned>((in.batch + rpw - 1) / rpw);
+      if (in.dtype == TI_F32) {
+        if (W) gpack_kernel<float, true, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+        else gpack_kernel<float, false, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+      } else {
+        if (W) gpack_kernel<double, true, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+        else gpack_kernel<double, false, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+      }
+      return hipGetLastError();
+    };
+    if (in.n <= PackCfg<4>::kElems) return launch(std::integral_constant<int, 4>{});
+    return launch(std::integral_constant<int, 8>{});
   }
   const unsigned tiles = static_cast<unsigned>(in.batch * gpn.tpr);
   const unsigned gsum_blocks = (tiles + kGsumTiles - 1) / kGsumTiles;
