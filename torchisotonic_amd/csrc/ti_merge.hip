@@ -568,10 +568,13 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
   while (span0 > kSpanMin && batch * ((n + span0 - 1) / span0) < (int64_t{1} << 17)) span0 >>= 1;
   // Where spans of up to kSpanMax make a row one group, and that still leaves 2^15 lanes, take
   // them: the span kernel's group merge then finishes each row, and no merge launch follows
-  // (1000 rows of 5000 float64: 150 -> 108 us).
-  int64_t one_group = kSpanMin;
-  while (one_group < kSpanMax && (n + one_group - 1) / one_group > kGroup) one_group <<= 1;
-  if ((n + one_group - 1) / one_group <= kGroup && batch * ((n + one_group - 1) / one_group) >= (int64_t{1} << 15))
+  // (1000 rows of 5000 float64: 150 -> 108 us). The span is the row split 64 ways (rounded up
+  // to 4 elements, 16-byte aligned spans), so the wave's lanes are all busy and each span is as
+  // short as one group allows (1000 rows of 5000: spans of 80 on 63 lanes, not 128 on 40;
+  // float64 108 -> 93 us).
+  int64_t one_group = (((n + kGroup - 1) / kGroup) + 3) & ~int64_t{3};
+  if (one_group < kSpanMin) one_group = kSpanMin;
+  if (one_group <= kSpanMax && (n + one_group - 1) / one_group <= kGroup && batch * ((n + one_group - 1) / one_group) >= (int64_t{1} << 15))
     span0 = span0 > one_group ? span0 : one_group;
   // Rows of at most kSpanMax elements in batches of thousands: one span per row, so the span
   // kernel runs one row per lane and 64 rows a wave (a wave per row would keep a few lanes busy;

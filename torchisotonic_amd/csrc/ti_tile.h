@@ -202,8 +202,9 @@ __device__ __forceinline__ bool hpools(const HPt& a, const HPt& b, const HPt& c)
   return pools<true>(dS1, dW1, dS2, dW2);
 }
 
-// Rows longer than 32 elements: one lane builds the hull of each span of span0 elements (a power
-// of two, kSpanMin..kSpanMax, chosen per call so that the span kernel has enough lanes), then
+// Rows longer than 32 elements: one lane builds the hull of each span of span0 elements
+// (kSpanMin..kSpanMax, a multiple of 4, chosen per call so that the span kernel has enough
+// lanes), then
 // workgroups merge G neighbouring hulls at a time until one hull per row remains.
 constexpr int kSpanMin = 32;
 constexpr int kSpanMax = 256;
