@@ -96,11 +96,13 @@ def test_exact_ties_partition(n: int) -> None:
         np.testing.assert_array_equal(starts, want_starts)
 
 
-def test_nan_rows_long() -> None:
+@pytest.mark.parametrize("n", [100, 500, 3000])
+def test_nan_rows_long(n: int) -> None:
+    # (rows of 100 and 500: several rows a wave of the span kernel, NaN rows among them)
     rng = np.random.default_rng(1)
-    y = rng.standard_normal((40, 3000))
+    y = rng.standard_normal((40, n))
     y[3, 17] = np.nan
-    y[39, 2999] = np.nan
+    y[39, n - 1] = np.nan
     y[20, 0] = np.nan
     check_fit(y)
     check_fit(y.astype(np.float32), increasing=False)
@@ -345,11 +347,7 @@ def test_weight_check_every_path(n: int, dtype: str) -> None:
     assert np.abs(got - want).max() <= tolerance(y.cpu().numpy())
 
 
-@pytest.mark.parametrize(("batch", "n"), [(10_000, 33), (9_000, 100), (8_192, 256), (140_000, 40)])
-def test_many_rows_of_one_span(batch: int, n: int) -> None:
-    # batches of thousands of rows of at most 256 elements: one span per row, one row per lane
-    # and 64 rows a wave, the span hulls the final hulls (no merge level)
-    print(f"one span a row batch={batch} n={n}", flush=True)
+def check_many_rows(batch: int, n: int) -> None:
     rng = np.random.default_rng(n)
     y = (np.linspace(0, 2, n) + rng.standard_normal((batch, n))).astype(np.float32)
     w = (rng.random((batch, n)) + 0.1).astype(np.float32)
@@ -372,3 +370,20 @@ def test_many_rows_of_one_span(batch: int, n: int) -> None:
         ey, _ = oracle.block_grad(starts, cf.astype(np.float64), None)
         # the mask is constant over a block (one fit value a block)
         np.testing.assert_allclose(gy, ey * inside, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize(("batch", "n"), [(10_000, 33), (9_000, 64), (40_000, 256), (140_000, 40)])
+def test_many_rows_of_one_span(batch: int, n: int) -> None:
+    # batches of thousands of rows of at most 256 elements (at most 64 below 32768 rows): one
+    # span per row, one row per lane and 64 rows a wave, the span hulls the final hulls (no
+    # merge level)
+    print(f"one span a row batch={batch} n={n}", flush=True)
+    check_many_rows(batch, n)
+
+
+@pytest.mark.parametrize(("batch", "n"), [(9_000, 100), (8_192, 256), (2_000, 512), (3_000, 1000), (5_000, 1500)])
+def test_several_rows_a_wave(batch: int, n: int) -> None:
+    # rows of at most 2048 elements: several rows a wave of the span kernel, a power-of-two
+    # number of spans each, merged per row in the wave
+    print(f"rows a wave batch={batch} n={n}", flush=True)
+    check_many_rows(batch, n)

@@ -584,6 +584,34 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
     while (s < n) s <<= 1;
     span0 = span0 > s ? span0 : s;
   }
+  // Rows of at most 2048 elements (which one wave's lanes cannot all share with spans of
+  // kSpanMin or more): several rows a wave, k lanes each (a power of two up to 32), the smallest
+  // k that gives about 2^17 lanes, each span at least 8 elements and none empty. Each row's k
+  // span hulls are merged in the wave (log2 k rounds), so the span kernel finishes the rows, with
+  // k times the lanes of one row per lane and no idle lanes (10000 rows of 256: 135 -> 89 us;
+  // 5000 rows of 100: 87 -> 49 us, float64 weighted 148 -> 44 us).
+  // Where that leaves spans longer than kSpanMin and the GPU short of lanes, one row a wave with
+  // spans of kSpanMin does better (shorter spans, the same idle SIMDs); and one row a lane
+  // ("packed", above) does better where it expands its rows itself or they are at most 64
+  // elements (30000 rows of 33: 97 us packed, 114 us four lanes a row; the rows' merge, rank
+  // and expansion launches cost more than the shorter spans save).
+  p.rows_per_wave = 1;
+  const bool packed_better = n <= kSpanMax && batch >= 8192 && (expand_here(batch) || n <= 64);
+  if (n <= 2048 && !packed_better) {
+    int64_t kmin = 1;
+    while (kmin * kSpanMax < n) kmin <<= 1;
+    int64_t k = kmin;
+    while (k < 32 && batch * k < (int64_t{1} << 17)) k <<= 1;
+    auto fits = [&](int64_t kk) {
+      const int64_t s = (n + kk - 1) / kk;
+      return s >= 8 && (kk - 1) * s < n;
+    };
+    while (k > kmin && !fits(k)) k >>= 1;
+    if (k > 1 && fits(k) && ((n + k - 1) / k <= kSpanMin || batch * k >= (int64_t{1} << 17))) {
+      span0 = (n + k - 1) / k;
+      p.rows_per_wave = static_cast<int>(kGroup / k);
+    }
+  }
   p.span0 = span0;
   int64_t npr = (n + span0 - 1) / span0;
   int64_t span = span0;  // elements per node at this level
@@ -613,7 +641,8 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   const bool W = t.w != nullptr;
   char* base = static_cast<char*>(ws);
   // level 0: span hulls
-  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0, base + p.off_buf[1], p.cap[1]);
+  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0, base + p.off_buf[1], p.cap[1],
+                          p.rows_per_wave);
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;

@@ -129,7 +129,9 @@ __device__ __forceinline__ bool hpools_nb(const HPt& a, const HPt& b, const HPt&
 // Merges the `nch` children in slots [0, total) into one hull in slots [0, result). On entry
 // rs.seg[0][c] holds the last slot of child c and every thread has passed a barrier since the
 // slots were written. NT >= 64 threads; the vertex tests take slots s = tid + k * NT, G of
-// them at a time in lockstep (their LDS reads in flight together).
+// them at a time in lockstep (their LDS reads in flight together). After max_rounds rounds it
+// stops: segment s (children [s * 2^R, (s + 1) * 2^R), R the rounds run) is then one hull, and
+// rs.seg[R & 1][s] its last slot.
 //
 // Which vertices can die: L keeps every vertex whose slope in is below R's first edge (R lies
 // above that edge's line, so no slope from the vertex to R is lower), R every vertex whose slope
@@ -144,14 +146,14 @@ __device__ __forceinline__ int lead_ones(uint64_t g, uint64_t gmask, int S) {
 }
 
 template <bool W, bool PR, int NT, int G>
-__device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, int nch) {
+__device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, int nch, int max_rounds = 6) {
   constexpr int NW = NT / kWave;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   int cur = 0;
 #pragma unroll 1
-  for (int r = 0; (1 << r) < nch; ++r) {
+  for (int r = 0; (1 << r) < nch && r < max_rounds; ++r) {
     const int nseg = (nch + (1 << r) - 1) >> r;
     const int npair = nseg >> 1;
     const int* se = rs.seg[cur];

@@ -40,6 +40,7 @@ struct SpanArgs {
   uint32_t* bad_weight;
   int64_t n, spr, nodes;  // row length, spans per row, spans in total
   int64_t gpr;            // groups of kGroup spans per row (one wave each)
+  int rpw;                // > 1: rows per wave, 64 / rpw spans each (spr == 64 / rpw)
   int64_t span0;          // elements per span
   unsigned flags;
   void* hulls;            // node array of the spans
@@ -101,29 +102,38 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
   __shared__ SpanLds<T, W, 2 * C, R> L;  // the chunk buffer holds two chunks
   const int lane = threadIdx.x;
-  // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle),
-  // or, where a row is one span (spr == 1), one row per lane and 64 rows a wave ("packed"): each
-  // span's hull is then its row's final hull, and there is nothing to merge.
+  // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle);
+  // where a row is one span (spr == 1), one row per lane and 64 rows a wave ("packed"): each
+  // span's hull is then its row's final hull, and there is nothing to merge; with rpw > 1, rpw
+  // rows a wave of kl = 64 / rpw spans each ("multi"), every span non-empty: the wave merges
+  // each row's spans into the row's hull.
   const bool packed = a.spr == 1;
+  const bool multi = a.rpw > 1;
+  const int kl = kSpanLanes / a.rpw;  // (multi) lanes, and spans, per row
   const int64_t batch = a.nodes / a.spr;
-  const int64_t row = packed ? static_cast<int64_t>(blockIdx.x) * kSpanLanes + lane : blockIdx.x / a.gpr;
-  const int64_t grp = packed ? 0 : blockIdx.x - row * a.gpr;
-  const int64_t span = packed ? 0 : grp * kSpanLanes + lane;
-  const bool active = packed ? row < batch : span < a.spr;
-  const int nch = static_cast<int>(min<int64_t>(kSpanLanes, a.spr - grp * kSpanLanes));
-  const int64_t node = packed ? (active ? row : 0) : row * a.spr + (active ? span : 0);
+  const int64_t row = packed  ? static_cast<int64_t>(blockIdx.x) * kSpanLanes + lane
+                      : multi ? static_cast<int64_t>(blockIdx.x) * a.rpw + lane / kl
+                              : blockIdx.x / a.gpr;
+  const int64_t grp = packed || multi ? 0 : blockIdx.x - row * a.gpr;
+  const int64_t span = packed ? 0 : multi ? lane % kl : grp * kSpanLanes + lane;
+  const bool active = packed || multi ? row < batch : span < a.spr;
+  const int nch = multi ? static_cast<int>(min<int64_t>(a.rpw, batch - static_cast<int64_t>(blockIdx.x) * a.rpw)) * kl
+                        : static_cast<int>(min<int64_t>(kSpanLanes, a.spr - grp * kSpanLanes));
+  const int64_t node = packed ? (active ? row : 0) : active ? row * a.spr + span : 0;
   const int64_t first = span * a.span0;
   const int len = active ? static_cast<int>(min<int64_t>(a.span0, a.n - first)) : 0;
   constexpr double sgn = INC ? 1.0 : -1.0;
-  // The wave's spans are consecutive elements (of one row, or of its 64 rows), so one buffer
+  // The wave's spans are consecutive elements (of one row, or of its rows), so one buffer
   // resource based at the first of them serves every lane.
-  const int64_t base = packed ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
-                              : row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
-  const int64_t total = batch * a.n;                                     // elements of the array
+  const int64_t base = packed  ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
+                       : multi ? static_cast<int64_t>(blockIdx.x) * a.rpw * a.n
+                               : row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
+  const int64_t total = batch * a.n;                                      // elements of the array
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + base, (total - base) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(W ? static_cast<const T*>(a.w) + base : a.y, (total - base) * sizeof(T));
-  // this lane's span (packed: its row)
-  const uint32_t loff = static_cast<uint32_t>(lane * (packed ? a.n : a.span0) * static_cast<int64_t>(sizeof(T)));
+  // this lane's span (packed: its row), as an element offset from base
+  const int64_t lel = packed ? lane * a.n : multi ? (lane / kl) * a.n + first : lane * a.span0;
+  const uint32_t loff = static_cast<uint32_t>(lel * static_cast<int64_t>(sizeof(T)));
   const NodeOut o = node_out(a.hulls, a.nodes, a.cap, W, node);
 
   auto ring_put = [&](int q, const HPt& p) {
@@ -394,8 +404,17 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
   // lane c's hull is child c, positions [0, depth), its first point shared with lane c - 1.
   const int own = active ? (lane == 0 ? depth : depth - 1) : 0;
+  // (multi: the wave's rows share one frame, so a row holding a NaN must not carry it into the
+  // rows after it. Its fit is NaN whatever its hull, and the backward needs only its weights:
+  // its sums are taken as 0, its weights kept.)
+  bool zero_s = false;
+  if (multi) {
+    const uint64_t bm = __ballot(active && bad);
+    const uint64_t kmask = kl == 64 ? ~uint64_t{0} : ((uint64_t{1} << kl) - 1);
+    zero_s = ((bm >> ((lane / kl) * kl)) & kmask) != 0;
+  }
   DD iw = active ? DD{W ? P : static_cast<double>(len), W ? PL : 0.0} : DD{0.0, 0.0};
-  DD is = active ? DD{S, SL} : DD{0.0, 0.0};
+  DD is = active && !zero_s ? DD{S, SL} : DD{0.0, 0.0};
   int islot = own;
 #pragma unroll
   for (int d = 1; d < kSpanLanes; d <<= 1) {
@@ -424,11 +443,12 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   DD es{__shfl_up(is.hi, 1, kSpanLanes), __shfl_up(is.lo, 1, kSpanLanes)};
   if (lane == 0) ew = es = DD{0.0, 0.0};
   const int off = islot - own;
-  const int lidx = lane * static_cast<int>(a.span0);
+  // (multi: the wave's rows are one sequence, each row's end point the next row's first point)
+  const int lidx = static_cast<int>(lel);
   const bool anybad = __any(active && bad);
   auto to_group = [&](HPt p) {
     p.i += lidx;
-    const DD Sd = dd_add(es, DD{p.s, p.sl});
+    const DD Sd = dd_add(es, zero_s ? DD{0.0, 0.0} : DD{p.s, p.sl});
     p.s = Sd.hi;
     p.sl = PR ? Sd.lo : 0.0;
     if constexpr (W) {
@@ -464,6 +484,56 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     rs.seg[0][lane] = off + own - 1;
   }
   __syncthreads();
+  if (multi) {
+    // log2(kl) rounds merge each row's spans and no further: segment r is then row r's hull,
+    // slots [seg[r - 1], seg[r]] (the first of them shared with row r - 1), in the frame of the
+    // wave's sequence; each row's hull goes out in its own frame (from its first point)
+    const int lgk = __builtin_ctz(kl);
+    merge_rounds<W, PR, kSpanLanes, 2>(v, rs, nslots, nch, lgk);
+    const int* se = rs.seg[lgk & 1];
+    const uint64_t badm = __ballot(active && bad);
+    const uint64_t kmask = kl == 64 ? ~uint64_t{0} : ((uint64_t{1} << kl) - 1);
+    for (int r = 0; r < nch / kl; ++r) {
+      const int f = r == 0 ? 0 : se[r - 1];
+      const int cnt = se[r] - f + 1;
+      const NodeOut pout = node_out(a.hulls1, a.k1, a.cap1, W, static_cast<int64_t>(blockIdx.x) * a.rpw + r);
+      const HPt x0 = sget(v, f);
+      auto rebase = [&](HPt x) {
+        x.i -= x0.i;
+        const DD Sd = dd_add(DD{x.s, x.sl}, DD{-x0.s, -x0.sl});
+        x.s = Sd.hi;
+        x.sl = PR ? Sd.lo : 0.0;
+        if constexpr (W) {
+          const DD Wd = dd_add(DD{x.w, x.wl}, DD{-x0.w, -x0.wl});
+          x.w = Wd.hi;
+          x.wl = PR ? Wd.lo : 0.0;
+        }
+        return x;
+      };
+      for (int q = lane; q < cnt; q += kSpanLanes) {
+        const HPt x = q == 0 ? HPt{0, 0.0, 0.0, 0.0, 0.0} : rebase(sget(v, f + q));
+        pout.idx[q] = x.i;
+        pout.shi[q] = x.s;
+        pout.slo[q] = x.sl;
+        if constexpr (W) {
+          pout.whi[q] = x.w;
+          pout.wlo[q] = x.wl;
+        }
+      }
+      if (lane == 0) {
+        const HPt e = rebase(sget(v, se[r]));  // the row's end point: its totals
+        *pout.count = cnt;
+        *pout.bad = ((badm >> (r * kl)) & kmask) != 0 ? 1 : 0;
+        pout.tot[0] = W ? e.w : static_cast<double>(e.i);
+        pout.tot[1] = W ? e.wl : 0.0;
+        pout.tot[2] = e.s;
+        pout.tot[3] = e.sl;
+      }
+    }
+    // every row merged: its first span's count says so to the merge kernel
+    if (active && span == 0) *o.count = -1;
+    return;
+  }
   const int count = merge_rounds<W, PR, kSpanLanes, 2>(v, rs, nslots, nch);
   const NodeOut pout = node_out(a.hulls1, a.k1, a.cap1, W, blockIdx.x);
   for (int k = lane; k < count; k += kSpanLanes) {
@@ -491,7 +561,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 }  // namespace
 
 hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, int64_t span0, void* hulls1,
-                     int64_t cap1) {
+                     int64_t cap1, int rows_per_wave) {
   SpanArgs a;
   a.y = t.y;
   a.w = t.w;
@@ -504,6 +574,7 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.cap = cap;
   a.span0 = span0;
   a.gpr = (spr + kSpanLanes - 1) / kSpanLanes;
+  a.rpw = rows_per_wave;
   a.hulls1 = hulls1;
   a.k1 = t.batch * a.gpr;
   a.cap1 = cap1;
@@ -511,8 +582,11 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.starts = t.starts;
   a.lo = t.lo;
   a.hi = t.hi;
-  // (rows of one span: one row per lane, and no first merge level to write)
-  const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes : t.batch * a.gpr);
+  // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
+  // rows_per_wave of them)
+  const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes
+                                              : rows_per_wave > 1 ? (t.batch + rows_per_wave - 1) / rows_per_wave
+                                                                  : t.batch * a.gpr);
   const bool W = t.w != nullptr;
   const bool inc = (t.flags & TI_INCREASING) != 0;
   auto go = [&](auto k_inc, auto k_dec) {

@@ -250,6 +250,7 @@ struct ExpandArgs {
 struct LongPlan {
   int64_t tiles_per_row;  // expansion (and backward) tiles
   int64_t span0;          // elements per span (the first node level)
+  int rows_per_wave;      // > 1: the span kernel's wave holds that many short rows, 64 / it lanes each
   int levels;
   int64_t npr[kMaxLevels + 1], cap[kMaxLevels + 1], span[kMaxLevels + 1];
   size_t off_buf[2], off_rank, bytes;
@@ -264,9 +265,11 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
 // work better (1e5 rows of 64: 256 -> 88 us fused; 1e4 rows of 256: 136 -> 175 us).
 inline bool expand_here(int64_t batch) { return batch >= 32768; }
 // Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
-// place into `hulls1` (cap1 vertices per group) and its first span's count set to -1.
+// place into `hulls1` (cap1 vertices per group) and its first span's count set to -1. With
+// rows_per_wave > 1, each wave holds that many rows of spans_per_row spans (a power of two) and
+// merges each row's spans into the row's hull.
 hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap, int64_t span0,
-                    void* hulls1, int64_t cap1);
+                    void* hulls1, int64_t cap1, int rows_per_wave);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {
