@@ -88,11 +88,13 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
 
 /*
  * ti_fwd, plus weights_read: a hipEvent_t (or NULL) that the call records on the stream as soon
- * as every weight has been read, i.e. once *bad_weight is final. For rows longer than 32 elements
- * that is after the first of the fit's several kernels, so a caller that must refuse
- * non-positive weights before it returns (the reference checks them with a synchronous read of
- * w before fitting, reference _api.py:60-61) waits on the event and reads bad_weight from
- * another stream while the rest of the fit still runs. No other counterpart in the reference.
+ * as every weight has been read, i.e. once *bad_weight is final. Up to 2^24 elements a kernel of
+ * its own reads w first, so the event comes before the fit; beyond, it comes after the first of
+ * the fit's several kernels (rows longer than 32 elements), which reads w once for both. Either
+ * way a caller that must refuse non-positive weights before it returns (the reference checks
+ * them with a synchronous read of w before fitting, reference _api.py:60-61) waits on the event
+ * and reads bad_weight while the rest of the fit still runs. No other counterpart in the
+ * reference.
  */
 int ti_fwd_ev(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
               int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,

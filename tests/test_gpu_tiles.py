@@ -372,6 +372,29 @@ def check_many_rows(batch: int, n: int) -> None:
         np.testing.assert_allclose(gy, ey * inside, rtol=2e-5, atol=2e-5)
 
 
+@pytest.mark.parametrize(("batch", "n"), [(1, 2**24 + 5), (1_100_000, 16)])
+def test_weight_check_large(batch: int, n: int) -> None:
+    # past 2^24 elements the fit's own first kernel checks the weights as it reads them (smaller
+    # fits check them in a kernel of their own first): a bad weight anywhere still raises
+    import torch
+
+    import torchisotonic_amd
+
+    print(f"weight check large batch={batch} n={n}", flush=True)
+    rng = np.random.default_rng(7)
+    y = torch.from_numpy(rng.standard_normal((batch, n)).astype(np.float32)).cuda()
+    good = torch.from_numpy((rng.random((batch, n)) + 0.1).astype(np.float32)).cuda()
+    for bad_value in (0.0, float("nan")):
+        for row, col in ((0, 0), (batch - 1, n // 2), (batch - 1, n - 1)):
+            w = good.clone()
+            w[row, col] = bad_value
+            with pytest.raises(ValueError, match="strictly positive"):
+                torchisotonic_amd.isotonic(y, w)
+    got = torchisotonic_amd.isotonic(y, good).cpu().numpy()
+    want, _ = oracle.pava(y.cpu().double().numpy(), good.cpu().double().numpy())
+    assert np.abs(got - want).max() <= tolerance(y.cpu().numpy())
+
+
 @pytest.mark.parametrize(("batch", "n"), [(10_000, 33), (9_000, 64), (40_000, 256), (140_000, 40)])
 def test_many_rows_of_one_span(batch: int, n: int) -> None:
     # batches of thousands of rows of at most 256 elements (at most 64 below 32768 rows): one
