@@ -16,6 +16,8 @@
 //                  the tile (ranks from rank_kernel), edge slopes in float64 rounded once, every
 //                  element the slope of its edge with the clamp fused, and the start bits. y is
 //                  not read again.
+#include <type_traits>
+
 #include "ti_common.h"
 #include "ti_kernels.h"
 #include "ti_slots.h"
@@ -556,6 +558,134 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   }
 }
 
+// Rows of at most 2048 elements (one tile) in place of rank_kernel and expand_kernel, whose
+// one-tile-a-row layout leaves most threads of a workgroup idle on such rows: whole rows packed
+// into a workgroup of 256 threads, E consecutive elements a thread (E = 4 for rows up to 1024
+// elements, 8 up to 2048). Per row (one lane each): its record, as rank_kernel forms it for a
+// row of one tile, and its edge count; per edge: its fit (the slope rounded once, then clamped,
+// as expand_kernel forms it), its first element and that element's start bit, in LDS; per
+// element: its edge (a binary search for a thread's first element, then at most one step per
+// element). A NaN row is one edge, fit NaN.
+constexpr int kXpackMaxN = 2048;
+
+template <typename T, bool W, int E>
+__global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles, int rows_per_wg) {
+  constexpr int NE = 256 * E;                  // elements a workgroup
+  constexpr int NR = NE / (kShortMax + 1);     // rows a workgroup (n > 32)
+  static_assert(NR <= kWave, "one lane per row");
+  __shared__ T sl[NE];                         // per edge of the workgroup's rows: the fit
+  __shared__ int16_t est[NE];                  // per edge: its first element within its row (< 2048)
+  __shared__ int roff[NR + 1];                 // per row: its first edge; [rows]: the edges in all
+  __shared__ uint8_t rbad[NR];
+  __shared__ uint32_t sbits[NE / 32 + NR];     // the rows' start-bit words, in order
+  const int tid = threadIdx.x;
+  const int n = static_cast<int>(a.n);
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
+  const int rows = static_cast<int>(min<int64_t>(rows_per_wg, a.batch - row0));
+  const int wpr = (n + 31) / 32;
+  const T tsgn = static_cast<T>((a.flags & TI_INCREASING) ? 1.0 : -1.0);
+  const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
+  const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
+
+  if (tid < kWave) {
+    int ne = 0;
+    if (tid < rows) {
+      const int64_t row = row0 + tid;
+      const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row);
+      const int count = *fin.count;
+      const bool bad = *fin.bad != 0;
+      TileRec r;
+      r.ra = 0;
+      r.rb = count - 1;
+      r.last = count - 1;
+      r.flags = kTileHead | (bad ? kTileBad : 0);
+      r.slope = 0.0;
+      r.unused = 0.0;
+      if (!bad && count == 2) {
+        const VArr v = dvarr_of(fin);
+        double dW, dS;
+        vdiff<W>(vload<W>(v, 0), vload<W>(v, 1), dW, dS);
+        r.slope = slope_div(dS, dW);
+      }
+      tiles[row] = r;
+      ne = bad ? 1 : count - 1;
+      rbad[tid] = bad ? 1 : 0;
+    }
+    int inc = ne;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_up(inc, d, kWave);
+      if (tid >= d) inc += o;
+    }
+    if (tid < rows) roff[tid] = inc - ne;
+    if (tid == rows - 1) roff[rows] = inc;
+  }
+  for (int wd = tid; wd < rows * wpr; wd += 256) sbits[wd] = 0u;
+  __syncthreads();
+
+  // edges: fit, first element, start bit
+  const int ntot = roff[rows];
+  for (int b = tid; b < ntot; b += 256) {
+    int rl = 0, rh = rows - 1;  // the row of edge b: the last with roff <= b
+    while (rl < rh) {
+      const int mid = (rl + rh + 1) >> 1;
+      if (roff[mid] <= b) rl = mid;
+      else rh = mid - 1;
+    }
+    int first = 0;
+    T val = quiet_nan<T>();
+    if (!rbad[rl]) {
+      const VArr v = dvarr_of(node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row0 + rl));
+      const int j = b - roff[rl];
+      const VPt p = vload<W>(v, j), q = vload<W>(v, j + 1);
+      double dW, dS;
+      vdiff<W>(p, q, dW, dS);
+      val = tsgn * static_cast<T>(slope_div(dS, dW));
+      first = p.i;
+    }
+    sl[b] = clip(val, use_lo, lo, use_hi, hi);
+    est[b] = static_cast<int16_t>(first);
+    atomicOr(&sbits[rl * wpr + (first >> 5)], 1u << (first & 31));
+  }
+  __syncthreads();
+
+  // elements
+  const int count = rows * n;
+  const int e0 = tid * E;
+  const int ecount = max(0, min(E, count - e0));
+  T fit[E];
+  if (ecount > 0) {
+    const DivBy div(static_cast<uint32_t>(n));  // (e, n <= 2048: e * n < 2^32)
+    int r = static_cast<int>(div(static_cast<uint32_t>(e0)));
+    int i = e0 - r * n;
+    int jl = roff[r], jh = roff[r + 1] - 1;  // the last edge of row r starting at or before i
+    while (jl < jh) {
+      const int mid = (jl + jh + 1) >> 1;
+      if (est[mid] <= i) jl = mid;
+      else jh = mid - 1;
+    }
+    int jj = jl;
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      if (k < ecount) {
+        if (k > 0) {
+          if (++i == n) {
+            i = 0;
+            jj = roff[++r];
+          } else if (jj + 1 < roff[r + 1] && est[jj + 1] <= i) {
+            ++jj;
+          }
+        }
+        fit[k] = sl[jj];
+      }
+    }
+  }
+  store_elems_any<T, E>(static_cast<T*>(a.out) + row0 * a.n + e0, ecount, fit);
+  if (a.starts != nullptr) {
+    for (int wd = tid; wd < rows * wpr; wd += 256) a.starts[row0 * wpr + wd] = sbits[wd];
+  }
+}
+
 }  // namespace
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
@@ -685,6 +815,37 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  const bool fused = p.levels == 0 && p.npr[0] == 1 && expand_here(t.batch);
+  if (t.n <= kXpackMaxN && !fused) {
+    // rows of one tile: records and fit together, whole rows a workgroup
+    ExpandArgs x;
+    x.hulls = base + p.off_buf[p.levels & 1];
+    x.batch = t.batch;
+    x.cap = p.cap[p.levels];
+    x.n = t.n;
+    x.tiles_per_row = 1;
+    x.out = t.out;
+    x.starts = t.starts;
+    x.tiles = nullptr;
+    x.flags = t.flags;
+    x.lo = t.lo;
+    x.hi = t.hi;
+    TileRec* recs = reinterpret_cast<TileRec*>(base + p.off_rank);
+    auto go = [&](auto E_) {
+      constexpr int E = decltype(E_)::value;
+      const int rpw = 256 * E / static_cast<int>(t.n);
+      const dim3 grid(static_cast<unsigned>((t.batch + rpw - 1) / rpw));
+      if (t.dtype == TI_F32) {
+        if (W) xpack_kernel<float, true, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+        else xpack_kernel<float, false, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+      } else {
+        if (W) xpack_kernel<double, true, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+        else xpack_kernel<double, false, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+      }
+      return hipGetLastError();
+    };
+    return t.n <= 1024 ? go(std::integral_constant<int, 4>{}) : go(std::integral_constant<int, 8>{});
+  }
   {
     const int64_t tiles = t.batch * p.tiles_per_row;
     const dim3 grid(static_cast<unsigned>((tiles + 255) / 256));
@@ -701,7 +862,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   }
   // rows of one span in large batches: the span kernel has written the fit and the start bits
   // already (the tile records above serve the backward)
-  if (p.levels == 0 && p.npr[0] == 1 && expand_here(t.batch)) return hipSuccess;
+  if (fused) return hipSuccess;
   ExpandArgs x;
   x.hulls = base + p.off_buf[p.levels & 1];
   x.batch = t.batch;
