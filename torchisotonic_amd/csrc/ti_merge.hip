@@ -722,11 +722,11 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
   // 5000 rows of 100: 87 -> 49 us, float64 weighted 148 -> 44 us).
   // Where that leaves spans longer than kSpanMin and the GPU short of lanes, one row a wave with
   // spans of kSpanMin does better (shorter spans, the same idle SIMDs); and one row a lane
-  // ("packed", above) does better where it expands its rows itself or they are at most 64
-  // elements (30000 rows of 33: 97 us packed, 114 us four lanes a row; the rows' merge, rank
-  // and expansion launches cost more than the shorter spans save).
+  // ("packed", above) does better in batches of 32768 rows or more, or for rows of at most 64
+  // elements, where the GPU has lanes enough without splitting rows (100000 rows of 128: 117 us
+  // packed, 158 us two lanes a row; float64 weighted 200 and 314 us).
   p.rows_per_wave = 1;
-  const bool packed_better = n <= kSpanMax && batch >= 8192 && (expand_here(batch) || n <= 64);
+  const bool packed_better = n <= kSpanMax && batch >= 8192 && (batch >= 32768 || n <= 64);
   if (n <= 2048 && !packed_better) {
     int64_t kmin = 1;
     while (kmin * kSpanMax < n) kmin <<= 1;
@@ -815,8 +815,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const bool fused = p.levels == 0 && p.npr[0] == 1 && expand_here(t.batch);
-  if (t.n <= kXpackMaxN && !fused) {
+  if (t.n <= kXpackMaxN) {
     // rows of one tile: records and fit together, whole rows a workgroup
     ExpandArgs x;
     x.hulls = base + p.off_buf[p.levels & 1];
@@ -860,9 +859,6 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  // rows of one span in large batches: the span kernel has written the fit and the start bits
-  // already (the tile records above serve the backward)
-  if (fused) return hipSuccess;
   ExpandArgs x;
   x.hulls = base + p.off_buf[p.levels & 1];
   x.batch = t.batch;

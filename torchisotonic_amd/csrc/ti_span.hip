@@ -47,11 +47,6 @@ struct SpanArgs {
   int64_t cap;
   void* hulls1;           // node array of the groups (the first merge level)
   int64_t k1, cap1;
-  // rows of one span in large batches: the fit and its start bits, written by the span kernel
-  // itself (out == nullptr: the expansion kernel writes them)
-  void* out;
-  uint32_t* starts;
-  double lo, hi;
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the chunk buffer (sums at
@@ -354,50 +349,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
       o.tot[3] = SL;
     }
   };
-  if (packed) {
-    // The row's hull is final: keep it (the backward reads it) and expand it here, block by
-    // block: each edge's slope in float64 rounded once (the expansion kernel's arithmetic), the
-    // clamp, the row's elements and its start bits.
+  if (packed) {  // the row's hull is final
     write_span_hull();
-    if (!active || a.out == nullptr) return;
-    const int n = static_cast<int>(a.n);
-    T* orow = static_cast<T*>(a.out) + row * a.n;
-    uint32_t* srow = a.starts != nullptr ? a.starts + row * ((a.n + 31) / 32) : nullptr;
-    const bool use_lo = (a.flags & TI_CLIP_MIN) != 0, use_hi = (a.flags & TI_CLIP_MAX) != 0;
-    const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
-    if (bad) {  // a NaN row: one block, NaN throughout
-      const T f = clip(quiet_nan<T>(), use_lo, lo, use_hi, hi);
-      for (int i = 0; i < n; ++i) orow[i] = f;
-      if (srow != nullptr) {
-        for (int wd = 0; wd <= (n - 1) >> 5; ++wd) srow[wd] = wd == 0 ? 1u : 0u;
-      }
-      return;
-    }
-    const T tsgn = static_cast<T>(sgn);
-    auto vtx = [&](int q) { return q >= r0 ? ring_get(q) : node_get(q); };
-    HPt pv = vtx(0);
-    uint32_t word = 0u;
-    int wd = 0;
-    for (int k = 1; k < depth; ++k) {
-      const HPt qv = vtx(k);
-      double dS, dW;
-      hdiff<W, PR>(pv, qv, dS, dW);
-      const T f = clip(tsgn * static_cast<T>(slope_div(dS, dW)), use_lo, lo, use_hi, hi);
-      for (int i = pv.i; i < qv.i; ++i) orow[i] = f;
-      // the start bit of the block (flushing the words before it)
-      for (; wd < (pv.i >> 5); ++wd) {
-        if (srow != nullptr) srow[wd] = word;
-        word = 0u;
-      }
-      word |= 1u << (pv.i & 31);
-      pv = qv;
-    }
-    if (srow != nullptr) {
-      for (; wd <= (n - 1) >> 5; ++wd) {
-        srow[wd] = word;
-        word = 0u;
-      }
-    }
     return;
   }
 
@@ -578,10 +531,6 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.hulls1 = hulls1;
   a.k1 = t.batch * a.gpr;
   a.cap1 = cap1;
-  a.out = spr == 1 && expand_here(t.batch) ? t.out : nullptr;
-  a.starts = t.starts;
-  a.lo = t.lo;
-  a.hi = t.hi;
   // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
   // rows_per_wave of them)
   const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes

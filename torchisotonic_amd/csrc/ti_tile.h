@@ -259,11 +259,6 @@ struct LongPlan {
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
 
-// Rows of one span (one row per lane in the span kernel): whether the span kernel expands them
-// itself. Its per-lane expansion costs a wave about the row's length in stores and pays where
-// there are enough waves to hide that; with few rows the expansion kernel's tiles spread the
-// work better (1e5 rows of 64: 256 -> 88 us fused; 1e4 rows of 256: 136 -> 175 us).
-inline bool expand_here(int64_t batch) { return batch >= 32768; }
 // Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
 // place into `hulls1` (cap1 vertices per group) and its first span's count set to -1. With
 // rows_per_wave > 1, each wave holds that many rows of spans_per_row spans (a power of two) and
