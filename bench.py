@@ -1,14 +1,16 @@
 """Throughput of the isotonic hot path on one MI355X, against the HBM roofline, with the
 reference CPU solver timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3[,grid]] [--no-cpu]
 
 Prints ONE JSON line. The headline ``value`` is BASELINE config C2: a forward
 ``torchisotonic_amd.isotonic`` of float32 y[1e6, 16] = -0.1 i + N(0, 1), unweighted,
 decreasing, inputs resident in HBM, K back-to-back calls of the public API between device
 synchronisations (Gelem/s = 1.6e7 K / seconds). ``extra`` holds the metric's other legs - C2
 forward+backward (dy), C4 (one row of 1e8, weighted 0/1 labels, integer counts) forward and
-forward+backward (dy, dw) - and the other BASELINE configs (C5 bootstrap, C1, C3).
+forward+backward (dy, dw) - and the other BASELINE configs (C5 bootstrap, C1, C3). With
+``--configs ...,grid`` (not in the default run) ``extra.grid`` also times the reference's own
+README table: its (batch, n) grid and data, each call synchronised, median and best of ten.
 
 Bytes per element (algorithmic, float32, each API tensor moved once): forward 8 unweighted
 (y in, fit out), 12 weighted (+w); backward 8 for dy alone (g in, gy out), 24 for dy and dw
@@ -216,6 +218,38 @@ def bench_c1_c3(steps: int, warmup: int) -> dict:
     return res
 
 
+# The reference's README table: its grid (reference bench/bench.py:31-33) and data (:108-110):
+# float32 rows of a noisy trend, reversed, fitted decreasing and unweighted.
+GRID = [(1_000_000, 16), (100_000, 128), (10_000, 1_000), (1_000, 10_000), (100, 100_000),
+        (10, 1_000_000), (1, 10_000_000), (100, 1_000), (10, 10_000), (1, 100_000),
+        (1, 1_000_000), (1, 100_000_000)]  # fmt: skip
+
+
+def bench_grid(repeats: int = 10) -> dict:
+    """Per (batch, n): seconds per call of the public API, each call followed by a device
+    synchronisation (the reference's method, bench/bench.py:47-64), median and best."""
+    out = {}
+    for b, n in GRID:
+        rng = np.random.default_rng(0)
+        trend = np.linspace(0, 3, n, dtype=np.float32)
+        data = (trend + rng.standard_normal((b, n), dtype=np.float32))[:, ::-1].copy()
+        x = torch.from_numpy(data).cuda()
+        del data
+        torchisotonic_amd.isotonic(x, increasing=False)  # warm-up (first call's allocations)
+        warm_gpu()
+        times = []
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            torchisotonic_amd.isotonic(x, increasing=False)
+            sync()
+            times.append(time.perf_counter() - t0)
+        out[f"{b}x{n}"] = {"median_ms": float(np.median(times)) * 1e3, "best_ms": float(np.min(times)) * 1e3}
+        log(f"  grid {b} x {n}: {out[f'{b}x{n}']['median_ms']:.3f} ms")
+        del x
+        torch.cuda.empty_cache()
+    return out
+
+
 # --- CPU baseline ---------------------------------------------------------------------------
 
 
@@ -319,6 +353,9 @@ def main() -> None:
     if "c1" in configs or "c3" in configs:
         log("C1/C3 ...")
         extra["c1_c3"] = bench_c1_c3(max(3, args.steps // 3), 2)
+    if "grid" in configs:
+        log("README grid ...")
+        extra["grid"] = bench_grid()
     elems = c2["elems"]
     k = c2["kernel_ms"]["short_fit_kernel<float,16,unweighted> (no starts)"]
     achieved = 8 * elems / (k * 1e-3) / 1e9
