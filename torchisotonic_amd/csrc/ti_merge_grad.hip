@@ -291,6 +291,12 @@ __global__ __launch_bounds__(256) void gscan_local_kernel(GradKArgs a) {
   if (tid == 0) {
     a.gt[2 * blockIdx.x] = total.hi;
     a.gt[2 * blockIdx.x + 1] = total.lo;
+    if (a.ngroups == 1) {  // (rows of one group: gscan_groups_kernel's results, which then does not run)
+      a.gp[4 * row] = 0.0;
+      a.gp[4 * row + 1] = 0.0;
+      a.gp[4 * row + 2] = total.hi;
+      a.gp[4 * row + 3] = total.lo;
+    }
   }
 }
 
@@ -655,9 +661,11 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
     gscan_local_kernel<<<dim3(static_cast<unsigned>(in.batch * gpn.ngroups)), dim3(256), 0, in.stream>>>(a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    gscan_groups_kernel<<<dim3(static_cast<unsigned>(in.batch)), dim3(256), 0, in.stream>>>(a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (gpn.ngroups > 1) {
+      gscan_groups_kernel<<<dim3(static_cast<unsigned>(in.batch)), dim3(256), 0, in.stream>>>(a);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
   }
   if (in.dtype == TI_F32) {
     if (W) gfill_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
