@@ -59,6 +59,14 @@ int64_t ti_starts_words(int64_t batch, int64_t n);
 /* Bytes of device workspace ti_fwd needs for this problem set (0 when none). */
 int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes);
 
+/* Diagnostic: the kernel geometry ti_fwd takes for rows of more than 32 elements - elements per
+ * span of its first kernel (one lane builds each span's hull), the merge launches that follow
+ * it, and the rows per wave of the first kernel (1: a wave holds spans of one row). Rows of at
+ * most 32 elements report 0, 0, 0. No counterpart in the reference: tests use it to show which
+ * geometry a case exercises. */
+int ti_fwd_geometry(int64_t batch, int64_t n, int weighted, int64_t* span0, int* levels,
+                    int* rows_per_wave);
+
 /*
  * The isotonic fit of every row of y, and optionally its block partition.
  * Replaces torchisotonic::isotonic_tiles (reference ops.cpp:47-49, implementation

@@ -37,6 +37,7 @@ SYMBOLS = (
     "ti_last_error",
     "ti_starts_words",
     "ti_fwd_workspace",
+    "ti_fwd_geometry",
     "ti_fwd",
     "ti_fwd_ev",
     "ti_bwd_workspace",
@@ -65,6 +66,8 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = _int
         fn.argtypes = [_i64, _i64, _int, _int, ctypes.POINTER(_sz)]
+    lib.ti_fwd_geometry.restype = _int
+    lib.ti_fwd_geometry.argtypes = [_i64, _i64, _int, ctypes.POINTER(_i64), ctypes.POINTER(_int), ctypes.POINTER(_int)]
     lib.ti_fwd.restype = _int
     lib.ti_fwd.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_fwd_ev.restype = _int
@@ -159,6 +162,17 @@ def _workspace_bytes(kind: str, batch: int, n: int, dtype: int, weighted: bool) 
     fn = load().ti_fwd_workspace if kind == "fwd" else load().ti_bwd_workspace
     _check(fn(batch, n, dtype, int(weighted), ctypes.byref(size)), f"{kind}_workspace")
     return int(size.value)
+
+
+def geometry(batch: int, n: int, weighted: bool) -> dict:
+    """The long-row forward's kernel geometry for a problem set (a diagnostic): elements per
+    span of its first kernel, merge launches after it, rows per wave of the first kernel."""
+    span0, levels, rpw = _i64(0), _int(0), _int(0)
+    _check(
+        load().ti_fwd_geometry(batch, n, int(weighted), ctypes.byref(span0), ctypes.byref(levels), ctypes.byref(rpw)),
+        "fwd_geometry",
+    )
+    return {"span0": int(span0.value), "levels": int(levels.value), "rows_per_wave": int(rpw.value)}
 
 
 def _workspace(kind: str, batch: int, n: int, dtype: int, weighted: bool, device: torch.device) -> Tensor | None:

@@ -100,6 +100,20 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   return ok();
 }
 
+int ti_fwd_geometry(int64_t batch, int64_t n, int weighted, int64_t* span0, int* levels, int* rows_per_wave) {
+  if (span0 == nullptr || levels == nullptr || rows_per_wave == nullptr) return fail(TI_EINVAL, "null output");
+  if (int rc = check_shape(batch, n, TI_F32)) return rc;
+  *span0 = 0;
+  *levels = 0;
+  *rows_per_wave = 0;
+  if (n <= ti::kShortMax) return ok();
+  const ti::LongPlan p = ti::long_plan(batch, n, weighted != 0);
+  *span0 = p.span0;
+  *levels = p.levels;
+  *rows_per_wave = p.rows_per_wave;
+  return ok();
+}
+
 }  // extern "C"
 
 namespace {

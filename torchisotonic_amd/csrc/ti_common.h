@@ -25,6 +25,9 @@ constexpr int kWave = 64;
 // each other (Sterbenz), and otherwise too large for the errors to change its sign; the
 // errors' difference only decides when the rounded products tie.
 __device__ __forceinline__ int cross_sign(double a, double b, double c, double d) {
+  // (no contraction: fused into an fma, p - q would become a*b - q exactly and count the
+  // product's rounding error twice)
+#pragma clang fp contract(off)
   const double p = a * b;
   const double q = c * d;
   const double ep = __builtin_fma(a, b, -p);
@@ -85,7 +88,10 @@ struct DD {
   double hi, lo;
 };
 
+// Error-free transformations hold only for separately rounded operations: contraction (an
+// fma formed from a product passed in and the sum here) is off in each of them.
 __device__ __forceinline__ DD two_sum(double a, double b) {
+#pragma clang fp contract(off)
   const double s = a + b;
   const double bb = s - a;
   const double e = (a - (s - bb)) + (b - bb);
@@ -93,6 +99,7 @@ __device__ __forceinline__ DD two_sum(double a, double b) {
 }
 
 __device__ __forceinline__ DD dd_add(DD a, DD b) {
+#pragma clang fp contract(off)
   DD s = two_sum(a.hi, b.hi);
   const double e = s.lo + (a.lo + b.lo);
   const double hi = s.hi + e;
@@ -100,6 +107,7 @@ __device__ __forceinline__ DD dd_add(DD a, DD b) {
 }
 
 __device__ __forceinline__ DD dd_add(DD a, double b) {
+#pragma clang fp contract(off)
   DD s = two_sum(a.hi, b);
   const double e = s.lo + a.lo;
   const double hi = s.hi + e;
@@ -108,6 +116,7 @@ __device__ __forceinline__ DD dd_add(DD a, double b) {
 
 // a - b, rounded once to a double.
 __device__ __forceinline__ double dd_diff(DD a, DD b) {
+#pragma clang fp contract(off)
   return (a.hi - b.hi) + (a.lo - b.lo);
 }
 

@@ -167,8 +167,10 @@ __device__ __forceinline__ int child_of_slot(const MergeSmall& sm, int nch, int 
   return lo;
 }
 
-// Vertex k of child c in the parent's coordinates. Float32 data keeps float64 coordinates
-// (the double-double offset rounded once); float64 data keeps the rounding errors.
+// Vertex k of child c in the parent's coordinates, double-double: the child's offset added
+// to its coordinates without re-rounding them, so the parent sees the child's hull exactly as
+// the child built it (re-rounded into the parent's larger coordinates, a convex child could
+// turn non-convex where sums cancel).
 template <bool W, bool PR>
 __device__ __forceinline__ HPt child_vertex(const MergeArgs& a, const MergeSmall& sm, int64_t row,
                                             int64_t c0, int c, int k) {
@@ -804,13 +806,9 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
 #define TI_MERGE_LAUNCH(Wv, PRv)                                                                 \
   launch(merge_kernel<Wv, PRv, 64, 4>, merge_kernel<Wv, PRv, 256, 2>, merge_kernel<Wv, PRv, 1024, 2>, \
          slot_bytes<Wv, PRv>())
-    if (t.dtype == TI_F32) {
-      if (W) TI_MERGE_LAUNCH(true, false);
-      else TI_MERGE_LAUNCH(false, false);
-    } else {
-      if (W) TI_MERGE_LAUNCH(true, true);
-      else TI_MERGE_LAUNCH(false, true);
-    }
+    // (node arrays and slots are double-double for both dtypes: see child_vertex)
+    if (W) TI_MERGE_LAUNCH(true, true);
+    else TI_MERGE_LAUNCH(false, true);
 #undef TI_MERGE_LAUNCH
     e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -93,6 +93,12 @@ template <typename T, bool W, int C, int R, int LC, bool INC>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert((R & (R - 1)) == 0 && 2 * C <= 32, "ring slots: a power of two; two chunks: a 32-bit mask");
   static_assert(LC % (2 * C) == 0, "a load block is a whole number of chunk pairs");
+  // PR: the span's own sums carry their rounding errors (float64 data). Within a span every
+  // test and every later slope uses the same span-relative coordinates, so float32 data needs
+  // none there; but a span's vertices moved into a larger frame (the group's, the row's) keep
+  // the translation's low part whatever the dtype (the merge slots and node arrays are always
+  // double-double): re-rounded there, a hull the span found convex can turn non-convex where
+  // sums cancel, and the fit would step down.
   constexpr bool PR = sizeof(T) == 8;
   static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
   __shared__ SpanLds<T, W, 2 * C, R> L;  // the chunk buffer holds two chunks
@@ -384,7 +390,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // (the round state first, then the slots, in the wave's LDS)
   constexpr size_t kRoundBytes = (sizeof(MergeRounds) + 63) & ~size_t(63);
   constexpr int kCap =
-      static_cast<int>(((sizeof(SpanLds<T, W, 2 * C, R>) - kRoundBytes) / slot_bytes<W, PR>()) & ~size_t(63));
+      static_cast<int>(((sizeof(SpanLds<T, W, 2 * C, R>) - kRoundBytes) / slot_bytes<W, true>()) & ~size_t(63));
   static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
   if (nslots > kCap) {
     // too many vertices: the span's hull goes to the span array, for the merge kernel
@@ -403,11 +409,11 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     p.i += lidx;
     const DD Sd = dd_add(es, zero_s ? DD{0.0, 0.0} : DD{p.s, p.sl});
     p.s = Sd.hi;
-    p.sl = PR ? Sd.lo : 0.0;
+    p.sl = Sd.lo;
     if constexpr (W) {
       const DD Wd = dd_add(ew, DD{p.w, p.wl});
       p.w = Wd.hi;
-      p.wl = PR ? Wd.lo : 0.0;
+      p.wl = Wd.lo;
     }
     return p;
   };
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   for (int k = 0; k < R; ++k) rv[k] = ring_get(r0 + k);
   char* const mem = reinterpret_cast<char*>(&L);
   MergeRounds& rs = *reinterpret_cast<MergeRounds*>(mem);
-  const Slots<W, PR> v = slots_carve<W, PR>(mem + kRoundBytes, kCap);
+  const Slots<W, true> v = slots_carve<W, true>(mem + kRoundBytes, kCap);
   const int q0 = lane == 0 ? 0 : 1;  // the first point of a later span is its left neighbour's last
   if (active) {
     for (int q = q0; q < r0; ++q) {
@@ -442,7 +448,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     // slots [seg[r - 1], seg[r]] (the first of them shared with row r - 1), in the frame of the
     // wave's sequence; each row's hull goes out in its own frame (from its first point)
     const int lgk = __builtin_ctz(kl);
-    merge_rounds<W, PR, kSpanLanes, 2>(v, rs, nslots, nch, lgk);
+    merge_rounds<W, true, kSpanLanes, 2>(v, rs, nslots, nch, lgk);
     const int* se = rs.seg[lgk & 1];
     const uint64_t badm = __ballot(active && bad);
     const uint64_t kmask = kl == 64 ? ~uint64_t{0} : ((uint64_t{1} << kl) - 1);
@@ -455,11 +461,11 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         x.i -= x0.i;
         const DD Sd = dd_add(DD{x.s, x.sl}, DD{-x0.s, -x0.sl});
         x.s = Sd.hi;
-        x.sl = PR ? Sd.lo : 0.0;
+        x.sl = Sd.lo;
         if constexpr (W) {
           const DD Wd = dd_add(DD{x.w, x.wl}, DD{-x0.w, -x0.wl});
           x.w = Wd.hi;
-          x.wl = PR ? Wd.lo : 0.0;
+          x.wl = Wd.lo;
         }
         return x;
       };
@@ -487,7 +493,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     if (active && span == 0) *o.count = -1;
     return;
   }
-  const int count = merge_rounds<W, PR, kSpanLanes, 2>(v, rs, nslots, nch);
+  const int count = merge_rounds<W, true, kSpanLanes, 2>(v, rs, nslots, nch);
   const NodeOut pout = node_out(a.hulls1, a.k1, a.cap1, W, blockIdx.x);
   for (int k = lane; k < count; k += kSpanLanes) {
     const HPt x = sget(v, k);
