@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 2
+#define TI_ABI_VERSION 3
 
 /* dtype codes */
 #define TI_F32 0
@@ -125,11 +125,11 @@ int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
  *
  *   starts  the partition ti_fwd wrote for the same y, w.
  *   fwd_workspace / fwd_workspace_bytes: the workspace ti_fwd filled for the same call (none
- *           for rows of up to 32 elements). Rows longer than 32 elements take their blocks'
- *           weights and fits from the final hulls ti_fwd left there, so F and the mask are the
- *           forward's bit for bit. A caller without it may pass NULL, 0 for rows of up to 4096
- *           elements (2048 weighted): their blocks' weights and fits are then recomputed from y
- *           and w (the same partition; a fit may differ from the forward's in its last bit).
+ *           for rows of up to 32 elements, which recompute their blocks' means from y and w as
+ *           the forward formed them). Rows longer than 32 elements take their blocks' weights
+ *           and fits from the final hulls ti_fwd left there, so F and the mask are the
+ *           forward's bit for bit; without it they fail with TI_EWORKSPACE (a caller holding
+ *           only the fit and the partition calls ti_grad).
  *   g       [batch, n] upstream gradient.
  *   w       weights or NULL (unweighted).
  *   y       [batch, n] input of the fit; needed when gw is wanted or a TI_CLIP_* flag is set.
@@ -141,6 +141,31 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
            const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
            int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
            size_t workspace_bytes, void* stream);
+
+/* Bytes of device workspace ti_grad needs for this problem set (0 when batch * n <= 2048). */
+int ti_grad_workspace(int64_t batch, int64_t n, int dtype, size_t* bytes);
+
+/*
+ * The reference's stateless gradient operator, torchisotonic::isotonic_grad(out, starts, g, w, y)
+ * (reference ops.cpp:50, implementation grad.cuh:304-413), for rows of any length: with G and W
+ * the sums of g and of w (the element count when w is NULL) over an element's block,
+ *   gy_i = w_i * G / W,          gw_i = (y_i - out_i) * G / W.
+ * No clamp: in the reference the clamp's backward is torch's, outside this operator.
+ *
+ *   out     [batch, n] the fit (unclamped), read only when y is given.
+ *   starts  the partition (ti_starts_words(batch, n) words, as ti_fwd writes it; element 0 of
+ *           every row counts as a start whatever its bit).
+ *   g       [batch, n] upstream gradient.
+ *   w       weights or NULL.
+ *   y       [batch, n] the data, or NULL: given (with w only, as in the reference), gw is
+ *           written; else gw is not touched and may be NULL.
+ *   gy, gw  outputs.
+ *   workspace / workspace_bytes: at least ti_grad_workspace() bytes, 256-byte aligned.
+ * Block sums are float64 within 8 elements and double-double beyond.
+ */
+int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* w, const void* y,
+            void* gy, void* gw, int64_t batch, int64_t n, int dtype, void* workspace,
+            size_t workspace_bytes, void* stream);
 
 /* Test hook: the starts bit array of a [batch, n] set as bytes (0/1), row-major - the
  * reference's bool starts tensor (reference tests/test_cuda.py:176 reads it). */

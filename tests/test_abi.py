@@ -109,9 +109,37 @@ def test_bwd_argument_errors() -> None:
     assert bwd(None, 2, None, None, 3, None, 4, 16, 1) == 1
     # nothing wanted: fine, no launch
     assert bwd(1, 2, None, None, None, None, 4, 16, 1) == 0
-    # a long row without the forward's workspace
-    assert bwd(1, 2, None, None, 3, None, 2, 100_000, 1) == 4
-    assert b"forward's workspace" in lib.ti_last_error()
+    # a row over 32 elements without the forward's workspace
+    for n in (33, 100_000):
+        assert bwd(1, 2, None, None, 3, None, 2, n, 1) == 4
+        assert b"forward's workspace" in lib.ti_last_error()
+
+
+def test_grad_argument_errors() -> None:
+    lib = _ext.load()
+
+    def grad(out, starts, g, w, y, gy, gw, batch, n, ws=None, wsb=0):
+        return lib.ti_grad(out, starts, g, w, y, gy, gw, batch, n, 0, ws, wsb, None)
+
+    size = ctypes.c_size_t(7)
+    assert lib.ti_grad_workspace(1000, 2, _ext.F32, ctypes.byref(size)) == 0 and size.value == 0
+    assert lib.ti_grad_workspace(1, 2048, _ext.F32, ctypes.byref(size)) == 0 and size.value == 0
+    assert lib.ti_grad_workspace(1, 2049, _ext.F64, ctypes.byref(size)) == 0 and size.value > 0
+    assert lib.ti_grad_workspace(1, 100_000_000, _ext.F32, ctypes.byref(size)) == 0
+    assert size.value < 100_000_000 // 8  # well under a byte an element
+    # y without w (the reference's check, grad.cuh:393)
+    assert grad(1, 2, 3, None, 5, 6, 7, 4, 16) == 1
+    assert b"y is only needed" in lib.ti_last_error()
+    # gw wanted without the fit
+    assert grad(None, 2, 3, 4, 5, 6, 7, 4, 16) == 1
+    # starts, g or gy missing
+    assert grad(1, None, 3, None, None, 6, None, 4, 16) == 1
+    assert grad(1, 2, None, None, None, 6, None, 4, 16) == 1
+    assert grad(1, 2, 3, None, None, None, None, 4, 16) == 1
+    # several tiles without a workspace
+    assert grad(1, 2, 3, None, None, 6, None, 2, 100_000) == 4
+    # empty batch: nothing to do
+    assert grad(None, None, None, None, None, None, None, 0, 16) == 0
 
 
 def test_errors_are_per_thread() -> None:

@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -42,6 +42,8 @@ SYMBOLS = (
     "ti_fwd_ev",
     "ti_bwd_workspace",
     "ti_bwd",
+    "ti_grad_workspace",
+    "ti_grad",
     "ti_starts_to_bool",
 )
 
@@ -74,6 +76,10 @@ def load() -> ctypes.CDLL:
     lib.ti_fwd_ev.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp]
     lib.ti_bwd.restype = _int
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_grad_workspace.restype = _int
+    lib.ti_grad_workspace.argtypes = [_i64, _i64, _int, ctypes.POINTER(_sz)]
+    lib.ti_grad.restype = _int
+    lib.ti_grad.argtypes = [_vp] * 7 + [_i64, _i64, _int, _vp, _sz, _vp]
     lib.ti_starts_to_bool.restype = _int
     lib.ti_starts_to_bool.argtypes = [_vp, _vp, _i64, _i64, _vp]
     got = lib.ti_abi_version()
@@ -344,18 +350,35 @@ def isotonic_tiles(
 def isotonic_grad(
     out: Tensor, starts: Tensor, g: Tensor, w: Tensor | None, y: Tensor | None
 ) -> list[Tensor | None]:
-    """The reference's gradient operator (reference _ext.py:34-40): the gradients of a fit
-    whose blocks start where the bool ``starts`` is set, w.r.t. y and, given y, the weights.
-    ``out`` is accepted for the signature's sake. Rows longer than one tile (4096 elements
-    unweighted, 2048 weighted) take their blocks from the forward's final hulls, which this
-    signature cannot carry: for them it raises, and the autograd path (``isotonic``), which
-    keeps the forward's workspace, is the way in."""
-    del out
-    if g.shape[-1] > (2048 if w is not None else 4096):
-        raise RuntimeError(
-            "torchisotonic_amd.isotonic_grad: rows longer than one tile need the forward's "
-            "workspace; use torchisotonic_amd.isotonic with autograd"
+    """The reference's gradient operator (reference _ext.py:34-40, grad.cuh:386-413): the
+    gradients w.r.t. y and, given ``y`` (with ``w``), w.r.t. the weights, of a fit ``out`` whose
+    blocks start where ``starts`` is set (bool [batch, n], or the packed int32 words), for the
+    upstream gradient ``g``; rows of any length. Returns ``[gy, gw]``, ``gw`` empty without
+    ``y`` (as the reference)."""
+    _on_gpu(g, "grad")
+    dtype = _dtype_code(g)
+    if g.dim() != 2 or out.shape != g.shape:
+        raise RuntimeError("torchisotonic_amd.isotonic_grad: out and g must be [batch, n] alike")
+    if y is not None and w is None:
+        raise RuntimeError("torchisotonic_amd.isotonic_grad: y is only needed for the weights' gradient")
+    batch, n = g.shape
+    packed = bool_to_starts(starts) if starts.dtype == torch.bool else starts.contiguous()
+    g = g.contiguous()
+    out = out.to(g.dtype).contiguous()
+    w = None if w is None else w.to(g.dtype).contiguous()
+    y = None if y is None else y.to(g.dtype).contiguous()
+    gy = torch.empty_like(g)
+    gw = torch.empty_like(g) if y is not None else torch.empty(0, dtype=g.dtype, device=g.device)
+    if g.numel() == 0:
+        return [gy, gw]
+    size = _sz(0)
+    _check(load().ti_grad_workspace(batch, n, dtype, ctypes.byref(size)), "grad_workspace")
+    ws = torch.empty(size.value, dtype=torch.uint8, device=g.device) if size.value else None
+    with _on_device(g.device):
+        rc = load().ti_grad(
+            _ptr(out), _ptr(packed), _ptr(g), _ptr(w), _ptr(y), _ptr(gy),
+            _ptr(gw) if y is not None else None, batch, n, dtype,
+            _ptr(ws), 0 if ws is None else ws.numel(), _stream(g),
         )
-    packed = bool_to_starts(starts) if starts.dtype == torch.bool else starts
-    gy, gw = grad(packed, None, g, w, y, True, y is not None)
+    _check(rc, "isotonic_grad")
     return [gy, gw]

@@ -203,18 +203,11 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
                         static_cast<hipStream_t>(stream)};
     return launched(ti::short_grad(a), "short-row gradient");
   }
-  const int64_t tn = ti::tile_elems(w != nullptr);
-  if (fwd_workspace == nullptr && n <= tn) {
-    // a caller holding only the partition: each block's weight and fit are recomputed from y
-    // and w, one workgroup per row
-    if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
-    ti::TileGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
-                       static_cast<hipStream_t>(stream)};
-    return launched(ti::tile_grad_single(a), "single-tile gradient");
-  }
   const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
   if (fwd_workspace == nullptr || fwd_workspace_bytes < plan.bytes)
-    return fail(TI_EWORKSPACE, "the forward's workspace (%zu bytes, rows of %lld elements) is needed, %zu given",
+    return fail(TI_EWORKSPACE,
+                "the forward's workspace (%zu bytes, rows of %lld elements) is needed, %zu given "
+                "(without it, ti_grad computes the gradients from the fit and the partition)",
                 plan.bytes, (long long)n, fwd_workspace_bytes);
   const size_t need = ti::long_grad_bytes(batch, n, w != nullptr);
   if (workspace == nullptr || workspace_bytes < need)
@@ -224,6 +217,31 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
   ti::LongGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
                      fwd_workspace, static_cast<hipStream_t>(stream)};
   return launched(ti::long_grad(a, plan, workspace), "multi-tile gradient");
+}
+
+int ti_grad_workspace(int64_t batch, int64_t n, int dtype, size_t* bytes) {
+  if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  *bytes = ti::seg_grad_bytes(batch, n);
+  return ok();
+}
+
+int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* w, const void* y, void* gy,
+            void* gw, int64_t batch, int64_t n, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  if (batch == 0) return ok();
+  if (starts == nullptr || g == nullptr || gy == nullptr) return fail(TI_EINVAL, "starts, g and gy must not be null");
+  if (y != nullptr && w == nullptr) return fail(TI_EINVAL, "y is only needed for the weights' gradient (give w)");
+  if (y != nullptr && (out == nullptr || gw == nullptr))
+    return fail(TI_EINVAL, "the weights' gradient needs the fit (out) and gw");
+  if (ti::seg_grad_tiles(batch, n) > 0x7FFFFFFF) return fail(TI_ESIZE, "too many tiles");
+  const size_t need = ti::seg_grad_bytes(batch, n);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspace must be 256-byte aligned");
+  ti::SegGradArgs a{out, starts, g, w, y, gy, y != nullptr ? gw : nullptr, batch, n, dtype,
+                    static_cast<hipStream_t>(stream)};
+  return launched(ti::seg_grad(a, workspace), "stateless gradient");
 }
 
 int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n, void* stream) {

@@ -13,9 +13,8 @@ namespace ti {
 
 constexpr int kWaves256 = 4;
 
-// The tiles of the expansion and of the long-row backward (and of the backward that recomputes
-// its blocks): 256 threads x E elements, E = 16 unweighted (4096-element tiles), 8 weighted
-// (2048).
+// The tiles of the expansion and of the long-row backward: 256 threads x E elements, E = 16
+// unweighted (4096-element tiles), 8 weighted (2048).
 template <bool W>
 struct TileCfg {
   static constexpr int kThreads = 256;
@@ -84,19 +83,22 @@ __host__ __device__ inline NodeOut node_out(void* base, int64_t K, int64_t cap, 
   return o;
 }
 
-struct TileGradArgs {
+// The stateless gradient (ti_grad): every element's block sums of g and w from the partition.
+struct SegGradArgs {
+  const void* fit;  // needed with y
   const uint32_t* starts;
   const void* g;
-  const void* w;
-  const void* y;
+  const void* w;  // null: weights of one
+  const void* y;  // null: no weight gradient
   void* gy;
   void* gw;
   int64_t batch, n;
   int dtype;
-  unsigned flags;
-  double lo, hi;
   hipStream_t stream;
 };
+size_t seg_grad_bytes(int64_t batch, int64_t n);
+int64_t seg_grad_tiles(int64_t batch, int64_t n);
+hipError_t seg_grad(const SegGradArgs& a, void* ws);
 
 // E consecutive elements of one thread (count of them valid): 16-byte loads when whole and
 // aligned, element by element otherwise.
@@ -285,6 +287,5 @@ size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted);
 hipError_t long_grad(const LongGradArgs& a, const LongPlan& p, void* ws);
 
 inline int64_t tile_elems(bool weighted) { return weighted ? TileCfg<true>::kN : TileCfg<false>::kN; }
-hipError_t tile_grad_single(const TileGradArgs& a);
 
 }  // namespace ti
