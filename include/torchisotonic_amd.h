@@ -108,6 +108,23 @@ int ti_fwd_ev(const void* y, const void* w, void* out, uint32_t* starts, uint32_
               int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
               void* workspace, size_t workspace_bytes, void* stream, void* weights_read);
 
+/*
+ * ti_fwd without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. The workspace is a file-scope device array of TI_NOALLOC_SCRATCH_BYTES (64 MiB)
+ * that each GPU the library runs on holds until the process ends; the call allocates nothing
+ * (no hipMalloc, hipFree or allocating library routine). Problem sets whose workspace
+ * (ti_fwd_workspace) exceeds it fail with TI_EWORKSPACE before any launch. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other host threads)
+ * race and must be ordered by the caller. A backward that needs the forward's workspace
+ * (ti_bwd, rows over 32 elements) cannot use this one's, which the next call overwrites; ti_grad
+ * takes the fit and the partition instead. Arguments and results otherwise as ti_fwd.
+ */
+#define TI_NOALLOC_SCRATCH_BYTES (64u << 20)
+int ti_fwd_noalloc(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                   int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+                   void* stream);
+
 /* Bytes of device workspace ti_bwd needs for this problem set (0 when none). */
 int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes);
 

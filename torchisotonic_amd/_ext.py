@@ -40,6 +40,7 @@ SYMBOLS = (
     "ti_fwd_geometry",
     "ti_fwd",
     "ti_fwd_ev",
+    "ti_fwd_noalloc",
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_grad_workspace",
@@ -74,6 +75,8 @@ def load() -> ctypes.CDLL:
     lib.ti_fwd.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_fwd_ev.restype = _int
     lib.ti_fwd_ev.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp]
+    lib.ti_fwd_noalloc.restype = _int
+    lib.ti_fwd_noalloc.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp]
     lib.ti_bwd.restype = _int
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_grad_workspace.restype = _int

@@ -6,6 +6,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "ti_kernels.h"
@@ -76,6 +77,33 @@ __global__ __launch_bounds__(256) void check_weights_kernel(const T* __restrict_
 // torch, forward and backward 161 -> 133 us). Beyond it the second read of w costs more than that
 // gap (1e8 elements: 400 MB).
 constexpr int64_t kEarlyCheckElems = int64_t{1} << 24;
+
+// ti_fwd_noalloc's workspace: one array per device, held from the library's first use on that
+// device until the process ends. In host code its name is only a host-side stand-in; its
+// device address comes from hipGetSymbolAddress (scratch_ptr) and only that address is used.
+static __device__ __align__(256) unsigned char scratch[TI_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up once per device (that device current).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(TI_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(TI_EINVAL, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(TI_ELAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TI_OK;
+}
 
 }  // namespace
 
@@ -168,6 +196,22 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
            void* workspace, size_t workspace_bytes, void* stream) {
   return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, workspace,
                   workspace_bytes, stream, nullptr);
+}
+
+int ti_fwd_noalloc(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                   int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* stream) {
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  const size_t need = n <= ti::kShortMax ? 0 : ti::long_plan(batch, n, w != nullptr).bytes;
+  if (need > TI_NOALLOC_SCRATCH_BYTES)
+    return fail(TI_EWORKSPACE,
+                "ti_fwd_noalloc: this problem set needs %zu bytes of workspace, its scratch holds %zu "
+                "(call ti_fwd with a workspace)",
+                need, static_cast<size_t>(TI_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_ptr(&ws)) return rc;
+  }
+  return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, ws, need, stream, nullptr);
 }
 
 int ti_fwd_ev(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
