@@ -60,7 +60,9 @@ def sync() -> None:
 
 
 def timed_calls(fn, steps: int, warmup: int) -> float:
-    """Seconds per call over `steps` back-to-back calls, bracketed by synchronisations."""
+    """Seconds per call over `steps` back-to-back calls, bracketed by synchronisations (after a
+    short clock-raising load and `warmup` untimed calls)."""
+    warm_gpu(0.05)
     for _ in range(warmup):
         fn()
     sync()
@@ -71,25 +73,27 @@ def timed_calls(fn, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) / steps
 
 
-def kernel_ms(launch, reps: int) -> float:
-    """Mean device time of `launch` over `reps` back-to-back launches: one HIP event pair recorded
-    on the launch stream around all of them, divided by reps. The launches queue behind a few
-    hundred microseconds of other device work first, so the GPU never waits for the host between
-    them and the interval holds kernel time only (an event pair per launch would add its own
-    overhead to every interval)."""
+def kernel_ms(launch, reps: int, repeats: int = 3) -> float:
+    """Device time of `launch` per launch: one HIP event pair recorded on the launch stream
+    around `reps` back-to-back launches, divided by reps; the best of `repeats` such intervals,
+    each after a short clock-raising load. The launches queue behind that load, so the GPU
+    never waits for the host between them and the interval holds kernel time only (an event
+    pair per launch would add its own overhead to every interval)."""
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    busy = torch.empty(1 << 26, device="cuda")
-    launch()  # (first-call set-up outside the interval)
-    sync()
-    for _ in range(6):
-        busy.mul_(1.0)
-    e0.record(stream)
-    for _ in range(reps):
-        launch()
-    e1.record(stream)
-    sync()
-    return e0.elapsed_time(e1) / reps
+    best = float("inf")
+    launch()  # (first-call set-up outside the intervals)
+    for _ in range(repeats):
+        warm_gpu(0.03)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(6):
+            _BUSY.mul_(1.0)
+        e0.record(stream)
+        for _ in range(reps):
+            launch()
+        e1.record(stream)
+        sync()
+        best = min(best, e0.elapsed_time(e1) / reps)
+    return best
 
 
 def copy_ceiling(mbytes: int = 128, reps: int = 50) -> dict:
@@ -102,12 +106,21 @@ def copy_ceiling(mbytes: int = 128, reps: int = 50) -> dict:
     return {"gbps": mbytes * 1e6 / (ms * 1e-3) / 1e9, "bytes": mbytes * 1_000_000, "ms": ms}
 
 
-def warm_gpu() -> None:
+_BUSY: torch.Tensor | None = None
+
+
+def warm_gpu(seconds: float = 0.3) -> None:
     # An idle GPU clocks down; keep it busy first (the reference's method, bench/bench.py:51-55).
-    x = torch.empty(1 << 26, device="cuda")
-    for _ in range(30):
-        x.mul_(1.0)
-    sync()
+    # A few milliseconds are not enough on this part: kernel times keep falling for about a
+    # tenth of a second of load (C2's forward kernel 33.5 -> 31.3 us).
+    global _BUSY
+    if _BUSY is None:
+        _BUSY = torch.empty(1 << 26, device="cuda")
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            _BUSY.mul_(1.0)
+        sync()
 
 
 def rate(elems: int, seconds: float, bytes_per_elem: float) -> dict:
@@ -357,6 +370,7 @@ def main() -> None:
     warm_gpu()
     log("C2 ...")
     c2 = bench_c2(args.steps, args.warmup)
+    ceiling = copy_ceiling()
     extra: dict = {"c2": c2}
     if "c4" in configs:
         log("C4 ...")
@@ -375,7 +389,6 @@ def main() -> None:
     achieved = 8 * elems / (k * 1e-3) / 1e9
     if k > c2["fwd"]["ms"]:
         log(f"warning: kernel time {k:.4f} ms exceeds the API's {c2['fwd']['ms']:.4f} ms per call")
-    ceiling = copy_ceiling()
     line = {
         "metric": METRIC,
         "value": c2["fwd"]["gelem_s"],
