@@ -83,6 +83,14 @@ __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t of
   }
 }
 
+// v, taken from the wave's first lane (for values the same in every lane).
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // A buffer resource over [base, base + bytes) (bytes clamped to the 32-bit range field).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
   const int nrec = static_cast<int>(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
@@ -126,9 +134,13 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   constexpr double sgn = INC ? 1.0 : -1.0;
   // The wave's spans are consecutive elements (of one row, or of its rows), so one buffer
   // resource based at the first of them serves every lane.
-  const int64_t base = packed  ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
-                       : multi ? static_cast<int64_t>(blockIdx.x) * a.rpw * a.n
-                               : row * a.n + grp * kSpanLanes * a.span0;  // wave-uniform
+  // (from the wave's own indices only, and read from the first lane: the compiler then keeps
+  // the buffer resources in scalar registers, where a per-lane value would put every load in a
+  // loop over the lanes' distinct resources)
+  const int64_t wrow = static_cast<int64_t>(blockIdx.x) / a.gpr;  // (one row a wave: its row)
+  const int64_t base = wave_uniform(packed  ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
+                                    : multi ? static_cast<int64_t>(blockIdx.x) * a.rpw * a.n
+                                            : wrow * a.n + (blockIdx.x - wrow * a.gpr) * kSpanLanes * a.span0);
   const int64_t total = batch * a.n;                                      // elements of the array
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + base, (total - base) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(W ? static_cast<const T*>(a.w) + base : a.y, (total - base) * sizeof(T));
@@ -227,6 +239,9 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         const bool close = !(__builtin_fabs(dd) > 0x1p-52 * __builtin_fabs(qq));
         bool pop = two && dd > 0.0;
         if (__any(two && close)) {
+          // (an empty statement with side effects: it keeps this rare path a branch, where the
+          // compiler would otherwise compute the exact test in every iteration and select)
+          asm volatile("");
           if (two && close) pop = cross_sign(dS1, dW2, dS2, dW1) >= 0;
         }
         const bool push = act && !pop;
