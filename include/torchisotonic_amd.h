@@ -184,6 +184,19 @@ int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* 
             void* gy, void* gw, int64_t batch, int64_t n, int dtype, void* workspace,
             size_t workspace_bytes, void* stream);
 
+/*
+ * The calibration step after a fit: out[i] = the piecewise-linear interpolation at x[i] of the
+ * m knots (xp, fp), xp sorted ascending, constant beyond the ends (np.interp's semantics). With
+ * j the first knot at or above x[i] (searchsorted, left) clamped to [1, m - 1]:
+ *   t = clamp((x - xp[j-1]) / max(xp[j] - xp[j-1], 1e-300), 0, 1),
+ *   out = fp[j-1] + t * (fp[j] - fp[j-1]),
+ * each operation rounded once, so equal to the reference's tensor formula bit for bit
+ * (reference examples/ctr_calibration/calibrate.py:163-168, the predict step of its isotonic
+ * calibration). One kernel; x, xp, fp, out of one dtype; NaN x gives NaN.
+ */
+int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m,
+              int dtype, void* stream);
+
 /* Test hook: the starts bit array of a [batch, n] set as bytes (0/1), row-major - the
  * reference's bool starts tensor (reference tests/test_cuda.py:176 reads it). */
 int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n,

@@ -159,3 +159,88 @@ def block_grad(
     if rc != 0:
         raise RuntimeError(f"oracle grad failed ({rc})")
     return gy.reshape(shape), None if gw is None else gw.reshape(shape)
+
+
+# --- consumers either side of the fit ------------------------------------------------------------
+
+
+def soft_rank(x: np.ndarray, eps: float, dtype: type = np.float64) -> tuple[np.ndarray, np.ndarray]:
+    """L2 soft ranks of every row of ``x`` ([batch, n]) with regularisation ``eps``, as the
+    reference wires torchsort's SoftRank to the isotonic solver (reference
+    paper/soft_rank.py:31-55; Blondel et al. 2020): w = (n, ..., 1), s = sort(x * (1 / eps))
+    descending, dual = the decreasing isotonic fit of z = s - w (float64 PAVA of z), ranks =
+    s - dual in x's order. The tensor steps round in ``dtype`` as the GPU pipeline does (for
+    float32: the scaled keys, z, the dual once from float64, the ranks). Returns the ranks and
+    the dual's block starts (in sorted order)."""
+    x = np.asarray(x).astype(dtype)
+    n = x.shape[-1]
+    theta = (x * dtype(1.0 / eps)).astype(dtype)
+    perm = np.argsort(-theta, axis=-1, kind="stable")
+    s = np.take_along_axis(theta, perm, -1)
+    z = (s - np.arange(n, 0, -1).astype(dtype)).astype(dtype)
+    dual, starts = pava(z.astype(np.float64), increasing=False, acc="f64")
+    ranks = np.empty_like(s)
+    np.put_along_axis(ranks, perm, (s - dual.astype(dtype)).astype(dtype), -1)
+    return ranks, starts
+
+
+def soft_rank_vjp(x: np.ndarray, eps: float, g: np.ndarray, dtype: type = np.float64) -> np.ndarray:
+    """The vector-Jacobian product of ``soft_rank`` for the upstream gradient ``g`` (float64):
+    with A the block-averaging map of the dual's partition (in sorted order),
+    dx = (g - P^T A P g) / eps (reference paper/soft_rank.py:47-54)."""
+    x = np.asarray(x).astype(dtype)
+    g = np.asarray(g, dtype=np.float64)
+    theta = (x * dtype(1.0 / eps)).astype(dtype)
+    perm = np.argsort(-theta, axis=-1, kind="stable")
+    _, starts = soft_rank(x, eps, dtype)
+    gs = np.take_along_axis(g, perm, -1)
+    avg, _ = block_grad(starts, gs)
+    back = np.empty_like(avg)
+    np.put_along_axis(back, perm, avg, -1)
+    return (g - back) * (1.0 / eps)
+
+
+def calibration_fit(
+    keys: np.ndarray,
+    y: np.ndarray,
+    weight: np.ndarray | None = None,
+    offset: np.ndarray | None = None,
+    increasing: bool = True,
+) -> tuple[np.ndarray, np.ndarray]:
+    """The knots (xp, fp) of an isotonic calibration (reference examples/ctr_calibration/
+    calibrate.py:171-187): sort the keys, pool equal keys into their (weighted) mean with their
+    count (total weight) as weight, fit float64 PAVA over the unique keys; ``offset`` (per
+    element) is added to the pooled means before the fit and subtracted after."""
+    keys = np.asarray(keys, dtype=np.float64)
+    y = np.asarray(y, dtype=np.float64)
+    order = np.argsort(keys, kind="stable")
+    ks, ys = keys[order], y[order]
+    w = np.ones_like(ys) if weight is None else np.asarray(weight, dtype=np.float64)[order]
+    xp, first, inverse = np.unique(ks, return_index=True, return_inverse=True)
+    sums = np.add.reduceat(w * ys, first)
+    weights = np.add.reduceat(w, first)
+    means = sums / weights
+    shift = np.zeros_like(means)
+    if offset is not None:
+        shift[inverse] = np.asarray(offset, dtype=np.float64)[order]
+    fit, _ = pava((means + shift)[None], weights[None], increasing=increasing, acc="f64")
+    return xp, fit[0] - shift
+
+
+def interp(x: np.ndarray, xp: np.ndarray, fp: np.ndarray) -> np.ndarray:
+    """Piecewise-linear interpolation through (xp, fp), constant beyond the ends, restating the
+    reference's tensor formula operation for operation (reference examples/ctr_calibration/
+    calibrate.py:163-168): j = searchsorted(xp, x) clamped to [1, m - 1],
+    t = clamp((x - xp[j-1]) / max(xp[j] - xp[j-1], 1e-300), 0, 1), fp[j-1] + t (fp[j] - fp[j-1])."""
+    x = np.asarray(x)
+    xp = np.asarray(xp, dtype=x.dtype)
+    fp = np.asarray(fp, dtype=x.dtype)
+    m = len(xp)
+    if m == 1:
+        return np.where(np.isnan(x), x, fp[0]).astype(x.dtype)
+    j = np.clip(np.searchsorted(xp, x, side="left"), 1, m - 1)
+    x0, x1, f0, f1 = xp[j - 1], xp[j], fp[j - 1], fp[j]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = (x - x0) / np.maximum(x1 - x0, x.dtype.type(1e-300))
+    t = np.where(t < 0, x.dtype.type(0), np.where(t > 1, x.dtype.type(1), t))
+    return (f0 + t * (f1 - f0)).astype(x.dtype)

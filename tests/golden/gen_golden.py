@@ -16,6 +16,10 @@ concatenated with an offsets array. Everything is float64 and loads with
   bound means "not given").
 - scipy_long.npz: long structured rows of the reference's tests/test_isotonic.py:103-117
   patterns (at n = 20000) and their scipy fits.
+- sklearn_calib.npz: ``sklearn.isotonic.IsotonicRegression`` fit on keys with ties (pooled
+  into their weighted mean, as the reference's calibration example does,
+  examples/ctr_calibration/calibrate.py:171-187) and its predictions (``out_of_bounds="clip"``,
+  piecewise linear) at new points.
 """
 
 from __future__ import annotations
@@ -99,6 +103,44 @@ def sklearn_clip(count: int = 300, seed: int = 2) -> None:
     )
 
 
+def sklearn_calib(count: int = 120, seed: int = 3) -> None:
+    """Isotonic calibration (sklearn's IsotonicRegression fit, then predict with
+    out_of_bounds="clip"): keys with ties (rounded), labels 0/1 or real values, optional
+    weights, both directions; predictions at points inside, at and beyond the knots."""
+    from sklearn.isotonic import IsotonicRegression
+
+    rng = np.random.default_rng(seed)
+    keys, ys, ws, qs, ps, inc, weighted = [], [], [], [], [], [], []
+    for k in range(count):
+        n = int(rng.integers(1, 200))
+        x = np.round(rng.normal(0.0, 1.0, n), int(rng.integers(1, 4)))
+        if k % 3 == 0:
+            y = (rng.random(n) < 1 / (1 + np.exp(-2 * x))).astype(np.float64)
+        else:
+            y = np.round(x + rng.normal(0.0, 0.7, n), 3)
+        w = None if k % 2 == 0 else rng.uniform(0.1, 5.0, n)
+        increasing = bool(k % 4 != 1)
+        model = IsotonicRegression(increasing=increasing, out_of_bounds="clip").fit(x, y, sample_weight=w)
+        q = np.concatenate([rng.normal(0.0, 1.5, 50), np.unique(x), [x.min() - 1, x.max() + 1]])
+        keys.append(x)
+        ys.append(y)
+        ws.append(np.ones_like(y) if w is None else w)
+        weighted.append(w is not None)
+        qs.append(q)
+        ps.append(np.asarray(model.predict(q), dtype=np.float64))
+        inc.append(increasing)
+    x, off = pack(keys)
+    y, _ = pack(ys)
+    w, _ = pack(ws)
+    q, qoff = pack(qs)
+    pr, _ = pack(ps)
+    np.savez_compressed(
+        HERE / "sklearn_calib.npz",
+        x=x, y=y, w=w, offsets=off, q=q, pred=pr, q_offsets=qoff,
+        increasing=np.array(inc), weighted=np.array(weighted),
+    )
+
+
 def long_patterns(n: int = 20000) -> np.ndarray:
     i = np.arange(n, dtype=np.float64)
     return np.stack([i, -i, (-1.0) ** i * i, np.full(n, 2.5), i % 97 - i / 1000])
@@ -118,5 +160,6 @@ if __name__ == "__main__":
     scipy_fits()
     sklearn_clip()
     scipy_long()
+    sklearn_calib()
     for f in sorted(HERE.glob("*.npz")):
         print(f.name, f.stat().st_size)

@@ -1,0 +1,158 @@
+"""The consumers either side of the fit on the GPU against the oracle: soft ranks forward and
+backward at the reference's shapes and strengths (reference paper/soft_rank.py:22-28), and
+isotonic calibration (fit over pooled keys, then interpolation) against the oracle and
+scikit-learn's IsotonicRegression (committed golden vectors)."""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from torchisotonic_amd import _ext
+from torchisotonic_amd.calibration import IsotonicCalibrator, calibration_fit, calibration_predict
+from torchisotonic_amd.soft_rank import soft_rank
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def say(*a: object) -> None:
+    print(*a, flush=True)
+
+
+# (batch, n): the reference's soft-rank shapes, and strengths 1 and 1/n
+SHAPES = [(1024, 100), (256, 1000), (64, 10_000), (8, 100_000), (1, 1_000_000)]
+
+
+@pytest.mark.parametrize(("batch", "n"), SHAPES)
+@pytest.mark.parametrize("strength", ["1", "1/n"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_soft_rank_matches_oracle(batch: int, n: int, strength: str, dtype: torch.dtype) -> None:
+    eps = 1.0 if strength == "1" else 1.0 / n
+    say(f"soft rank {batch}x{n} eps={strength} {dtype}")
+    gen = torch.Generator().manual_seed(batch + n)
+    x = torch.randn(batch, n, generator=gen, dtype=torch.float64)
+    g = torch.randn(batch, n, generator=gen, dtype=torch.float64)
+    xr = x.to(dtype).cuda().requires_grad_()
+    r = soft_rank(xr, eps)
+    (dx,) = torch.autograd.grad(r, xr, g.to(dtype).cuda())
+    # the oracle on the same inputs, its tensor steps rounded in the same dtype (so its dual
+    # has the GPU's partition); sums and the fit in float64
+    npdt = np.float32 if dtype == torch.float32 else np.float64
+    xx = xr.detach().cpu().numpy()
+    want, _ = oracle.soft_rank(xx, eps, npdt)
+    want_dx = oracle.soft_rank_vjp(xx, eps, g.to(dtype).double().numpy(), npdt)
+    scale = max(float(np.abs(xx).max()) / eps, float(n))  # the largest sort key or rank
+    if dtype == torch.float64:
+        tol_r, tol_g = 1e-12 * scale, 1e-10  # (the float64 fit bar: 1e-12 of the data scale)
+    else:
+        # float32: the dual is the float64 fit rounded once, the ranks one float32 difference
+        tol_r, tol_g = 4 * 2.0**-23 * scale, 2e-5
+    np.testing.assert_allclose(r.detach().double().cpu().numpy(), want.astype(np.float64), rtol=0, atol=tol_r)
+    scale = float(np.abs(want_dx).max())
+    np.testing.assert_allclose(dx.double().cpu().numpy(), want_dx, rtol=tol_g, atol=tol_g * scale)
+
+
+def test_soft_rank_limits_and_gradcheck() -> None:
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(6, 50, generator=gen, dtype=torch.float64).cuda()
+    hard = torch.argsort(torch.argsort(x, -1), -1).double() + 1
+    # (s - (s - w) with s near 1e9 is w to within the float64 spacing there)
+    torch.testing.assert_close(soft_rank(x, 1e-9), hard, rtol=0, atol=1e-6)
+    torch.testing.assert_close(soft_rank(x, 1e9), torch.full_like(x, 25.5), rtol=0, atol=1e-6)
+    torch.testing.assert_close(soft_rank(x, 0.3).sum(-1), torch.full((6,), 50 * 51 / 2, dtype=torch.float64, device="cuda"))
+    xs = torch.randn(2, 12, generator=gen, dtype=torch.float64).cuda().requires_grad_()
+    assert torch.autograd.gradcheck(lambda t: soft_rank(t, 0.7), (xs,))
+
+
+def test_soft_rank_backward_twice() -> None:
+    # the graph is kept (as in the reference), so a second backward works
+    x = torch.randn(3, 40, dtype=torch.float64, device="cuda").requires_grad_()
+    r = soft_rank(x, 0.5)
+    g = torch.randn_like(r)
+    (a,) = torch.autograd.grad(r, x, g, retain_graph=True)
+    (b,) = torch.autograd.grad(r, x, g)
+    torch.testing.assert_close(a, b, rtol=0, atol=0)
+
+
+# --- calibration ----------------------------------------------------------------------------------
+
+
+def golden_calib():
+    d = np.load(GOLDEN / "sklearn_calib.npz", allow_pickle=False)
+    off, qoff = d["offsets"], d["q_offsets"]
+    for k in range(len(off) - 1):
+        sl, ql = slice(off[k], off[k + 1]), slice(qoff[k], qoff[k + 1])
+        w = d["w"][sl] if d["weighted"][k] else None
+        yield d["x"][sl], d["y"][sl], w, bool(d["increasing"][k]), d["q"][ql], d["pred"][ql]
+
+
+def test_calibration_matches_sklearn_golden() -> None:
+    say("calibration: sklearn golden vectors")
+    for x, y, w, inc, q, pred in golden_calib():
+        cal = IsotonicCalibrator(increasing=inc).fit(
+            torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda(), None if w is None else torch.from_numpy(w).cuda()
+        )
+        got = cal.predict(torch.from_numpy(q).cuda()).cpu().numpy()
+        np.testing.assert_allclose(got, pred, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("n", [1000, 200_000, 5_000_000])
+def test_calibration_matches_oracle(n: int) -> None:
+    # scores with heavy ties (rounded), 0/1 labels, optional weights: knots against the oracle,
+    # predictions bit for bit against the oracle's restatement of the reference formula
+    say(f"calibration n={n}")
+    rng = np.random.default_rng(n)
+    s = np.round(rng.normal(0.0, 1.5, n), 3)
+    y = (rng.random(n) < 1 / (1 + np.exp(-s))).astype(np.float64)
+    w = rng.uniform(0.5, 2.0, n)
+    for ww in (None, w):
+        xp, fp = calibration_fit(torch.from_numpy(s).cuda(), torch.from_numpy(y).cuda(),
+                                 None if ww is None else torch.from_numpy(ww).cuda())
+        wxp, wfp = oracle.calibration_fit(s, y, ww)
+        np.testing.assert_array_equal(xp.cpu().numpy(), wxp)
+        np.testing.assert_allclose(fp.cpu().numpy(), wfp, rtol=0, atol=1e-12)
+        q = np.concatenate([rng.normal(0.0, 2.0, 100_000), wxp, [np.nan, -np.inf, np.inf]])
+        got = calibration_predict(torch.from_numpy(q).cuda(), xp, fp).cpu().numpy()
+        want = oracle.interp(q, xp.cpu().numpy(), fp.cpu().numpy())
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_interp_kernel_is_the_reference_formula(dtype: torch.dtype) -> None:
+    # ti_interp against the reference's tensor formula (calibrate.py:163-168) run with torch
+    # ops on the same inputs, bit for bit, and against the oracle
+    say(f"interp kernel {dtype}")
+    gen = torch.Generator().manual_seed(5)
+    xp = torch.sort(torch.randn(777, generator=gen, dtype=torch.float64))[0].to(dtype)
+    fp = torch.cumsum(torch.rand(777, generator=gen, dtype=torch.float64), 0).to(dtype)
+    x = (torch.randn(300_000, generator=gen, dtype=torch.float64) * 2).to(dtype)
+    xd, xpd, fpd = x.cuda(), xp.cuda(), fp.cuda()
+    i = torch.searchsorted(xpd, xd).clamp(1, len(xpd) - 1)
+    x0, x1, f0, f1 = xpd[i - 1], xpd[i], fpd[i - 1], fpd[i]
+    t = ((xd - x0) / (x1 - x0).clamp_min(1e-300)).clamp(0, 1)
+    ref = f0 + t * (f1 - f0)
+    got = _ext.interp(xd, xpd, fpd)
+    assert torch.equal(got, ref)
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle.interp(x.numpy(), xp.numpy(), fp.numpy()))
+    # one knot, and NaN
+    one = _ext.interp(torch.tensor([-1.0, 3.0, float("nan")], dtype=dtype, device="cuda"),
+                      torch.tensor([0.5], dtype=dtype, device="cuda"), torch.tensor([2.0], dtype=dtype, device="cuda"))
+    assert one[:2].tolist() == [2.0, 2.0] and torch.isnan(one[2])
+
+
+def test_calibration_offsets_fit_segments_at_once() -> None:
+    # the reference's per-segment calibration: one fit, segments kept apart by offsets
+    rng = np.random.default_rng(6)
+    keys = np.r_[rng.random(500), rng.random(500) + 3.0]
+    y = np.r_[(rng.random(500) < 0.3), (rng.random(500) < 0.7)].astype(np.float64)
+    off = np.r_[np.zeros(500), np.full(500, 1e3)]
+    xp, fp = calibration_fit(torch.from_numpy(keys).cuda(), torch.from_numpy(y).cuda(), offset=torch.from_numpy(off).cuda())
+    wxp, wfp = oracle.calibration_fit(keys, y, offset=off)
+    np.testing.assert_array_equal(xp.cpu().numpy(), wxp)
+    np.testing.assert_allclose(fp.cpu().numpy(), wfp, rtol=0, atol=1e-12)

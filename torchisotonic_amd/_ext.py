@@ -45,6 +45,7 @@ SYMBOLS = (
     "ti_bwd",
     "ti_grad_workspace",
     "ti_grad",
+    "ti_interp",
     "ti_starts_to_bool",
 )
 
@@ -83,6 +84,8 @@ def load() -> ctypes.CDLL:
     lib.ti_grad_workspace.argtypes = [_i64, _i64, _int, ctypes.POINTER(_sz)]
     lib.ti_grad.restype = _int
     lib.ti_grad.argtypes = [_vp] * 7 + [_i64, _i64, _int, _vp, _sz, _vp]
+    lib.ti_interp.restype = _int
+    lib.ti_interp.argtypes = [_vp] * 4 + [_i64, _i64, _int, _vp]
     lib.ti_starts_to_bool.restype = _int
     lib.ti_starts_to_bool.argtypes = [_vp, _vp, _i64, _i64, _vp]
     got = lib.ti_abi_version()
@@ -309,6 +312,24 @@ def grad(
         )
     _check(rc, "grad")
     return gy, gw
+
+
+def interp(x: Tensor, xp: Tensor, fp: Tensor) -> Tensor:
+    """Piecewise-linear interpolation of the knots (xp, fp) at x (one kernel, ti_interp): the
+    reference calibration example's interp (reference examples/ctr_calibration/calibrate.py:
+    163-168) bit for bit. x of any shape; xp, fp 1-D of one length, xp ascending."""
+    _on_gpu(x, "x")
+    if xp.dim() != 1 or fp.shape != xp.shape or xp.numel() == 0:
+        raise RuntimeError("torchisotonic_amd.interp: xp and fp must be 1-D, non-empty and of one length")
+    dtype = _dtype_code(x)
+    xc = x.contiguous()
+    xpc = xp.to(device=x.device, dtype=x.dtype).contiguous()
+    fpc = fp.to(device=x.device, dtype=x.dtype).contiguous()
+    out = torch.empty_like(xc)
+    with _on_device(x.device):
+        rc = load().ti_interp(_ptr(xc), _ptr(xpc), _ptr(fpc), _ptr(out), xc.numel(), xpc.numel(), dtype, _stream(xc))
+    _check(rc, "interp")
+    return out
 
 
 def starts_to_bool(starts: Tensor, batch: int, n: int) -> Tensor:

@@ -288,6 +288,15 @@ int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* 
   return launched(ti::seg_grad(a, workspace), "stateless gradient");
 }
 
+int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m, int dtype,
+              void* stream) {
+  if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
+  if (n < 0 || m < 1) return fail(TI_EINVAL, "need n >= 0 and m >= 1 knots, got n=%lld m=%lld", (long long)n, (long long)m);
+  if (n == 0) return ok();
+  if (x == nullptr || xp == nullptr || fp == nullptr || out == nullptr) return fail(TI_EINVAL, "null pointer");
+  return launched(ti::interp(x, xp, fp, out, n, m, dtype, static_cast<hipStream_t>(stream)), "interp");
+}
+
 int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n, void* stream) {
   if (batch < 0 || n < 0) return fail(TI_EINVAL, "negative size");
   if (batch == 0 || n == 0) return ok();

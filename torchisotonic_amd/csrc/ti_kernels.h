@@ -38,6 +38,10 @@ struct ShortGradArgs {
   hipStream_t stream;
 };
 
+// Calibration: piecewise-linear interpolation of (xp, fp) (m knots, xp sorted) at n points.
+hipError_t interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m, int dtype,
+                  hipStream_t stream);
+
 int64_t short_grid(int64_t batch, int64_t n, bool weighted);
 hipError_t short_fit(const ShortArgs& a);
 hipError_t short_grad(const ShortGradArgs& a);
