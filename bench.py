@@ -1,14 +1,16 @@
 """Throughput of the isotonic hot path on one MI355X, against the HBM roofline, with the
 reference CPU solver timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3[,grid]] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3,next[,grid]] [--no-cpu]
 
 Prints ONE JSON line. The headline ``value`` is BASELINE config C2: a forward
 ``torchisotonic_amd.isotonic`` of float32 y[1e6, 16] = -0.1 i + N(0, 1), unweighted,
 decreasing, inputs resident in HBM, K back-to-back calls of the public API between device
 synchronisations (Gelem/s = 1.6e7 K / seconds). ``extra`` holds the metric's other legs - C2
 forward+backward (dy), C4 (one row of 1e8, weighted 0/1 labels, integer counts) forward and
-forward+backward (dy, dw) - and the other BASELINE configs (C5 bootstrap, C1, C3). With
+forward+backward (dy, dw) - the other BASELINE configs (C5 bootstrap, C1, C3), and the rows
+either side of the path (``next``: C2's rows at their own lengths with offsets, soft ranks,
+calibration). With
 ``--configs ...,grid`` (not in the default run) ``extra.grid`` also times the reference's own
 README table: its (batch, n) grid and data, each call synchronised, median and best of ten.
 
@@ -245,6 +247,91 @@ def bench_c1_c3(steps: int, warmup: int) -> dict:
     return res
 
 
+# --- the rows either side of the path: ragged rows, soft ranks, calibration -------------------
+
+
+def bench_next(steps: int, warmup: int) -> dict:
+    """The consumers around the fit, timed like the configs above (back-to-back calls of the
+    public API between synchronisations): C2's rows at their own lengths (len ~ U{4..16}, seed 2;
+    the padded variant is the C2 forward above), packed with offsets, forward and forward+backward
+    (8 and 16 B per element); soft ranks at the reference's shapes and strengths (reference
+    paper/soft_rank.py:23-28; x, g ~ N(0, 1) float32); and calibration (fit over pooled keys,
+    then interpolation) of 6.5 million float32 scores, about one day of the reference's Criteo
+    example (examples/ctr_calibration/calibrate.py:171-187)."""
+    res: dict = {}
+    rng = np.random.default_rng(0)
+    b, n = 1_000_000, 16
+    y = (-0.1 * np.arange(n) + rng.standard_normal((b, n))).astype(np.float32)
+    lens = np.random.default_rng(2).integers(4, n + 1, b)
+    packed = torch.from_numpy(y[np.arange(n)[None, :] < lens[:, None]]).cuda()
+    off = torch.from_numpy(np.r_[0, np.cumsum(lens)]).cuda()
+    g = torch.randn_like(packed)
+    elems = packed.numel()
+    fwd = lambda: torchisotonic_amd.isotonic_ragged(packed, off, increasing=False)  # noqa: E731
+    pr = packed.detach().requires_grad_()
+
+    def fb() -> None:
+        torch.autograd.grad(torchisotonic_amd.isotonic_ragged(pr, off, increasing=False), pr, g)
+
+    lib = _ext.load()
+    out = torch.empty_like(packed)
+    bits = torch.zeros((elems + 31) // 32, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    raw = lambda: lib.ti_fwd_ragged(packed.data_ptr(), None, out.data_ptr(), None, None, off.data_ptr(), b, n, 0, 0, 0.0, 0.0, s)  # noqa: E731
+    assert raw() == 0
+    res["c2_ragged"] = {
+        "elems": elems,
+        "fwd": rate(elems, timed_calls(fwd, steps, warmup), 8),
+        "fwd_bwd": rate(elems, timed_calls(fb, steps, warmup), 16),
+        "kernel_ms": {"ragged_fit_kernel<float,16,unweighted> (no starts)": kernel_ms(raw, 100)},
+    }
+    del bits
+    soft = {}
+    for sb, sn in ((1024, 100), (256, 1000), (64, 10_000), (8, 100_000), (1, 1_000_000)):
+        torch.manual_seed(0)
+        x = torch.randn(sb, sn, device="cuda")
+        gx = torch.randn(sb, sn, device="cuda")
+        for name, eps in (("1", 1.0), ("1/n", 1.0 / sn)):
+            xr = x.detach().requires_grad_()
+
+            def sfb(xr=xr, eps=eps, gx=gx) -> None:
+                torch.autograd.grad(torchisotonic_amd.soft_rank(xr, eps), xr, gx)
+
+            soft[f"{sb}x{sn} eps={name}"] = {
+                "fwd_ms": 1e3 * timed_calls(lambda x=x, eps=eps: torchisotonic_amd.soft_rank(x, eps), steps, warmup),
+                "fwd_bwd_ms": 1e3 * timed_calls(sfb, steps, warmup),
+            }
+    res["soft_rank"] = soft
+    m = 6_500_000
+    cr = np.random.default_rng(3)
+    logit = cr.normal(-1.2, 1.5, m)
+    scores = torch.from_numpy((1 / (1 + np.exp(-logit))).astype(np.float32)).cuda()
+    labels = torch.from_numpy((cr.random(m) < 1 / (1 + np.exp(-(logit * 0.8 + 0.3)))).astype(np.float32)).cuda()
+    t_fit = timed_calls(lambda: torchisotonic_amd.calibration_fit(scores, labels), max(5, steps // 4), 1)
+    xp, fp = torchisotonic_amd.calibration_fit(scores, labels)
+    q = scores.double()
+    interp_out = torch.empty_like(q)
+    ilaunch = lambda: lib.ti_interp(q.data_ptr(), xp.data_ptr(), fp.data_ptr(), interp_out.data_ptr(), m, xp.numel(), _ext.F64, s)  # noqa: E731
+    assert ilaunch() == 0
+    k = kernel_ms(ilaunch, 50)
+
+    def torch_interp() -> torch.Tensor:  # the reference's tensor formula (calibrate.py:163-168)
+        i = torch.searchsorted(xp, q).clamp(1, xp.numel() - 1)
+        x0, x1, f0, f1 = xp[i - 1], xp[i], fp[i - 1], fp[i]
+        return f0 + ((q - x0) / (x1 - x0).clamp_min(1e-300)).clamp(0, 1) * (f1 - f0)
+
+    res["calibration"] = {
+        "scores": m,
+        "knots": xp.numel(),
+        "fit_ms": 1e3 * t_fit,
+        "predict": rate(m, timed_calls(lambda: torchisotonic_amd.calibration_predict(q, xp, fp), steps, warmup), 16),
+        "interp_kernel_ms": k,
+        "interp_kernel_pct_roofline": 100 * 16 * m / (k * 1e-3) / 1e9 / PEAK_GBPS,
+        "interp_torch_formula_ms": 1e3 * timed_calls(torch_interp, steps, warmup),
+    }
+    return res
+
+
 # The reference's README table: its grid (reference bench/bench.py:31-33) and data (:108-110):
 # float32 rows of a noisy trend, reversed, fitted decreasing and unweighted.
 GRID = [(1_000_000, 16), (100_000, 128), (10_000, 1_000), (1_000, 10_000), (100, 100_000),
@@ -353,7 +440,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c2,c4,c5,c1,c3")
+    ap.add_argument("--configs", default="c2,c4,c5,c1,c3,next")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -381,6 +468,9 @@ def main() -> None:
     if "c1" in configs or "c3" in configs:
         log("C1/C3 ...")
         extra["c1_c3"] = bench_c1_c3(max(20, args.steps), 2)
+    if "next" in configs:
+        log("ragged rows, soft ranks, calibration ...")
+        extra.update(bench_next(args.steps, args.warmup))
     if "grid" in configs:
         log("README grid ...")
         extra["grid"] = bench_grid()

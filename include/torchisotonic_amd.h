@@ -159,6 +159,33 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
            int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
            size_t workspace_bytes, void* stream);
 
+/*
+ * The fit of ragged rows, packed end to end: row r is y[offsets[r], offsets[r + 1]) (offsets:
+ * nrows + 1 non-decreasing device int64 values). Rows of 1 to max_len elements (max_len <= 32)
+ * are fitted in one launch (one thread per row, no padding pass); a longer row is not fitted
+ * (its elements of out are not written) and gets its first start bit only, and an empty row
+ * nothing, so the caller fits longer rows by other calls (ti_fwd on each). No counterpart in
+ * the reference, whose callers pad ragged rows or lay them end to end (reference README.md:
+ * 100-103, examples/ctr_calibration/README.md:25-27).
+ *   starts  flat bits of the packed array: bit e (word e / 32, bit e % 32) set where a block
+ *           starts, OR-ed into the caller's zeroed array of (offsets[nrows] + 31) / 32 words;
+ *           or NULL. ti_grad over the packed array as one row (batch 1) takes these bits.
+ *   other arguments as ti_fwd (flags, clamp, bad_weight for the fitted rows' weights).
+ */
+int ti_fwd_ragged(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                  const int64_t* offsets, int64_t nrows, int64_t max_len, int dtype, unsigned flags,
+                  double y_min, double y_max, void* stream);
+
+/*
+ * The plan of a ragged set, one pass over its offsets (device int64, nrows + 1 values), into
+ * four device words the caller has zeroed: plan[0] bit 0 set if offsets[0] != 0, bit 1 if
+ * offsets[nrows] != total, bit 2 if a row has a negative length (offsets decrease); plan[1] the
+ * longest row of at most 32 elements (the max_len ti_fwd_ragged takes), plan[2] the number of
+ * longer rows, plan[3] the longest row. The host reads them back to validate the offsets and
+ * size the launches. No counterpart in the reference (see ti_fwd_ragged).
+ */
+int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, void* stream);
+
 /* Bytes of device workspace ti_grad needs for this problem set (0 when batch * n <= 2048). */
 int ti_grad_workspace(int64_t batch, int64_t n, int dtype, size_t* bytes);
 

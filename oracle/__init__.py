@@ -244,3 +244,29 @@ def interp(x: np.ndarray, xp: np.ndarray, fp: np.ndarray) -> np.ndarray:
         t = (x - x0) / np.maximum(x1 - x0, x.dtype.type(1e-300))
     t = np.where(t < 0, x.dtype.type(0), np.where(t > 1, x.dtype.type(1), t))
     return (f0 + t * (f1 - f0)).astype(x.dtype)
+
+
+def pava_ragged(
+    values: np.ndarray,
+    offsets: np.ndarray,
+    w: np.ndarray | None = None,
+    increasing: bool = True,
+    acc: str = "f64",
+) -> tuple[np.ndarray, np.ndarray]:
+    """The isotonic fit of every row of a ragged set (row r is values[offsets[r]:offsets[r+1]])
+    and the flat block starts (uint8, packed like values): ``pava`` of each row on its own, the
+    rows grouped by length so that each length is one batched call."""
+    values = np.asarray(values)
+    offsets = np.asarray(offsets, dtype=np.int64)
+    lengths = np.diff(offsets)
+    fit = np.empty(values.shape, dtype=np.float64 if acc in ("f64", "f64x") else values.dtype)
+    starts = np.zeros(values.shape, dtype=np.uint8)
+    for n in np.unique(lengths):
+        if n == 0:
+            continue
+        rows = np.flatnonzero(lengths == n)
+        idx = offsets[rows][:, None] + np.arange(n)[None, :]
+        f, s = pava(values[idx], None if w is None else np.asarray(w)[idx], increasing=increasing, acc=acc)
+        fit[idx] = f
+        starts[idx] = s
+    return fit, starts

@@ -1,0 +1,182 @@
+"""Ragged rows (packed end to end with offsets) on the GPU against the oracle's per-row fits:
+short rows in one launch and longer rows through the regular kernels, with block starts, the
+backward (the stateless gradient over the packed array), the clamp, and C2's padded variant
+(lengths U{4..16}: a padded row's first len_b fitted values equal the ragged row's fit;
+reference README.md:100-103)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import tolerance
+from torchisotonic_amd import _ext, isotonic, isotonic_ragged
+from torchisotonic_amd import ragged as rg
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a: object) -> None:
+    print(*a, flush=True)
+
+
+def ragged_set(lengths: np.ndarray, dtype: type, seed: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    rng = np.random.default_rng(seed)
+    off = np.zeros(len(lengths) + 1, dtype=np.int64)
+    np.cumsum(lengths, out=off[1:])
+    pos = np.arange(off[-1]) - np.repeat(off[:-1], lengths)  # index within the row
+    y = (0.1 * pos + rng.standard_normal(off[-1])).astype(dtype)
+    w = (rng.random(off[-1]) + 0.1).astype(dtype)
+    return y, w, off
+
+
+def run(y: np.ndarray, w: np.ndarray | None, off: np.ndarray, increasing: bool):
+    yt = torch.from_numpy(y).cuda()
+    wt = None if w is None else torch.from_numpy(w).cuda()
+    off_t, short_max, spans, bits, bad = rg._offsets(torch.from_numpy(off).cuda(), None, yt, wt is not None)
+    out, long_rows = rg._fit(yt, wt, off_t, short_max, spans, bits, bad, increasing)
+    starts = _ext.starts_to_bool(bits, 1, len(y))[0].cpu().numpy().astype(np.uint8)
+    for a, b, s, _ in long_rows:  # a longer row's own partition
+        starts[a:b] = _ext.starts_to_bool(s, 1, b - a)[0].cpu().numpy()
+    return out.cpu().numpy(), starts
+
+
+def check(y, w, off, increasing):
+    got, starts = run(y, w, off, increasing)
+    want, want_starts = oracle.pava_ragged(y, off, w, increasing=increasing, acc="f64")
+    assert got.dtype == y.dtype
+    diff = np.abs(got.astype(np.float64) - want)
+    assert diff.size == 0 or float(diff.max()) <= tolerance(y), (float(diff.max()), tolerance(y))
+    np.testing.assert_array_equal(starts, want_starts)
+
+
+LENGTH_SETS = {
+    "1..32": lambda rng: rng.integers(1, 33, 20_000),
+    "0..40": lambda rng: rng.integers(0, 41, 5_000),     # empty rows, and rows past 32
+    "ones": lambda rng: np.ones(3_000, dtype=np.int64),
+    "mixed": lambda rng: np.r_[rng.integers(1, 9, 3000), [33, 1000, 70_000], rng.integers(1, 33, 3000), [0, 0]],
+    "long": lambda rng: np.array([40, 5000, 33]),        # no short row
+}
+
+
+@pytest.mark.parametrize("lengths", list(LENGTH_SETS))
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("increasing", [True, False])
+def test_matches_oracle(lengths: str, dtype: type, weighted: bool, increasing: bool) -> None:
+    say(f"ragged {lengths} {np.dtype(dtype).name} weighted={weighted} increasing={increasing}")
+    rng = np.random.default_rng(len(lengths) * 7 + weighted)
+    ln = LENGTH_SETS[lengths](rng).astype(np.int64)
+    y, w, off = ragged_set(ln, dtype, int(ln.sum()))
+    check(y, w if weighted else None, off, increasing)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_unaligned_base(dtype: type) -> None:
+    # values starting one element past a 16-byte boundary: the kernel stages element by element
+    rng = np.random.default_rng(9)
+    ln = rng.integers(0, 20, 4000)
+    y, w, off = ragged_set(ln, dtype, 9)
+    big = torch.from_numpy(np.r_[np.zeros(1, dtype=dtype), y]).cuda()
+    wb = torch.from_numpy(np.r_[np.ones(1, dtype=dtype), w]).cuda()
+    assert big[1:].data_ptr() % 16 != 0
+    for ww, wt in ((None, None), (w, wb[1:])):
+        got = isotonic_ragged(big[1:], torch.from_numpy(off).cuda(), weight=wt).cpu().numpy()
+        want, _ = oracle.pava_ragged(y, off, ww, acc="f64")
+        assert float(np.abs(got.astype(np.float64) - want).max()) <= tolerance(y)
+
+
+def test_nan_rows_and_ties() -> None:
+    # a NaN row is all NaN with its first start only; its neighbours are untouched; ties pool
+    y, _, off = ragged_set(np.array([5, 7, 3, 40, 6]), np.float64, 3)
+    y[off[1] + 2] = np.nan
+    y[off[3] + 10] = np.nan
+    y[off[4]:off[5]] = 1.0
+    got, starts = run(y, None, off, True)
+    for r in (1, 3):
+        assert np.isnan(got[off[r]:off[r + 1]]).all()
+        assert starts[off[r]] == 1 and not starts[off[r] + 1:off[r + 1]].any()
+    for r in (0, 2):
+        want, ws = oracle.pava(y[off[r]:off[r + 1]][None], acc="f64")
+        np.testing.assert_allclose(got[off[r]:off[r + 1]], want[0], rtol=0, atol=1e-12)
+        np.testing.assert_array_equal(starts[off[r]:off[r + 1]], ws[0])
+    assert (got[off[4]:] == 1.0).all() and starts[off[4]:].tolist() == [1, 0, 0, 0, 0, 0]
+
+
+def test_c2_padded_variant() -> None:
+    # C2 [1e6, 16] f32 decreasing, rows of len_b ~ U{4..16} (seed 2) padded with min - 1: the
+    # padded fit's first len_b values equal the ragged fit of the unpadded rows
+    say("C2 padded variant")
+    batch, n = 1_000_000, 16
+    rng = np.random.default_rng(0)
+    y = (-0.1 * np.arange(n, dtype=np.float32)[None, :] + rng.standard_normal((batch, n), dtype=np.float32)).astype(np.float32)
+    lens = np.random.default_rng(2).integers(4, 17, batch)
+    keep = np.arange(n)[None, :] < lens[:, None]
+    pad = np.where(keep, y, np.inf).min(axis=1) - 1
+    yp = np.where(keep, y, pad[:, None]).astype(np.float32)
+    padded = isotonic(torch.from_numpy(yp).cuda(), increasing=False).cpu().numpy()
+    packed = y[keep]
+    off = np.zeros(batch + 1, dtype=np.int64)
+    np.cumsum(lens, out=off[1:])
+    got = isotonic_ragged(torch.from_numpy(packed).cuda(), torch.from_numpy(off), increasing=False).cpu().numpy()
+    np.testing.assert_array_equal(got, padded[keep])
+    want, _ = oracle.pava_ragged(packed, off, increasing=False, acc="f64")
+    assert float(np.abs(got - want).max()) <= tolerance(packed)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_backward_matches_block_gradient(dtype: type, weighted: bool) -> None:
+    say(f"ragged backward {np.dtype(dtype).name} weighted={weighted}")
+    rng = np.random.default_rng(11)
+    ln = np.r_[rng.integers(0, 33, 20_000), [100, 5000], rng.integers(1, 33, 100)].astype(np.int64)
+    y, w, off = ragged_set(ln, dtype, 12)
+    g = rng.standard_normal(len(y)).astype(dtype)
+    yt = torch.from_numpy(y).cuda().requires_grad_()
+    wt = torch.from_numpy(w).cuda().requires_grad_() if weighted else None
+    out = isotonic_ragged(yt, torch.from_numpy(off).cuda(), weight=wt)
+    grads = torch.autograd.grad(out, [yt] + ([wt] if weighted else []), torch.from_numpy(g).cuda())
+    fit, starts = oracle.pava_ragged(y, off, w if weighted else None, acc="f64")
+    ey, ew = oracle.block_grad(starts, g.astype(np.float64), w.astype(np.float64) if weighted else None,
+                               y.astype(np.float64) if weighted else None, fit, want_w=weighted)
+    tol = 1e-11 if dtype == np.float64 else 1e-5
+    for got, exp in zip(grads, (ey, ew)):
+        scale = max(float(np.abs(exp).max()), 1e-300)
+        np.testing.assert_allclose(got.double().cpu().numpy(), exp, rtol=tol, atol=tol * scale)
+
+
+def test_lengths_clamp_and_gradcheck() -> None:
+    gen = torch.Generator().manual_seed(4)
+    ln = torch.tensor([3, 0, 7, 1, 40, 12])
+    y = torch.randn(int(ln.sum()), generator=gen, dtype=torch.float64).cuda()
+    a = isotonic_ragged(y, lengths=ln, y_min=-0.2, y_max=0.5)
+    off = np.r_[0, np.cumsum(ln.numpy())]
+    want, _ = oracle.pava_ragged(y.cpu().numpy(), off, acc="f64")
+    np.testing.assert_allclose(a.cpu().numpy(), np.clip(want, -0.2, 0.5), rtol=0, atol=1e-12)
+    yy = y.clone().requires_grad_()
+    ww = (torch.rand(len(y), generator=gen, dtype=torch.float64) + 0.5).cuda().requires_grad_()
+    assert torch.autograd.gradcheck(lambda t, u: isotonic_ragged(t, lengths=ln, weight=u, increasing=False), (yy, ww))
+
+
+def test_argument_errors() -> None:
+    y = torch.randn(10, device="cuda")
+    with pytest.raises(ValueError, match="offsets"):
+        isotonic_ragged(y, torch.tensor([0, 4, 9]))
+    with pytest.raises(ValueError, match="decrease"):
+        isotonic_ragged(y, torch.tensor([0, 6, 4, 10]))
+    with pytest.raises(ValueError, match="non-negative"):
+        isotonic_ragged(y, lengths=[6, -1, 5])
+    with pytest.raises(ValueError, match="integer"):
+        isotonic_ragged(y, torch.tensor([0.0, 10.0]))
+    with pytest.raises(ValueError, match="exactly one"):
+        isotonic_ragged(y)
+    with pytest.raises(ValueError, match="positive"):
+        isotonic_ragged(y, lengths=torch.tensor([4, 6]), weight=torch.zeros(10, device="cuda"))
+    with pytest.raises(ValueError, match="positive"):
+        isotonic_ragged(torch.randn(50, device="cuda"), lengths=torch.tensor([10, 40]),
+                        weight=torch.cat([torch.ones(10), -torch.ones(40)]).cuda())
+    with pytest.raises(RuntimeError, match="GPU"):
+        isotonic_ragged(torch.randn(10), lengths=torch.tensor([10]))
+    assert isotonic_ragged(torch.empty(0, device="cuda"), lengths=torch.tensor([0, 0])).numel() == 0

@@ -130,3 +130,28 @@ def test_calibration_offsets_keep_segments_apart() -> None:
     xb, fb = oracle.calibration_fit(x2, y2)
     np.testing.assert_allclose(fp, np.r_[fa, fb], rtol=0, atol=1e-9)
     np.testing.assert_array_equal(xp, np.r_[xa, xb])
+
+
+# --- ragged rows ----------------------------------------------------------------------------------
+
+
+def test_pava_ragged_is_each_row_on_its_own() -> None:
+    # grouping rows by length is the per-row fit; rows never pool across (each starts a block)
+    rng = np.random.default_rng(7)
+    ln = np.r_[rng.integers(0, 12, 300), [0, 1, 50]]
+    off = np.r_[0, np.cumsum(ln)]
+    y = rng.standard_normal(off[-1])
+    w = rng.random(off[-1]) + 0.1
+    for ww in (None, w):
+        fit, starts = oracle.pava_ragged(y, off, ww, increasing=False)
+        for r in range(len(ln)):
+            sl = slice(off[r], off[r + 1])
+            if ln[r] == 0:
+                continue
+            f, s = oracle.pava(y[sl][None], None if ww is None else ww[sl][None], increasing=False, acc="f64")
+            np.testing.assert_array_equal(fit[sl], f[0])
+            np.testing.assert_array_equal(starts[sl], s[0])
+            assert starts[off[r]] == 1
+    # one fit of the packed values as a single row pools across row ends
+    whole, _ = oracle.pava(y[None], increasing=False, acc="f64")
+    assert not np.allclose(whole[0], oracle.pava_ragged(y, off, increasing=False)[0])

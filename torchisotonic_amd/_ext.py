@@ -41,6 +41,8 @@ SYMBOLS = (
     "ti_fwd",
     "ti_fwd_ev",
     "ti_fwd_noalloc",
+    "ti_fwd_ragged",
+    "ti_ragged_plan",
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_grad_workspace",
@@ -78,6 +80,10 @@ def load() -> ctypes.CDLL:
     lib.ti_fwd_ev.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp]
     lib.ti_fwd_noalloc.restype = _int
     lib.ti_fwd_noalloc.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp]
+    lib.ti_fwd_ragged.restype = _int
+    lib.ti_fwd_ragged.argtypes = [_vp] * 6 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp]
+    lib.ti_ragged_plan.restype = _int
+    lib.ti_ragged_plan.argtypes = [_vp, _i64, _i64, _vp, _vp]
     lib.ti_bwd.restype = _int
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_grad_workspace.restype = _int
@@ -229,8 +235,10 @@ def fit(
     with_starts: bool = False,
     y_min: float | None = None,
     y_max: float | None = None,
+    out: Tensor | None = None,
 ) -> tuple[Tensor, Tensor, Tensor | None, Tensor | None]:
-    """The fit of every row of ``y`` ([batch, n], float32/float64, on the GPU), clamped to
+    """The fit of every row of ``y`` ([batch, n], float32/float64, on the GPU; into ``out`` when
+    given, a contiguous tensor of y's shape and dtype), clamped to
     [y_min, y_max] where given; the packed partition (int32 words) if ``with_starts`` (else an
     empty tensor); for weighted fits, whether some weight was not positive (the caller raises;
     known once the kernels have read w, which for long rows is before the fit has finished),
@@ -247,7 +255,10 @@ def fit(
         if w.shape != y.shape or w.dtype != y.dtype or w.device != y.device:
             raise RuntimeError("torchisotonic_amd.fit: w must match y in shape, dtype and device")
         w = w.contiguous()
-    out = torch.empty_like(y)
+    if out is None:
+        out = torch.empty_like(y)
+    elif out.shape != y.shape or out.dtype != y.dtype or not out.is_contiguous():
+        raise RuntimeError("torchisotonic_amd.fit: out must be contiguous and match y")
     starts = torch.empty(
         starts_words(batch, n) if with_starts else 0, dtype=torch.int32, device=y.device
     )

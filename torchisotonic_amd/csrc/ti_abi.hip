@@ -288,6 +288,31 @@ int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* 
   return launched(ti::seg_grad(a, workspace), "stateless gradient");
 }
 
+int ti_fwd_ragged(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                  const int64_t* offsets, int64_t nrows, int64_t max_len, int dtype, unsigned flags, double y_min,
+                  double y_max, void* stream) {
+  if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
+  if (nrows < 0) return fail(TI_EINVAL, "need nrows >= 0, got %lld", (long long)nrows);
+  if (max_len < 1 || max_len > ti::kShortMax)
+    return fail(TI_ESIZE, "max_len must be in [1, %lld], got %lld", (long long)ti::kShortMax, (long long)max_len);
+  if (nrows == 0) return ok();
+  if (y == nullptr || out == nullptr || offsets == nullptr) return fail(TI_EINVAL, "y, out and offsets must not be null");
+  if (out == y || (w != nullptr && out == w)) return fail(TI_EINVAL, "out must not alias y or w");
+  if (ti::ragged_grid(nrows, max_len, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "too many rows");
+  ti::RaggedArgs a{y, w, out, starts, bad_weight, offsets, nrows, max_len, dtype, flags, y_min, y_max,
+                   static_cast<hipStream_t>(stream)};
+  return launched(ti::ragged_fit(a), "ragged fit");
+}
+
+int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, void* stream) {
+  if (nrows < 0 || total < 0) return fail(TI_EINVAL, "need nrows >= 0 and total >= 0");
+  if (offsets == nullptr || plan == nullptr) return fail(TI_EINVAL, "offsets and plan must not be null");
+  if ((reinterpret_cast<uintptr_t>(plan) & 7) != 0) return fail(TI_EINVAL, "plan must be 8-byte aligned");
+  return launched(ti::ragged_plan(offsets, nrows, total, reinterpret_cast<unsigned long long*>(plan),
+                                  static_cast<hipStream_t>(stream)),
+                  "ragged plan");
+}
+
 int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m, int dtype,
               void* stream) {
   if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);

@@ -42,6 +42,26 @@ struct ShortGradArgs {
 hipError_t interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m, int dtype,
                   hipStream_t stream);
 
+// Ragged rows of at most max_len (<= kShortMax) elements: row r is y[offsets[r], offsets[r + 1]).
+struct RaggedArgs {
+  const void* y;
+  const void* w;  // null: unweighted
+  void* out;
+  uint32_t* starts;      // flat bits of the packed array (zeroed by the caller), or null
+  uint32_t* bad_weight;  // null: not checked
+  const int64_t* offsets;
+  int64_t nrows, max_len;
+  int dtype;
+  unsigned flags;
+  double lo, hi;
+  hipStream_t stream;
+};
+int64_t ragged_grid(int64_t nrows, int64_t max_len, bool weighted);
+hipError_t ragged_fit(const RaggedArgs& a);
+// plan: four zeroed device words (see ragged_plan_kernel)
+hipError_t ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, unsigned long long* plan,
+                       hipStream_t stream);
+
 int64_t short_grid(int64_t batch, int64_t n, bool weighted);
 hipError_t short_fit(const ShortArgs& a);
 hipError_t short_grad(const ShortGradArgs& a);

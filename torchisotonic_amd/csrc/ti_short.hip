@@ -15,6 +15,7 @@
 //     partition is one 32-bit word of start bits per row.
 // The backward moves g (and w, y) the same way; block sums of g (and w) and the block mean
 // for the clamp mask and the weight gradient are formed per thread, in registers.
+#include <algorithm>
 #include <type_traits>
 
 #include "ti_common.h"
@@ -185,63 +186,20 @@ constexpr RcpTable make_rcp_table() {
 
 __constant__ RcpTable kRcp = make_rcp_table();
 
-template <typename T, int NMAX, bool W, bool DIRECT, bool INC>
-__global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
-    const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
-    uint32_t* __restrict__ starts, uint32_t* __restrict__ bad_weight, int64_t batch, int n,
-    unsigned flags, T lo, T hi) {
+// The fit of one row per thread from its values in registers: float64 cumulative sums, the
+// candidate points, the monotone chain (the vertex mask), the block means, NaN rows and the
+// clamp. Every thread of the workgroup calls it (RCP_BARRIER: it meets a barrier before the
+// chain, once the reciprocal table is in LDS). colS / colW: the workgroup's point columns,
+// [NMAX + 1][THREADS] each; rcp: the reciprocal table (unweighted rows).
+template <typename T, int NMAX, bool W, bool INC, bool RCP_BARRIER>
+__device__ __forceinline__ void row_fit(const T (&yv)[NMAX], const T (&wv)[W ? NMAX : 1], const int nn,
+                                        const bool active, double* colS, double* colW, const double* rcp,
+                                        uint32_t* __restrict__ bad_weight, unsigned flags, T lo, T hi,
+                                        T (&fit)[NMAX], typename MaskOf<NMAX>::type& m_out, bool& bad_out) {
   constexpr int THREADS = short_threads<NMAX, W>();
   constexpr bool EXACT = W || sizeof(T) == 8;
-  __shared__ double lds[short_lds_doubles<NMAX, W>()];
-  T* stg = reinterpret_cast<T*>(lds);
-  double* colS = lds;                        // [NMAX + 1][THREADS]
-  double* colW = lds + (NMAX + 1) * THREADS;  // weighted only
-
-  const int tid = threadIdx.x;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
-  const int rows = static_cast<int>(min<int64_t>(THREADS, batch - row0));
-  const int count = rows * n;
-  const DivBy div(static_cast<uint32_t>(n));
-  const bool active = tid < rows;
   constexpr double sgn = INC ? 1.0 : -1.0;
-  __shared__ double rcp[W ? 1 : kRcpN];
-  if constexpr (!W) {
-    if (tid < kRcpN) rcp[tid] = kRcp.v[tid];
-  }
-
-  T yv[NMAX];
-  T wv[W ? NMAX : 1];
-  if constexpr (DIRECT) {
-    if (active) {
-      load_row<T, NMAX>(y + (row0 + tid) * NMAX, yv);
-      if constexpr (W) load_row<T, NMAX>(w + (row0 + tid) * NMAX, wv);
-    }
-  } else {
-    Span<T, THREADS, NMAX> sy;
-    Span<T, THREADS, NMAX> sw;
-    sy.load(y + row0 * n, count);
-    if constexpr (W) sw.load(w + row0 * n, count);
-    sy.to_lds(y + row0 * n, stg, count, div);
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < NMAX; ++c) {
-      if (c < n) yv[c] = stg[tid * (n + 1) + c];
-    }
-    if constexpr (W) {
-      __syncthreads();
-      sw.to_lds(w + row0 * n, stg, count, div);
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < n) wv[c] = stg[tid * (n + 1) + c];
-      }
-    }
-    __syncthreads();  // staging is dead from here: the area becomes the point columns
-  }
-
-  // The row length: a constant when each thread moves whole rows of NMAX.
-  const int nn = DIRECT ? NMAX : n;
-
+  const int tid = threadIdx.x;
   // Cumulative sums in float64 (of sgn * y: a decreasing fit is minus the increasing fit of -y).
   double S[NMAX + 1];
   double P[W ? NMAX + 1 : 1];
@@ -276,7 +234,7 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
       }
     }
   }
-  if constexpr (DIRECT && !W) __syncthreads();  // the reciprocals (staged rows met barriers already)
+  if constexpr (RCP_BARRIER) __syncthreads();  // the reciprocals (staged rows met barriers already)
 
   // Lower hull of P_0..P_n by the monotone chain, run as an event loop: every iteration either
   // pops the last vertex or pushes the next candidate, so a wave iterates max over its lanes of
@@ -362,7 +320,6 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     }
   }
 
-  T fit[NMAX];
   const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
   if constexpr (!W) {
     // Left to right: at a vertex i the block runs to the next vertex v (found from the mask, so
@@ -416,6 +373,71 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     for (int i = 0; i < NMAX; ++i) fit[i] = clip(fit[i], use_lo, lo, use_hi, hi);
   }
 
+  m_out = m;
+  bad_out = bad;
+}
+
+template <typename T, int NMAX, bool W, bool DIRECT, bool INC>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
+    const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
+    uint32_t* __restrict__ starts, uint32_t* __restrict__ bad_weight, int64_t batch, int n,
+    unsigned flags, T lo, T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  __shared__ double lds[short_lds_doubles<NMAX, W>()];
+  T* stg = reinterpret_cast<T*>(lds);
+  double* colS = lds;                        // [NMAX + 1][THREADS]
+  double* colW = lds + (NMAX + 1) * THREADS;  // weighted only
+
+  const int tid = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
+  const int rows = static_cast<int>(min<int64_t>(THREADS, batch - row0));
+  const int count = rows * n;
+  const DivBy div(static_cast<uint32_t>(n));
+  const bool active = tid < rows;
+  __shared__ double rcp[W ? 1 : kRcpN];
+  if constexpr (!W) {
+    if (tid < kRcpN) rcp[tid] = kRcp.v[tid];
+  }
+
+  T yv[NMAX];
+  T wv[W ? NMAX : 1];
+  if constexpr (DIRECT) {
+    if (active) {
+      load_row<T, NMAX>(y + (row0 + tid) * NMAX, yv);
+      if constexpr (W) load_row<T, NMAX>(w + (row0 + tid) * NMAX, wv);
+    }
+  } else {
+    Span<T, THREADS, NMAX> sy;
+    Span<T, THREADS, NMAX> sw;
+    sy.load(y + row0 * n, count);
+    if constexpr (W) sw.load(w + row0 * n, count);
+    sy.to_lds(y + row0 * n, stg, count, div);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n) yv[c] = stg[tid * (n + 1) + c];
+    }
+    if constexpr (W) {
+      __syncthreads();
+      sw.to_lds(w + row0 * n, stg, count, div);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < n) wv[c] = stg[tid * (n + 1) + c];
+      }
+    }
+    __syncthreads();  // staging is dead from here: the area becomes the point columns
+  }
+
+  // The row length: a constant when each thread moves whole rows of NMAX.
+  const int nn = DIRECT ? NMAX : n;
+
+  T fit[NMAX];
+  typename MaskOf<NMAX>::type m;
+  bool bad;
+  row_fit<T, NMAX, W, INC, DIRECT && !W>(yv, wv, nn, active, colS, colW, rcp, bad_weight, flags, lo, hi, fit, m,
+                                           bad);
+
   if (starts != nullptr && active) {
     const uint32_t low = nn >= 32 ? 0xFFFFFFFFu : ((1u << nn) - 1u);
     starts[row0 + tid] = bad ? 1u : static_cast<uint32_t>(m) & low;
@@ -431,6 +453,249 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     }
     __syncthreads();
     stage_out<T, THREADS>(out + row0 * n, stg, count, div);
+  }
+}
+
+// Ragged rows: row r is y[offsets[r], offsets[r + 1]) of a packed array, one thread per row as
+// above. A workgroup whose rows lie within THREADS * NMAX elements stages them through LDS:
+// 16-byte loads and stores of the aligned chunks that cover its range (element by element in
+// the two partial end chunks, or throughout if a base pointer is not 16-byte aligned). A row
+// longer than NMAX is not fitted (its elements of out are not written: a workgroup holding one
+// stores through an ownership bitmap) and gets its first start bit only, which keeps it apart
+// from its neighbours in a segmented pass over the packed array. A workgroup whose range is
+// longer than THREADS * NMAX holds such a row; each thread then reads and writes its own row.
+// The start bits are flat (bit e of the packed array, word e / 32) in a zeroed array: a
+// workgroup's first and last words are shared with its neighbours' (OR-ed in with atomics),
+// the words between hold its elements only (stored).
+template <typename T, int NMAX, bool W, bool INC>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_fit_kernel(
+    const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out, uint32_t* __restrict__ starts,
+    uint32_t* __restrict__ bad_weight, const int64_t* __restrict__ offsets, int64_t nrows, unsigned flags, T lo,
+    T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  constexpr int CAP = THREADS * NMAX;        // elements a workgroup stages
+  constexpr int V = Vec16<T>::kN;            // elements per 16-byte chunk
+  using VT = typename Vec16<T>::type;
+  constexpr int KI = (CAP / V + 2 + THREADS - 1) / THREADS;  // chunks per thread (two partial)
+  constexpr int WORDS = CAP / 32 + 2;        // start-bit (or ownership) words of the range
+  __shared__ __align__(16) double lds[short_lds_doubles<NMAX, W>()];
+  __shared__ uint32_t own[WORDS];            // staged elements that belong to a fitted row
+  __shared__ uint32_t sbits[WORDS];          // start bits of the staged range, from bit e0 % 32
+  __shared__ double rcp[W ? 1 : kRcpN];
+  static_assert(short_lds_doubles<NMAX, W>() * 8 >= (CAP + 2 * V) * static_cast<int>(sizeof(T)), "staging fits");
+  T* stg = reinterpret_cast<T*>(lds);
+  double* colS = lds;
+  double* colW = lds + (NMAX + 1) * THREADS;
+  const int tid = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
+  const int rows = static_cast<int>(min<int64_t>(THREADS, nrows - row0));
+  const bool active = tid < rows;
+  if constexpr (!W) {
+    if (tid < kRcpN) rcp[tid] = kRcp.v[tid];
+  }
+  const int64_t e0 = offsets[row0], e1 = offsets[row0 + rows];
+  const int64_t my0 = active ? offsets[row0 + tid] : e1;
+  const int64_t my1 = active ? offsets[row0 + tid + 1] : e1;
+  const bool fits = active && my1 > my0 && my1 - my0 <= NMAX;  // (empty rows: nothing to fit)
+  const int len = fits ? static_cast<int>(my1 - my0) : 0;
+  const int64_t total = e1 - e0;
+  const bool staged = total <= CAP;  // (the same in every thread)
+  const int b0 = static_cast<int>(e0 & 31);    // bit of e0 within its word
+  const int rel = static_cast<int>(my0 - e0);  // (staged: this row's first element in the range)
+  // staged: the range as 16-byte chunks from a0 (LDS element k is y[a0 + k])
+  const int64_t a0 = e0 - e0 % V;
+  const int sh = static_cast<int>(e0 - a0);
+  const int nch = staged ? static_cast<int>((e1 - a0 + V - 1) / V) : 0;
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out) |
+                          (W ? reinterpret_cast<uintptr_t>(w) : uintptr_t{0});
+  const bool vec = (bases & 15) == 0;
+
+  auto stage_in = [&](const T* __restrict__ src) {
+    VT buf[KI];
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+      const int k = tid + j * THREADS;
+      const int64_t g = a0 + static_cast<int64_t>(k) * V;
+      buf[j] = VT{};
+      if (k < nch) {
+        if (vec && g >= e0 && g + V <= e1) {
+          buf[j] = *reinterpret_cast<const VT*>(src + g);
+        } else {
+#pragma unroll
+          for (int t = 0; t < V; ++t) {
+            if (g + t >= e0 && g + t < e1) buf[j][t] = src[g + t];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+      const int k = tid + j * THREADS;
+      if (k < nch) *reinterpret_cast<VT*>(stg + k * V) = buf[j];
+    }
+  };
+
+  T yv[NMAX];
+  T wv[W ? NMAX : 1];
+  bool has_long = false;
+  if (staged) {
+    has_long = __syncthreads_or(active && my1 - my0 > NMAX);
+    for (int k = tid; k < WORDS; k += THREADS) {
+      own[k] = 0u;
+      sbits[k] = 0u;
+    }
+    stage_in(y);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) yv[c] = stg[sh + rel + c];
+    }
+    if (has_long && len > 0) {  // mark this row's elements as fitted (at most two words)
+      const uint32_t mask = len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u);
+      const int bit = rel + b0;
+      atomicOr(&own[bit >> 5], mask << (bit & 31));
+      if ((bit & 31) + len > 32) atomicOr(&own[(bit >> 5) + 1], mask >> (32 - (bit & 31)));
+    }
+    if constexpr (W) {
+      __syncthreads();
+      stage_in(w);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < len) wv[c] = stg[sh + rel + c];
+      }
+    }
+    __syncthreads();  // staging is dead from here: the area becomes the point columns
+  } else {
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) {
+        yv[c] = y[my0 + c];
+        if constexpr (W) wv[c] = w[my0 + c];
+      }
+    }
+  }
+
+  T fit[NMAX];
+  typename MaskOf<NMAX>::type m;
+  bool bad;
+  row_fit<T, NMAX, W, INC, !W>(yv, wv, len, fits, colS, colW, rcp, bad_weight, flags, lo, hi, fit, m, bad);
+  // this row's start bits (a long row: its first element only)
+  const uint32_t rbits = !active ? 0u : (!fits || bad) ? 1u : static_cast<uint32_t>(m) & (len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u));
+
+  if (staged) {
+    __syncthreads();  // every thread is done with the point columns
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) stg[sh + rel + c] = fit[c];
+    }
+    if (active && my1 > my0) {
+      const int bit = rel + b0;
+      atomicOr(&sbits[bit >> 5], rbits << (bit & 31));
+      if ((bit & 31) != 0 && (rbits >> (32 - (bit & 31))) != 0) atomicOr(&sbits[(bit >> 5) + 1], rbits >> (32 - (bit & 31)));
+    }
+    __syncthreads();
+    if (!has_long) {  // every element of the range is a fitted row's
+#pragma unroll
+      for (int j = 0; j < KI; ++j) {
+        const int k = tid + j * THREADS;
+        const int64_t g = a0 + static_cast<int64_t>(k) * V;
+        if (k < nch) {
+          if (vec && g >= e0 && g + V <= e1) {
+            *reinterpret_cast<VT*>(out + g) = *reinterpret_cast<const VT*>(stg + k * V);
+          } else {
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+              if (g + t >= e0 && g + t < e1) out[g + t] = stg[k * V + t];
+            }
+          }
+        }
+      }
+    } else {
+      for (int e = tid; e < total; e += THREADS) {
+        const int bit = e + b0;
+        if ((own[bit >> 5] >> (bit & 31)) & 1u) out[e0 + e] = stg[sh + e];
+      }
+    }
+    if (starts != nullptr) {
+      const int nwords = static_cast<int>((total + b0 + 31) >> 5);
+      for (int k = tid; k < nwords; k += THREADS) {
+        const uint32_t v = sbits[k];
+        if (k == 0 || k == nwords - 1) {
+          if (v != 0u) atomicOr(&starts[(e0 >> 5) + k], v);
+        } else {
+          starts[(e0 >> 5) + k] = v;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) out[my0 + c] = fit[c];
+    }
+    if (starts != nullptr && active && my1 > my0) {
+      const int64_t bit = my0;
+      atomicOr(&starts[bit >> 5], rbits << (bit & 31));
+      if ((bit & 31) != 0 && (rbits >> (32 - (bit & 31))) != 0) atomicOr(&starts[(bit >> 5) + 1], rbits >> (32 - (bit & 31)));
+    }
+  }
+}
+
+// The plan of a ragged set, one pass over its offsets: plan[0] bit 0 set if offsets[0] != 0,
+// bit 1 if offsets[nrows] != total, bit 2 if some row has a negative length; plan[1] the longest
+// row of at most kShortMax elements, plan[2] the number of longer rows, plan[3] the longest
+// row. plan: four zeroed words. Each workgroup reduces its rows through its waves and LDS, then
+// one thread folds the result into plan (the grid is kept small, so few atomics meet there).
+constexpr int kPlanThreads = 256;
+constexpr int kPlanBlocks = 256;
+
+__device__ __forceinline__ void plan_fold(unsigned long long v[4], unsigned long long o[4]) {
+  v[0] |= o[0];
+  v[1] = o[1] > v[1] ? o[1] : v[1];
+  v[2] += o[2];
+  v[3] = o[3] > v[3] ? o[3] : v[3];
+}
+
+__global__ __launch_bounds__(kPlanThreads) void ragged_plan_kernel(const int64_t* __restrict__ offsets,
+                                                                  int64_t nrows, int64_t total,
+                                                                  unsigned long long* __restrict__ plan) {
+  __shared__ unsigned long long part[kPlanThreads / 64][4];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
+  unsigned long long v[4] = {0, 0, 0, 0};  // errors, longest short row, long rows, longest row
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; r < nrows; r += stride) {
+    const int64_t len = offsets[r + 1] - offsets[r];
+    if (len < 0) {
+      v[0] |= 4u;
+    } else {
+      const unsigned long long l = static_cast<unsigned long long>(len);
+      if (len <= kShortMax) v[1] = l > v[1] ? l : v[1];
+      else v[2] += 1;
+      v[3] = l > v[3] ? l : v[3];
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (offsets[0] != 0) v[0] |= 1u;
+    if (offsets[nrows] != total) v[0] |= 2u;
+  }
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    unsigned long long o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __shfl_xor(v[k], s);
+    plan_fold(v, o);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) part[wave][k] = v[k];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < kPlanThreads / 64; ++q) plan_fold(v, part[q]);
+    if (v[0] != 0) atomicOr(&plan[0], v[0]);
+    if (v[1] != 0) atomicMax(&plan[1], v[1]);
+    if (v[2] != 0) atomicAdd(&plan[2], v[2]);
+    if (v[3] != 0) atomicMax(&plan[3], v[3]);
   }
 }
 
@@ -669,6 +934,47 @@ int64_t short_grid(int64_t batch, int64_t n, bool weighted) {
   else if (n <= 16) threads = weighted ? short_threads<16, true>() : short_threads<16, false>();
   else threads = weighted ? short_threads<32, true>() : short_threads<32, false>();
   return (batch + threads - 1) / threads;
+}
+
+template <typename T, bool W>
+hipError_t ragged_by_len(const RaggedArgs& a) {
+  const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
+  const bool inc = (a.flags & TI_INCREASING) != 0;
+  auto go = [&](auto nmax) -> hipError_t {
+    constexpr int NMAX = decltype(nmax)::value;
+    constexpr int TH = short_threads<NMAX, W>();
+    const dim3 grid(static_cast<unsigned>((a.nrows + TH - 1) / TH));
+    const T* y = static_cast<const T*>(a.y);
+    const T* w = static_cast<const T*>(a.w);
+    T* out = static_cast<T*>(a.out);
+    if (inc)
+      ragged_fit_kernel<T, NMAX, W, true><<<grid, dim3(TH), 0, a.stream>>>(y, w, out, a.starts, a.bad_weight, a.offsets,
+                                                                          a.nrows, a.flags, lo, hi);
+    else
+      ragged_fit_kernel<T, NMAX, W, false><<<grid, dim3(TH), 0, a.stream>>>(y, w, out, a.starts, a.bad_weight, a.offsets,
+                                                                           a.nrows, a.flags, lo, hi);
+    return hipGetLastError();
+  };
+  if (a.max_len <= 4) return go(std::integral_constant<int, 4>{});
+  if (a.max_len <= 8) return go(std::integral_constant<int, 8>{});
+  if (a.max_len <= 16) return go(std::integral_constant<int, 16>{});
+  return go(std::integral_constant<int, 32>{});
+}
+
+int64_t ragged_grid(int64_t nrows, int64_t max_len, bool weighted) { return short_grid(nrows, max_len, weighted); }
+
+hipError_t ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, unsigned long long* plan,
+                       hipStream_t stream) {
+  const int64_t blocks = std::min<int64_t>(std::max<int64_t>((nrows + kPlanThreads - 1) / kPlanThreads, 1), kPlanBlocks);
+  ragged_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPlanThreads), 0, stream>>>(offsets, nrows, total,
+                                                                                            plan);
+  return hipGetLastError();
+}
+
+hipError_t ragged_fit(const RaggedArgs& a) {
+  const bool weighted = a.w != nullptr;
+  if (a.dtype == TI_F32) return weighted ? ragged_by_len<float, true>(a) : ragged_by_len<float, false>(a);
+  return weighted ? ragged_by_len<double, true>(a) : ragged_by_len<double, false>(a);
 }
 
 hipError_t short_fit(const ShortArgs& a) {

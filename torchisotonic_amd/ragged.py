@@ -1,0 +1,187 @@
+"""Isotonic regression of ragged rows: rows of different lengths packed end to end, with their
+offsets, fitted without a padding pass.
+
+The reference fits equal-length rows only; its users pad ragged rows (tail values that never
+pool into the data: above the row's maximum for an increasing fit, below its minimum for a
+decreasing one) or lay them end to end with offsets
+(reference README.md:100-103, examples/ctr_calibration/README.md:25-27). Here the packed values
+and the row offsets (CSR layout) go to the GPU as they are:
+
+- rows of 1 to 32 elements, the short-row regime, are fitted together in one HIP launch
+  (``ti_fwd_ragged``: one thread per row, a workgroup's rows staged through LDS);
+- longer rows are fitted row by row by the regular kernels (``ti_fwd`` on each row in place);
+- the backward is ``ti_grad`` (the stateless gradient operator) over the whole packed array as
+  one sequence: the forward's flat start bits separate the rows, since every row starts a
+  block; longer rows then take their gradients from their own forward's hulls (``ti_bwd``).
+
+The clamp to [y_min, y_max] is torch.clamp after the fit, as in the reference (_api.py:68-69).
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+from torch import Tensor
+
+from torchisotonic_amd import _ext
+
+_SHORT = 32  # the longest rows the one-launch kernel fits
+
+
+_local = threading.local()
+
+
+def _host_words(device: torch.device) -> Tensor:
+    """Per thread and device: four pinned host words the plan is copied into."""
+    cache = getattr(_local, "plan", None)
+    if cache is None:
+        cache = _local.plan = {}
+    if device.index not in cache:
+        cache[device.index] = torch.empty(4, dtype=torch.int64, pin_memory=True)
+    return cache[device.index]
+
+
+def _offsets(offsets, lengths, values: Tensor, weighted: bool):
+    """The row offsets as a device int64 tensor, validated; the longest row of at most 32
+    elements (0 if none); the (start, end) of every longer row; and zeroed device words for the
+    fit: the flat start bits and the weight flag. One kernel (ti_ragged_plan) checks the offsets
+    and sizes the rows, and four words come back to the host: the offsets themselves are never
+    copied whole."""
+    if (offsets is None) == (lengths is None):
+        raise ValueError("give exactly one of offsets and lengths")
+    dev = values.device
+    src = offsets if offsets is not None else lengths
+    t = src if isinstance(src, Tensor) else torch.as_tensor(src)
+    if t.ndim != 1 or t.is_floating_point() or t.is_complex() or t.dtype == torch.bool:
+        raise ValueError("offsets / lengths must be a 1-D integer sequence")
+    t = t.to(device=dev, dtype=torch.int64)
+    if offsets is None:
+        off = torch.zeros(t.numel() + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(t, 0, out=off[1:])
+    else:
+        if t.numel() < 1:
+            raise ValueError("offsets must hold at least one value")
+        off = t.contiguous()
+    nrows, total = off.numel() - 1, values.numel()
+    # one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
+    zeros = torch.zeros(10 + (total + 31) // 32, dtype=torch.int32, device=dev)
+    plan, bad, bits = zeros[:8].view(torch.int64), zeros[8:9], zeros[10:]
+    host = _host_words(dev)
+    with _ext._on_device(dev):
+        _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), _ext._stream(values)),
+                    "isotonic_ragged")
+        host.copy_(plan, non_blocking=True)
+        torch.cuda.current_stream(dev).synchronize()
+    err, short_max, n_long, _ = host.tolist()
+    if err & 4:
+        raise ValueError("lengths must be non-negative" if offsets is None else "offsets must not decrease")
+    if err & 3:
+        raise ValueError(f"offsets must run from 0 to values.numel() = {total}")
+    long_rows: list[tuple[int, int]] = []
+    if n_long:
+        ln = off[1:] - off[:-1]
+        r = torch.nonzero(ln > _SHORT).view(-1)
+        long_rows = [(int(x), int(y)) for x, y in torch.stack([off[r], off[r + 1]], 1).tolist()]
+    return off, int(short_max), long_rows, bits, (bad if weighted else None)
+
+
+def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spans: list[tuple[int, int]],
+         bits: Tensor, bad: Tensor | None, increasing: bool) -> tuple[Tensor, list]:
+    """The fits of every row (packed like values) with the flat start bits of the short rows
+    in ``bits`` (a longer row has its first bit only), and per longer row (start, end, its own
+    packed starts, its forward workspace)."""
+    out = torch.empty_like(values)
+    if short_max > 0:
+        flags = (_ext.INCREASING if increasing else 0) | _ext.EXACT
+        with _ext._on_device(values.device):
+            rc = _ext.load().ti_fwd_ragged(
+                values.data_ptr(), _ext._ptr(w), out.data_ptr(), bits.data_ptr(), _ext._ptr(bad),
+                off.data_ptr(), off.numel() - 1, short_max, _ext._dtype_code(values), flags,
+                0.0, 0.0, _ext._stream(values),
+            )
+        _ext._check(rc, "isotonic_ragged")
+    long_rows = []
+    for a, b in long_spans:
+        wr = None if w is None else w[a:b].view(1, b - a)
+        _, starts, bad_r, ws = _ext.fit(values[a:b].view(1, b - a), wr, increasing, True, True,
+                                        out=out[a:b].view(1, b - a))
+        if bad_r:
+            raise ValueError("weight must be strictly positive")
+        long_rows.append((a, b, starts, ws))
+    if bad is not None and short_max > 0 and bool(bad.item()):
+        raise ValueError("weight must be strictly positive")
+    return out, long_rows
+
+
+class _RaggedFit(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, values: Tensor, w: Tensor | None, off: Tensor, short_max: int,  # type: ignore[override]
+                long_spans: list, bits: Tensor, bad: Tensor | None, increasing: bool) -> Tensor:
+        out, long_rows = _fit(values, w, off, short_max, long_spans, bits, bad, increasing)
+        ctx.increasing = increasing
+        ctx.long_rows = long_rows
+        ctx.has_w = w is not None
+        ctx.save_for_backward(values, w if w is not None else torch.empty(0, device=values.device), out, bits)
+        return out
+
+    @staticmethod
+    def backward(ctx, g: Tensor):  # type: ignore[override]
+        values, w, out, bits = ctx.saved_tensors
+        w = w if ctx.has_w else None
+        want_y = ctx.needs_input_grad[0]
+        want_w = ctx.has_w and ctx.needs_input_grad[1]
+        if not want_y and not want_w:
+            return (None,) * 8
+        g = g.contiguous()
+        total = values.numel()
+        # the whole packed array as one sequence: rows are apart, each starting a block
+        gy, gw = _ext.isotonic_grad(out.view(1, total), bits, g.view(1, total),
+                                    None if w is None else w.view(1, total),
+                                    values.view(1, total) if want_w else None)
+        gy = gy.view(total)
+        gw = gw.view(total) if want_w else None
+        for a, b, starts, ws in ctx.long_rows:
+            ry, rw = _ext.grad(starts, ws, g[a:b].view(1, b - a), None if w is None else w[a:b].view(1, b - a),
+                               values[a:b].view(1, b - a), True, want_w, increasing=ctx.increasing)
+            gy[a:b] = ry.view(b - a)
+            if want_w:
+                gw[a:b] = rw.view(b - a)
+        return (gy if want_y else None), gw, None, None, None, None, None, None
+
+
+def isotonic_ragged(
+    values: Tensor,
+    offsets: Tensor | None = None,
+    *,
+    lengths: Tensor | None = None,
+    weight: Tensor | None = None,
+    increasing: bool = True,
+    y_min: float | None = None,
+    y_max: float | None = None,
+) -> Tensor:
+    """Isotonic regression of every row of a ragged set: row r is ``values[offsets[r]:
+    offsets[r + 1]]`` (or give ``lengths``, its row lengths). ``values`` (and ``weight``, shaped
+    like it, positive) is 1-D on a ROCm device; offsets run from 0 to ``values.numel()``. Returns
+    the fits packed like ``values``, clamped to [y_min, y_max] where given; differentiable in
+    ``values`` and ``weight``. Dtype rules as ``isotonic``."""
+    if not isinstance(values, Tensor):
+        raise TypeError(f"values must be a torch.Tensor, got {type(values).__name__}")
+    if values.ndim != 1:
+        raise ValueError("values must be 1-D (rows packed end to end)")
+    out_dtype = values.dtype if values.is_floating_point() else torch.get_default_dtype()
+    acc = torch.float64 if out_dtype == torch.float64 else torch.float32
+    _ext._on_gpu(values, "values")
+    v = values.to(acc).contiguous()
+    w = None
+    if weight is not None:
+        if not isinstance(weight, Tensor) or weight.shape != values.shape:
+            raise ValueError("weight must be a tensor shaped like values")
+        w = weight.to(device=values.device, dtype=acc).contiguous()
+    off, short_max, long_spans, bits, bad = _offsets(offsets, lengths, values, w is not None)
+    if values.numel() == 0:
+        return values.to(out_dtype, copy=True)
+    fit = _RaggedFit.apply(v, w, off, short_max, long_spans, bits, bad, increasing)
+    if y_min is not None or y_max is not None:
+        fit = fit.clamp(min=y_min, max=y_max)
+    return fit.to(out_dtype)
