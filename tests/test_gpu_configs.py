@@ -77,3 +77,29 @@ def test_c5_bootstrap_rows() -> None:
                                fit.astype(np.float64), want_w=True)
     np.testing.assert_allclose(gy, ey, rtol=2e-5, atol=2e-5)
     np.testing.assert_allclose(gw, ew, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize(("batch", "n"), [(1000, 5000), (100_000, 16), (3, 70_000)])
+def test_exact_false_through_the_api(batch: int, n: int) -> None:
+    # exact=False (C3's float32 leg in the reference) gives the exact path's results bit for
+    # bit, fit and gradients, and so meets the reference's exact=False bar: within 1e-4 of the
+    # float32-accumulating CPU path (reference tests/test_cuda.py:26-28)
+    import torch
+
+    import torchisotonic_amd
+
+    print(f"exact=False {batch}x{n}", flush=True)
+    rng = np.random.default_rng(n)
+    y = (1 / (1 + np.exp(-(np.linspace(-4, 4, n) + 0.5 * rng.standard_normal((batch, n)))))).astype(np.float32)
+    w = (rng.random((batch, n)) + 0.1).astype(np.float32)
+    c = torch.from_numpy(rng.standard_normal((batch, n)).astype(np.float32)).cuda()
+    out = {}
+    for exact in (True, False):
+        yy = torch.from_numpy(y).cuda().requires_grad_()
+        ww = torch.from_numpy(w).cuda().requires_grad_()
+        fit = torchisotonic_amd.isotonic(yy, ww, increasing=False, y_min=0.0, y_max=1.0, exact=exact)
+        out[exact] = (fit.detach(), *torch.autograd.grad((fit * c).sum(), (yy, ww)))
+    for a, b in zip(out[True], out[False]):
+        assert torch.equal(a, b)
+    ref32, _ = oracle.pava(y, w, increasing=False)
+    np.testing.assert_allclose(out[False][0].cpu().numpy(), np.clip(ref32, 0.0, 1.0), rtol=1e-4, atol=1e-4)

@@ -32,21 +32,21 @@ def isotonic(
     dim: int = -1,
     exact: bool = True,
 ) -> Tensor:
-    """Isotonic regression of every 1-D slice of ``y`` along ``dim``.
+    """Fit a monotone sequence to each 1-D slice of ``y`` taken along ``dim``.
 
-    For each slice, returns the non-decreasing (or, with ``increasing=False``,
-    non-increasing) sequence closest to it in weighted least squares, like
-    ``sklearn.isotonic.isotonic_regression``. ``weight`` must be positive and shaped like
-    ``y`` (or broadcast to it). Results are clipped to ``[y_min, y_max]`` if given. A slice
-    containing NaN comes back as NaN. Integer input becomes the default float dtype; float
-    input keeps its dtype, with float16/bfloat16 computed in float32.
+    Every slice is replaced by its weighted least-squares projection onto the monotone
+    sequences: non-decreasing by default, non-increasing when ``increasing=False`` (the
+    result sklearn's ``isotonic_regression`` gives). ``weight``, if given, holds positive
+    weights of y's shape or a shape that broadcasts to it. ``y_min`` / ``y_max`` clamp the
+    result. Slices with a NaN return all NaN. The result has y's float dtype (float16 and
+    bfloat16 are fitted in float32); integer input gives torch's default float dtype.
 
-    Differentiable in ``y`` and ``weight``: the fit is constant on blocks of neighbouring
-    elements, each the weighted mean of ``y`` over its block, so a gradient is averaged over
-    the blocks.
+    Gradients flow to ``y`` and ``weight``. The fit is piecewise constant: each run of equal
+    values (a block) is the weighted mean of ``y`` over the run, so an element's gradient is
+    its weight times the block's summed upstream gradient over the block's total weight.
 
-    ``exact`` is accepted for compatibility with torchisotonic; the kernels always form sums
-    and hull tests in float64 and round the float32 fit once, so it changes nothing.
+    ``exact`` exists so calls written for torchisotonic work unchanged. These kernels always
+    accumulate and compare in float64 and round a float32 fit once, whatever it is set to.
     """
     # Argument checks and messages: reference _api.py:43-61.
     if not isinstance(y, Tensor):
