@@ -64,7 +64,9 @@ def isotonic(
         if not isinstance(weight, Tensor):
             raise TypeError(f"weight must be a torch.Tensor, got {type(weight).__name__}")
         try:
-            w = weight.to(device=y.device, dtype=acc).broadcast_to(y.shape)
+            w = weight.to(device=y.device, dtype=acc)
+            if w.shape != y.shape:
+                w = w.broadcast_to(y.shape)
             w = w if last else w.movedim(dim, -1)
         except RuntimeError as e:
             raise ValueError(f"weight of shape {tuple(weight.shape)} does not fit y") from e
@@ -74,13 +76,17 @@ def isotonic(
     shape = rows.shape
     if rows.numel() == 0:
         return y.to(out_dtype, copy=True)
-    flat_y = rows.reshape(-1, shape[-1]).to(acc)
-    flat_w = None if w is None else w.reshape(-1, shape[-1])
+    # (no view where the rows already are [batch, n]: every view is one more node for the
+    # autograd engine to run in the backward, a few microseconds of host time each)
+    two_d = rows.ndim == 2
+    flat_y = (rows if two_d else rows.reshape(-1, shape[-1])).to(acc)
+    flat_w = None if w is None else (w if two_d else w.reshape(-1, shape[-1]))
     lo = None if y_min is None else float(y_min)
     hi = None if y_max is None else float(y_max)
     _ext._on_gpu(flat_y, "y")
     # the clamped fit with its autograd node in C++ (csrc/ti_torch.cpp; the reference's Python
     # autograd.Function, _api.py:73-97, plus torch.clamp's backward)
     out: Tensor = _ext.ops().isotonic_fit(flat_y, flat_w, increasing, lo, hi)
-    out = out.reshape(shape)
+    if not two_d:
+        out = out.reshape(shape)
     return (out if last else out.movedim(-1, dim)).to(out_dtype)

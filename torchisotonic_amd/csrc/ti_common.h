@@ -120,6 +120,21 @@ __device__ __forceinline__ double dd_diff(DD a, DD b) {
   return (a.hi - b.hi) + (a.lo - b.lo);
 }
 
+// v, taken from the wave's first lane (for values the same in every lane).
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// A buffer resource over [base, base + bytes) (bytes clamped to the 32-bit range field). Loads
+// past its end return zero and stores past it are dropped, without a fault.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int nrec = static_cast<int>(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), nrec, 0x00020000);
+}
+
 template <typename T>
 __device__ __forceinline__ T quiet_nan();
 template <>

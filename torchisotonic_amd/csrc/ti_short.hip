@@ -16,6 +16,7 @@
 // The backward moves g (and w, y) the same way; block sums of g (and w) and the block mean
 // for the clamp mask and the weight gradient are formed per thread, in registers.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "ti_common.h"
@@ -265,58 +266,90 @@ __device__ __forceinline__ void row_fit(const T (&yv)[NMAX], const T (&wv)[W ? N
         if (keep) cand |= Mask(1) << k;
       }
     }
-    // stack: t1 (last vertex) and t2 (< 0: none) with their sums and weights; the stack itself
-    // is the mask m. The candidate being pushed is k; rest holds the candidates after it.
-    // The first candidate goes on the stack at once (with only point 0 below it there is
-    // nothing to test), which spares every lane the loop's first iteration.
-    Mask rest = cand & ~Mask(1);
-    int t1 = lowest_bit(rest);  // point nn is always a candidate
-    rest &= rest - 1;
-    int t2 = 0;
-    double s1 = colS[t1 * THREADS + tid], s2 = 0.0;
-    double w1 = W ? colW[W ? t1 * THREADS + tid : 0] : static_cast<double>(t1), w2 = 0.0;
-    m |= Mask(1) << t1;
-    int k = rest ? lowest_bit(rest) : -1;
-    rest &= rest - 1;
-    double sk = colS[(k > 0 ? k : 0) * THREADS + tid];
-    double wk = W ? colW[W ? (k > 0 ? k : 0) * THREADS + tid : 0] : static_cast<double>(k);
-    while (k >= 0) {
-      bool pop = false;
-      if constexpr (W) {
-        pop = t2 >= 0 && pools<EXACT>(s1 - s2, w1 - w2, sk - s1, wk - w1);
-      } else {
-        pop = t2 >= 0 && pools<EXACT>(s1 - s2, static_cast<double>(t1 - t2), sk - s1,
-                                      static_cast<double>(k - t1));
+    if constexpr (!W) {
+      // Unweighted rows: the stack is the mask m alone (its highest bit t1 the top vertex), the
+      // candidates still to push are `rest`. Each iteration takes the vertex t2 below the top
+      // and the next candidate k by bit scans, reads the three sums from the point column
+      // (independent reads; a point's weight is its index) and pops t1 or pushes k: two masks
+      // and one index are the whole state, so the loop carries no sums from one iteration to
+      // the next (about 26 VALU instructions an iteration, where carrying the top two vertices
+      // and the next candidate in registers took about 40 in selects and moves).
+      // The first candidate goes on the stack at once (with only point 0 below it there is
+      // nothing to test), which spares every lane the loop's first iteration.
+      Mask rest = cand & ~Mask(1);
+      int t1 = lowest_bit(rest);  // point nn is always a candidate
+      rest &= rest - 1;
+      m |= Mask(1) << t1;
+      while (rest) {
+        // (point 0 never leaves the bottom; with it alone on the stack there is nothing to pop,
+        // and the bit scan below then reads point 0 again)
+        const Mask below = m & ~(Mask(1) << t1);
+        const int t2 = highest_bit(below | Mask(1));
+        const int k = lowest_bit(rest);
+        const double sA = colS[t2 * THREADS + tid];
+        const double sB = colS[t1 * THREADS + tid];
+        const double sk = colS[k * THREADS + tid];
+        const bool pop =
+            below != 0 && pools<EXACT>(sB - sA, static_cast<double>(t1 - t2), sk - sB, static_cast<double>(k - t1));
+        // (selects, not branches: a wave whose lanes differ would run both)
+        m = pop ? below : (m | (Mask(1) << k));
+        t1 = pop ? t2 : k;
+        rest = pop ? rest : (rest & (rest - 1));
       }
-      // Both possible successors are read before the choice: the vertex below t2 (a pop makes
-      // it the second vertex) and the candidate after k (a push makes it the next candidate).
-      const Mask below = t2 > 0 ? (m & ((Mask(1) << t2) - Mask(1))) : Mask(0);
-      const int t3 = below ? highest_bit(below) : -1;
-      const int kn = rest ? lowest_bit(rest) : -1;
-      const double s3 = colS[(t3 > 0 ? t3 : 0) * THREADS + tid];
-      const double skn = colS[(kn > 0 ? kn : 0) * THREADS + tid];
-      double w3 = 0.0, wkn = 0.0;
-      if constexpr (W) {
-        w3 = colW[(t3 > 0 ? t3 : 0) * THREADS + tid];
-        wkn = colW[(kn > 0 ? kn : 0) * THREADS + tid];
-      } else {
-        wkn = static_cast<double>(kn);
+    } else {
+      // stack: t1 (last vertex) and t2 (< 0: none) with their sums and weights; the stack itself
+      // is the mask m. The candidate being pushed is k; rest holds the candidates after it.
+      // The first candidate goes on the stack at once (with only point 0 below it there is
+      // nothing to test), which spares every lane the loop's first iteration.
+      Mask rest = cand & ~Mask(1);
+      int t1 = lowest_bit(rest);  // point nn is always a candidate
+      rest &= rest - 1;
+      int t2 = 0;
+      double s1 = colS[t1 * THREADS + tid], s2 = 0.0;
+      double w1 = W ? colW[W ? t1 * THREADS + tid : 0] : static_cast<double>(t1), w2 = 0.0;
+      m |= Mask(1) << t1;
+      int k = rest ? lowest_bit(rest) : -1;
+      rest &= rest - 1;
+      double sk = colS[(k > 0 ? k : 0) * THREADS + tid];
+      double wk = W ? colW[W ? (k > 0 ? k : 0) * THREADS + tid : 0] : static_cast<double>(k);
+      while (k >= 0) {
+        bool pop = false;
+        if constexpr (W) {
+          pop = t2 >= 0 && pools<EXACT>(s1 - s2, w1 - w2, sk - s1, wk - w1);
+        } else {
+          pop = t2 >= 0 && pools<EXACT>(s1 - s2, static_cast<double>(t1 - t2), sk - s1,
+                                        static_cast<double>(k - t1));
+        }
+        // Both possible successors are read before the choice: the vertex below t2 (a pop makes
+        // it the second vertex) and the candidate after k (a push makes it the next candidate).
+        const Mask below = t2 > 0 ? (m & ((Mask(1) << t2) - Mask(1))) : Mask(0);
+        const int t3 = below ? highest_bit(below) : -1;
+        const int kn = rest ? lowest_bit(rest) : -1;
+        const double s3 = colS[(t3 > 0 ? t3 : 0) * THREADS + tid];
+        const double skn = colS[(kn > 0 ? kn : 0) * THREADS + tid];
+        double w3 = 0.0, wkn = 0.0;
+        if constexpr (W) {
+          w3 = colW[(t3 > 0 ? t3 : 0) * THREADS + tid];
+          wkn = colW[(kn > 0 ? kn : 0) * THREADS + tid];
+        } else {
+          wkn = static_cast<double>(kn);
+        }
+        // (selects, not branches: a wave whose lanes differ would run both)
+        m = pop ? (m & ~(Mask(1) << t1)) : (m | (Mask(1) << k));
+        const int nt1 = pop ? t2 : k, nt2 = pop ? t3 : t1;
+        const double ns1 = pop ? s2 : sk, ns2 = pop ? s3 : s1;
+        const double nw1 = pop ? w2 : wk, nw2 = pop ? w3 : w1;
+        t1 = nt1;
+        t2 = nt2;
+        s1 = ns1;
+        s2 = ns2;
+        w1 = nw1;
+        w2 = nw2;
+        k = pop ? k : kn;
+        sk = pop ? sk : skn;
+        wk = pop ? wk : wkn;
+        rest = pop ? rest : (rest & (rest - 1));
       }
-      // (selects, not branches: a wave whose lanes differ would run both)
-      m = pop ? (m & ~(Mask(1) << t1)) : (m | (Mask(1) << k));
-      const int nt1 = pop ? t2 : k, nt2 = pop ? t3 : t1;
-      const double ns1 = pop ? s2 : sk, ns2 = pop ? s3 : s1;
-      const double nw1 = pop ? w2 : wk, nw2 = pop ? w3 : w1;
-      t1 = nt1;
-      t2 = nt2;
-      s1 = ns1;
-      s2 = ns2;
-      w1 = nw1;
-      w2 = nw2;
-      k = pop ? k : kn;
-      sk = pop ? sk : skn;
-      wk = pop ? wk : wkn;
-      rest = pop ? rest : (rest & (rest - 1));
     }
   }
 
@@ -699,6 +732,93 @@ __global__ __launch_bounds__(kPlanThreads) void ragged_plan_kernel(const int64_t
   }
 }
 
+// One row's backward (block sums of g, and w; the block's fit as the forward formed it for the
+// clamp mask and gw): gy = w * mask * G / W into oy, gw = (y - fit) * mask * G / W into ow
+// (need_mean: gw or a clamp asks for the fit). bits: the row's start bits, bit 0 set.
+template <typename T, int NMAX, bool W>
+__device__ __forceinline__ void row_grad(const T (&gv)[NMAX], const T (&wv)[W ? NMAX : 1], const T (&yv)[NMAX],
+                                         uint32_t bits, int n, bool need_mean, bool use_lo, T lo, bool use_hi, T hi,
+                                         T (&oy)[NMAX], T (&ow)[NMAX]) {
+  // Cumulative sums of w*y and w exactly as the forward forms them (increasing sign).
+  double S[NMAX + 1];
+  double P[W ? NMAX + 1 : 1];
+  S[0] = 0.0;
+  if constexpr (W) P[0] = 0.0;
+  if (need_mean) {
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n) {
+        const double yc = static_cast<double>(yv[c]);
+        if constexpr (W) {
+          const double wc = static_cast<double>(wv[c]);
+          S[c + 1] = S[c] + wc * yc;
+          P[c + 1] = P[c] + wc;
+        } else {
+          S[c + 1] = S[c] + yc;
+        }
+      }
+    }
+  }
+  auto Wk = [&](int k) -> double {
+    if constexpr (W) return P[k];
+    else return static_cast<double>(k);
+  };
+
+  // Backwards: per block start i, q[i] = mask * G / W and fitv[i] = the block's fit.
+  double q[NMAX];
+  T fitv[NMAX];
+  {
+    double ga = 0.0, wa = 0.0, se = 0.0, we = 0.0;
+    int end = n;
+#pragma unroll
+    for (int i = NMAX - 1; i >= 0; --i) {
+      if (i < n) {
+        if (i == n - 1 && need_mean) {
+          se = S[i + 1];
+          we = Wk(i + 1);
+        }
+        ga += static_cast<double>(gv[i]);
+        if constexpr (W) wa += static_cast<double>(wv[i]);
+        if ((bits >> i) & 1u) {
+          const double wsum = W ? wa : static_cast<double>(end - i);
+          bool pass = true;
+          if (need_mean) {
+            // the forward's block mean, bit for bit
+            const T f = W ? static_cast<T>(slope_div(se - S[i], we - Wk(i)))
+                          : static_cast<T>((se - S[i]) * (1.0 / static_cast<double>(end - i)));
+            fitv[i] = f;
+            pass = !(use_lo || use_hi) || clip_passes(f, use_lo, lo, use_hi, hi);
+            se = S[i];
+            we = Wk(i);
+          }
+          q[i] = pass ? ga / wsum : 0.0;
+          ga = 0.0;
+          wa = 0.0;
+          end = i;
+        }
+      }
+    }
+  }
+  {
+    double cq = 0.0;
+    T cf = T(0);
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      if (i < n) {
+        if ((bits >> i) & 1u) {
+          cq = q[i];
+          if (need_mean) cf = fitv[i];
+        }
+        const double wi = W ? static_cast<double>(wv[W ? i : 0]) : 1.0;
+        oy[i] = static_cast<T>(wi * cq);
+        if (need_mean) {
+          ow[i] = static_cast<T>((static_cast<double>(yv[i]) - static_cast<double>(cf)) * cq);
+        }
+      }
+    }
+  }
+}
+
 // Backward: gy = w * mask * G / W, gw = (y - fit) * mask * G / W over each block, the block's
 // fit recomputed from the same float64 cumulative sums and division the forward used (so
 // bit-identical to it).
@@ -761,85 +881,8 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_kernel(
     }
   }
 
-  // Cumulative sums of w*y and w exactly as the forward forms them (increasing sign).
-  double S[NMAX + 1];
-  double P[W ? NMAX + 1 : 1];
-  S[0] = 0.0;
-  if constexpr (W) P[0] = 0.0;
-  if (need_mean) {
-#pragma unroll
-    for (int c = 0; c < NMAX; ++c) {
-      if (c < n) {
-        const double yc = static_cast<double>(yv[c]);
-        if constexpr (W) {
-          const double wc = static_cast<double>(wv[c]);
-          S[c + 1] = S[c] + wc * yc;
-          P[c + 1] = P[c] + wc;
-        } else {
-          S[c + 1] = S[c] + yc;
-        }
-      }
-    }
-  }
-  auto Wk = [&](int k) -> double {
-    if constexpr (W) return P[k];
-    else return static_cast<double>(k);
-  };
-
-  // Backwards: per block start i, q[i] = mask * G / W and fitv[i] = the block's fit.
-  double q[NMAX];
-  T fitv[NMAX];
-  {
-    double ga = 0.0, wa = 0.0, se = 0.0, we = 0.0;
-    int end = n;
-#pragma unroll
-    for (int i = NMAX - 1; i >= 0; --i) {
-      if (i < n) {
-        if (i == n - 1 && need_mean) {
-          se = S[i + 1];
-          we = Wk(i + 1);
-        }
-        ga += static_cast<double>(gv[i]);
-        if constexpr (W) wa += static_cast<double>(wv[i]);
-        if ((bits >> i) & 1u) {
-          const double wsum = W ? wa : static_cast<double>(end - i);
-          bool pass = true;
-          if (need_mean) {
-            // the forward's block mean, bit for bit
-            const T f = W ? static_cast<T>(slope_div(se - S[i], we - Wk(i)))
-                          : static_cast<T>((se - S[i]) * (1.0 / static_cast<double>(end - i)));
-            fitv[i] = f;
-            pass = !(use_lo || use_hi) || clip_passes(f, use_lo, lo, use_hi, hi);
-            se = S[i];
-            we = Wk(i);
-          }
-          q[i] = pass ? ga / wsum : 0.0;
-          ga = 0.0;
-          wa = 0.0;
-          end = i;
-        }
-      }
-    }
-  }
   T oy[NMAX], ow[NMAX];
-  {
-    double cq = 0.0;
-    T cf = T(0);
-#pragma unroll
-    for (int i = 0; i < NMAX; ++i) {
-      if (i < n) {
-        if ((bits >> i) & 1u) {
-          cq = q[i];
-          if (need_mean) cf = fitv[i];
-        }
-        const double wi = W ? static_cast<double>(wv[W ? i : 0]) : 1.0;
-        oy[i] = static_cast<T>(wi * cq);
-        if (need_mean) {
-          ow[i] = static_cast<T>((static_cast<double>(yv[i]) - static_cast<double>(cf)) * cq);
-        }
-      }
-    }
-  }
+  row_grad<T, NMAX, W>(gv, wv, yv, bits, n, need_mean, use_lo, lo, use_hi, hi, oy, ow);
   if constexpr (DIRECT) {
     if (active) {
       if (gy != nullptr) store_row<T, NMAX>(gy + (row0 + tid) * NMAX, oy);
@@ -867,6 +910,224 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_kernel(
   }
 }
 
+// A wave's 64 consecutive rows of NMAX values (a whole number of 16-byte chunks each), moved
+// between memory and one row per lane through LDS: memory sees coalesced 16-byte accesses (lane l
+// takes chunks l, l + 64, ...) and each lane gets its whole row. (Each lane reading its own row
+// with 16-byte accesses 64 bytes apart moved C2's 128 MB in 25 us where a coalesced copy takes
+// 19.) `at(o)` maps byte o of the wave's 64 * NMAX * sizeof(T) bytes to its LDS address; LDS
+// operations of a wave complete in order, so a wave-scope fence between the writes and the reads
+// is all the ordering the exchange needs. Chunk q is kept at chunk position q ^ ((q >> 4) & 15)
+// (within its own 256 bytes): in row order lanes 4 apart would otherwise hit the same banks.
+template <typename T, int NMAX>
+struct WaveRows {
+  static constexpr int kRowBytes = NMAX * sizeof(T);
+  static constexpr int kChunks = kRowBytes / 16;  // 16-byte chunks per lane
+  static constexpr int V = Vec16<T>::kN;
+  using VT = typename Vec16<T>::type;
+  using IT = unsigned __attribute__((ext_vector_type(4)));
+  static_assert(kRowBytes % 16 == 0, "whole 16-byte chunks");
+
+  IT c[kChunks];
+
+  __device__ __forceinline__ static int pos(int q) { return (q ^ ((q >> 4) & 15)) * 16; }
+
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int lane) {
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) c[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (lane + j * kWave) * 16, 0, 0);
+  }
+
+  template <class At>
+  __device__ __forceinline__ void to_row(At at, int lane, T (&v)[NMAX]) const {
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) *reinterpret_cast<IT*>(at(pos(lane + j * kWave))) = c[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+      const VT x = *reinterpret_cast<const VT*>(at(pos(lane * kChunks + j)));
+#pragma unroll
+      for (int t = 0; t < V; ++t) v[j * V + t] = x[t];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  template <class At>
+  __device__ __forceinline__ static void store(At at, int lane, const T (&v)[NMAX], __amdgpu_buffer_rsrc_t r) {
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+      VT x;
+#pragma unroll
+      for (int t = 0; t < V; ++t) x[t] = v[j * V + t];
+      *reinterpret_cast<VT*>(at(pos(lane * kChunks + j))) = x;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+      const IT x = *reinterpret_cast<const IT*>(at(pos(lane + j * kWave)));
+      __builtin_amdgcn_raw_buffer_store_b128(x, r, (lane + j * kWave) * 16, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+};
+
+// Whole rows of NMAX values that are a whole number of 16-byte chunks (n == NMAX, aligned): one
+// row per lane, moved by WaveRows through the wave's own slice of the point columns (free while
+// the rows move in and out). A workgroup walks blocks of THREADS rows (its own index, then every
+// gridDim.x-th block after it), the next block's loads in flight while it fits the current one:
+// two register buffers in turn (a copy from one to the other would make the compiler wait for the
+// loads at the copy). Loads and stores go through buffer resources based at each wave's rows, so
+// rows past the batch's end (the last block's) read zeros and store nothing, and every memory
+// instruction is unconditional.
+template <typename T, int NMAX, bool W, bool INC>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void short_rows_kernel(
+    const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
+    uint32_t* __restrict__ starts, uint32_t* __restrict__ bad_weight, int64_t batch, unsigned flags,
+    T lo, T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  using WR = WaveRows<T, NMAX>;
+  constexpr int64_t kRowBytes = WR::kRowBytes;
+  __shared__ double lds[(NMAX + 1) * THREADS * (W ? 2 : 1)];
+  double* colS = lds;                        // [NMAX + 1][THREADS]
+  double* colW = lds + (NMAX + 1) * THREADS;  // weighted only
+  __shared__ double rcp[W ? 1 : kRcpN];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  if constexpr (!W) {
+    if (tid < kRcpN) rcp[tid] = kRcp.v[tid];
+    __syncthreads();
+  }
+  // the wave's staging: byte o of its 64 rows in row o / 512 of a point-column array, at the
+  // wave's 512 bytes of that row (64 * NMAX * sizeof(T) <= 512 * NMAX bytes: the array has NMAX + 1
+  // rows)
+  auto at_s = [&](int o) { return reinterpret_cast<char*>(colS) + (o >> 9) * (THREADS * 8) + wave * 512 + (o & 511); };
+  auto at_w = [&](int o) { return reinterpret_cast<char*>(colW) + (o >> 9) * (THREADS * 8) + wave * 512 + (o & 511); };
+  const int64_t nblk = (batch + THREADS - 1) / THREADS;
+  const int64_t stride = gridDim.x;
+  // (every resource from the block index alone, so it stays in scalar registers)
+  auto rsrc = [&](const void* base, int64_t b, int64_t row_bytes) {
+    const int64_t first = wave_uniform(b * THREADS + wave * kWave);
+    const int64_t left = first < batch ? (batch - first) * row_bytes : 0;
+    return make_rsrc(static_cast<const char*>(base) + (first < batch ? first : 0) * row_bytes, left);
+  };
+  struct Buf {
+    WR y, w;
+  };
+  auto load = [&](int64_t b, Buf& bf) {
+    bf.y.load(rsrc(y, b, kRowBytes), lane);
+    if constexpr (W) bf.w.load(rsrc(w, b, kRowBytes), lane);
+  };
+  auto fit_block = [&](int64_t b, const Buf& bf) {
+    const bool active = b * THREADS + tid < batch;
+    T yv[NMAX], wv[W ? NMAX : 1];
+    bf.y.to_row(at_s, lane, yv);
+    if constexpr (W) bf.w.to_row(at_w, lane, wv);
+    T fit[NMAX];
+    typename MaskOf<NMAX>::type m;
+    bool bad;
+    row_fit<T, NMAX, W, INC, false>(yv, wv, NMAX, active, colS, colW, rcp, bad_weight, flags, lo, hi, fit, m, bad);
+    WR::store(at_s, lane, fit, rsrc(out, b, kRowBytes));
+    if (starts != nullptr) {
+      const uint32_t low = NMAX >= 32 ? 0xFFFFFFFFu : ((1u << NMAX) - 1u);
+      const uint32_t bits = bad ? 1u : static_cast<uint32_t>(m) & low;
+      __builtin_amdgcn_raw_buffer_store_b32(bits, rsrc(starts, b, 4), lane * 4, 0, 0);
+    }
+  };
+  Buf ba, bb;
+  int64_t blk = blockIdx.x;
+  load(blk, ba);
+  while (blk < nblk) {
+    load(blk + stride, bb);
+    fit_block(blk, ba);
+    blk += stride;
+    if (blk >= nblk) break;
+    load(blk + stride, ba);
+    fit_block(blk, bb);
+    blk += stride;
+  }
+}
+
+// Workgroups for a kernel that walks `blocks` blocks: as many as the GPU holds at once (per CU,
+// the lesser of what LDS and threads allow), or fewer where there are fewer blocks.
+unsigned resident_grid(int64_t blocks, size_t lds_bytes, int threads) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int cu = cus[dev].load(std::memory_order_relaxed);
+  if (cu <= 0) {
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cu <= 0) cu = 256;
+    cus[dev].store(cu, std::memory_order_relaxed);
+  }
+  const int by_lds = static_cast<int>((160 * 1024) / (lds_bytes > 0 ? lds_bytes : 1));
+  const int by_threads = 2048 / threads;
+  const int64_t per_cu = std::max(1, std::min(by_lds, by_threads));
+  return static_cast<unsigned>(std::min<int64_t>(blocks, per_cu * cu));
+}
+
+// The backward of whole 16-byte-chunk rows (n == NMAX, aligned), laid out like short_rows_kernel:
+// a persistent grid, the next block's loads in flight, coalesced accesses through a per-wave LDS
+// staging area (64 rows of one array at a time). NEEDY: y is read (gw, or a clamp's mask, needs
+// the block's fit).
+template <typename T, int NMAX, bool W, bool NEEDY>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_rows_kernel(
+    const uint32_t* __restrict__ starts, const T* __restrict__ g, const T* __restrict__ w,
+    const T* __restrict__ y, T* __restrict__ gy, T* __restrict__ gw, int64_t batch, unsigned flags, T lo,
+    T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  using WR = WaveRows<T, NMAX>;
+  constexpr int kRowBytes = WR::kRowBytes;
+  __shared__ __align__(16) char stg[THREADS * kRowBytes];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  auto at = [&](int o) { return stg + wave * (kWave * kRowBytes) + o; };
+  const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
+  const int64_t nblk = (batch + THREADS - 1) / THREADS;
+  const int64_t stride = gridDim.x;
+  auto rsrc = [&](const void* base, int64_t b, int64_t row_bytes) {
+    const int64_t first = wave_uniform(b * THREADS + wave * kWave);
+    const int64_t left = first < batch ? (batch - first) * row_bytes : 0;
+    return make_rsrc(static_cast<const char*>(base) + (first < batch ? first : 0) * row_bytes, left);
+  };
+  struct Buf {
+    WR g, w, y;
+    uint32_t bits;
+  };
+  auto load = [&](int64_t b, Buf& bf) {
+    bf.bits = __builtin_amdgcn_raw_buffer_load_b32(rsrc(starts, b, 4), lane * 4, 0, 0);
+    bf.g.load(rsrc(g, b, kRowBytes), lane);
+    if constexpr (W) bf.w.load(rsrc(w, b, kRowBytes), lane);
+    if constexpr (NEEDY) bf.y.load(rsrc(y, b, kRowBytes), lane);
+  };
+  auto grad_block = [&](int64_t b, const Buf& bf) {
+    T gv[NMAX], wv[W ? NMAX : 1], yv[NMAX];
+    bf.g.to_row(at, lane, gv);
+    if constexpr (W) bf.w.to_row(at, lane, wv);
+    if constexpr (NEEDY) bf.y.to_row(at, lane, yv);
+    T oy[NMAX], ow[NMAX];
+    row_grad<T, NMAX, W>(gv, wv, yv, bf.bits | 1u, NMAX, NEEDY, use_lo, lo, use_hi, hi, oy, ow);
+    if (gy != nullptr) WR::store(at, lane, oy, rsrc(gy, b, kRowBytes));
+    if constexpr (NEEDY) {
+      if (gw != nullptr) WR::store(at, lane, ow, rsrc(gw, b, kRowBytes));
+    }
+  };
+  Buf ba, bb;
+  int64_t blk = blockIdx.x;
+  load(blk, ba);
+  while (blk < nblk) {
+    load(blk + stride, bb);
+    grad_block(blk, ba);
+    blk += stride;
+    if (blk >= nblk) break;
+    load(blk + stride, ba);
+    grad_block(blk, bb);
+    blk += stride;
+  }
+}
+
 bool aligned16(const void* p) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
@@ -884,8 +1145,17 @@ hipError_t launch_fit(const ShortArgs& a) {
   };
   const bool inc = (a.flags & TI_INCREASING) != 0;
   if constexpr ((NMAX * sizeof(T)) % 16 == 0) {
-    if (a.n == NMAX && aligned16(a.y) && aligned16(a.w) && aligned16(a.out))
-      return inc ? run(short_fit_kernel<T, NMAX, W, true, true>) : run(short_fit_kernel<T, NMAX, W, true, false>);
+    if (a.n == NMAX && aligned16(a.y) && aligned16(a.w) && aligned16(a.out)) {
+      const size_t lds = (static_cast<size_t>(NMAX + 1) * THREADS * (W ? 2 : 1) + (W ? 1 : kRcpN)) * sizeof(double);
+      const unsigned grid = resident_grid(blocks, lds, THREADS);
+      auto rows = [&](auto kernel) {
+        kernel<<<dim3(grid), dim3(THREADS), 0, a.stream>>>(static_cast<const T*>(a.y), static_cast<const T*>(a.w),
+                                                          static_cast<T*>(a.out), a.starts, a.bad_weight, a.batch,
+                                                          a.flags, static_cast<T>(a.lo), static_cast<T>(a.hi));
+        return hipGetLastError();
+      };
+      return inc ? rows(short_rows_kernel<T, NMAX, W, true>) : rows(short_rows_kernel<T, NMAX, W, false>);
+    }
   }
   return inc ? run(short_fit_kernel<T, NMAX, W, false, true>) : run(short_fit_kernel<T, NMAX, W, false, false>);
 }
@@ -903,8 +1173,18 @@ hipError_t launch_grad(const ShortGradArgs& a) {
   };
   if constexpr ((NMAX * sizeof(T)) % 16 == 0) {
     if (a.n == NMAX && aligned16(a.g) && aligned16(a.w) && aligned16(a.y) && aligned16(a.gy) &&
-        aligned16(a.gw))
-      return run(short_grad_kernel<T, NMAX, W, true>);
+        aligned16(a.gw)) {
+      const bool needy = a.gw != nullptr || (a.flags & (TI_CLIP_MIN | TI_CLIP_MAX)) != 0;
+      const unsigned grid = resident_grid(blocks, static_cast<size_t>(THREADS) * NMAX * sizeof(T), THREADS);
+      auto rows = [&](auto kernel) {
+        kernel<<<dim3(grid), dim3(THREADS), 0, a.stream>>>(
+            a.starts, static_cast<const T*>(a.g), static_cast<const T*>(a.w), static_cast<const T*>(a.y),
+            static_cast<T*>(a.gy), static_cast<T*>(a.gw), a.batch, a.flags, static_cast<T>(a.lo),
+            static_cast<T>(a.hi));
+        return hipGetLastError();
+      };
+      return needy ? rows(short_grad_rows_kernel<T, NMAX, W, true>) : rows(short_grad_rows_kernel<T, NMAX, W, false>);
+    }
   }
   return run(short_grad_kernel<T, NMAX, W, false>);
 }

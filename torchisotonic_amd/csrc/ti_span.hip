@@ -64,6 +64,10 @@ struct SpanLds {
   double rsl[PR ? R : 0][kSpanLanes];
   double rw[W ? R : 0][kSpanLanes];
   double rwl[W && PR ? R : 0][kSpanLanes];
+  // Weighted float32 runs two waves a SIMD (its registers allow no more), so eight waves share
+  // a CU's 160 KB of LDS: the rest of a wave's 20 KB becomes merge slots for the group's merge
+  // (C4's groups need up to about 420 slots).
+  char pad[(W && !PR) ? 20480 - (C * 8 * 2 + R * (4 + 8 * 2)) * kSpanLanes : 0];
 };
 
 // N consecutive values at byte offset `off` of a buffer resource, 16 bytes per load. Reads past
@@ -81,20 +85,6 @@ __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t of
 #pragma unroll
     for (int t = 0; t < V; ++t) v[j * V + t] = x[t];
   }
-}
-
-// v, taken from the wave's first lane (for values the same in every lane).
-__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
-  const uint64_t u = static_cast<uint64_t>(v);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// A buffer resource over [base, base + bytes) (bytes clamped to the 32-bit range field).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int nrec = static_cast<int>(bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), nrec, 0x00020000);
 }
 
 template <typename T, bool W, int C, int R, int LC, bool INC>
@@ -405,8 +395,9 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // (the round state first, then the slots, in the wave's LDS)
   constexpr size_t kRoundBytes = (sizeof(MergeRounds) + 63) & ~size_t(63);
   constexpr int kCap =
-      static_cast<int>(((sizeof(SpanLds<T, W, 2 * C, R>) - kRoundBytes) / slot_bytes<W, true>()) & ~size_t(63));
+      static_cast<int>((sizeof(SpanLds<T, W, 2 * C, R>) - kRoundBytes) / slot_bytes<W, true>());
   static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
+  static_assert(!(W && !PR) || sizeof(SpanLds<T, W, 2 * C, R>) == 20480, "weighted float32: 20 KB a wave");
   if (nslots > kCap) {
     // too many vertices: the span's hull goes to the span array, for the merge kernel
     write_span_hull();
