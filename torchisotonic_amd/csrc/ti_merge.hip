@@ -174,7 +174,7 @@ __device__ __forceinline__ int child_of_slot(const MergeSmall& sm, int nch, int 
 template <bool W, bool PR>
 __device__ __forceinline__ HPt child_vertex(const MergeArgs& a, const MergeSmall& sm, int64_t row,
                                             int64_t c0, int c, int k) {
-  const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + c);
+  const NodeOut ci = node_out(a.in, W, row * a.in.npr + c0 + c);
   HPt p;
   p.i = ci.idx[k] + static_cast<int>(c * a.child_elems);
   const DD S = dd_add(DD{sm.tot[2][c], sm.tot[3][c]}, DD{ci.shi[k], PR ? ci.slo[k] : 0.0});
@@ -238,23 +238,30 @@ __device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, MergeRounds&
 // The merge in the parent's global array, for children with more vertices than LDS holds
 // (hulls of trend-like data, where few vertices drop): children laid end to end, then pairwise
 // rounds of bridges (one lane per pair) and moves of each right part's surviving suffix.
-template <bool W, bool PR>
+template <bool W, bool PR, int NT>
 __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, int64_t c0, int nch,
                              const NodeOut& pout) {
   const int tid = threadIdx.x;
   const int total = sm.total;
   const VArr v = dvarr_of(pout);
-  // (the first wave does the work; every thread of a larger workgroup meets the barriers)
-  for (int s = tid < kWave ? tid : total; s < total; s += kWave) {
-    const int c = child_of_slot(sm, nch, s);
-    const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
+  // The children end to end, in the parent's frame, where they lie (the parent's vertices take
+  // the place of its children's): slot s comes from its child's vertex at or after s, so NT slots
+  // at a time, read before any is written, in increasing order, never overwrite a vertex still to
+  // be read.
+  for (int s0 = 0; s0 < total; s0 += NT) {
+    const int s = s0 + tid;
     VPt p;
-    p.i = h.i;
-    p.s = DD{h.s, h.sl};
-    p.w = DD{h.w, h.wl};
-    vstore<W>(v, s, p);
+    if (s < total) {
+      const int c = child_of_slot(sm, nch, s);
+      const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
+      p.i = h.i;
+      p.s = DD{h.s, h.sl};
+      p.w = DD{h.w, h.wl};
+    }
+    __syncthreads();
+    if (s < total) vstore<W>(v, s, p);
+    __syncthreads();
   }
-  __syncthreads();
 #pragma unroll 1
   for (int span = 1; span < nch; span <<= 1) {
     const int nm = (nch + 2 * span - 1) / (2 * span);  // merges this round
@@ -320,13 +327,13 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
   __shared__ MergeRounds rs;
   extern __shared__ __align__(16) char lds_dyn[];
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x / a.npr_out;
-  const int64_t j = blockIdx.x - row * a.npr_out;
+  const int64_t row = blockIdx.x / a.out.npr;
+  const int64_t j = blockIdx.x - row * a.out.npr;
   const int64_t c0 = j * kGroup;  // first child within the row
-  const int nch = static_cast<int>(min<int64_t>(kGroup, a.npr_in - c0));
-  const NodeOut pout = node_out(a.out, a.k_out, a.cap_out, W, row * a.npr_out + j);
+  const int nch = static_cast<int>(min<int64_t>(kGroup, a.in.npr - c0));
+  const NodeOut pout = node_out(a.out, W, row * a.out.npr + j);
   // (a first child's count of -1: the span kernel merged this group already)
-  if (*node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0).count < 0) return;
+  if (*node_out(a.in, W, row * a.in.npr + c0).count < 0) return;
 
   // Children (first wave): counts, NaN flags, and offsets within the parent (double-double scan).
   if (tid < kWave) {
@@ -334,7 +341,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
     int cnt = 0, bad = 0;
     DD tw{0.0, 0.0}, ts{0.0, 0.0};
     if (lane < nch) {
-      const NodeOut ci = node_out(const_cast<void*>(a.in), a.k_in, a.cap_in, W, row * a.npr_in + c0 + lane);
+      const NodeOut ci = node_out(a.in, W, row * a.in.npr + c0 + lane);
       cnt = *ci.count;
       bad = *ci.bad;
       tw = DD{ci.tot[0], ci.tot[1]};
@@ -380,7 +387,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
   if (sm.total <= cap_lds) {
     merge_lds<W, PR, NT, G>(a, sm, rs, slots_carve<W, PR>(lds_dyn, cap_lds), row, c0, nch, pout);
   } else {
-    merge_global<W, PR>(a, sm, row, c0, nch, pout);
+    merge_global<W, PR, NT>(a, sm, row, c0, nch, pout);
   }
   if (tid == 0) {
     *pout.bad = sm.bad;
@@ -397,14 +404,14 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
 // one edge covers the tile, its slope. All tiles search at once, so the expansion and the
 // backward start from one read per tile.
 template <bool W>
-__global__ __launch_bounds__(256) void rank_kernel(const void* hulls, int64_t batch, int64_t cap, int64_t n,
+__global__ __launch_bounds__(256) void rank_kernel(NodeLevel hulls, int64_t batch, int64_t n,
                                                    int64_t tile_n, int64_t tpr, TileRec* tiles) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (g >= batch * tpr) return;
   const int64_t row = g / tpr;
   const int64_t ta = (g - row * tpr) * tile_n;
   const int64_t tb = min(ta + tile_n, n);
-  const NodeOut fin = node_out(const_cast<void*>(hulls), batch, cap, W, row);
+  const NodeOut fin = node_out(hulls, W, row);
   const int* idx = fin.idx;
   const int count = *fin.count;
   const bool bad = *fin.bad != 0;
@@ -516,7 +523,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       write_starts((t0 == 0 && (rec[u].flags & kTileHead)) ? 1u : 0u);
       continue;
     }
-    const VArr v = dvarr_of(node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row));
+    const VArr v = dvarr_of(node_out(a.hulls, W, row));
     // (holds for any well-formed hull; it keeps the reads in bounds regardless)
     const int rB = min(min(rec[u].rb, rA + C::kN + 1), rec[u].last);
 
@@ -593,7 +600,7 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
     int ne = 0;
     if (tid < rows) {
       const int64_t row = row0 + tid;
-      const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row);
+      const NodeOut fin = node_out(a.hulls, W, row);
       const int count = *fin.count;
       const bool bad = *fin.bad != 0;
       TileRec r;
@@ -637,7 +644,7 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
     int first = 0;
     T val = quiet_nan<T>();
     if (!rbad[rl]) {
-      const VArr v = dvarr_of(node_out(const_cast<void*>(a.hulls), a.batch, a.cap, W, row0 + rl));
+      const VArr v = dvarr_of(node_out(a.hulls, W, row0 + rl));
       const int j = b - roff[rl];
       const VPt p = vload<W>(v, j), q = vload<W>(v, j + 1);
       double dW, dS;
@@ -745,26 +752,29 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
     }
   }
   p.span0 = span0;
+  p.batch = batch;
+  p.weighted = weighted;
   int64_t npr = (n + span0 - 1) / span0;
   int64_t span = span0;  // elements per node at this level
-  size_t buf[2] = {0, 0};
+  int64_t spn = 1;       // spans per node at this level
+  size_t off = 0;
   int level = 0;
   for (;;) {
-    const int64_t cap = (span < n ? span : n) + 1;
     p.npr[level] = npr;
-    p.cap[level] = cap;
     p.span[level] = span;
-    const size_t bytes = node_array_bytes(batch * npr, cap, weighted);
-    buf[level & 1] = buf[level & 1] > bytes ? buf[level & 1] : bytes;
+    p.spn[level] = spn;
+    p.off_meta[level] = off;
+    off += align256(node_meta_bytes(batch * npr));
     if (npr == 1) break;
     npr = (npr + kGroup - 1) / kGroup;
     span *= kGroup;
+    spn *= kGroup;
     ++level;
   }
   p.levels = level;  // merge launches; the final hulls are at level p.levels
-  p.off_buf[0] = 0;
-  p.off_buf[1] = align256(buf[0]);
-  p.off_rank = p.off_buf[1] + align256(buf[1]);
+  p.slots = batch * p.npr[0] * (span0 + 1);
+  p.off_store = off;
+  p.off_rank = p.off_store + align256(vertex_store_bytes(p.slots, weighted));
   p.bytes = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
   return p;
 }
@@ -772,22 +782,16 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   const bool W = t.w != nullptr;
   char* base = static_cast<char*>(ws);
-  // level 0: span hulls
-  hipError_t e = span_run(t, base + p.off_buf[0], p.npr[0], p.cap[0], p.span0, base + p.off_buf[1], p.cap[1],
-                          p.rows_per_wave);
+  const NodeLevel fin = p.level(ws, p.levels);
+  // level 0: span hulls (and the first merge level, fused, where there is one)
+  hipError_t e = span_run(t, p.level(ws, 0), p.span0, p.level(ws, p.levels >= 1 ? 1 : 0), p.rows_per_wave);
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
   for (int l = 1; l <= p.levels; ++l) {
     MergeArgs m;
-    m.in = base + p.off_buf[(l - 1) & 1];
-    m.k_in = t.batch * p.npr[l - 1];
-    m.cap_in = p.cap[l - 1];
-    m.npr_in = p.npr[l - 1];
-    m.out = base + p.off_buf[l & 1];
-    m.k_out = t.batch * p.npr[l];
-    m.cap_out = p.cap[l];
-    m.npr_out = p.npr[l];
+    m.in = p.level(ws, l - 1);
+    m.out = p.level(ws, l);
     m.child_elems = p.span[l - 1];
     const unsigned grid = static_cast<unsigned>(t.batch * p.npr[l]);
     // Workgroup size and LDS slots by how many merges share the GPU: one wave and 768 slots
@@ -816,9 +820,8 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   if (t.n <= kXpackMaxN) {
     // rows of one tile: records and fit together, whole rows a workgroup
     ExpandArgs x;
-    x.hulls = base + p.off_buf[p.levels & 1];
+    x.hulls = fin;
     x.batch = t.batch;
-    x.cap = p.cap[p.levels];
     x.n = t.n;
     x.tiles_per_row = 1;
     x.out = t.out;
@@ -848,19 +851,16 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     const dim3 grid(static_cast<unsigned>((tiles + 255) / 256));
     TileRec* recs = reinterpret_cast<TileRec*>(base + p.off_rank);
     if (W) {
-      rank_kernel<true><<<grid, dim3(256), 0, t.stream>>>(base + p.off_buf[p.levels & 1], t.batch,
-                                                         p.cap[p.levels], t.n, tile_elems(W), p.tiles_per_row, recs);
+      rank_kernel<true><<<grid, dim3(256), 0, t.stream>>>(fin, t.batch, t.n, tile_elems(W), p.tiles_per_row, recs);
     } else {
-      rank_kernel<false><<<grid, dim3(256), 0, t.stream>>>(base + p.off_buf[p.levels & 1], t.batch,
-                                                          p.cap[p.levels], t.n, tile_elems(W), p.tiles_per_row, recs);
+      rank_kernel<false><<<grid, dim3(256), 0, t.stream>>>(fin, t.batch, t.n, tile_elems(W), p.tiles_per_row, recs);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   ExpandArgs x;
-  x.hulls = base + p.off_buf[p.levels & 1];
+  x.hulls = fin;
   x.batch = t.batch;
-  x.cap = p.cap[p.levels];
   x.n = t.n;
   x.tiles_per_row = p.tiles_per_row;
   x.out = t.out;

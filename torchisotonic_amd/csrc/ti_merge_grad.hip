@@ -44,7 +44,7 @@ GradPlan grad_plan(int64_t batch, int64_t n, bool weighted) {
   GradPlan g{};
   g.tpr = lp.tiles_per_row;
   g.ngroups = (g.tpr + kScanTiles - 1) / kScanTiles;
-  g.cap_final = lp.cap[lp.levels];
+  g.cap_final = lp.npr[0] * (lp.span0 + 1);  // a row's slots: room for any final hull
   size_t off = 0;
   g.off_tg = off;
   off += align256(static_cast<size_t>(batch * g.tpr) * 16);
@@ -70,7 +70,7 @@ struct GradKArgs {
   int64_t batch, n, tpr, ngroups, cap_final;
   unsigned flags;
   double lo, hi;
-  const void* hulls;     // the forward's final node array
+  NodeLevel hulls;       // the forward's final level
   const TileRec* tiles;  // the forward's per-tile records
   double* tg;            // [batch * tpr][2]: tile totals of g
   double* lp;            // [batch * tpr][2]: exclusive prefix within the tile's group
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
   const int t0 = tid * E;
   const int ecount = max(0, min(E, len - t0));
-  const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+  const NodeOut fin = node_out(a.hulls, W, row);
   const TileRec rec = a.tiles[blockIdx.x];
   const bool bad = (rec.flags & kTileBad) != 0;
   const int count = rec.last + 1;
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
   for (int b = tid; b < nb; b += 256) {
     const int r = brow[b];
     const int64_t row = row0 + r;
-    const NodeOut fin = node_out(const_cast<void*>(a.hulls), a.batch, a.cap_final, W, row);
+    const NodeOut fin = node_out(a.hulls, W, row);
     const double G = qv[b];
     double q;
     T mean;
@@ -622,7 +622,7 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.flags = in.flags;
   a.lo = in.lo;
   a.hi = in.hi;
-  a.hulls = fbase + p.off_buf[p.levels & 1];
+  a.hulls = p.level(const_cast<char*>(fbase), p.levels);
   a.tiles = reinterpret_cast<const TileRec*>(fbase + p.off_rank);
   a.tg = reinterpret_cast<double*>(base + gpn.off_tg);
   a.lp = reinterpret_cast<double*>(base + gpn.off_lp);

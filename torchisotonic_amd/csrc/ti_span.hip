@@ -43,10 +43,8 @@ struct SpanArgs {
   int rpw;                // > 1: rows per wave, 64 / rpw spans each (spr == 64 / rpw)
   int64_t span0;          // elements per span
   unsigned flags;
-  void* hulls;            // node array of the spans
-  int64_t cap;
-  void* hulls1;           // node array of the groups (the first merge level)
-  int64_t k1, cap1;
+  NodeLevel hulls;        // the spans' level
+  NodeLevel hulls1;       // the groups' (the first merge level; with rpw > 1, the rows')
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the chunk buffer (sums at
@@ -137,7 +135,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // this lane's span (packed: its row), as an element offset from base
   const int64_t lel = packed ? lane * a.n : multi ? (lane / kl) * a.n + first : lane * a.span0;
   const uint32_t loff = static_cast<uint32_t>(lel * static_cast<int64_t>(sizeof(T)));
-  const NodeOut o = node_out(a.hulls, a.nodes, a.cap, W, node);
+  const NodeOut o = node_out(a.hulls, W, node);
 
   auto ring_put = [&](int q, const HPt& p) {
     const int r = q & (R - 1);
@@ -461,7 +459,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     for (int r = 0; r < nch / kl; ++r) {
       const int f = r == 0 ? 0 : se[r - 1];
       const int cnt = se[r] - f + 1;
-      const NodeOut pout = node_out(a.hulls1, a.k1, a.cap1, W, static_cast<int64_t>(blockIdx.x) * a.rpw + r);
+      const NodeOut pout = node_out(a.hulls1, W, static_cast<int64_t>(blockIdx.x) * a.rpw + r);
       const HPt x0 = sget(v, f);
       auto rebase = [&](HPt x) {
         x.i -= x0.i;
@@ -500,7 +498,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     return;
   }
   const int count = merge_rounds<W, true, kSpanLanes, 2>(v, rs, nslots, nch);
-  const NodeOut pout = node_out(a.hulls1, a.k1, a.cap1, W, blockIdx.x);
+  const NodeOut pout = node_out(a.hulls1, W, blockIdx.x);
   for (int k = lane; k < count; k += kSpanLanes) {
     const HPt x = sget(v, k);
     pout.idx[k] = x.i;
@@ -525,8 +523,9 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 
 }  // namespace
 
-hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, int64_t span0, void* hulls1,
-                     int64_t cap1, int rows_per_wave) {
+hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, const NodeLevel& hulls1,
+                     int rows_per_wave) {
+  const int64_t spr = hulls.npr;
   SpanArgs a;
   a.y = t.y;
   a.w = t.w;
@@ -536,13 +535,10 @@ hipError_t span_run(const TileArgs& t, void* hulls, int64_t spr, int64_t cap, in
   a.nodes = t.batch * spr;
   a.flags = t.flags;
   a.hulls = hulls;
-  a.cap = cap;
   a.span0 = span0;
   a.gpr = (spr + kSpanLanes - 1) / kSpanLanes;
   a.rpw = rows_per_wave;
   a.hulls1 = hulls1;
-  a.k1 = t.batch * a.gpr;
-  a.cap1 = cap1;
   // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
   // rows_per_wave of them)
   const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes

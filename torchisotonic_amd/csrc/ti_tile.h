@@ -37,9 +37,9 @@ struct TileArgs {
   hipEvent_t weights_read = nullptr;  // recorded once every weight has been read, if given
 };
 
-// One node's hull array in a node array of K nodes with `cap` vertices each: vertex indices
-// relative to the node's first element, cumulative sums (double-double) relative to the node's
-// first point, the vertex count, a NaN flag and the node totals (W hi, W lo, S hi, S lo).
+// One node's hull: vertex indices relative to the node's first element, cumulative sums
+// (double-double) relative to the node's first point, the vertex count, a NaN flag and the node
+// totals (W hi, W lo, S hi, S lo).
 struct NodeOut {
   int* count;
   int* bad;
@@ -50,33 +50,54 @@ struct NodeOut {
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-__host__ __device__ inline size_t node_array_bytes(int64_t K, int64_t cap, bool weighted) {
-  const size_t k = static_cast<size_t>(K), c = static_cast<size_t>(cap);
-  size_t b = align256(k * 4) * 2 + align256(k * 32);
-  b += align256(k * c * 4) + align256(k * c * 8) * (weighted ? 4 : 2);
-  return b;
+// One level of node hulls. Every level keeps its vertices in one shared store: a row's spans
+// take r0 = span0 + 1 slots each, one after another, and a node's vertices start at the slot of
+// the first span it covers. A node never has more vertices than its spans have slots (a hull of
+// e elements has at most e + 1), so a parent's hull is written where its children's were, and
+// the levels need no second store. Per level only the counts, NaN flags and totals are apart.
+struct NodeLevel {
+  char* meta;     // count[K], bad[K], tot[K][4]
+  char* store;    // the shared vertex arrays: idx, shi, slo (and whi, wlo weighted), `slots` each
+  int64_t K;      // nodes of the level
+  int64_t npr;    // nodes per row
+  int64_t spn;    // spans per node (its first span: j * spn of its row)
+  int64_t npr0;   // spans per row
+  int64_t r0;     // slots per span
+  int64_t slots;  // slots of the store
+};
+
+__host__ __device__ inline size_t node_meta_bytes(int64_t K) {
+  const size_t k = static_cast<size_t>(K);
+  return align256(k * 4) * 2 + align256(k * 32);
 }
 
-__host__ __device__ inline NodeOut node_out(void* base, int64_t K, int64_t cap, bool weighted, int64_t k) {
-  char* p = static_cast<char*>(base);
-  const size_t kk = static_cast<size_t>(K), c = static_cast<size_t>(cap);
+__host__ __device__ inline size_t vertex_store_bytes(int64_t slots, bool weighted) {
+  const size_t c = static_cast<size_t>(slots);
+  return align256(c * 4) + align256(c * 8) * (weighted ? 4 : 2);
+}
+
+__host__ __device__ inline NodeOut node_out(const NodeLevel& L, bool weighted, int64_t k) {
   NodeOut o;
+  char* p = L.meta;
+  const size_t kk = static_cast<size_t>(L.K), c = static_cast<size_t>(L.slots);
   o.count = reinterpret_cast<int*>(p) + k;
   p += align256(kk * 4);
   o.bad = reinterpret_cast<int*>(p) + k;
   p += align256(kk * 4);
   o.tot = reinterpret_cast<double*>(p) + 4 * k;
-  p += align256(kk * 32);
-  o.idx = reinterpret_cast<int*>(p) + k * cap;
-  p += align256(kk * c * 4);
-  o.shi = reinterpret_cast<double*>(p) + k * cap;
-  p += align256(kk * c * 8);
-  o.slo = reinterpret_cast<double*>(p) + k * cap;
-  p += align256(kk * c * 8);
+  const int64_t row = k / L.npr, j = k - row * L.npr;
+  const int64_t v0 = (row * L.npr0 + j * L.spn) * L.r0;
+  char* q = L.store;
+  o.idx = reinterpret_cast<int*>(q) + v0;
+  q += align256(c * 4);
+  o.shi = reinterpret_cast<double*>(q) + v0;
+  q += align256(c * 8);
+  o.slo = reinterpret_cast<double*>(q) + v0;
+  q += align256(c * 8);
   if (weighted) {
-    o.whi = reinterpret_cast<double*>(p) + k * cap;
-    p += align256(kk * c * 8);
-    o.wlo = reinterpret_cast<double*>(p) + k * cap;
+    o.whi = reinterpret_cast<double*>(q) + v0;
+    q += align256(c * 8);
+    o.wlo = reinterpret_cast<double*>(q) + v0;
   } else {
     o.whi = o.wlo = nullptr;
   }
@@ -214,10 +235,7 @@ constexpr int kGroup = 64;
 constexpr int kMaxLevels = 8;
 
 struct MergeArgs {
-  const void* in;
-  int64_t k_in, cap_in, npr_in;  // child node array: nodes, capacity, nodes per row
-  void* out;
-  int64_t k_out, cap_out, npr_out;
+  NodeLevel in, out;    // the children's level and the parents'
   int64_t child_elems;  // elements per child node
 };
 
@@ -238,8 +256,8 @@ constexpr int kTileHead = 2;  // a block starts at the tile's first element: a v
                               // (on a NaN row: the tile is the row's first)
 
 struct ExpandArgs {
-  const void* hulls;  // final node array: one node per row
-  int64_t batch, cap, n, tiles_per_row;
+  NodeLevel hulls;  // the final level: one node per row
+  int64_t batch, n, tiles_per_row;
   void* out;
   uint32_t* starts;
   const TileRec* tiles;  // per tile (rank_kernel's)
@@ -247,26 +265,34 @@ struct ExpandArgs {
   double lo, hi;
 };
 
-// Workspace of a long-row fit: two node arrays used in turn by the span hulls and the merge
-// levels (the final hulls end in buffer levels & 1), and the per-tile records of the expansion.
+// Workspace of a long-row fit: the shared vertex store of every level (span0 + 1 slots per span),
+// each level's counts, NaN flags and totals, and the per-tile records of the expansion.
 struct LongPlan {
   int64_t tiles_per_row;  // expansion (and backward) tiles
   int64_t span0;          // elements per span (the first node level)
   int rows_per_wave;      // > 1: the span kernel's wave holds that many short rows, 64 / it lanes each
   int levels;
-  int64_t npr[kMaxLevels + 1], cap[kMaxLevels + 1], span[kMaxLevels + 1];
-  size_t off_buf[2], off_rank, bytes;
+  int64_t batch;
+  int64_t npr[kMaxLevels + 1], spn[kMaxLevels + 1], span[kMaxLevels + 1];
+  int64_t slots;  // of the store: batch * npr[0] * (span0 + 1)
+  size_t off_meta[kMaxLevels + 1], off_store, off_rank, bytes;
+  bool weighted;
+
+  NodeLevel level(void* ws, int l) const {
+    char* base = static_cast<char*>(ws);
+    return NodeLevel{base + off_meta[l], base + off_store, batch * npr[l], npr[l], spn[l], npr[0], span0 + 1, slots};
+  }
 };
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
 
 // Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
-// place into `hulls1` (cap1 vertices per group) and its first span's count set to -1. With
+// place into its level-1 node of `hulls1` and its first span's count set to -1. With
 // rows_per_wave > 1, each wave holds that many rows of spans_per_row spans (a power of two) and
 // merges each row's spans into the row's hull.
-hipError_t span_run(const TileArgs& t, void* hulls, int64_t spans_per_row, int64_t cap, int64_t span0,
-                    void* hulls1, int64_t cap1, int rows_per_wave);
+hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, const NodeLevel& hulls1,
+                    int rows_per_wave);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {
