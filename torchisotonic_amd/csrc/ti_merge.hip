@@ -248,18 +248,28 @@ __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, in
   // the place of its children's): slot s comes from its child's vertex at or after s, so NT slots
   // at a time, read before any is written, in increasing order, never overwrite a vertex still to
   // be read.
-  for (int s0 = 0; s0 < total; s0 += NT) {
-    const int s = s0 + tid;
-    VPt p;
-    if (s < total) {
-      const int c = child_of_slot(sm, nch, s);
-      const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
-      p.i = h.i;
-      p.s = DD{h.s, h.sl};
-      p.w = DD{h.w, h.wl};
+  // (B slots a thread, their loads in flight together: near-monotone data leaves hulls of
+  // millions of vertices, and a slot at a time made this loop a chain of round trips to memory)
+  constexpr int B = 4;
+  for (int s0 = 0; s0 < total; s0 += NT * B) {
+    VPt p[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int s = s0 + u * NT + tid;
+      if (s < total) {
+        const int c = child_of_slot(sm, nch, s);
+        const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
+        p[u].i = h.i;
+        p[u].s = DD{h.s, h.sl};
+        p[u].w = DD{h.w, h.wl};
+      }
     }
     __syncthreads();
-    if (s < total) vstore<W>(v, s, p);
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int s = s0 + u * NT + tid;
+      if (s < total) vstore<W>(v, s, p[u]);
+    }
     __syncthreads();
   }
 #pragma unroll 1
@@ -273,8 +283,9 @@ __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, in
       sm.from[tid] = from;
     }
     __syncthreads();
-    // Move each right part's kept suffix next to its left part's kept prefix.
-    const int gsz = kWave / nm >= 1 ? kWave / nm : 1;
+    // Move each right part's kept suffix next to its left part's kept prefix (every thread: NT / nm
+    // a merge).
+    const int gsz = NT / nm >= 1 ? NT / nm : 1;
     const int m = tid / gsz;
     const int r = tid - m * gsz;
     int len = 0, src = 0, dst = 0;
