@@ -23,7 +23,7 @@ pair on the launch stream around K back-to-back raw C-ABI launches on preallocat
 achieved = algorithmic bytes per launch / (interval / K); peak = 8 TB/s. ``copy_ceiling`` is a
 128 MB device copy timed the same way in the same run. ``traffic`` is that kernel's
 HBM bytes per launch from the rocprofv3 FETCH_SIZE and WRITE_SIZE passes summarised in
-profiles/short_fit_kernel_c2_traffic.json (each counter scaled by what it reads for a copy-like
+profiles/short_rows_kernel_c2_traffic.json (each counter scaled by what it reads for a copy-like
 kernel of known size), or null where that summary is absent.
 
 ``cpu_baseline`` times the reference's own pava.h (compiled from the reference checkout into
@@ -169,9 +169,9 @@ def bench_c2(steps: int, warmup: int) -> dict:
         "fwd": rate(elems, t_fwd, 8),
         "fwd_bwd": rate(elems, t_fb, 16),
         "kernel_ms": {
-            "short_fit_kernel<float,16,unweighted> (no starts)": kernel_ms(fwd, 100),
-            "short_fit_kernel<float,16,unweighted> (with starts)": kernel_ms(fwd_s, 100),
-            "short_grad_kernel<float,16,unweighted> (dy)": kernel_ms(bwd, 100),
+            "short_rows_kernel<float,16,unweighted> (no starts)": kernel_ms(fwd, 100),
+            "short_rows_kernel<float,16,unweighted> (with starts)": kernel_ms(fwd_s, 100),
+            "short_grad_rows_kernel<float,16,unweighted> (dy)": kernel_ms(bwd, 100),
         },
     }
 
@@ -416,7 +416,7 @@ def cpu_c4(n: int = 10_000_000) -> dict:
 
 def measured_traffic() -> float | None:
     """HBM bytes per launch of the headline kernel, from the committed counter summary."""
-    f = ROOT / "profiles" / "short_fit_kernel_c2_traffic.json"
+    f = ROOT / "profiles" / "short_rows_kernel_c2_traffic.json"
     try:
         t = json.loads(f.read_text())
         kib = t["fetch_size_kib"] * t["fetch_scale"] + t["write_size_kib"] * t["write_scale"]
@@ -475,7 +475,7 @@ def main() -> None:
         log("README grid ...")
         extra["grid"] = bench_grid()
     elems = c2["elems"]
-    k = c2["kernel_ms"]["short_fit_kernel<float,16,unweighted> (no starts)"]
+    k = c2["kernel_ms"]["short_rows_kernel<float,16,unweighted> (no starts)"]
     achieved = 8 * elems / (k * 1e-3) / 1e9
     if k > c2["fwd"]["ms"]:
         log(f"warning: kernel time {k:.4f} ms exceeds the API's {c2['fwd']['ms']:.4f} ms per call")
@@ -505,7 +505,7 @@ def main() -> None:
             "unit": "GB/s",
             "frac": achieved / PEAK_GBPS,
             "traffic": measured_traffic(),
-            "kernel": "short_fit_kernel<float,16,unweighted>",
+            "kernel": "short_rows_kernel<float,16,unweighted>",
             "kernel_ms": k,
             "algorithmic_bytes_per_launch": 8 * elems,
             "copy_ceiling": ceiling,

@@ -57,10 +57,16 @@ def test_workspace_queries() -> None:
     assert size.value == 0  # short rows: no workspace
     assert lib.ti_fwd_workspace(1000, 33, _ext.F32, 0, ctypes.byref(size)) == 0
     assert size.value > 0  # longer rows: span hulls, merges and tile records
-    assert lib.ti_fwd_workspace(1, 100_000_000, _ext.F32, 1, ctypes.byref(size)) == 0
-    # two node arrays of 36 bytes per vertex slot (one slot per element, rounded up to whole
-    # nodes of the level), and the tile ranks
-    assert 6e9 < size.value < 9e9
+    # one vertex store shared by every merge level: span0 + 1 slots per span of span0 elements,
+    # 36 bytes a slot weighted (index, double-double sums and weights), 20 unweighted; per-level
+    # counts and totals and the tile records are small beside it
+    n = 100_000_000
+    assert lib.ti_fwd_workspace(1, n, _ext.F32, 1, ctypes.byref(size)) == 0
+    slots = -(-n // 256) * 257  # C4's spans of 256
+    assert 36 * slots < size.value < 36 * slots * 1.01
+    assert size.value < 3.7e9
+    assert lib.ti_fwd_workspace(1, n, _ext.F32, 0, ctypes.byref(size)) == 0
+    assert 20 * slots < size.value < 20 * slots * 1.02
     assert lib.ti_bwd_workspace(1000, 16, _ext.F64, 1, ctypes.byref(size)) == 0
     assert size.value == 0
     assert lib.ti_bwd_workspace(1000, 65536, _ext.F32, 1, ctypes.byref(size)) == 0

@@ -48,6 +48,21 @@ def isotonic(
     ``exact`` exists so calls written for torchisotonic work unchanged. These kernels always
     accumulate and compare in float64 and round a float32 fit once, whatever it is set to.
     """
+    # The common call, a [batch, n] float32/float64 tensor on the GPU fitted along its last axis
+    # without weights, straight to the operator (the checks below all pass for it; a call's host
+    # time matters where the GPU work is tens of microseconds).
+    if (
+        weight is None
+        and type(y) is Tensor
+        and y.ndim == 2
+        and (dim == -1 or dim == 1)
+        and y.is_cuda
+        and (y.dtype is torch.float32 or y.dtype is torch.float64)
+        and y.numel() > 0
+    ):
+        return _ext.ops().isotonic_fit(
+            y, None, increasing, None if y_min is None else float(y_min), None if y_max is None else float(y_max)
+        )
     # Argument checks and messages: reference _api.py:43-61.
     if not isinstance(y, Tensor):
         raise TypeError(f"y must be a torch.Tensor, got {type(y).__name__}")

@@ -123,29 +123,28 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
       TORCH_CHECK_VALUE(*static_cast<volatile uint32_t*>(wc.host) == 0u, "weight must be strictly positive");
     }
     if (want) {
-      ctx->save_for_backward({yc, w, starts});
-      ctx->saved_data["ws"] = ws.defined() ? c10::IValue(ws) : c10::IValue();
-      ctx->saved_data["flags"] = static_cast<int64_t>(flags);
-      ctx->saved_data["lo"] = lo;
-      ctx->saved_data["hi"] = hi;
-      ctx->saved_data["has_w"] = w.defined();
+      // (the workspace, when there is one, rides along as a fourth saved tensor; the scalars in
+      // one entry: each saved_data entry is a hash-map insert and lookup of host time per call)
+      if (ws.defined()) ctx->save_for_backward({yc, w, starts, ws});
+      else ctx->save_for_backward({yc, w, starts});
+      ctx->saved_data["p"] = c10::List<double>({static_cast<double>(flags), lo, hi, w.defined() ? 1.0 : 0.0});
     }
     return out;
   }
 
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const c10::List<double> prm = ctx->saved_data["p"].toDoubleList();
+    const unsigned flags = static_cast<unsigned>(prm.get(0));
+    const double lo = prm.get(1), hi = prm.get(2);
     // (a missing w is no input of the node: y's is its only gradient edge then)
-    const bool has_w = ctx->saved_data["has_w"].toBool();
+    const bool has_w = prm.get(3) != 0.0;
     const bool want_y = ctx->needs_input_grad(0), want_w = has_w && ctx->needs_input_grad(1);
     if (!want_y && !want_w) return {at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
     const variable_list saved = ctx->get_saved_variables();
     const at::Tensor& y = saved[0];
     const at::Tensor& w = saved[1];
     const at::Tensor& starts = saved[2];
-    const c10::IValue wsv = ctx->saved_data["ws"];
-    const at::Tensor ws = wsv.isTensor() ? wsv.toTensor() : at::Tensor();
-    const unsigned flags = static_cast<unsigned>(ctx->saved_data["flags"].toInt());
-    const double lo = ctx->saved_data["lo"].toDouble(), hi = ctx->saved_data["hi"].toDouble();
+    const at::Tensor ws = saved.size() > 3 ? saved[3] : at::Tensor();
     const at::Tensor g = grads[0].contiguous();
     TORCH_CHECK(g.sizes() == y.sizes() && g.scalar_type() == y.scalar_type(),
                 "torchisotonic_amd: the upstream gradient must match the fit");
