@@ -2,15 +2,18 @@
 //
 // Replaces the reference's packed regime (reference src/torchisotonic/csrc/tiles.cuh:920-1112,
 // packed_kernel; grad.cuh:200-290 with E=1 for the backward) with a design for wave64:
-//   - a workgroup owns THREADS consecutive rows, i.e. one contiguous span of THREADS * n
-//     elements. When a row is a whole number of 16-byte vectors (n * sizeof(T) % 16 == 0, the
-//     headline [1e6, 16] float32 case) each thread moves its own row with 16-byte loads and
-//     stores ("direct"); otherwise the workgroup moves its span with coalesced 16-byte
-//     accesses through LDS, rows padded to n + 1 entries ("staged");
+//   - rows that are a whole number of 16-byte chunks (n * sizeof(T) % 16 == 0, aligned: the
+//     headline [1e6, 16] float32 case) take short_rows_kernel / short_grad_rows_kernel: a
+//     persistent grid whose workgroups walk blocks of rows with the next block's loads in
+//     flight, each wave moving its 64 rows through LDS with coalesced 16-byte accesses and
+//     transposing them to one row per lane; other rows take short_fit_kernel /
+//     short_grad_kernel, one block of THREADS consecutive rows a workgroup, the block's span
+//     moved with coalesced 16-byte accesses through LDS, rows padded to n + 1 entries;
 //   - each thread builds its row's cumulative sums in float64 registers and runs the monotone
 //     chain (Andrew) for the lower hull of the n + 1 points, keeping the hull as a bit mask
-//     and the points in a per-thread LDS column for the pops' random access (the third
-//     vertex is prefetched, so a pop does not wait on LDS before the next test);
+//     and the points in a per-thread LDS column for the chain's random access (unweighted
+//     rows: the mask alone is the stack; weighted rows carry the top two vertices and read
+//     both possible successors before each choice);
 //   - the fit is one float64 slope per block, rounded once, with the clamp fused; the
 //     partition is one 32-bit word of start bits per row.
 // The backward moves g (and w, y) the same way; block sums of g (and w) and the block mean
@@ -44,36 +47,6 @@ struct Vec16 {
   static constexpr int kN = 16 / sizeof(T);
   using type = T __attribute__((ext_vector_type(kN)));
 };
-
-// One row of NMAX values (n == NMAX, 16-byte aligned) straight into / out of registers.
-template <typename T, int NMAX>
-__device__ __forceinline__ void load_row(const T* __restrict__ p, T (&v)[NMAX]) {
-  constexpr int V = Vec16<T>::kN;
-  using VT = typename Vec16<T>::type;
-  const VT* q = reinterpret_cast<const VT*>(p);
-  VT buf[NMAX / V];
-#pragma unroll
-  for (int j = 0; j < NMAX / V; ++j) buf[j] = q[j];
-#pragma unroll
-  for (int j = 0; j < NMAX / V; ++j) {
-#pragma unroll
-    for (int t = 0; t < V; ++t) v[j * V + t] = buf[j][t];
-  }
-}
-
-template <typename T, int NMAX>
-__device__ __forceinline__ void store_row(T* __restrict__ p, const T (&v)[NMAX]) {
-  constexpr int V = Vec16<T>::kN;
-  using VT = typename Vec16<T>::type;
-  VT* q = reinterpret_cast<VT*>(p);
-#pragma unroll
-  for (int j = 0; j < NMAX / V; ++j) {
-    VT x;
-#pragma unroll
-    for (int t = 0; t < V; ++t) x[t] = v[j * V + t];
-    q[j] = x;
-  }
-}
 
 // The staged path: this workgroup's span of `count` = rows * n elements, read with coalesced
 // 16-byte loads (all issued before any is used), into registers; then written to LDS row r at
@@ -410,7 +383,7 @@ __device__ __forceinline__ void row_fit(const T (&yv)[NMAX], const T (&wv)[W ? N
   bad_out = bad;
 }
 
-template <typename T, int NMAX, bool W, bool DIRECT, bool INC>
+template <typename T, int NMAX, bool W, bool INC>
 __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
     const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out,
     uint32_t* __restrict__ starts, uint32_t* __restrict__ bad_weight, int64_t batch, int n,
@@ -434,59 +407,44 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
 
   T yv[NMAX];
   T wv[W ? NMAX : 1];
-  if constexpr (DIRECT) {
-    if (active) {
-      load_row<T, NMAX>(y + (row0 + tid) * NMAX, yv);
-      if constexpr (W) load_row<T, NMAX>(w + (row0 + tid) * NMAX, wv);
-    }
-  } else {
-    Span<T, THREADS, NMAX> sy;
-    Span<T, THREADS, NMAX> sw;
-    sy.load(y + row0 * n, count);
-    if constexpr (W) sw.load(w + row0 * n, count);
-    sy.to_lds(y + row0 * n, stg, count, div);
+  Span<T, THREADS, NMAX> sy;
+  Span<T, THREADS, NMAX> sw;
+  sy.load(y + row0 * n, count);
+  if constexpr (W) sw.load(w + row0 * n, count);
+  sy.to_lds(y + row0 * n, stg, count, div);
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NMAX; ++c) {
+    if (c < n) yv[c] = stg[tid * (n + 1) + c];
+  }
+  if constexpr (W) {
+    __syncthreads();
+    sw.to_lds(w + row0 * n, stg, count, div);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < NMAX; ++c) {
-      if (c < n) yv[c] = stg[tid * (n + 1) + c];
+      if (c < n) wv[c] = stg[tid * (n + 1) + c];
     }
-    if constexpr (W) {
-      __syncthreads();
-      sw.to_lds(w + row0 * n, stg, count, div);
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < n) wv[c] = stg[tid * (n + 1) + c];
-      }
-    }
-    __syncthreads();  // staging is dead from here: the area becomes the point columns
   }
-
-  // The row length: a constant when each thread moves whole rows of NMAX.
-  const int nn = DIRECT ? NMAX : n;
+  __syncthreads();  // staging is dead from here: the area becomes the point columns
 
   T fit[NMAX];
   typename MaskOf<NMAX>::type m;
   bool bad;
-  row_fit<T, NMAX, W, INC, DIRECT && !W>(yv, wv, nn, active, colS, colW, rcp, bad_weight, flags, lo, hi, fit, m,
-                                           bad);
+  row_fit<T, NMAX, W, INC, false>(yv, wv, n, active, colS, colW, rcp, bad_weight, flags, lo, hi, fit, m, bad);
 
   if (starts != nullptr && active) {
-    const uint32_t low = nn >= 32 ? 0xFFFFFFFFu : ((1u << nn) - 1u);
+    const uint32_t low = n >= 32 ? 0xFFFFFFFFu : ((1u << n) - 1u);
     starts[row0 + tid] = bad ? 1u : static_cast<uint32_t>(m) & low;
   }
 
-  if constexpr (DIRECT) {
-    if (active) store_row<T, NMAX>(out + (row0 + tid) * NMAX, fit);
-  } else {
-    __syncthreads();  // every thread is done with the point columns
+  __syncthreads();  // every thread is done with the point columns
 #pragma unroll
-    for (int c = 0; c < NMAX; ++c) {
-      if (c < n && active) stg[tid * (n + 1) + c] = fit[c];
-    }
-    __syncthreads();
-    stage_out<T, THREADS>(out + row0 * n, stg, count, div);
+  for (int c = 0; c < NMAX; ++c) {
+    if (c < n && active) stg[tid * (n + 1) + c] = fit[c];
   }
+  __syncthreads();
+  stage_out<T, THREADS>(out + row0 * n, stg, count, div);
 }
 
 // Ragged rows: row r is y[offsets[r], offsets[r + 1]) of a packed array, one thread per row as
@@ -822,14 +780,14 @@ __device__ __forceinline__ void row_grad(const T (&gv)[NMAX], const T (&wv)[W ? 
 // Backward: gy = w * mask * G / W, gw = (y - fit) * mask * G / W over each block, the block's
 // fit recomputed from the same float64 cumulative sums and division the forward used (so
 // bit-identical to it).
-template <typename T, int NMAX, bool W, bool DIRECT>
+template <typename T, int NMAX, bool W>
 __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_kernel(
     const uint32_t* __restrict__ starts, const T* __restrict__ g, const T* __restrict__ w,
     const T* __restrict__ y, T* __restrict__ gy, T* __restrict__ gw, int64_t batch, int n,
     unsigned flags, T lo, T hi) {
   constexpr int THREADS = short_threads<NMAX, W>();
   // staging only (no point columns), one array of T at a time
-  __shared__ T stg[DIRECT ? 1 : (NMAX + 1) * THREADS];
+  __shared__ T stg[(NMAX + 1) * THREADS];
 
   const int tid = threadIdx.x;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
@@ -844,69 +802,54 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_grad_kernel(
   T wv[W ? NMAX : 1];
   T yv[NMAX];
   const uint32_t bits = (active ? starts[row0 + tid] : 0u) | 1u;
-  if constexpr (DIRECT) {
-    if (active) {
-      load_row<T, NMAX>(g + (row0 + tid) * NMAX, gv);
-      if constexpr (W) load_row<T, NMAX>(w + (row0 + tid) * NMAX, wv);
-      if (need_mean) load_row<T, NMAX>(y + (row0 + tid) * NMAX, yv);
-    }
-  } else {
-    Span<T, THREADS, NMAX> sg, sw, sy;
-    sg.load(g + row0 * n, count);
-    if constexpr (W) sw.load(w + row0 * n, count);
-    if (need_mean) sy.load(y + row0 * n, count);
-    sg.to_lds(g + row0 * n, stg, count, div);
+  Span<T, THREADS, NMAX> sg, sw, sy;
+  sg.load(g + row0 * n, count);
+  if constexpr (W) sw.load(w + row0 * n, count);
+  if (need_mean) sy.load(y + row0 * n, count);
+  sg.to_lds(g + row0 * n, stg, count, div);
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NMAX; ++c) {
+    if (c < n) gv[c] = stg[tid * (n + 1) + c];
+  }
+  if constexpr (W) {
+    __syncthreads();
+    sw.to_lds(w + row0 * n, stg, count, div);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < NMAX; ++c) {
-      if (c < n) gv[c] = stg[tid * (n + 1) + c];
+      if (c < n) wv[c] = stg[tid * (n + 1) + c];
     }
-    if constexpr (W) {
-      __syncthreads();
-      sw.to_lds(w + row0 * n, stg, count, div);
-      __syncthreads();
+  }
+  if (need_mean) {
+    __syncthreads();
+    sy.to_lds(y + row0 * n, stg, count, div);
+    __syncthreads();
 #pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < n) wv[c] = stg[tid * (n + 1) + c];
-      }
-    }
-    if (need_mean) {
-      __syncthreads();
-      sy.to_lds(y + row0 * n, stg, count, div);
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < n) yv[c] = stg[tid * (n + 1) + c];
-      }
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n) yv[c] = stg[tid * (n + 1) + c];
     }
   }
 
   T oy[NMAX], ow[NMAX];
   row_grad<T, NMAX, W>(gv, wv, yv, bits, n, need_mean, use_lo, lo, use_hi, hi, oy, ow);
-  if constexpr (DIRECT) {
-    if (active) {
-      if (gy != nullptr) store_row<T, NMAX>(gy + (row0 + tid) * NMAX, oy);
-      if (gw != nullptr) store_row<T, NMAX>(gw + (row0 + tid) * NMAX, ow);
-    }
-  } else {
-    if (gy != nullptr) {
-      __syncthreads();
+  if (gy != nullptr) {
+    __syncthreads();
 #pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < n && active) stg[tid * (n + 1) + c] = oy[c];
-      }
-      __syncthreads();
-      stage_out<T, THREADS>(gy + row0 * n, stg, count, div);
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n && active) stg[tid * (n + 1) + c] = oy[c];
     }
-    if (gw != nullptr) {
-      __syncthreads();
+    __syncthreads();
+    stage_out<T, THREADS>(gy + row0 * n, stg, count, div);
+  }
+  if (gw != nullptr) {
+    __syncthreads();
 #pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < n && active) stg[tid * (n + 1) + c] = ow[c];
-      }
-      __syncthreads();
-      stage_out<T, THREADS>(gw + row0 * n, stg, count, div);
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < n && active) stg[tid * (n + 1) + c] = ow[c];
     }
+    __syncthreads();
+    stage_out<T, THREADS>(gw + row0 * n, stg, count, div);
   }
 }
 
@@ -1157,7 +1100,7 @@ hipError_t launch_fit(const ShortArgs& a) {
       return inc ? rows(short_rows_kernel<T, NMAX, W, true>) : rows(short_rows_kernel<T, NMAX, W, false>);
     }
   }
-  return inc ? run(short_fit_kernel<T, NMAX, W, false, true>) : run(short_fit_kernel<T, NMAX, W, false, false>);
+  return inc ? run(short_fit_kernel<T, NMAX, W, true>) : run(short_fit_kernel<T, NMAX, W, false>);
 }
 
 template <typename T, int NMAX, bool W>
@@ -1186,7 +1129,7 @@ hipError_t launch_grad(const ShortGradArgs& a) {
       return needy ? rows(short_grad_rows_kernel<T, NMAX, W, true>) : rows(short_grad_rows_kernel<T, NMAX, W, false>);
     }
   }
-  return run(short_grad_kernel<T, NMAX, W, false>);
+  return run(short_grad_kernel<T, NMAX, W>);
 }
 
 template <typename T, bool W>
