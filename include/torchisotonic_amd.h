@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 3
+#define TI_ABI_VERSION 4
 
 /* dtype codes */
 #define TI_F32 0
@@ -158,6 +158,65 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
            const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
            int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
            size_t workspace_bytes, void* stream);
+
+/*
+ * Keeping less than the forward's workspace for the backward. No counterpart in the reference,
+ * whose autograd keeps the partition and calls the stateless gradient (reference
+ * _api.py:73-97, grad.cuh:304-413). Here the backward of rows longer than 32 elements reads
+ * only the final hulls and the per-tile records of the forward's workspace (ti_bwd), so a caller
+ * that holds the workspace from forward to backward (an autograd node) keeps these instead:
+ *
+ *   1. ti_fwd_ev_hulls: the forward, reporting a bound on the final hulls' vertex counts;
+ *   2. ti_keep_bytes, ti_keep: a buffer of that size, and the copy into it, after which the
+ *      workspace is free for work the stream orders later;
+ *   3. ti_bwd_kept_workspace, ti_bwd_kept: the backward from the kept buffer, with results
+ *      identical to ti_bwd's from the workspace.
+ *
+ * The kept buffer holds each row's final hull in max_vertices slots (20 bytes a slot, 36
+ * weighted) and 32 bytes a tile of 4096 elements (2048 weighted): about 1.6 MB for one weighted
+ * row of 1e8 with a final hull of about a thousand vertices, against 3.6 GB of workspace. A row
+ * whose hull has every element as a vertex (monotone data) keeps as much as the workspace, and
+ * a caller may then keep the workspace itself.
+ */
+
+/*
+ * ti_fwd_ev, plus: for rows of more than 32 elements, a bound on the final hulls' vertex counts
+ * (at least the largest over the rows, at most n + 1: the vertices a row has two merge levels
+ * before the last) is written to *max_vertices (one int64 that the device writes: device memory,
+ * or the device pointer of pinned host memory), and hulls_ready (a hipEvent_t, or NULL) is
+ * recorded on the stream once it is written. The last merges and the expansion run after it, so
+ * a caller waiting on the event sizes and allocates its kept buffer while the fit finishes. For
+ * rows of at most 32 elements nothing is written and the event is recorded after the fit.
+ */
+int ti_fwd_ev_hulls(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                    int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+                    void* workspace, size_t workspace_bytes, void* stream, void* weights_read,
+                    void* hulls_ready, int64_t* max_vertices);
+
+/* Bytes of the kept buffer for final hulls of at most max_vertices vertices (0 for rows of at
+ * most 32 elements, which keep nothing). */
+int ti_keep_bytes(int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices, size_t* bytes);
+
+/*
+ * Copies the final hulls and per-tile records out of the workspace that ti_fwd / ti_fwd_ev_hulls
+ * filled (rows of more than 32 elements) into kept (at least ti_keep_bytes() bytes, 256-byte
+ * aligned), on the stream. max_vertices: the value ti_fwd_ev_hulls wrote for that forward (one
+ * below a row's final hull count cuts that hull short, and the backward's results are then
+ * wrong).
+ */
+int ti_keep(const void* fwd_workspace, size_t fwd_workspace_bytes, void* kept, size_t kept_bytes,
+            int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices, void* stream);
+
+/* Bytes of device workspace ti_bwd_kept needs (0 when none). */
+int ti_bwd_kept_workspace(int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices,
+                          size_t* bytes);
+
+/* ti_bwd, from the buffer ti_keep filled (kept, kept_bytes, and the forward's max_vertices) in
+ * place of the forward's workspace; the other arguments and the results as ti_bwd's. */
+int ti_bwd_kept(const uint32_t* starts, const void* kept, size_t kept_bytes, int64_t max_vertices,
+                const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
+                int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 /*
  * The fit of ragged rows, packed end to end: row r is y[offsets[r], offsets[r + 1]) (offsets:

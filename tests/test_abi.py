@@ -75,6 +75,37 @@ def test_workspace_queries() -> None:
     assert lib.ti_fwd_workspace(10, 16, 0, 0, None) == 1  # TI_EINVAL
 
 
+def test_kept_state_sizes() -> None:
+    # what a backward keeps in place of the forward's workspace: each row's final hull in
+    # max_vertices slots (36 bytes weighted, 20 unweighted), its count, NaN flag and totals
+    # (40 bytes) and 32 bytes a tile (2048 elements weighted, 4096 unweighted), against the
+    # workspace's slot for every element
+    lib = _ext.load()
+    size, ws = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    n = 100_000_000
+    assert lib.ti_keep_bytes(1, n, _ext.F32, 1, 1083, ctypes.byref(size)) == 0
+    tiles = -(-n // 2048)
+    assert 36 * 1083 + 32 * tiles + 40 <= size.value < 36 * 1083 + 32 * tiles + 40 + 8 * 256
+    assert size.value < 2e6
+    assert lib.ti_fwd_workspace(1, n, _ext.F32, 1, ctypes.byref(ws)) == 0
+    assert size.value * 1000 < ws.value
+    assert lib.ti_keep_bytes(1000, 65536, _ext.F32, 0, 300, ctypes.byref(size)) == 0
+    assert 1000 * (20 * 300 + 32 * 16 + 40) <= size.value < 1000 * (20 * 300 + 32 * 16 + 40) + 8 * 256
+    # the backward's workspace from a kept state: per-tile scans and 16 bytes a kept slot,
+    # against 16 bytes an element from the workspace
+    kb, wb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert lib.ti_bwd_kept_workspace(1, n, _ext.F32, 1, 1083, ctypes.byref(kb)) == 0
+    assert lib.ti_bwd_workspace(1, n, _ext.F32, 1, ctypes.byref(wb)) == 0
+    assert kb.value < 4e6 and wb.value > 16 * n
+    # short rows keep nothing; max_vertices must be a hull's vertex count of such rows
+    assert lib.ti_keep_bytes(1000, 32, _ext.F32, 1, 0, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert lib.ti_keep_bytes(10, 100, _ext.F32, 1, 0, ctypes.byref(size)) == 1
+    assert lib.ti_keep_bytes(10, 100, _ext.F32, 1, 102, ctypes.byref(size)) == 1
+    assert lib.ti_bwd_kept_workspace(10, 100, _ext.F32, 1, 0, ctypes.byref(size)) == 1
+    assert b"max_vertices" in lib.ti_last_error()
+
+
 def call_fwd(y: int | None, out: int | None, batch: int, n: int, dtype: int = 0) -> int:
     return _ext.load().ti_fwd(y, None, out, None, None, batch, n, dtype, 1, 0.0, 0.0, None, 0, None)
 

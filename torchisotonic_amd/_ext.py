@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -45,6 +45,11 @@ SYMBOLS = (
     "ti_ragged_plan",
     "ti_bwd_workspace",
     "ti_bwd",
+    "ti_fwd_ev_hulls",
+    "ti_keep_bytes",
+    "ti_keep",
+    "ti_bwd_kept_workspace",
+    "ti_bwd_kept",
     "ti_grad_workspace",
     "ti_grad",
     "ti_interp",
@@ -86,6 +91,16 @@ def load() -> ctypes.CDLL:
     lib.ti_ragged_plan.argtypes = [_vp, _i64, _i64, _vp, _vp]
     lib.ti_bwd.restype = _int
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_fwd_ev_hulls.restype = _int
+    lib.ti_fwd_ev_hulls.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp, _vp, _vp]
+    lib.ti_keep_bytes.restype = _int
+    lib.ti_keep_bytes.argtypes = [_i64, _i64, _int, _int, _i64, ctypes.POINTER(_sz)]
+    lib.ti_keep.restype = _int
+    lib.ti_keep.argtypes = [_vp, _sz, _vp, _sz, _i64, _i64, _int, _int, _i64, _vp]
+    lib.ti_bwd_kept_workspace.restype = _int
+    lib.ti_bwd_kept_workspace.argtypes = [_i64, _i64, _int, _int, _i64, ctypes.POINTER(_sz)]
+    lib.ti_bwd_kept.restype = _int
+    lib.ti_bwd_kept.argtypes = [_vp, _vp, _sz, _i64] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_grad_workspace.restype = _int
     lib.ti_grad_workspace.argtypes = [_i64, _i64, _int, ctypes.POINTER(_sz)]
     lib.ti_grad.restype = _int

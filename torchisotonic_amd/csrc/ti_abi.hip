@@ -146,15 +146,19 @@ int ti_fwd_geometry(int64_t batch, int64_t n, int weighted, int64_t* span0, int*
 
 namespace {
 
-// ti_fwd, recording weights_read (when given) on the stream once every weight has been read.
+// ti_fwd, recording weights_read (when given) on the stream once every weight has been read,
+// and for rows over 32 elements writing the final hulls' largest vertex count to *max_vertices
+// (when given) and recording hulls_ready (when given) once it is written.
 int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
              int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
-             void* workspace, size_t workspace_bytes, void* stream, hipEvent_t weights_read) {
+             void* workspace, size_t workspace_bytes, void* stream, hipEvent_t weights_read,
+             hipEvent_t hulls_ready = nullptr, int64_t* max_vertices = nullptr) {
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  // the one-kernel paths read the weights in their only kernel
+  // the one-kernel paths read the weights in their only kernel (and have no hulls to keep)
   auto then_record = [&](int rc) -> int {
-    if (rc != TI_OK || weights_read == nullptr) return rc;
-    return launched(hipEventRecord(weights_read, hs), "weights-read event");
+    if (rc == TI_OK && weights_read != nullptr) rc = launched(hipEventRecord(weights_read, hs), "weights-read event");
+    if (rc == TI_OK && hulls_ready != nullptr) rc = launched(hipEventRecord(hulls_ready, hs), "hulls-ready event");
+    return rc;
   };
   if (int rc = check_shape(batch, n, dtype)) return rc;
   if (batch == 0) return then_record(ok());
@@ -184,7 +188,54 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
   if (batch * plan.tiles_per_row > 0x7FFFFFFF) return fail(TI_ESIZE, "too many tiles");
   ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
   a.weights_read = weights_read;  // after the span kernel, the first of several
+  a.hulls_ready = hulls_ready;    // after the merges
+  a.max_vertices = max_vertices;
   return launched(ti::long_fit(a, plan, workspace), "multi-tile fit");
+}
+
+// ti_bwd from the forward's workspace (fwd_ws) or from what ti_keep kept of it (kept).
+int bwd_impl(const uint32_t* starts, const void* fwd_ws, size_t fwd_ws_bytes, const void* kept,
+             size_t kept_bytes, int64_t kept_maxc, const void* g, const void* w, const void* y, void* gy,
+             void* gw, int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+             void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  if (batch == 0) return ok();
+  if (starts == nullptr || g == nullptr) return fail(TI_EINVAL, "starts and g must not be null");
+  const bool clipping = (flags & (TI_CLIP_MIN | TI_CLIP_MAX)) != 0;
+  if ((gw != nullptr || clipping) && y == nullptr)
+    return fail(TI_EINVAL, "y is needed for the weight gradient and for the clamp's mask");
+  if (gy == nullptr && gw == nullptr) return ok();
+  if (n <= ti::kShortMax) {
+    if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
+    ti::ShortGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
+                        static_cast<hipStream_t>(stream)};
+    return launched(ti::short_grad(a), "short-row gradient");
+  }
+  const bool W = w != nullptr;
+  const ti::LongPlan plan = ti::long_plan(batch, n, W);
+  if (kept != nullptr || kept_bytes > 0 || kept_maxc != 0) {
+    if (kept_maxc < 1 || kept_maxc > n + 1)
+      return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)kept_maxc);
+    const size_t kneed = ti::keep_plan(batch, n, W, kept_maxc).bytes;
+    if (kept == nullptr || kept_bytes < kneed)
+      return fail(TI_EWORKSPACE, "the kept state (%zu bytes) is needed, %zu given", kneed, kept_bytes);
+    if ((reinterpret_cast<uintptr_t>(kept) & 255) != 0) return fail(TI_EINVAL, "the kept state must be 256-byte aligned");
+  } else {
+    if (fwd_ws == nullptr || fwd_ws_bytes < plan.bytes)
+      return fail(TI_EWORKSPACE,
+                  "the forward's workspace (%zu bytes, rows of %lld elements) is needed, %zu given "
+                  "(without it, ti_grad computes the gradients from the fit and the partition)",
+                  plan.bytes, (long long)n, fwd_ws_bytes);
+    if ((reinterpret_cast<uintptr_t>(fwd_ws) & 255) != 0) return fail(TI_EINVAL, "workspaces must be 256-byte aligned");
+  }
+  const size_t need = ti::long_grad_bytes(batch, n, W, kept != nullptr ? kept_maxc : 0);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspaces must be 256-byte aligned");
+  ti::LongGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
+                     kept != nullptr ? nullptr : fwd_ws, kept, kept != nullptr ? kept_maxc : 0,
+                     static_cast<hipStream_t>(stream)};
+  return launched(ti::long_grad(a, plan, workspace), "multi-tile gradient");
 }
 
 }  // namespace
@@ -234,33 +285,67 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
            const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
            int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
            size_t workspace_bytes, void* stream) {
+  return bwd_impl(starts, fwd_workspace, fwd_workspace_bytes, nullptr, 0, 0, g, w, y, gy, gw, batch, n, dtype,
+                  flags, y_min, y_max, workspace, workspace_bytes, stream);
+}
+
+int ti_fwd_ev_hulls(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                    int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+                    void* workspace, size_t workspace_bytes, void* stream, void* weights_read,
+                    void* hulls_ready, int64_t* max_vertices) {
+  return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, workspace,
+                  workspace_bytes, stream, static_cast<hipEvent_t>(weights_read),
+                  static_cast<hipEvent_t>(hulls_ready), max_vertices);
+}
+
+int ti_keep_bytes(int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices, size_t* bytes) {
+  if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
   if (int rc = check_shape(batch, n, dtype)) return rc;
-  if (batch == 0) return ok();
-  if (starts == nullptr || g == nullptr) return fail(TI_EINVAL, "starts and g must not be null");
-  const bool clipping = (flags & (TI_CLIP_MIN | TI_CLIP_MAX)) != 0;
-  if ((gw != nullptr || clipping) && y == nullptr)
-    return fail(TI_EINVAL, "y is needed for the weight gradient and for the clamp's mask");
-  if (gy == nullptr && gw == nullptr) return ok();
-  if (n <= ti::kShortMax) {
-    if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
-    ti::ShortGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
-                        static_cast<hipStream_t>(stream)};
-    return launched(ti::short_grad(a), "short-row gradient");
-  }
-  const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
+  *bytes = 0;
+  if (n <= ti::kShortMax || batch == 0) return ok();
+  if (max_vertices < 1 || max_vertices > n + 1)
+    return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)max_vertices);
+  *bytes = ti::keep_plan(batch, n, weighted != 0, max_vertices).bytes;
+  return ok();
+}
+
+int ti_keep(const void* fwd_workspace, size_t fwd_workspace_bytes, void* kept, size_t kept_bytes,
+            int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices, void* stream) {
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  if (n <= ti::kShortMax || batch == 0) return ok();
+  if (max_vertices < 1 || max_vertices > n + 1)
+    return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)max_vertices);
+  const ti::LongPlan plan = ti::long_plan(batch, n, weighted != 0);
   if (fwd_workspace == nullptr || fwd_workspace_bytes < plan.bytes)
-    return fail(TI_EWORKSPACE,
-                "the forward's workspace (%zu bytes, rows of %lld elements) is needed, %zu given "
-                "(without it, ti_grad computes the gradients from the fit and the partition)",
-                plan.bytes, (long long)n, fwd_workspace_bytes);
-  const size_t need = ti::long_grad_bytes(batch, n, w != nullptr);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0 || (reinterpret_cast<uintptr_t>(fwd_workspace) & 255) != 0)
-    return fail(TI_EINVAL, "workspaces must be 256-byte aligned");
-  ti::LongGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
-                     fwd_workspace, static_cast<hipStream_t>(stream)};
-  return launched(ti::long_grad(a, plan, workspace), "multi-tile gradient");
+    return fail(TI_EWORKSPACE, "the forward's workspace (%zu bytes) is needed, %zu given", plan.bytes,
+                fwd_workspace_bytes);
+  const ti::KeepPlan kp = ti::keep_plan(batch, n, weighted != 0, max_vertices);
+  if (kept == nullptr || kept_bytes < kp.bytes)
+    return fail(TI_EWORKSPACE, "a kept buffer of %zu bytes is needed, %zu given", kp.bytes, kept_bytes);
+  if ((reinterpret_cast<uintptr_t>(kept) & 255) != 0 || (reinterpret_cast<uintptr_t>(fwd_workspace) & 255) != 0)
+    return fail(TI_EINVAL, "the workspace and the kept buffer must be 256-byte aligned");
+  if (batch > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
+  return launched(ti::long_keep(plan, fwd_workspace, kp, kept, static_cast<hipStream_t>(stream)), "keep");
+}
+
+int ti_bwd_kept_workspace(int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices, size_t* bytes) {
+  if (bytes == nullptr) return fail(TI_EINVAL, "bytes is null");
+  if (int rc = check_shape(batch, n, dtype)) return rc;
+  *bytes = 0;
+  if (n <= ti::kShortMax) return ok();
+  if (max_vertices < 1 || max_vertices > n + 1)
+    return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)max_vertices);
+  *bytes = ti::long_grad_bytes(batch, n, weighted != 0, max_vertices);
+  return ok();
+}
+
+int ti_bwd_kept(const uint32_t* starts, const void* kept, size_t kept_bytes, int64_t max_vertices,
+                const void* g, const void* w, const void* y, void* gy, void* gw, int64_t batch,
+                int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (n > ti::kShortMax && kept == nullptr) return fail(TI_EWORKSPACE, "the kept state is needed");
+  return bwd_impl(starts, nullptr, 0, kept, kept_bytes, max_vertices, g, w, y, gy, gw, batch, n, dtype, flags,
+                  y_min, y_max, workspace, workspace_bytes, stream);
 }
 
 int ti_grad_workspace(int64_t batch, int64_t n, int dtype, size_t* bytes) {

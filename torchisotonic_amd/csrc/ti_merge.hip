@@ -16,6 +16,7 @@
 //                  the tile (ranks from rank_kernel), edge slopes in float64 rounded once, every
 //                  element the slope of its edge with the clamp fused, and the start bits. y is
 //                  not read again.
+#include <algorithm>
 #include <type_traits>
 
 #include "ti_common.h"
@@ -706,6 +707,111 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
   }
 }
 
+// A bound on the final hulls' vertex counts: the largest over the rows of a row's vertices at
+// `level` (the sum of its nodes' counts there, a row's final hull having no vertex its nodes'
+// hulls lack), at most n + 1. One workgroup writes it to *out (which may be pinned host memory:
+// one store); with more rows, each workgroup's maximum goes to partial[blockIdx.x] and a second
+// launch of one workgroup takes the maximum of those.
+constexpr int kMaxcBlocks = 256;
+constexpr int64_t kMaxcRowsOne = 256 * 64;  // rows one workgroup takes alone
+
+__device__ __forceinline__ int64_t block_max_i64(int64_t v, int64_t* sh) {
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) {
+    const int64_t o = __shfl_xor(v, d, kWave);
+    v = o > v ? o : v;
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
+  __syncthreads();
+  int64_t m = sh[0];
+#pragma unroll
+  for (int k = 1; k < kWaves256; ++k) m = sh[k] > m ? sh[k] : m;
+  return m;
+}
+
+// P lanes a row (a power of two up to 64, at least the row's node count where that is at most
+// 64), 256 / P rows a workgroup, the workgroups striding over the rows.
+__global__ __launch_bounds__(256) void maxc_rows_kernel(const int* __restrict__ count, int64_t batch, int64_t npr,
+                                                        int lg_p, int64_t cap, int64_t* __restrict__ out,
+                                                        int64_t* __restrict__ partial) {
+  __shared__ int64_t sh[kWaves256];
+  const int P = 1 << lg_p;
+  const int sub = threadIdx.x & (P - 1);
+  const int64_t rows_per_wg = 256 >> lg_p;
+  int64_t v = 0;
+  for (int64_t r0 = blockIdx.x * rows_per_wg; r0 < batch; r0 += rows_per_wg * gridDim.x) {
+    const int64_t r = r0 + (threadIdx.x >> lg_p);
+    int64_t t = 0;
+    if (r < batch) {
+      for (int64_t j = sub; j < npr; j += P) t += count[r * npr + j];
+    }
+    for (int d = P / 2; d >= 1; d >>= 1) t += __shfl_xor(t, d, kWave);
+    v = t > v ? t : v;
+  }
+  const int64_t m = block_max_i64(v, sh);
+  if (threadIdx.x == 0) {
+    if (gridDim.x == 1) *out = m < cap ? m : cap;
+    else partial[blockIdx.x] = m;
+  }
+}
+
+__global__ __launch_bounds__(256) void maxc_final_kernel(const int64_t* __restrict__ partial, int parts, int64_t cap,
+                                                         int64_t* __restrict__ out) {
+  __shared__ int64_t sh[kWaves256];
+  int64_t v = 0;
+  for (int k = threadIdx.x; k < parts; k += 256) v = partial[k] > v ? partial[k] : v;
+  const int64_t m = block_max_i64(v, sh);
+  if (threadIdx.x == 0) *out = m < cap ? m : cap;
+}
+
+// The first hull_blocks workgroups: cpr of them a row, 256 slots each, the row's final hull
+// (vertices; and, in the row's first, its count, NaN flag and totals) into the kept layout, whose
+// rows hold maxc slots (a longer hull, which a wrong maxc would mean, is cut there). The others:
+// the tile records, four 16-byte words a thread, every load before any store.
+template <bool W>
+__global__ __launch_bounds__(256) void keep_kernel(NodeLevel fin, NodeLevel kept, int64_t maxc, int64_t cpr,
+                                                   int64_t hull_blocks, const uint4* __restrict__ tiles_in,
+                                                   uint4* __restrict__ tiles_out, int64_t tile_words) {
+  const int64_t blk = blockIdx.x;
+  if (blk < hull_blocks) {
+    const int64_t row = blk / cpr;
+    const int64_t chunk = blk - row * cpr;
+    const NodeOut s = node_out(fin, W, row);
+    const NodeOut d = node_out(kept, W, row);
+    const int cnt = static_cast<int>(min<int64_t>(*s.count, maxc));
+    const int q = static_cast<int>(chunk * 256) + threadIdx.x;
+    if (q < cnt) {
+      d.idx[q] = s.idx[q];
+      d.shi[q] = s.shi[q];
+      d.slo[q] = s.slo[q];
+      if constexpr (W) {
+        d.whi[q] = s.whi[q];
+        d.wlo[q] = s.wlo[q];
+      }
+    }
+    if (chunk == 0) {
+      if (threadIdx.x < 4) d.tot[threadIdx.x] = s.tot[threadIdx.x];
+      if (threadIdx.x == 0) {
+        *d.count = cnt;
+        *d.bad = *s.bad;
+      }
+    }
+    return;
+  }
+  const int64_t k0 = (blk - hull_blocks) * 1024 + threadIdx.x;
+  uint4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t k = k0 + u * 256;
+    if (k < tile_words) v[u] = tiles_in[k];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t k = k0 + u * 256;
+    if (k < tile_words) tiles_out[k] = v[u];
+  }
+}
+
 }  // namespace
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
@@ -783,11 +889,51 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
     ++level;
   }
   p.levels = level;  // merge launches; the final hulls are at level p.levels
+  // the level whose vertex counts bound the final hulls' for a caller keeping them (ti_keep): two
+  // below the final level (its merges, and then the expansion, overlap that caller's wait and
+  // allocation), but not level 0, whose counts the span kernel's fused merge overwrites
+  p.keep_level = p.levels <= 1 ? p.levels : std::max(1, p.levels - 2);
   p.slots = batch * p.npr[0] * (span0 + 1);
   p.off_store = off;
   p.off_rank = p.off_store + align256(vertex_store_bytes(p.slots, weighted));
-  p.bytes = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
+  p.off_maxc = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
+  p.bytes = p.off_maxc + align256(kMaxcBlocks * sizeof(int64_t));
   return p;
+}
+
+KeepPlan keep_plan(int64_t batch, int64_t n, bool weighted, int64_t maxc) {
+  KeepPlan k{};
+  k.batch = batch;
+  k.maxc = maxc;
+  k.tiles = batch * long_plan(batch, n, weighted).tiles_per_row;
+  size_t off = 0;
+  k.off_meta = off;
+  off += align256(node_meta_bytes(batch));
+  k.off_store = off;
+  off += align256(vertex_store_bytes(batch * maxc, weighted));
+  k.off_tiles = off;
+  off += align256(static_cast<size_t>(k.tiles) * sizeof(TileRec));
+  k.bytes = off;
+  return k;
+}
+
+hipError_t long_keep(const LongPlan& p, const void* ws, const KeepPlan& k, void* kept, hipStream_t stream) {
+  const NodeLevel fin = p.level(const_cast<void*>(ws), p.levels);
+  const NodeLevel kl = k.level(kept);
+  const int64_t words = k.tiles * static_cast<int64_t>(sizeof(TileRec) / sizeof(uint4));
+  const auto* tin = reinterpret_cast<const uint4*>(static_cast<const char*>(ws) + p.off_rank);
+  auto* tout = reinterpret_cast<uint4*>(static_cast<char*>(kept) + k.off_tiles);
+  const int64_t cpr = (k.maxc + 255) / 256;
+  const int64_t hull_blocks = k.batch * cpr;
+  const int64_t grid = hull_blocks + (words + 1023) / 1024;
+  if (grid > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+  if (p.weighted)
+    keep_kernel<true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(fin, kl, k.maxc, cpr, hull_blocks,
+                                                                                tin, tout, words);
+  else
+    keep_kernel<false><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(fin, kl, k.maxc, cpr, hull_blocks,
+                                                                                 tin, tout, words);
+  return hipGetLastError();
 }
 
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
@@ -799,6 +945,27 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
+  // for a caller that keeps only the final hulls: a bound on their vertex counts, from the
+  // counts of level keep_level once it is merged
+  auto report = [&](int l) -> hipError_t {
+    if (l != p.keep_level) return hipSuccess;
+    if (t.max_vertices != nullptr) {
+      const NodeLevel kl = p.level(ws, l);
+      int lg_p = 0;
+      while (lg_p < 6 && (int64_t{1} << lg_p) < p.npr[l]) ++lg_p;
+      const int64_t rows_one = kMaxcRowsOne >> lg_p;  // (a workgroup's 256 / P rows, 64 times over)
+      const int parts = static_cast<int>(
+          t.batch <= rows_one ? 1 : std::min<int64_t>(kMaxcBlocks, (t.batch + rows_one - 1) / rows_one));
+      int64_t* partial = reinterpret_cast<int64_t*>(base + p.off_maxc);
+      maxc_rows_kernel<<<dim3(parts), dim3(256), 0, t.stream>>>(reinterpret_cast<const int*>(kl.meta), t.batch,
+                                                                p.npr[l], lg_p, t.n + 1, t.max_vertices, partial);
+      if (parts > 1) maxc_final_kernel<<<dim3(1), dim3(256), 0, t.stream>>>(partial, parts, t.n + 1, t.max_vertices);
+      const hipError_t le = hipGetLastError();
+      if (le != hipSuccess) return le;
+    }
+    return t.hulls_ready != nullptr ? hipEventRecord(t.hulls_ready, t.stream) : hipSuccess;
+  };
+  if ((e = report(0)) != hipSuccess) return e;
   for (int l = 1; l <= p.levels; ++l) {
     MergeArgs m;
     m.in = p.level(ws, l - 1);
@@ -827,6 +994,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
 #undef TI_MERGE_LAUNCH
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if ((e = report(l)) != hipSuccess) return e;
   }
   if (t.n <= kXpackMaxN) {
     // rows of one tile: records and fit together, whole rows a workgroup

@@ -2,9 +2,9 @@
 //
 // Replaces the reference's long-row gradient (reference src/torchisotonic/csrc/grad.cuh:
 // 165-195 tile summaries, 346-370 ATen tile scan, 200-290 fill), which reads starts, g and w
-// twice and runs about fifteen ATen kernels in between. Here the forward's final hulls (kept in
-// its workspace) give every block's weight and fit; only the block sums of g are new, and they
-// are differences of a prefix sum of g taken at the hull's vertices:
+// twice and runs about fifteen ATen kernels in between. Here the forward's final hulls (in its
+// workspace, or copied out of it by ti_keep) give every block's weight and fit; only the block
+// sums of g are new, and they are differences of a prefix sum of g taken at the hull's vertices:
 //
 //   gsum_kernel    per tile (two to a workgroup, their loads in flight together): reads g
 //                  once; the tile's total, and the prefix of g (within the tile, double-double)
@@ -39,12 +39,14 @@ struct GradPlan {
   size_t off_tg, off_lp, off_gt, off_gp, off_lv, bytes;
 };
 
-GradPlan grad_plan(int64_t batch, int64_t n, bool weighted) {
+// kept_maxc > 0: the final hulls come from a kept state, at most that many vertices a row
+GradPlan grad_plan(int64_t batch, int64_t n, bool weighted, int64_t kept_maxc) {
   const LongPlan lp = long_plan(batch, n, weighted);
   GradPlan g{};
   g.tpr = lp.tiles_per_row;
   g.ngroups = (g.tpr + kScanTiles - 1) / kScanTiles;
-  g.cap_final = lp.npr[0] * (lp.span0 + 1);  // a row's slots: room for any final hull
+  // a row's slots (room for any final hull), or the kept hulls' largest
+  g.cap_final = kept_maxc > 0 ? kept_maxc : lp.npr[0] * (lp.span0 + 1);
   size_t off = 0;
   g.off_tg = off;
   off += align256(static_cast<size_t>(batch * g.tpr) * 16);
@@ -600,11 +602,14 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
 
 }  // namespace
 
-size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted) { return grad_plan(batch, n, weighted).bytes; }
+size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted, int64_t kept_maxc) {
+  return grad_plan(batch, n, weighted, kept_maxc).bytes;
+}
 
 hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   const bool W = in.w != nullptr;
-  const GradPlan gpn = grad_plan(in.batch, in.n, W);
+  const int64_t kmaxc = in.kept != nullptr ? in.kept_maxc : 0;
+  const GradPlan gpn = grad_plan(in.batch, in.n, W, kmaxc);
   char* base = static_cast<char*>(ws);
   const char* fbase = static_cast<const char*>(in.fwd_ws);
   GradKArgs a;
@@ -622,8 +627,14 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.flags = in.flags;
   a.lo = in.lo;
   a.hi = in.hi;
-  a.hulls = p.level(const_cast<char*>(fbase), p.levels);
-  a.tiles = reinterpret_cast<const TileRec*>(fbase + p.off_rank);
+  if (in.kept != nullptr) {
+    const KeepPlan kp = keep_plan(in.batch, in.n, W, kmaxc);
+    a.hulls = kp.level(const_cast<void*>(in.kept));
+    a.tiles = reinterpret_cast<const TileRec*>(static_cast<const char*>(in.kept) + kp.off_tiles);
+  } else {
+    a.hulls = p.level(const_cast<char*>(fbase), p.levels);
+    a.tiles = reinterpret_cast<const TileRec*>(fbase + p.off_rank);
+  }
   a.tg = reinterpret_cast<double*>(base + gpn.off_tg);
   a.lp = reinterpret_cast<double*>(base + gpn.off_lp);
   a.gt = reinterpret_cast<double*>(base + gpn.off_gt);

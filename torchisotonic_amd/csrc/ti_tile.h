@@ -35,6 +35,11 @@ struct TileArgs {
   double lo, hi;
   hipStream_t stream;
   hipEvent_t weights_read = nullptr;  // recorded once every weight has been read, if given
+  // Where given (rows over 32 elements): a bound on the final hulls' vertex counts (at least the
+  // largest, at most n + 1) is written here (a device-visible word) and hulls_ready recorded once
+  // it is, before the last merges and the expansion run.
+  int64_t* max_vertices = nullptr;
+  hipEvent_t hulls_ready = nullptr;
 };
 
 // One node's hull: vertex indices relative to the node's first element, cumulative sums
@@ -272,10 +277,11 @@ struct LongPlan {
   int64_t span0;          // elements per span (the first node level)
   int rows_per_wave;      // > 1: the span kernel's wave holds that many short rows, 64 / it lanes each
   int levels;
+  int keep_level;  // the level whose vertex counts bound the final hulls' (see long_fit)
   int64_t batch;
   int64_t npr[kMaxLevels + 1], spn[kMaxLevels + 1], span[kMaxLevels + 1];
   int64_t slots;  // of the store: batch * npr[0] * (span0 + 1)
-  size_t off_meta[kMaxLevels + 1], off_store, off_rank, bytes;
+  size_t off_meta[kMaxLevels + 1], off_store, off_rank, off_maxc, bytes;
   bool weighted;
 
   NodeLevel level(void* ws, int l) const {
@@ -286,6 +292,20 @@ struct LongPlan {
 
 LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
+
+// The part of a long-row forward's workspace that its backward reads, kept on its own
+// (ti_keep): the final hulls, each row's in a stretch of maxc slots (maxc: a bound on the final
+// hulls' vertex counts), and the per-tile records.
+struct KeepPlan {
+  int64_t batch, maxc, tiles;
+  size_t off_meta, off_store, off_tiles, bytes;
+  NodeLevel level(void* kept) const {
+    char* b = static_cast<char*>(kept);
+    return NodeLevel{b + off_meta, b + off_store, batch, 1, 1, 1, maxc, batch * maxc};
+  }
+};
+KeepPlan keep_plan(int64_t batch, int64_t n, bool weighted, int64_t maxc);
+hipError_t long_keep(const LongPlan& p, const void* ws, const KeepPlan& k, void* kept, hipStream_t stream);
 
 // Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
 // place into its level-1 node of `hulls1` and its first span's count set to -1. With
@@ -306,10 +326,14 @@ struct LongGradArgs {
   int dtype;
   unsigned flags;
   double lo, hi;
-  const void* fwd_ws;
+  const void* fwd_ws;  // the forward's workspace, or
+  const void* kept;    // what ti_keep kept of it (fwd_ws null)
+  int64_t kept_maxc;   // the kept hulls' slots a row
   hipStream_t stream;
 };
-size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted);
+// kept_maxc > 0: the workspace of a backward from a kept state (its vertex prefixes sized for
+// hulls of that many vertices instead of a row's every slot)
+size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted, int64_t kept_maxc = 0);
 hipError_t long_grad(const LongGradArgs& a, const LongPlan& p, void* ws);
 
 inline int64_t tile_elems(bool weighted) { return weighted ? TileCfg<true>::kN : TileCfg<false>::kN; }
