@@ -11,7 +11,8 @@
 //                      the whole tile if it holds none), its "tail" (from its last start to its
 //                      end) and whether it holds a start. Only the threads that overlap the
 //                      head or the tail read g and w; where blocks are short the kernel reads
-//                      little beyond the start bits.
+//                      little beyond the start bits, and a tile without a start is summed
+//                      plainly.
 //   seg_scan_kernel    per group of 256 tiles: segmented scans of the tile summaries, forward
 //                      (a block's sum before a tile: the previous tile's tail, plus the heads of
 //                      start-free tiles before it) and backward (after a tile: the following
@@ -20,7 +21,8 @@
 //   seg_fill_kernel    per tile: within each thread, the sum over each block's elements there;
 //                      across the workgroup, the same segmented scans over the threads (seeded
 //                      with the tile's carries from both sides); then gy = w G / W and
-//                      gw = (y - fit) G / W.
+//                      gw = (y - fit) G / W. A tile without a start lies inside one block whose
+//                      sums the carries and its total give: it reads w (and y, fit) only.
 // A problem set of one tile runs seg_fill_kernel alone. Sums are float64 within a thread and
 // double-double across threads, tiles and groups.
 #include <type_traits>
@@ -92,6 +94,7 @@ struct SegArgs {
   void* gy;
   void* gw;
   int64_t n, total, ntiles, ngroups;
+  bool flat;  // one row, or rows of a multiple of 32 elements: bit e of the set is bit e % 32 of word e / 32
   // workspace (null for a problem set of one tile)
   SegSt* tfwd;   // [ntiles] per tile: forward state (tail, or the whole tile)
   SegSt* tbwd;   // [ntiles] per tile: backward state (head)
@@ -106,6 +109,18 @@ struct SegArgs {
 __device__ __forceinline__ uint32_t thread_starts(const SegArgs& a, int64_t e0, int& count) {
   count = static_cast<int>(max<int64_t>(0, min<int64_t>(kSegE, a.total - e0)));
   if (count == 0) return 0u;
+  if (a.flat) {
+    // one word holds the thread's bits (e0 is a multiple of kSegE, which divides 32), and a row
+    // start can fall only on e0 (rows are one, or a multiple of 32 elements long)
+    static_assert(32 % kSegE == 0, "a thread's start bits lie in one word");
+    uint32_t sb = (a.starts[e0 >> 5] >> (e0 & 31)) & ((1u << kSegE) - 1u);
+    if (count < kSegE) sb &= (1u << count) - 1u;
+    // e0 % n without a 64-bit division: the quotient from float64 (exact to one either way)
+    int64_t q = static_cast<int64_t>(static_cast<double>(e0) / static_cast<double>(a.n));
+    int64_t r = e0 - q * a.n;
+    r = r < 0 ? r + a.n : (r >= a.n ? r - a.n : r);
+    return sb | (r == 0 ? 1u : 0u);
+  }
   const int64_t wpr = (a.n + 31) / 32;
   int64_t row = e0 / a.n;
   int64_t i = e0 - row * a.n;
@@ -182,9 +197,32 @@ __global__ __launch_bounds__(kSegThreads) void seg_ends_kernel(SegArgs a) {
   __syncthreads();
   const int fs = first_start, ls = last_start;
   const int p0 = tid * kSegE;
-  // (threads with nothing before the first start or after the last one read nothing)
-  const bool need = count > 0 && (p0 < fs || (ls >= 0 && p0 + count > ls));
   DD head[2] = {DD{0.0, 0.0}, DD{0.0, 0.0}}, tail[2] = {DD{0.0, 0.0}, DD{0.0, 0.0}};
+  if (ls < 0) {
+    // no start in the tile (long blocks: most tiles): its total, each thread's part summed in
+    // float64 (double-double for float64 data)
+    if (count > 0) {
+      double v[2][kSegE];
+      load_gw<T, W>(a, e0, count, v);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if constexpr (sizeof(T) == 8) {
+#pragma unroll
+          for (int k = 0; k < kSegE; ++k) head[q] = dd_add(head[q], v[q][k]);
+        } else {
+          double t = 0.0;
+#pragma unroll
+          for (int k = 0; k < kSegE; ++k) t += v[q][k];
+          head[q] = DD{t, 0.0};
+        }
+      }
+    }
+    block_sum2(head, red[0]);
+    if (tid == 0) a.tbwd[tile] = a.tfwd[tile] = SegSt{0, {head[0], head[1]}};
+    return;
+  }
+  // (threads with nothing before the first start or after the last one read nothing)
+  const bool need = count > 0 && (p0 < fs || p0 + count > ls);
   if (need) {
     double v[2][kSegE];
     load_gw<T, W>(a, e0, count, v);
@@ -194,16 +232,15 @@ __global__ __launch_bounds__(kSegThreads) void seg_ends_kernel(SegArgs a) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         if (p < fs) head[q] = dd_add(head[q], v[q][k]);
-        if (ls >= 0 && p >= ls) tail[q] = dd_add(tail[q], v[q][k]);
+        if (p >= ls) tail[q] = dd_add(tail[q], v[q][k]);
       }
     }
   }
   block_sum2(head, red[0]);
   block_sum2(tail, red[1]);
   if (tid == 0) {
-    const int f = ls >= 0 ? 1 : 0;
-    a.tbwd[tile] = SegSt{f, {head[0], head[1]}};
-    a.tfwd[tile] = f ? SegSt{1, {tail[0], tail[1]}} : SegSt{0, {head[0], head[1]}};
+    a.tbwd[tile] = SegSt{1, {head[0], head[1]}};
+    a.tfwd[tile] = SegSt{1, {tail[0], tail[1]}};
   }
 }
 
@@ -291,6 +328,37 @@ __global__ __launch_bounds__(kSegThreads) void seg_fill_kernel(SegArgs a) {
   const int tid = threadIdx.x;
   const int64_t tile = blockIdx.x;
   const int64_t e0 = tile * kSegTile + tid * kSegE;
+  if (a.cfwd != nullptr && a.tbwd[tile].f == 0) {
+    // a tile inside one block: its block sums are the carry from the left, the tile's total and
+    // the carry from the right, the same for every element, so g is not read again
+    const int64_t grp = tile / kSegGroup;
+    SegSt cf = a.cfwd[tile], cb = a.cbwd[tile];
+    if (a.ngroups > 1) {
+      cf = comb_fwd(a.gfwd[grp], cf);
+      cb = comb_bwd(cb, a.gbwd[grp]);
+    }
+    const SegSt tt = a.tbwd[tile];
+    const DD G = dd_add(dd_add(cf.v[0], tt.v[0]), cb.v[0]);
+    const DD Wt = dd_add(dd_add(cf.v[1], tt.v[1]), cb.v[1]);
+    const double q = (G.hi + G.lo) / (Wt.hi + Wt.lo);
+    const int count = static_cast<int>(max<int64_t>(0, min<int64_t>(kSegE, a.total - e0)));
+    if (count == 0) return;
+    T wv[W ? kSegE : 1], yv[WANT_W ? kSegE : 1], fv[WANT_W ? kSegE : 1];
+    if constexpr (W) load_elems_any<T, kSegE>(static_cast<const T*>(a.w) + e0, count, wv);
+    if constexpr (WANT_W) {
+      load_elems_any<T, kSegE>(static_cast<const T*>(a.y) + e0, count, yv);
+      load_elems_any<T, kSegE>(static_cast<const T*>(a.fit) + e0, count, fv);
+    }
+    T oy[kSegE], ow[kSegE];
+#pragma unroll
+    for (int k = 0; k < kSegE; ++k) {
+      oy[k] = static_cast<T>((W ? static_cast<double>(wv[W ? k : 0]) : 1.0) * q);
+      if constexpr (WANT_W) ow[k] = static_cast<T>((static_cast<double>(yv[k]) - static_cast<double>(fv[k])) * q);
+    }
+    store_elems_any<T, kSegE>(static_cast<T*>(a.gy) + e0, count, oy);
+    if constexpr (WANT_W) store_elems_any<T, kSegE>(static_cast<T*>(a.gw) + e0, count, ow);
+    return;
+  }
   int count;
   const uint32_t sb = thread_starts(a, e0, count);
   double v[2][kSegE];
@@ -427,6 +495,7 @@ hipError_t seg_grad(const SegGradArgs& in, void* ws) {
   a.gw = in.gw;
   a.n = in.n;
   a.total = in.batch * in.n;
+  a.flat = in.batch == 1 || in.n % 32 == 0;
   a.ntiles = p.ntiles;
   a.ngroups = p.ngroups;
   if (p.bytes > 0) {
