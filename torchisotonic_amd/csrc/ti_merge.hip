@@ -739,14 +739,23 @@ __global__ __launch_bounds__(256) void maxc_rows_kernel(const int* __restrict__ 
   const int sub = threadIdx.x & (P - 1);
   const int64_t rows_per_wg = 256 >> lg_p;
   int64_t v = 0;
-  for (int64_t r0 = blockIdx.x * rows_per_wg; r0 < batch; r0 += rows_per_wg * gridDim.x) {
-    const int64_t r = r0 + (threadIdx.x >> lg_p);
-    int64_t t = 0;
-    if (r < batch) {
-      for (int64_t j = sub; j < npr; j += P) t += count[r * npr + j];
+  // (four stretches of rows at a time, their loads in flight together)
+  constexpr int U = 4;
+  for (int64_t r0 = blockIdx.x * rows_per_wg; r0 < batch; r0 += U * rows_per_wg * gridDim.x) {
+    int64_t t[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + u * rows_per_wg * gridDim.x + (threadIdx.x >> lg_p);
+      t[u] = 0;
+      if (r < batch) {
+        for (int64_t j = sub; j < npr; j += P) t[u] += count[r * npr + j];
+      }
     }
-    for (int d = P / 2; d >= 1; d >>= 1) t += __shfl_xor(t, d, kWave);
-    v = t > v ? t : v;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      for (int d = P / 2; d >= 1; d >>= 1) t[u] += __shfl_xor(t[u], d, kWave);
+      v = t[u] > v ? t[u] : v;
+    }
   }
   const int64_t m = block_max_i64(v, sh);
   if (threadIdx.x == 0) {
@@ -778,15 +787,27 @@ __global__ __launch_bounds__(256) void keep_kernel(NodeLevel fin, NodeLevel kept
     const int64_t chunk = blk - row * cpr;
     const NodeOut s = node_out(fin, W, row);
     const NodeOut d = node_out(kept, W, row);
-    const int cnt = static_cast<int>(min<int64_t>(*s.count, maxc));
     const int q = static_cast<int>(chunk * 256) + threadIdx.x;
-    if (q < cnt) {
-      d.idx[q] = s.idx[q];
-      d.shi[q] = s.shi[q];
-      d.slo[q] = s.slo[q];
+    // (the slot is read before the count is known, so the two reads overlap: slots below maxc
+    // lie within the row's store, whose span0 + 1 slots a span exceed n + 1)
+    HPt x{};
+    if (q < maxc) {
+      x.i = s.idx[q];
+      x.s = s.shi[q];
+      x.sl = s.slo[q];
       if constexpr (W) {
-        d.whi[q] = s.whi[q];
-        d.wlo[q] = s.wlo[q];
+        x.w = s.whi[q];
+        x.wl = s.wlo[q];
+      }
+    }
+    const int cnt = static_cast<int>(min<int64_t>(*s.count, maxc));
+    if (q < cnt) {
+      d.idx[q] = x.i;
+      d.shi[q] = x.s;
+      d.slo[q] = x.sl;
+      if constexpr (W) {
+        d.whi[q] = x.w;
+        d.wlo[q] = x.wl;
       }
     }
     if (chunk == 0) {
