@@ -172,11 +172,12 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
  *   3. ti_bwd_kept_workspace, ti_bwd_kept: the backward from the kept buffer, with results
  *      identical to ti_bwd's from the workspace.
  *
- * The kept buffer holds each row's final hull in max_vertices slots (20 bytes a slot, 36
- * weighted) and 32 bytes a tile of 4096 elements (2048 weighted): about 1.6 MB for one weighted
- * row of 1e8 with a final hull of about a thousand vertices, against 3.6 GB of workspace. A row
- * whose hull has every element as a vertex (monotone data) keeps as much as the workspace, and
- * a caller may then keep the workspace itself.
+ * The kept buffer holds each row's final hull in max_vertices slots (float32 data: 12 bytes a
+ * slot, 20 weighted; float64: 20 and 36) and 32 bytes a tile of 4096 elements (2048 weighted):
+ * about 1.6 MB for one weighted float32 row of 1e8 with a final hull of about a thousand
+ * vertices, against 2.0 GB of workspace. A row whose hull has every element as a vertex
+ * (monotone data) keeps as much as the workspace, and a caller may then keep the workspace
+ * itself.
  */
 
 /*

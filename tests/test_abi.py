@@ -57,16 +57,18 @@ def test_workspace_queries() -> None:
     assert size.value == 0  # short rows: no workspace
     assert lib.ti_fwd_workspace(1000, 33, _ext.F32, 0, ctypes.byref(size)) == 0
     assert size.value > 0  # longer rows: span hulls, merges and tile records
-    # one vertex store shared by every merge level: span0 + 1 slots per span of span0 elements,
-    # 36 bytes a slot weighted (index, double-double sums and weights), 20 unweighted; per-level
-    # counts and totals and the tile records are small beside it
+    # one vertex store shared by every merge level: span0 + 1 slots per span of span0 elements;
+    # float32 data: 20 bytes a slot weighted (index, sums and weights rounded to float64), 12
+    # unweighted; float64 data: 36 and 20 (double-double sums); per-level counts and totals and
+    # the tile records are small beside it
     n = 100_000_000
-    assert lib.ti_fwd_workspace(1, n, _ext.F32, 1, ctypes.byref(size)) == 0
     slots = -(-n // 256) * 257  # C4's spans of 256
-    assert 36 * slots < size.value < 36 * slots * 1.01
-    assert size.value < 3.7e9
-    assert lib.ti_fwd_workspace(1, n, _ext.F32, 0, ctypes.byref(size)) == 0
-    assert 20 * slots < size.value < 20 * slots * 1.02
+    for dtype, weighted, per_slot in ((_ext.F32, 1, 20), (_ext.F32, 0, 12), (_ext.F64, 1, 36), (_ext.F64, 0, 20)):
+        assert lib.ti_fwd_workspace(1, n, dtype, weighted, ctypes.byref(size)) == 0
+        assert per_slot * slots < size.value < per_slot * slots * 1.03, (dtype, weighted, size.value)
+    # C4 (one weighted float32 row of 1e8) within 2.5 GB
+    assert lib.ti_fwd_workspace(1, n, _ext.F32, 1, ctypes.byref(size)) == 0
+    assert size.value < 2.1e9
     assert lib.ti_bwd_workspace(1000, 16, _ext.F64, 1, ctypes.byref(size)) == 0
     assert size.value == 0
     assert lib.ti_bwd_workspace(1000, 65536, _ext.F32, 1, ctypes.byref(size)) == 0
@@ -77,20 +79,22 @@ def test_workspace_queries() -> None:
 
 def test_kept_state_sizes() -> None:
     # what a backward keeps in place of the forward's workspace: each row's final hull in
-    # max_vertices slots (36 bytes weighted, 20 unweighted), its count, NaN flag and totals
-    # (40 bytes) and 32 bytes a tile (2048 elements weighted, 4096 unweighted), against the
-    # workspace's slot for every element
+    # max_vertices slots (float32: 20 bytes weighted, 12 unweighted; float64: 36, 20), its count,
+    # NaN flag and totals (40 bytes) and 32 bytes a tile (2048 elements weighted, 4096
+    # unweighted), against the workspace's slot for every element
     lib = _ext.load()
     size, ws = ctypes.c_size_t(0), ctypes.c_size_t(0)
     n = 100_000_000
     assert lib.ti_keep_bytes(1, n, _ext.F32, 1, 1083, ctypes.byref(size)) == 0
     tiles = -(-n // 2048)
-    assert 36 * 1083 + 32 * tiles + 40 <= size.value < 36 * 1083 + 32 * tiles + 40 + 8 * 256
+    assert 20 * 1083 + 32 * tiles + 40 <= size.value < 20 * 1083 + 32 * tiles + 40 + 8 * 256
     assert size.value < 2e6
     assert lib.ti_fwd_workspace(1, n, _ext.F32, 1, ctypes.byref(ws)) == 0
     assert size.value * 1000 < ws.value
     assert lib.ti_keep_bytes(1000, 65536, _ext.F32, 0, 300, ctypes.byref(size)) == 0
-    assert 1000 * (20 * 300 + 32 * 16 + 40) <= size.value < 1000 * (20 * 300 + 32 * 16 + 40) + 8 * 256
+    assert 1000 * (12 * 300 + 32 * 16 + 40) <= size.value < 1000 * (12 * 300 + 32 * 16 + 40) + 8 * 256
+    assert lib.ti_keep_bytes(1000, 65536, _ext.F64, 1, 300, ctypes.byref(size)) == 0
+    assert 1000 * (36 * 300 + 32 * 32 + 40) <= size.value < 1000 * (36 * 300 + 32 * 32 + 40) + 8 * 256
     # the backward's workspace from a kept state: per-tile scans and 16 bytes a kept slot,
     # against 16 bytes an element from the workspace
     kb, wb = ctypes.c_size_t(0), ctypes.c_size_t(0)

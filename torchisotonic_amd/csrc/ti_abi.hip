@@ -124,7 +124,7 @@ int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
   if (n <= ti::kShortMax) return ok();
-  *bytes = ti::long_plan(batch, n, weighted != 0).bytes;
+  *bytes = ti::long_plan(batch, n, weighted != 0, dtype == TI_F64).bytes;
   return ok();
 }
 
@@ -135,7 +135,7 @@ int ti_fwd_geometry(int64_t batch, int64_t n, int weighted, int64_t* span0, int*
   *levels = 0;
   *rows_per_wave = 0;
   if (n <= ti::kShortMax) return ok();
-  const ti::LongPlan p = ti::long_plan(batch, n, weighted != 0);
+  const ti::LongPlan p = ti::long_plan(batch, n, weighted != 0, false);  // (the geometry is the dtype's either way)
   *span0 = p.span0;
   *levels = p.levels;
   *rows_per_wave = p.rows_per_wave;
@@ -181,7 +181,7 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
     ti::ShortArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
     return then_record(launched(ti::short_fit(a), "short-row fit"));
   }
-  const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr);
+  const ti::LongPlan plan = ti::long_plan(batch, n, w != nullptr, dtype == TI_F64);
   if (workspace == nullptr || workspace_bytes < plan.bytes)
     return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", plan.bytes, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspace must be 256-byte aligned");
@@ -212,11 +212,11 @@ int bwd_impl(const uint32_t* starts, const void* fwd_ws, size_t fwd_ws_bytes, co
     return launched(ti::short_grad(a), "short-row gradient");
   }
   const bool W = w != nullptr;
-  const ti::LongPlan plan = ti::long_plan(batch, n, W);
+  const ti::LongPlan plan = ti::long_plan(batch, n, W, dtype == TI_F64);
   if (kept != nullptr || kept_bytes > 0 || kept_maxc != 0) {
     if (kept_maxc < 1 || kept_maxc > n + 1)
       return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)kept_maxc);
-    const size_t kneed = ti::keep_plan(batch, n, W, kept_maxc).bytes;
+    const size_t kneed = ti::keep_plan(batch, n, W, dtype == TI_F64, kept_maxc).bytes;
     if (kept == nullptr || kept_bytes < kneed)
       return fail(TI_EWORKSPACE, "the kept state (%zu bytes) is needed, %zu given", kneed, kept_bytes);
     if ((reinterpret_cast<uintptr_t>(kept) & 255) != 0) return fail(TI_EINVAL, "the kept state must be 256-byte aligned");
@@ -228,7 +228,7 @@ int bwd_impl(const uint32_t* starts, const void* fwd_ws, size_t fwd_ws_bytes, co
                   plan.bytes, (long long)n, fwd_ws_bytes);
     if ((reinterpret_cast<uintptr_t>(fwd_ws) & 255) != 0) return fail(TI_EINVAL, "workspaces must be 256-byte aligned");
   }
-  const size_t need = ti::long_grad_bytes(batch, n, W, kept != nullptr ? kept_maxc : 0);
+  const size_t need = ti::long_grad_bytes(batch, n, W, dtype == TI_F64, kept != nullptr ? kept_maxc : 0);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(TI_EWORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(TI_EINVAL, "workspaces must be 256-byte aligned");
@@ -252,7 +252,7 @@ int ti_fwd(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* 
 int ti_fwd_noalloc(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
                    int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max, void* stream) {
   if (int rc = check_shape(batch, n, dtype)) return rc;
-  const size_t need = n <= ti::kShortMax ? 0 : ti::long_plan(batch, n, w != nullptr).bytes;
+  const size_t need = n <= ti::kShortMax ? 0 : ti::long_plan(batch, n, w != nullptr, dtype == TI_F64).bytes;
   if (need > TI_NOALLOC_SCRATCH_BYTES)
     return fail(TI_EWORKSPACE,
                 "ti_fwd_noalloc: this problem set needs %zu bytes of workspace, its scratch holds %zu "
@@ -277,7 +277,7 @@ int ti_bwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* 
   if (int rc = check_shape(batch, n, dtype)) return rc;
   *bytes = 0;
   if (n <= ti::kShortMax) return ok();
-  *bytes = ti::long_grad_bytes(batch, n, weighted != 0);
+  *bytes = ti::long_grad_bytes(batch, n, weighted != 0, dtype == TI_F64);
   return ok();
 }
 
@@ -305,7 +305,7 @@ int ti_keep_bytes(int64_t batch, int64_t n, int dtype, int weighted, int64_t max
   if (n <= ti::kShortMax || batch == 0) return ok();
   if (max_vertices < 1 || max_vertices > n + 1)
     return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)max_vertices);
-  *bytes = ti::keep_plan(batch, n, weighted != 0, max_vertices).bytes;
+  *bytes = ti::keep_plan(batch, n, weighted != 0, dtype == TI_F64, max_vertices).bytes;
   return ok();
 }
 
@@ -315,11 +315,11 @@ int ti_keep(const void* fwd_workspace, size_t fwd_workspace_bytes, void* kept, s
   if (n <= ti::kShortMax || batch == 0) return ok();
   if (max_vertices < 1 || max_vertices > n + 1)
     return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)max_vertices);
-  const ti::LongPlan plan = ti::long_plan(batch, n, weighted != 0);
+  const ti::LongPlan plan = ti::long_plan(batch, n, weighted != 0, dtype == TI_F64);
   if (fwd_workspace == nullptr || fwd_workspace_bytes < plan.bytes)
     return fail(TI_EWORKSPACE, "the forward's workspace (%zu bytes) is needed, %zu given", plan.bytes,
                 fwd_workspace_bytes);
-  const ti::KeepPlan kp = ti::keep_plan(batch, n, weighted != 0, max_vertices);
+  const ti::KeepPlan kp = ti::keep_plan(batch, n, weighted != 0, dtype == TI_F64, max_vertices);
   if (kept == nullptr || kept_bytes < kp.bytes)
     return fail(TI_EWORKSPACE, "a kept buffer of %zu bytes is needed, %zu given", kp.bytes, kept_bytes);
   if ((reinterpret_cast<uintptr_t>(kept) & 255) != 0 || (reinterpret_cast<uintptr_t>(fwd_workspace) & 255) != 0)
@@ -335,7 +335,7 @@ int ti_bwd_kept_workspace(int64_t batch, int64_t n, int dtype, int weighted, int
   if (n <= ti::kShortMax) return ok();
   if (max_vertices < 1 || max_vertices > n + 1)
     return fail(TI_EINVAL, "max_vertices must be in [1, n + 1], got %lld", (long long)max_vertices);
-  *bytes = ti::long_grad_bytes(batch, n, weighted != 0, max_vertices);
+  *bytes = ti::long_grad_bytes(batch, n, weighted != 0, dtype == TI_F64, max_vertices);
   return ok();
 }
 

@@ -44,8 +44,8 @@ template <bool W>
 __device__ __forceinline__ VPt vload(const VArr& a, int k) {
   VPt p;
   p.i = a.idx[k];
-  p.s = DD{a.shi[k], a.slo[k]};
-  if constexpr (W) p.w = DD{a.whi[k], a.wlo[k]};
+  p.s = DD{a.shi[k], lo_at(a.slo, k)};
+  if constexpr (W) p.w = DD{a.whi[k], lo_at(a.wlo, k)};
   else p.w = DD{static_cast<double>(p.i), 0.0};
   return p;
 }
@@ -53,12 +53,8 @@ __device__ __forceinline__ VPt vload(const VArr& a, int k) {
 template <bool W>
 __device__ __forceinline__ void vstore(const VArr& a, int k, const VPt& p) {
   a.idx[k] = p.i;
-  a.shi[k] = p.s.hi;
-  a.slo[k] = p.s.lo;
-  if constexpr (W) {
-    a.whi[k] = p.w.hi;
-    a.wlo[k] = p.w.lo;
-  }
+  put_dd(a.shi, a.slo, k, p.s.hi, p.s.lo);
+  if constexpr (W) put_dd(a.whi, a.wlo, k, p.w.hi, p.w.lo);
 }
 
 template <bool W>
@@ -146,6 +142,68 @@ __device__ void vbridge(const VArr& v, int ba, int cA, int bb, int cB, int& keep
 
 __device__ VArr dvarr_of(const NodeOut& o) { return VArr{o.idx, o.shi, o.slo, o.whi, o.wlo}; }
 
+// Float32 data keeps its hull sums rounded to float64 in the vertex store (NodeOut). Rounded one
+// by one, a hull that the double-double merges found convex can turn slightly non-convex in the
+// stored values where points are nearly collinear, and the fit (its slopes) would step down
+// there. Each final hull is made convex in the stored values: a vertex on or above the chord
+// between its neighbours is no vertex of the lower hull of the stored points, so every such
+// vertex goes at once, and the row is tested again (most rows pass the first test). One
+// workgroup per row; the removal compacts the row in place a chunk at a time, the chunk's
+// original vertices (and its neighbours outside it) staged in LDS before any of its slots is
+// written.
+constexpr int kRepairThreads = 256;
+
+template <bool W>
+__global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin) {
+  __shared__ int any;
+  __shared__ int wcount[kRepairThreads / kWave];
+  __shared__ VPt tile[kRepairThreads + 2];
+  __shared__ VPt prev;  // the original vertex before the chunk
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int64_t row = blockIdx.x;
+  const NodeOut o = node_out(fin, W, row);
+  if (*o.bad != 0) return;  // (a NaN row's fit is NaN whatever its hull)
+  const VArr v = dvarr_of(o);
+  int cnt = *o.count;
+  for (int pass = 0; pass < 64; ++pass) {
+    if (tid == 0) any = 0;
+    __syncthreads();
+    bool found = false;
+    for (int i = 1 + tid; i < cnt - 1; i += kRepairThreads)
+      found |= vpools<W>(vload<W>(v, i - 1), vload<W>(v, i), vload<W>(v, i + 1));
+    if (__any(found) && lane == 0) any = 1;
+    __syncthreads();
+    if (any == 0) break;
+    int base = 0;
+    for (int c0 = 0; c0 < cnt; c0 += kRepairThreads) {
+      const int i = c0 + tid;
+      if (i < cnt) tile[tid + 1] = vload<W>(v, i);
+      if (tid == 0) {
+        if (c0 > 0) tile[0] = prev;
+        if (c0 + kRepairThreads < cnt) tile[kRepairThreads + 1] = vload<W>(v, c0 + kRepairThreads);
+      }
+      __syncthreads();
+      const bool keep = i < cnt && (i == 0 || i == cnt - 1 || !vpools<W>(tile[tid], tile[tid + 1], tile[tid + 2]));
+      const uint64_t m = __ballot(keep);
+      if (lane == 0) wcount[wave] = __popcll(m);
+      __syncthreads();
+      int before = base, all = 0;
+      for (int k = 0; k < kRepairThreads / kWave; ++k) {
+        before += k < wave ? wcount[k] : 0;
+        all += wcount[k];
+      }
+      const VPt x = tile[tid + 1];
+      if (tid == kRepairThreads - 1) prev = x;  // (read in the next chunk, after its barrier)
+      __syncthreads();  // every read of this chunk's slots is done
+      if (keep) vstore<W>(v, before + __popcll(m & ((uint64_t{1} << lane) - 1)), x);
+      base += all;
+    }
+    cnt = base;
+    __syncthreads();
+  }
+  if (tid == 0) *o.count = cnt;
+}
+
 // Per merge: the children (vertex counts, first slots, offsets within the parent) and the
 // fallback's pairwise-round bookkeeping.
 struct MergeSmall {
@@ -178,13 +236,13 @@ __device__ __forceinline__ HPt child_vertex(const MergeArgs& a, const MergeSmall
   const NodeOut ci = node_out(a.in, W, row * a.in.npr + c0 + c);
   HPt p;
   p.i = ci.idx[k] + static_cast<int>(c * a.child_elems);
-  const DD S = dd_add(DD{sm.tot[2][c], sm.tot[3][c]}, DD{ci.shi[k], PR ? ci.slo[k] : 0.0});
+  const DD S = dd_add(DD{sm.tot[2][c], sm.tot[3][c]}, DD{ci.shi[k], PR ? lo_at(ci.slo, k) : 0.0});
   p.s = S.hi;
   p.sl = PR ? S.lo : 0.0;
   p.w = 0.0;
   p.wl = 0.0;
   if constexpr (W) {
-    const DD Wd = dd_add(DD{sm.tot[0][c], sm.tot[1][c]}, DD{ci.whi[k], PR ? ci.wlo[k] : 0.0});
+    const DD Wd = dd_add(DD{sm.tot[0][c], sm.tot[1][c]}, DD{ci.whi[k], PR ? lo_at(ci.wlo, k) : 0.0});
     p.w = Wd.hi;
     p.wl = PR ? Wd.lo : 0.0;
   }
@@ -226,12 +284,8 @@ __device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, MergeRounds&
   for (int s = tid; s < count; s += NT) {
     const HPt x = sget(v, s);
     pout.idx[s] = x.i;
-    pout.shi[s] = x.s;
-    pout.slo[s] = x.sl;
-    if constexpr (W) {
-      pout.whi[s] = x.w;
-      pout.wlo[s] = x.wl;
-    }
+    put_dd(pout.shi, pout.slo, s, x.s, x.sl);
+    if constexpr (W) put_dd(pout.whi, pout.wlo, s, x.w, x.wl);
   }
   if (tid == 0) *pout.count = count;
 }
@@ -794,21 +848,17 @@ __global__ __launch_bounds__(256) void keep_kernel(NodeLevel fin, NodeLevel kept
     if (q < maxc) {
       x.i = s.idx[q];
       x.s = s.shi[q];
-      x.sl = s.slo[q];
+      x.sl = lo_at(s.slo, q);
       if constexpr (W) {
         x.w = s.whi[q];
-        x.wl = s.wlo[q];
+        x.wl = lo_at(s.wlo, q);
       }
     }
     const int cnt = static_cast<int>(min<int64_t>(*s.count, maxc));
     if (q < cnt) {
       d.idx[q] = x.i;
-      d.shi[q] = x.s;
-      d.slo[q] = x.sl;
-      if constexpr (W) {
-        d.whi[q] = x.w;
-        d.wlo[q] = x.wl;
-      }
+      put_dd(d.shi, d.slo, q, x.s, x.sl);
+      if constexpr (W) put_dd(d.whi, d.wlo, q, x.w, x.wl);
     }
     if (chunk == 0) {
       if (threadIdx.x < 4) d.tot[threadIdx.x] = s.tot[threadIdx.x];
@@ -835,8 +885,9 @@ __global__ __launch_bounds__(256) void keep_kernel(NodeLevel fin, NodeLevel kept
 
 }  // namespace
 
-LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
+LongPlan long_plan(int64_t batch, int64_t n, bool weighted, bool lo) {
   LongPlan p{};
+  p.lo = lo;
   const int64_t tn = tile_elems(weighted);
   p.tiles_per_row = (n + tn - 1) / tn;
   // The longest span that still gives the span kernel about 2^17 lanes (two waves per SIMD),
@@ -916,22 +967,23 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted) {
   p.keep_level = p.levels <= 1 ? p.levels : std::max(1, p.levels - 2);
   p.slots = batch * p.npr[0] * (span0 + 1);
   p.off_store = off;
-  p.off_rank = p.off_store + align256(vertex_store_bytes(p.slots, weighted));
+  p.off_rank = p.off_store + align256(vertex_store_bytes(p.slots, weighted, lo));
   p.off_maxc = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
   p.bytes = p.off_maxc + align256(kMaxcBlocks * sizeof(int64_t));
   return p;
 }
 
-KeepPlan keep_plan(int64_t batch, int64_t n, bool weighted, int64_t maxc) {
+KeepPlan keep_plan(int64_t batch, int64_t n, bool weighted, bool lo, int64_t maxc) {
   KeepPlan k{};
+  k.lo = lo;
   k.batch = batch;
   k.maxc = maxc;
-  k.tiles = batch * long_plan(batch, n, weighted).tiles_per_row;
+  k.tiles = batch * long_plan(batch, n, weighted, lo).tiles_per_row;
   size_t off = 0;
   k.off_meta = off;
   off += align256(node_meta_bytes(batch));
   k.off_store = off;
-  off += align256(vertex_store_bytes(batch * maxc, weighted));
+  off += align256(vertex_store_bytes(batch * maxc, weighted, lo));
   k.off_tiles = off;
   off += align256(static_cast<size_t>(k.tiles) * sizeof(TileRec));
   k.bytes = off;
@@ -1016,6 +1068,14 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if ((e = report(l)) != hipSuccess) return e;
+  }
+  if (!p.lo && p.levels >= 1) {
+    // (float32 data: the final hulls convex in their stored values; span hulls, the final hulls
+    // of rows of one span, are exact and convex already)
+    if (W) repair_kernel<true><<<dim3(static_cast<unsigned>(t.batch)), dim3(kRepairThreads), 0, t.stream>>>(fin);
+    else repair_kernel<false><<<dim3(static_cast<unsigned>(t.batch)), dim3(kRepairThreads), 0, t.stream>>>(fin);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
   if (t.n <= kXpackMaxN) {
     // rows of one tile: records and fit together, whole rows a workgroup

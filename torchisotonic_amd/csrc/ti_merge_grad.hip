@@ -40,8 +40,8 @@ struct GradPlan {
 };
 
 // kept_maxc > 0: the final hulls come from a kept state, at most that many vertices a row
-GradPlan grad_plan(int64_t batch, int64_t n, bool weighted, int64_t kept_maxc) {
-  const LongPlan lp = long_plan(batch, n, weighted);
+GradPlan grad_plan(int64_t batch, int64_t n, bool weighted, bool lo, int64_t kept_maxc) {
+  const LongPlan lp = long_plan(batch, n, weighted, lo);
   GradPlan g{};
   g.tpr = lp.tiles_per_row;
   g.ngroups = (g.tpr + kScanTiles - 1) / kScanTiles;
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(256) void gscan_groups_kernel(GradKArgs a) {
 
 template <bool W>
 __device__ __forceinline__ DD vertex_w(const NodeOut& f, int r) {
-  if constexpr (W) return DD{f.whi[r], f.wlo[r]};
+  if constexpr (W) return DD{f.whi[r], lo_at(f.wlo, r)};
   else return DD{static_cast<double>(f.idx[r]), 0.0};
 }
 
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
       const double G = dd_diff(gb, ga);
       double dW, dS;
       dW = dd_diff(vertex_w<W>(fin, jb + 1), vertex_w<W>(fin, jb));
-      dS = dd_diff(DD{fin.shi[jb + 1], fin.slo[jb + 1]}, DD{fin.shi[jb], fin.slo[jb]});
+      dS = dd_diff(DD{fin.shi[jb + 1], lo_at(fin.slo, jb + 1)}, DD{fin.shi[jb], lo_at(fin.slo, jb)});
       const T mean = static_cast<T>(sgn * slope_div(dS, dW));
       double q = G / dW;
       if ((use_lo || use_hi) && !clip_passes(mean, use_lo, lo, use_hi, hi)) q = 0.0;
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
     } else {
       const int j = b - rowbase[r];
       const double dW = dd_diff(vertex_w<W>(fin, j + 1), vertex_w<W>(fin, j));
-      const double dS = dd_diff(DD{fin.shi[j + 1], fin.slo[j + 1]}, DD{fin.shi[j], fin.slo[j]});
+      const double dS = dd_diff(DD{fin.shi[j + 1], lo_at(fin.slo, j + 1)}, DD{fin.shi[j], lo_at(fin.slo, j)});
       mean = static_cast<T>(sgn * slope_div(dS, dW));
       q = G / dW;
       if ((use_lo || use_hi) && !clip_passes(mean, use_lo, lo, use_hi, hi)) q = 0.0;
@@ -602,14 +602,15 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
 
 }  // namespace
 
-size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted, int64_t kept_maxc) {
-  return grad_plan(batch, n, weighted, kept_maxc).bytes;
+size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted, bool lo, int64_t kept_maxc) {
+  return grad_plan(batch, n, weighted, lo, kept_maxc).bytes;
 }
 
 hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   const bool W = in.w != nullptr;
   const int64_t kmaxc = in.kept != nullptr ? in.kept_maxc : 0;
-  const GradPlan gpn = grad_plan(in.batch, in.n, W, kmaxc);
+  const bool lo = in.dtype == TI_F64;
+  const GradPlan gpn = grad_plan(in.batch, in.n, W, lo, kmaxc);
   char* base = static_cast<char*>(ws);
   const char* fbase = static_cast<const char*>(in.fwd_ws);
   GradKArgs a;
@@ -628,7 +629,7 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.lo = in.lo;
   a.hi = in.hi;
   if (in.kept != nullptr) {
-    const KeepPlan kp = keep_plan(in.batch, in.n, W, kmaxc);
+    const KeepPlan kp = keep_plan(in.batch, in.n, W, lo, kmaxc);
     a.hulls = kp.level(const_cast<void*>(in.kept));
     a.tiles = reinterpret_cast<const TileRec*>(static_cast<const char*>(in.kept) + kp.off_tiles);
   } else {

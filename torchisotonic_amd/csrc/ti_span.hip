@@ -158,20 +158,16 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // node arrays hold double-double sums; float32 data has no rounding errors to carry (lo = 0)
   auto node_put = [&](int q, const HPt& p) {
     o.idx[q] = p.i;
-    o.shi[q] = p.s;
-    o.slo[q] = p.sl;
-    if constexpr (W) {
-      o.whi[q] = p.w;
-      o.wlo[q] = p.wl;
-    }
+    put_dd(o.shi, o.slo, q, p.s, p.sl);
+    if constexpr (W) put_dd(o.whi, o.wlo, q, p.w, p.wl);
   };
   auto node_get = [&](int q) -> HPt {
     HPt p;
     p.i = o.idx[q];
     p.s = o.shi[q];
-    p.sl = PR ? o.slo[q] : 0.0;
+    p.sl = PR ? lo_at(o.slo, q) : 0.0;
     p.w = W ? o.whi[q] : 0.0;
-    p.wl = (W && PR) ? o.wlo[q] : 0.0;
+    p.wl = (W && PR) ? lo_at(o.wlo, q) : 0.0;
     return p;
   };
 
@@ -476,12 +472,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
       for (int q = lane; q < cnt; q += kSpanLanes) {
         const HPt x = q == 0 ? HPt{0, 0.0, 0.0, 0.0, 0.0} : rebase(sget(v, f + q));
         pout.idx[q] = x.i;
-        pout.shi[q] = x.s;
-        pout.slo[q] = x.sl;
-        if constexpr (W) {
-          pout.whi[q] = x.w;
-          pout.wlo[q] = x.wl;
-        }
+        put_dd(pout.shi, pout.slo, q, x.s, x.sl);
+        if constexpr (W) put_dd(pout.whi, pout.wlo, q, x.w, x.wl);
       }
       if (lane == 0) {
         const HPt e = rebase(sget(v, se[r]));  // the row's end point: its totals
@@ -502,12 +494,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   for (int k = lane; k < count; k += kSpanLanes) {
     const HPt x = sget(v, k);
     pout.idx[k] = x.i;
-    pout.shi[k] = x.s;
-    pout.slo[k] = x.sl;
-    if constexpr (W) {
-      pout.whi[k] = x.w;
-      pout.wlo[k] = x.wl;
-    }
+    put_dd(pout.shi, pout.slo, k, x.s, x.sl);
+    if constexpr (W) put_dd(pout.whi, pout.wlo, k, x.w, x.wl);
   }
   if (lane == nch - 1) {
     *pout.count = count;

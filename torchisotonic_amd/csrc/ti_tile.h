@@ -43,8 +43,10 @@ struct TileArgs {
 };
 
 // One node's hull: vertex indices relative to the node's first element, cumulative sums
-// (double-double) relative to the node's first point, the vertex count, a NaN flag and the node
-// totals (W hi, W lo, S hi, S lo).
+// relative to the node's first point, the vertex count, a NaN flag and the node totals (W hi,
+// W lo, S hi, S lo). Float64 data keeps the sums double-double; float32 data keeps them rounded
+// to float64 (slo, wlo null), which halves the store (the merges still work in double-double in
+// LDS, and the final hulls are made convex in the stored values: see repair_kernel).
 struct NodeOut {
   int* count;
   int* bad;
@@ -52,6 +54,18 @@ struct NodeOut {
   int* idx;
   double *shi, *slo, *whi, *wlo;
 };
+
+// The sums of vertex k of a node, whichever way they are stored.
+__device__ __forceinline__ double lo_at(const double* lo, int64_t k) { return lo != nullptr ? lo[k] : 0.0; }
+// Stores a double-double value: hi and lo, or, without a low array, their sum rounded once.
+__device__ __forceinline__ void put_dd(double* hi, double* lo, int64_t k, double h, double l) {
+  if (lo != nullptr) {
+    hi[k] = h;
+    lo[k] = l;
+  } else {
+    hi[k] = h + l;
+  }
+}
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -69,6 +83,7 @@ struct NodeLevel {
   int64_t npr0;   // spans per row
   int64_t r0;     // slots per span
   int64_t slots;  // slots of the store
+  bool lo;        // the store keeps low parts (float64 data)
 };
 
 __host__ __device__ inline size_t node_meta_bytes(int64_t K) {
@@ -76,9 +91,9 @@ __host__ __device__ inline size_t node_meta_bytes(int64_t K) {
   return align256(k * 4) * 2 + align256(k * 32);
 }
 
-__host__ __device__ inline size_t vertex_store_bytes(int64_t slots, bool weighted) {
+__host__ __device__ inline size_t vertex_store_bytes(int64_t slots, bool weighted, bool lo) {
   const size_t c = static_cast<size_t>(slots);
-  return align256(c * 4) + align256(c * 8) * (weighted ? 4 : 2);
+  return align256(c * 4) + align256(c * 8) * ((weighted ? 2 : 1) * (lo ? 2 : 1));
 }
 
 __host__ __device__ inline NodeOut node_out(const NodeLevel& L, bool weighted, int64_t k) {
@@ -97,14 +112,15 @@ __host__ __device__ inline NodeOut node_out(const NodeLevel& L, bool weighted, i
   q += align256(c * 4);
   o.shi = reinterpret_cast<double*>(q) + v0;
   q += align256(c * 8);
-  o.slo = reinterpret_cast<double*>(q) + v0;
-  q += align256(c * 8);
+  o.slo = o.whi = o.wlo = nullptr;
+  if (L.lo) {
+    o.slo = reinterpret_cast<double*>(q) + v0;
+    q += align256(c * 8);
+  }
   if (weighted) {
     o.whi = reinterpret_cast<double*>(q) + v0;
     q += align256(c * 8);
-    o.wlo = reinterpret_cast<double*>(q) + v0;
-  } else {
-    o.whi = o.wlo = nullptr;
+    if (L.lo) o.wlo = reinterpret_cast<double*>(q) + v0;
   }
   return o;
 }
@@ -283,14 +299,16 @@ struct LongPlan {
   int64_t slots;  // of the store: batch * npr[0] * (span0 + 1)
   size_t off_meta[kMaxLevels + 1], off_store, off_rank, off_maxc, bytes;
   bool weighted;
+  bool lo;  // the vertex store keeps low parts (float64 data)
 
   NodeLevel level(void* ws, int l) const {
     char* base = static_cast<char*>(ws);
-    return NodeLevel{base + off_meta[l], base + off_store, batch * npr[l], npr[l], spn[l], npr[0], span0 + 1, slots};
+    return NodeLevel{base + off_meta[l], base + off_store, batch * npr[l], npr[l], spn[l], npr[0], span0 + 1, slots, lo};
   }
 };
 
-LongPlan long_plan(int64_t batch, int64_t n, bool weighted);
+// lo: float64 data (its vertex store keeps double-double sums)
+LongPlan long_plan(int64_t batch, int64_t n, bool weighted, bool lo);
 hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
 
 // The part of a long-row forward's workspace that its backward reads, kept on its own
@@ -299,12 +317,13 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws);
 struct KeepPlan {
   int64_t batch, maxc, tiles;
   size_t off_meta, off_store, off_tiles, bytes;
+  bool lo;
   NodeLevel level(void* kept) const {
     char* b = static_cast<char*>(kept);
-    return NodeLevel{b + off_meta, b + off_store, batch, 1, 1, 1, maxc, batch * maxc};
+    return NodeLevel{b + off_meta, b + off_store, batch, 1, 1, 1, maxc, batch * maxc, lo};
   }
 };
-KeepPlan keep_plan(int64_t batch, int64_t n, bool weighted, int64_t maxc);
+KeepPlan keep_plan(int64_t batch, int64_t n, bool weighted, bool lo, int64_t maxc);
 hipError_t long_keep(const LongPlan& p, const void* ws, const KeepPlan& k, void* kept, hipStream_t stream);
 
 // Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
@@ -333,7 +352,7 @@ struct LongGradArgs {
 };
 // kept_maxc > 0: the workspace of a backward from a kept state (its vertex prefixes sized for
 // hulls of that many vertices instead of a row's every slot)
-size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted, int64_t kept_maxc = 0);
+size_t long_grad_bytes(int64_t batch, int64_t n, bool weighted, bool lo, int64_t kept_maxc = 0);
 hipError_t long_grad(const LongGradArgs& a, const LongPlan& p, void* ws);
 
 inline int64_t tile_elems(bool weighted) { return weighted ? TileCfg<true>::kN : TileCfg<false>::kN; }
