@@ -156,6 +156,53 @@ def test_bwd_argument_errors() -> None:
         assert b"forward's workspace" in lib.ti_last_error()
 
 
+def test_kept_state_argument_errors() -> None:
+    # ti_keep and ti_bwd_kept refuse what they cannot use before any launch
+    lib = _ext.load()
+    n = 100_000
+    ws = ctypes.c_size_t(0)
+    assert lib.ti_fwd_workspace(2, n, _ext.F32, 1, ctypes.byref(ws)) == 0
+    kb = ctypes.c_size_t(0)
+    assert lib.ti_keep_bytes(2, n, _ext.F32, 1, 500, ctypes.byref(kb)) == 0
+
+    def keep(fws, fwsb, kept, keptb, mv=500, batch=2, nn=n):
+        return lib.ti_keep(fws, fwsb, kept, keptb, batch, nn, _ext.F32, 1, mv, None)
+
+    # no forward workspace, or one too small
+    assert keep(None, 0, 256, kb.value) == 4
+    assert keep(256, ws.value - 1, 256, kb.value) == 4
+    assert b"forward's workspace" in lib.ti_last_error()
+    # a kept buffer too small
+    assert keep(256, ws.value, 256, kb.value - 1) == 4
+    # unaligned
+    assert keep(256, ws.value, 264, kb.value) == 1
+    # a bound no hull of these rows can have
+    assert keep(256, ws.value, 256, kb.value, mv=0) == 1
+    assert keep(256, ws.value, 256, kb.value, mv=n + 2) == 1
+    assert b"max_vertices" in lib.ti_last_error()
+    # rows of at most 32 elements keep nothing
+    assert keep(None, 0, None, 0, mv=0, nn=32) == 0
+
+    def bwd_kept(kept, keptb, mv, g=2, gy=3, batch=2, nn=n, ws_=None, wsb=0):
+        # (weighted, as the kept state above: w given)
+        return lib.ti_bwd_kept(1, kept, keptb, mv, g, 5, None, gy, None, batch, nn, _ext.F32,
+                               _ext.INCREASING, 0.0, 0.0, ws_, wsb, None)
+
+    bws = ctypes.c_size_t(0)
+    assert lib.ti_bwd_kept_workspace(2, n, _ext.F32, 1, 500, ctypes.byref(bws)) == 0
+    assert bws.value > 0
+    assert bwd_kept(None, 0, 500, ws_=256, wsb=bws.value) == 4
+    assert b"kept state" in lib.ti_last_error()
+    assert bwd_kept(256, kb.value - 1, 500, ws_=256, wsb=bws.value) == 4
+    assert b"kept state" in lib.ti_last_error()
+    assert bwd_kept(256, kb.value, 0, ws_=256, wsb=bws.value) == 1
+    assert b"max_vertices" in lib.ti_last_error()
+    assert bwd_kept(256, kb.value, 500, ws_=None, wsb=0) == 4  # (no backward workspace)
+    assert b"workspace of" in lib.ti_last_error()
+    # rows of at most 32 elements: the short-row backward, no kept state needed
+    assert bwd_kept(None, 0, 0, gy=None, nn=16) == 0
+
+
 def test_grad_argument_errors() -> None:
     lib = _ext.load()
 
