@@ -17,6 +17,7 @@
 //                  element the slope of its edge with the clamp fused, and the start bits. y is
 //                  not read again.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "ti_common.h"
@@ -145,24 +146,46 @@ __device__ VArr dvarr_of(const NodeOut& o) { return VArr{o.idx, o.shi, o.slo, o.
 // Float32 data keeps its hull sums rounded to float64 in the vertex store (NodeOut). Rounded one
 // by one, a hull that the double-double merges found convex can turn slightly non-convex in the
 // stored values where points are nearly collinear, and the fit (its slopes) would step down
-// there. Each final hull is made convex in the stored values: a vertex on or above the chord
-// between its neighbours is no vertex of the lower hull of the stored points, so every such
-// vertex goes at once, and the row is tested again (most rows pass the first test). One
-// workgroup per row; the removal compacts the row in place a chunk at a time, the chunk's
-// original vertices (and its neighbours outside it) staged in LDS before any of its slots is
-// written.
+// there. Each final hull is made convex in the stored values, in two launches:
+//
+//   convex_check_kernel  `chunks` workgroups a row test every vertex against its neighbours; a
+//                        vertex on or above the chord between them marks its row (flag = the
+//                        call's epoch, so the flags need no clearing between calls);
+//   repair_kernel        one workgroup a marked row: a vertex on or above the chord between its
+//                        neighbours is no vertex of the lower hull of the stored points, so every
+//                        such vertex goes at once, and the row is tested again. The removal
+//                        compacts the row in place a chunk at a time, the chunk's original
+//                        vertices (and its neighbours outside it) staged in LDS before any of its
+//                        slots is written.
 constexpr int kRepairThreads = 256;
 
 template <bool W>
-__global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin) {
+__global__ __launch_bounds__(kRepairThreads) void convex_check_kernel(NodeLevel fin, int chunks, unsigned epoch,
+                                                                      unsigned* __restrict__ flag) {
+  const int64_t row = blockIdx.x / chunks;
+  const int c = static_cast<int>(blockIdx.x - row * chunks);
+  const NodeOut o = node_out(fin, W, row);
+  if (*o.bad != 0) return;  // (a NaN row's fit is NaN whatever its hull)
+  const int cnt = *o.count;
+  const VArr v = dvarr_of(o);
+  bool found = false;
+  for (int i = 1 + c * kRepairThreads + static_cast<int>(threadIdx.x); i < cnt - 1; i += chunks * kRepairThreads)
+    found |= vpools<W>(vload<W>(v, i - 1), vload<W>(v, i), vload<W>(v, i + 1));
+  if (found) flag[row] = epoch;
+}
+
+template <bool W>
+__global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, unsigned epoch,
+                                                                const unsigned* __restrict__ flag) {
   __shared__ int any;
   __shared__ int wcount[kRepairThreads / kWave];
   __shared__ VPt tile[kRepairThreads + 2];
   __shared__ VPt prev;  // the original vertex before the chunk
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int64_t row = blockIdx.x;
+  if (flag[row] != epoch) return;  // (convex already)
   const NodeOut o = node_out(fin, W, row);
-  if (*o.bad != 0) return;  // (a NaN row's fit is NaN whatever its hull)
+  if (*o.bad != 0) return;
   const VArr v = dvarr_of(o);
   int cnt = *o.count;
   for (int pass = 0; pass < 64; ++pass) {
@@ -969,7 +992,8 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted, bool lo) {
   p.off_store = off;
   p.off_rank = p.off_store + align256(vertex_store_bytes(p.slots, weighted, lo));
   p.off_maxc = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
-  p.bytes = p.off_maxc + align256(kMaxcBlocks * sizeof(int64_t));
+  p.off_rflag = p.off_maxc + align256(kMaxcBlocks * sizeof(int64_t));
+  p.bytes = p.off_rflag + align256(static_cast<size_t>(batch) * sizeof(unsigned));
   return p;
 }
 
@@ -1071,9 +1095,20 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   }
   if (!p.lo && p.levels >= 1) {
     // (float32 data: the final hulls convex in their stored values; span hulls, the final hulls
-    // of rows of one span, are exact and convex already)
-    if (W) repair_kernel<true><<<dim3(static_cast<unsigned>(t.batch)), dim3(kRepairThreads), 0, t.stream>>>(fin);
-    else repair_kernel<false><<<dim3(static_cast<unsigned>(t.batch)), dim3(kRepairThreads), 0, t.stream>>>(fin);
+    // of rows of one span, are exact and convex already). Enough check workgroups a row for a
+    // hull of every element (4096 vertices each), at most 256.
+    static std::atomic<unsigned> calls{0};
+    const unsigned epoch = calls.fetch_add(1, std::memory_order_relaxed) * 2u + 1u;  // (odd: never 0)
+    const int chunks = static_cast<int>(std::min<int64_t>(256, std::max<int64_t>(1, (t.n + 4096) / 4096)));
+    unsigned* flag = reinterpret_cast<unsigned*>(base + p.off_rflag);
+    const dim3 cgrid(static_cast<unsigned>(t.batch * chunks)), rgrid(static_cast<unsigned>(t.batch));
+    if (W) {
+      convex_check_kernel<true><<<cgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, chunks, epoch, flag);
+      repair_kernel<true><<<rgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, epoch, flag);
+    } else {
+      convex_check_kernel<false><<<cgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, chunks, epoch, flag);
+      repair_kernel<false><<<rgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, epoch, flag);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -297,7 +297,7 @@ struct LongPlan {
   int64_t batch;
   int64_t npr[kMaxLevels + 1], spn[kMaxLevels + 1], span[kMaxLevels + 1];
   int64_t slots;  // of the store: batch * npr[0] * (span0 + 1)
-  size_t off_meta[kMaxLevels + 1], off_store, off_rank, off_maxc, bytes;
+  size_t off_meta[kMaxLevels + 1], off_store, off_rank, off_maxc, off_rflag, bytes;
   bool weighted;
   bool lo;  // the vertex store keeps low parts (float64 data)
 
