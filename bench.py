@@ -311,9 +311,17 @@ def bench_next(steps: int, warmup: int) -> dict:
     xp, fp = torchisotonic_amd.calibration_fit(scores, labels)
     q = scores.double()
     interp_out = torch.empty_like(q)
-    ilaunch = lambda: lib.ti_interp(q.data_ptr(), xp.data_ptr(), fp.data_ptr(), interp_out.data_ptr(), m, xp.numel(), _ext.F64, s)  # noqa: E731
-    assert ilaunch() == 0
+    index = _ext.interp_index(xp)
+    xlaunch = lambda: lib.ti_interp_index(xp.data_ptr(), xp.numel(), _ext.F64, index.data_ptr(), index.numel(), s)  # noqa: E731
+    ilaunch = lambda: lib.ti_interp_indexed(q.data_ptr(), xp.data_ptr(), fp.data_ptr(), index.data_ptr(), index.numel(),  # noqa: E731
+                                            interp_out.data_ptr(), m, xp.numel(), _ext.F64, s)
+    flaunch = lambda: lib.ti_interp(q.data_ptr(), xp.data_ptr(), fp.data_ptr(), interp_out.data_ptr(), m, xp.numel(), _ext.F64, s)  # noqa: E731
+    assert xlaunch() == 0 and ilaunch() == 0 and flaunch() == 0
     k = kernel_ms(ilaunch, 50)
+    kx = kernel_ms(xlaunch, 50)
+    kf = kernel_ms(flaunch, 20)
+    cal = torchisotonic_amd.IsotonicCalibrator()
+    cal.xp, cal.fp, cal.index = xp, fp, index
 
     def torch_interp() -> torch.Tensor:  # the reference's tensor formula (calibrate.py:163-168)
         i = torch.searchsorted(xp, q).clamp(1, xp.numel() - 1)
@@ -325,8 +333,11 @@ def bench_next(steps: int, warmup: int) -> dict:
         "knots": xp.numel(),
         "fit_ms": 1e3 * t_fit,
         "predict": rate(m, timed_calls(lambda: torchisotonic_amd.calibration_predict(q, xp, fp), steps, warmup), 16),
+        "predict_kept_index": rate(m, timed_calls(lambda: cal.predict(q), steps, warmup), 16),
         "interp_kernel_ms": k,
         "interp_kernel_pct_roofline": 100 * 16 * m / (k * 1e-3) / 1e9 / PEAK_GBPS,
+        "interp_index_kernel_ms": kx,
+        "interp_full_search_kernel_ms": kf,
         "interp_torch_formula_ms": 1e3 * timed_calls(torch_interp, steps, warmup),
     }
     return res

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 4
+#define TI_ABI_VERSION 5
 
 /* dtype codes */
 #define TI_F32 0
@@ -283,6 +283,25 @@ int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* 
  */
 int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m,
               int dtype, void* stream);
+
+/* The knot index: ti_interp's output bit for bit with each query's search narrowed from all m
+ * knots (~log2 m dependent reads, most of them misses) to one bucket of about four. Buckets of
+ * equal width cover [xp[0], xp[m-1]] (B = ceil(m / 4)); first[b] is the first knot whose bucket
+ * is b or later, so the first knot at or above x lies between first[b] and first[b+1] for x's
+ * bucket b (bucket() is monotone). Knots whose ends are not finite, or all equal, give an index
+ * under which every query searches all knots. Same semantics as ti_interp (reference
+ * examples/ctr_calibration/calibrate.py:163-168); an index depends on xp only, so one built
+ * after a fit serves every later call with those knots.
+ *
+ * ti_interp_index_bytes: the index's size for m knots (m < 2^32).
+ * ti_interp_index: build it from xp (m knots, ascending) into `index` (256-byte aligned).
+ * ti_interp_indexed: ti_interp through an index built from the same xp. An index of other knots
+ *   gives wrong values but reads nothing outside x, xp, fp and the index's index_bytes. */
+int ti_interp_index_bytes(int64_t m, int dtype, size_t* bytes);
+int ti_interp_index(const void* xp, int64_t m, int dtype, void* index, size_t index_bytes,
+                    void* stream);
+int ti_interp_indexed(const void* x, const void* xp, const void* fp, const void* index,
+                      size_t index_bytes, void* out, int64_t n, int64_t m, int dtype, void* stream);
 
 /* Test hook: the starts bit array of a [batch, n] set as bytes (0/1), row-major - the
  * reference's bool starts tensor (reference tests/test_cuda.py:176 reads it). */

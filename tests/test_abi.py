@@ -230,6 +230,35 @@ def test_grad_argument_errors() -> None:
     assert grad(None, None, None, None, None, None, None, 0, 16) == 0
 
 
+def test_interp_index_sizes_and_argument_errors() -> None:
+    lib = _ext.load()
+    size = ctypes.c_size_t(0)
+    # a 256-byte header, then one 4-byte entry a bucket of four knots (and one more), rounded up
+    assert lib.ti_interp_index_bytes(1, _ext.F64, ctypes.byref(size)) == 0 and size.value == 512
+    assert lib.ti_interp_index_bytes(6_000_000, _ext.F64, ctypes.byref(size)) == 0
+    assert 256 + 4 * 1_500_001 <= size.value < 256 + 4 * 1_500_001 + 256 and size.value % 256 == 0
+    assert lib.ti_interp_index_bytes(6_000_000, _ext.F32, ctypes.byref(size)) == 0  # the same for float32
+    assert lib.ti_interp_index_bytes(0, _ext.F64, ctypes.byref(size)) == 1
+    assert lib.ti_interp_index_bytes(1 << 32, _ext.F64, ctypes.byref(size)) == 3
+    assert lib.ti_interp_index_bytes(10, 7, ctypes.byref(size)) == 2
+    assert lib.ti_interp_index_bytes(10, _ext.F64, None) == 1
+    assert lib.ti_interp_index_bytes(1000, _ext.F64, ctypes.byref(size)) == 0
+    need = size.value
+    # build: missing xp or index, an index too small, a misaligned index
+    assert lib.ti_interp_index(None, 1000, _ext.F64, 256, need, None) == 1
+    assert lib.ti_interp_index(8, 1000, _ext.F64, None, need, None) == 1
+    assert lib.ti_interp_index(8, 1000, _ext.F64, 256, need - 1, None) == 4
+    assert b"need" in lib.ti_last_error()
+    assert lib.ti_interp_index(8, 1000, _ext.F64, 264, need, None) == 1
+    # interpolate: the same index checks, then the buffers; no queries is no work
+    assert lib.ti_interp_indexed(8, 16, 24, 256, need - 1, 32, 10, 1000, _ext.F64, None) == 4
+    assert lib.ti_interp_indexed(8, 16, 24, None, need, 32, 10, 1000, _ext.F64, None) == 1
+    assert lib.ti_interp_indexed(8, 16, 24, 264, need, 32, 10, 1000, _ext.F64, None) == 1
+    assert lib.ti_interp_indexed(None, 16, 24, 256, need, 32, 10, 1000, _ext.F64, None) == 1
+    assert lib.ti_interp_indexed(8, 16, 24, 256, need, 32, -1, 1000, _ext.F64, None) == 1
+    assert lib.ti_interp_indexed(None, None, None, 256, need, None, 0, 1000, _ext.F64, None) == 0
+
+
 def test_errors_are_per_thread() -> None:
     import threading
 

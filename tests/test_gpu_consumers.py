@@ -146,6 +146,82 @@ def test_interp_kernel_is_the_reference_formula(dtype: torch.dtype) -> None:
     assert one[:2].tolist() == [2.0, 2.0] and torch.isnan(one[2])
 
 
+def _plain_interp(x: torch.Tensor, xp: torch.Tensor, fp: torch.Tensor) -> torch.Tensor:
+    # ti_interp: the full binary search over all knots, no index
+    out = torch.empty_like(x)
+    code = _ext.F32 if x.dtype == torch.float32 else _ext.F64
+    rc = _ext.load().ti_interp(x.data_ptr(), xp.data_ptr(), fp.data_ptr(), out.data_ptr(), x.numel(), xp.numel(),
+                               code, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    return out
+
+
+def _knot_sets(rng: np.random.Generator) -> dict[str, np.ndarray]:
+    logit = rng.normal(-1.2, 1.5, 400_000)
+    scores = np.unique((1 / (1 + np.exp(-logit))).astype(np.float32)).astype(np.float64)
+    return {
+        # float32 scores of a CTR model: dense in the middle, sparse in the tails
+        "scores": scores,
+        # uniform, and one dense cluster beside a far point (most knots in one bucket: searched)
+        "uniform": np.sort(rng.random(300_000)),
+        "cluster": np.r_[np.sort(rng.random(200_000) * 1e-6), 1e3],
+        # repeated knots (non-decreasing), a few knots, two knots
+        "repeats": np.sort(np.round(rng.normal(0, 1, 50_000), 2)),
+        "few": np.sort(rng.normal(0, 1, 37)),
+        "two": np.array([-1.0, 2.0]),
+        # ends that give the index no scale: infinite or NaN last knot, all knots equal
+        "inf_end": np.r_[np.sort(rng.random(5000)), np.inf],
+        "nan_end": np.r_[np.sort(rng.random(5000)), np.nan],
+        "equal": np.full(1000, 0.25),
+    }
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_interp_index_gives_the_full_search_bit_for_bit(dtype: torch.dtype) -> None:
+    # ti_interp_indexed against ti_interp on knot sets that stress the buckets (dense, sparse,
+    # clustered, repeated, degenerate ends), at queries on, between and beyond the knots
+    rng = np.random.default_rng(17)
+    for name, xp_np in _knot_sets(rng).items():
+        say(f"interp index {name} {dtype}")
+        m = xp_np.size
+        fin = xp_np[np.isfinite(xp_np)]
+        lo, hi = fin.min(), fin.max()
+        q = np.concatenate([
+            rng.uniform(lo - 0.1 * (hi - lo + 1), hi + 0.1 * (hi - lo + 1), 200_000),
+            xp_np, np.nextafter(fin, np.inf), np.nextafter(fin, -np.inf),
+            [np.nan, -np.inf, np.inf, 0.0, -0.0, lo, hi],
+        ])
+        xp = torch.from_numpy(xp_np).to(dtype).cuda()
+        fp = torch.cumsum(torch.rand(m, dtype=torch.float64, generator=torch.Generator().manual_seed(m)), 0)
+        fp = fp.to(dtype).cuda()
+        x = torch.from_numpy(q).to(dtype).cuda()
+        want = _plain_interp(x, xp, fp)
+        index = _ext.interp_index(xp)
+        got = _ext.interp(x, xp, fp, index)
+        torch.cuda.synchronize()
+        assert torch.equal(got.isnan(), want.isnan()), name
+        ok = ~want.isnan()
+        assert torch.equal(got[ok], want[ok]), name
+    # one index serves every later call; a smaller second call through the same index
+    xp = torch.from_numpy(np.sort(rng.random(100_000))).to(dtype).cuda()
+    fp = torch.rand(100_000, dtype=torch.float64).to(dtype).cuda()
+    index = _ext.interp_index(xp)
+    for n in (300_000, 1000):
+        x = torch.rand(n, dtype=torch.float64).to(dtype).cuda()
+        assert torch.equal(_ext.interp(x, xp, fp, index), _plain_interp(x, xp, fp))
+
+
+def test_calibrator_keeps_its_knot_index() -> None:
+    say("calibrator knot index")
+    rng = np.random.default_rng(21)
+    s = rng.random(100_000)
+    y = (rng.random(100_000) < s).astype(np.float64)
+    cal = IsotonicCalibrator().fit(torch.from_numpy(s).cuda(), torch.from_numpy(y).cuda())
+    assert cal.index is not None and cal.index.dtype == torch.uint8
+    q = torch.from_numpy(rng.uniform(-0.5, 1.5, 50_000)).cuda()
+    assert torch.equal(cal.predict(q), _plain_interp(q, cal.xp, cal.fp))
+
+
 def test_calibration_offsets_fit_segments_at_once() -> None:
     # the reference's per-segment calibration: one fit, segments kept apart by offsets
     rng = np.random.default_rng(6)

@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -53,6 +53,9 @@ SYMBOLS = (
     "ti_grad_workspace",
     "ti_grad",
     "ti_interp",
+    "ti_interp_index_bytes",
+    "ti_interp_index",
+    "ti_interp_indexed",
     "ti_starts_to_bool",
 )
 
@@ -107,6 +110,12 @@ def load() -> ctypes.CDLL:
     lib.ti_grad.argtypes = [_vp] * 7 + [_i64, _i64, _int, _vp, _sz, _vp]
     lib.ti_interp.restype = _int
     lib.ti_interp.argtypes = [_vp] * 4 + [_i64, _i64, _int, _vp]
+    lib.ti_interp_index_bytes.restype = _int
+    lib.ti_interp_index_bytes.argtypes = [_i64, _int, ctypes.POINTER(_sz)]
+    lib.ti_interp_index.restype = _int
+    lib.ti_interp_index.argtypes = [_vp, _i64, _int, _vp, _sz, _vp]
+    lib.ti_interp_indexed.restype = _int
+    lib.ti_interp_indexed.argtypes = [_vp] * 4 + [_sz, _vp, _i64, _i64, _int, _vp]
     lib.ti_starts_to_bool.restype = _int
     lib.ti_starts_to_bool.argtypes = [_vp, _vp, _i64, _i64, _vp]
     got = lib.ti_abi_version()
@@ -340,10 +349,31 @@ def grad(
     return gy, gw
 
 
-def interp(x: Tensor, xp: Tensor, fp: Tensor) -> Tensor:
-    """Piecewise-linear interpolation of the knots (xp, fp) at x (one kernel, ti_interp): the
-    reference calibration example's interp (reference examples/ctr_calibration/calibrate.py:
-    163-168) bit for bit. x of any shape; xp, fp 1-D of one length, xp ascending."""
+def interp_index(xp: Tensor) -> Tensor:
+    """The knot index of ``xp`` (1-D, ascending, on the GPU; ti_interp_index): a uint8 tensor
+    that ``interp`` takes to narrow each query's search to about four knots. It depends on
+    ``xp`` only (its values and dtype), so one built after a fit serves every later call."""
+    _on_gpu(xp, "xp")
+    if xp.dim() != 1 or xp.numel() == 0:
+        raise RuntimeError("torchisotonic_amd.interp_index: xp must be 1-D and non-empty")
+    dtype = _dtype_code(xp)
+    xpc = xp.contiguous()
+    nbytes = _sz()
+    lib = load()
+    _check(lib.ti_interp_index_bytes(xpc.numel(), dtype, ctypes.byref(nbytes)), "interp_index")
+    index = torch.empty(nbytes.value, dtype=torch.uint8, device=xp.device)
+    with _on_device(xp.device):
+        rc = lib.ti_interp_index(_ptr(xpc), xpc.numel(), dtype, _ptr(index), index.numel(), _stream(xpc))
+    _check(rc, "interp_index")
+    return index
+
+
+def interp(x: Tensor, xp: Tensor, fp: Tensor, index: Tensor | None = None) -> Tensor:
+    """Piecewise-linear interpolation of the knots (xp, fp) at x: the reference calibration
+    example's interp (reference examples/ctr_calibration/calibrate.py:163-168) bit for bit.
+    x of any shape; xp, fp 1-D of one length, xp ascending. Runs through a knot index
+    (``interp_index(xp)``, built here when not given; ti_interp_indexed), whose output is
+    ti_interp's bit for bit."""
     _on_gpu(x, "x")
     if xp.dim() != 1 or fp.shape != xp.shape or xp.numel() == 0:
         raise RuntimeError("torchisotonic_amd.interp: xp and fp must be 1-D, non-empty and of one length")
@@ -351,9 +381,14 @@ def interp(x: Tensor, xp: Tensor, fp: Tensor) -> Tensor:
     xc = x.contiguous()
     xpc = xp.to(device=x.device, dtype=x.dtype).contiguous()
     fpc = fp.to(device=x.device, dtype=x.dtype).contiguous()
+    if index is None:
+        index = interp_index(xpc)
+    elif index.dtype != torch.uint8 or index.dim() != 1 or index.device != x.device:
+        raise RuntimeError("torchisotonic_amd.interp: index must be interp_index's uint8 tensor on x's device")
     out = torch.empty_like(xc)
     with _on_device(x.device):
-        rc = load().ti_interp(_ptr(xc), _ptr(xpc), _ptr(fpc), _ptr(out), xc.numel(), xpc.numel(), dtype, _stream(xc))
+        rc = load().ti_interp_indexed(_ptr(xc), _ptr(xpc), _ptr(fpc), _ptr(index), index.numel(), _ptr(out),
+                                      xc.numel(), xpc.numel(), dtype, _stream(xc))
     _check(rc, "interp")
     return out
 

@@ -12,9 +12,11 @@ calibrate.py:163-187, README.md:42-57):
   and subtracted after: segments placed far enough apart never pool across, so one fit serves
   many segments (the reference's per-segment calibration, calibrate.py:171-187).
 - ``calibration_predict(x, xp, fp)``: piecewise-linear interpolation through the knots,
-  constant beyond the ends (np.interp's semantics), in one HIP kernel (``ti_interp``).
+  constant beyond the ends (np.interp's semantics), in one HIP kernel (``ti_interp_indexed``)
+  through a knot index that narrows each query's search to about four knots.
 
-``IsotonicCalibrator`` wraps both, with sklearn's ``y_min`` / ``y_max`` clip and direction.
+``IsotonicCalibrator`` wraps both, with sklearn's ``y_min`` / ``y_max`` clip and direction; it
+builds the knot index once, after the fit, for all later predictions.
 Sums run in float64 whatever the input dtype (the reference casts its scores to float64).
 """
 
@@ -85,11 +87,12 @@ def calibration_fit(
     return xp, fit
 
 
-def calibration_predict(x: Tensor, xp: Tensor, fp: Tensor) -> Tensor:
+def calibration_predict(x: Tensor, xp: Tensor, fp: Tensor, index: Tensor | None = None) -> Tensor:
     """Calibrated values at ``x``: the piecewise-linear interpolation through ``(xp, fp)``,
     constant beyond the ends (reference calibrate.py:163-168, np.interp's semantics), computed
-    in float64 and returned as float64."""
-    return _ext.interp(x.to(torch.float64), xp.to(torch.float64), fp.to(torch.float64))
+    in float64 and returned as float64. ``index``: the knot index of the float64 ``xp``
+    (``torchisotonic_amd._ext.interp_index``), built here when not given."""
+    return _ext.interp(x.to(torch.float64), xp.to(torch.float64), fp.to(torch.float64), index)
 
 
 class IsotonicCalibrator:
@@ -102,16 +105,18 @@ class IsotonicCalibrator:
         self.y_max = y_max
         self.xp: Tensor | None = None
         self.fp: Tensor | None = None
+        self.index: Tensor | None = None
 
     def fit(self, scores: Tensor, labels: Tensor, weight: Tensor | None = None) -> "IsotonicCalibrator":
         self.xp, self.fp = calibration_fit(
             scores, labels, weight, increasing=self.increasing, y_min=self.y_min, y_max=self.y_max
         )
+        self.index = _ext.interp_index(self.xp)
         return self
 
     def predict(self, scores: Tensor) -> Tensor:
         if self.xp is None or self.fp is None:
             raise RuntimeError("IsotonicCalibrator: call fit first")
-        return calibration_predict(scores, self.xp, self.fp)
+        return calibration_predict(scores, self.xp, self.fp, self.index)
 
     __call__ = predict

@@ -407,6 +407,40 @@ int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t 
   return launched(ti::interp(x, xp, fp, out, n, m, dtype, static_cast<hipStream_t>(stream)), "interp");
 }
 
+int ti_interp_index_bytes(int64_t m, int dtype, size_t* bytes) {
+  if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
+  if (bytes == nullptr) return fail(TI_EINVAL, "null pointer");
+  if (m < 1) return fail(TI_EINVAL, "need m >= 1 knots, got %lld", (long long)m);
+  if (m >= (int64_t{1} << 32)) return fail(TI_ESIZE, "%lld knots exceed the index's limit of 2^32 - 1", (long long)m);
+  *bytes = ti::interp_index_bytes(m);
+  return ok();
+}
+
+int ti_interp_index(const void* xp, int64_t m, int dtype, void* index, size_t index_bytes, void* stream) {
+  size_t need = 0;
+  if (int rc = ti_interp_index_bytes(m, dtype, &need)) return rc;
+  if (xp == nullptr || index == nullptr) return fail(TI_EINVAL, "null pointer");
+  if (index_bytes < need)
+    return fail(TI_EWORKSPACE, "index of %zu bytes, need %zu", index_bytes, need);
+  if ((reinterpret_cast<uintptr_t>(index) & 255) != 0) return fail(TI_EINVAL, "index must be 256-byte aligned");
+  return launched(ti::interp_index(xp, m, dtype, index, static_cast<hipStream_t>(stream)), "interp index");
+}
+
+int ti_interp_indexed(const void* x, const void* xp, const void* fp, const void* index, size_t index_bytes,
+                      void* out, int64_t n, int64_t m, int dtype, void* stream) {
+  size_t need = 0;
+  if (int rc = ti_interp_index_bytes(m, dtype, &need)) return rc;
+  if (n < 0) return fail(TI_EINVAL, "need n >= 0, got %lld", (long long)n);
+  if (index == nullptr) return fail(TI_EINVAL, "null pointer");
+  if (index_bytes < need)
+    return fail(TI_EWORKSPACE, "index of %zu bytes, need %zu", index_bytes, need);
+  if ((reinterpret_cast<uintptr_t>(index) & 255) != 0) return fail(TI_EINVAL, "index must be 256-byte aligned");
+  if (n == 0) return ok();
+  if (x == nullptr || xp == nullptr || fp == nullptr || out == nullptr) return fail(TI_EINVAL, "null pointer");
+  return launched(ti::interp_indexed(x, xp, fp, index, index_bytes, out, n, m, dtype, static_cast<hipStream_t>(stream)),
+                  "interp");
+}
+
 int ti_starts_to_bool(const uint32_t* starts, uint8_t* out, int64_t batch, int64_t n, void* stream) {
   if (batch < 0 || n < 0) return fail(TI_EINVAL, "negative size");
   if (batch == 0 || n == 0) return ok();

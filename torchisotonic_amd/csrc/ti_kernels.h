@@ -41,6 +41,12 @@ struct ShortGradArgs {
 // Calibration: piecewise-linear interpolation of (xp, fp) (m knots, xp sorted) at n points.
 hipError_t interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m, int dtype,
                   hipStream_t stream);
+// The knot index that narrows each query's search to a bucket of about four knots: its size
+// for m knots, its build from xp, and interp through it (the same output bit for bit).
+size_t interp_index_bytes(int64_t m);
+hipError_t interp_index(const void* xp, int64_t m, int dtype, void* index, hipStream_t stream);
+hipError_t interp_indexed(const void* x, const void* xp, const void* fp, const void* index, size_t index_bytes,
+                          void* out, int64_t n, int64_t m, int dtype, hipStream_t stream);
 
 // Ragged rows of at most max_len (<= kShortMax) elements: row r is y[offsets[r], offsets[r + 1]).
 struct RaggedArgs {
