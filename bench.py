@@ -273,19 +273,39 @@ def bench_next(steps: int, warmup: int) -> dict:
     def fb() -> None:
         torch.autograd.grad(torchisotonic_amd.isotonic_ragged(pr, off, increasing=False), pr, g)
 
+    # with the rows' length bound (the padded length, 16) the fit starts before the plan's wait
+    fwd16 = lambda: torchisotonic_amd.isotonic_ragged(packed, off, increasing=False, max_len=n)  # noqa: E731
+
+    def fb16() -> None:
+        torch.autograd.grad(torchisotonic_amd.isotonic_ragged(pr, off, increasing=False, max_len=n), pr, g)
+
     lib = _ext.load()
     out = torch.empty_like(packed)
     bits = torch.zeros((elems + 31) // 32, dtype=torch.int32, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
-    raw = lambda: lib.ti_fwd_ragged(packed.data_ptr(), None, out.data_ptr(), None, None, off.data_ptr(), b, n, 0, 0, 0.0, 0.0, s)  # noqa: E731
+    raw = lambda: lib.ti_fwd_ragged(packed.data_ptr(), None, out.data_ptr(), None, None, off.data_ptr(), b, elems, n, 0, 0, 0.0, 0.0, s)  # noqa: E731
     assert raw() == 0
+    # the backward's kernel, from the bits of a forward that wrote them
+    gy = torch.empty_like(packed)
+    assert lib.ti_fwd_ragged(packed.data_ptr(), None, out.data_ptr(), bits.data_ptr(), None, off.data_ptr(), b, elems, n, _ext.F32, 0, 0.0, 0.0, s) == 0
+    rawb = lambda: lib.ti_bwd_ragged(bits.data_ptr(), g.data_ptr(), None, None, gy.data_ptr(), None, off.data_ptr(), b, elems, n, _ext.F32, 0, 0.0, 0.0, s)  # noqa: E731
+    assert rawb() == 0
+    plan = torch.zeros(4, dtype=torch.int64, device="cuda")  # (repeated plans fold into it: a timing only)
+    rawp = lambda: lib.ti_ragged_plan(off.data_ptr(), b, elems, plan.data_ptr(), s)  # noqa: E731
+    assert rawp() == 0
     res["c2_ragged"] = {
         "elems": elems,
         "fwd": rate(elems, timed_calls(fwd, steps, warmup), 8),
         "fwd_bwd": rate(elems, timed_calls(fb, steps, warmup), 16),
-        "kernel_ms": {"ragged_fit_kernel<float,16,unweighted> (no starts)": kernel_ms(raw, 100)},
+        "fwd_max_len": rate(elems, timed_calls(fwd16, steps, warmup), 8),
+        "fwd_bwd_max_len": rate(elems, timed_calls(fb16, steps, warmup), 16),
+        "kernel_ms": {
+            "ragged_fit_kernel<float,16,unweighted> (no starts)": kernel_ms(raw, 100),
+            "ragged_grad_kernel<float,16,unweighted> (dy)": kernel_ms(rawb, 100),
+            "ragged_plan_kernel": kernel_ms(rawp, 100),
+        },
     }
-    del bits
+    del bits, gy
     soft = {}
     for sb, sn in ((1024, 100), (256, 1000), (64, 10_000), (8, 100_000), (1, 1_000_000)):
         torch.manual_seed(0)

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 5
+#define TI_ABI_VERSION 6
 
 /* dtype codes */
 #define TI_F32 0
@@ -233,8 +233,21 @@ int ti_bwd_kept(const uint32_t* starts, const void* kept, size_t kept_bytes, int
  *   other arguments as ti_fwd (flags, clamp, bad_weight for the fitted rows' weights).
  */
 int ti_fwd_ragged(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
-                  const int64_t* offsets, int64_t nrows, int64_t max_len, int dtype, unsigned flags,
-                  double y_min, double y_max, void* stream);
+                  const int64_t* offsets, int64_t nrows, int64_t total, int64_t max_len, int dtype,
+                  unsigned flags, double y_min, double y_max, void* stream);
+
+/* The backward of ti_fwd_ragged's rows of at most max_len (<= 32) elements: gy = w * mask * G / W
+ * and gw = (y - fit) * mask * G / W over each block of each row, the blocks read from the
+ * forward's flat start bits (`starts`), the block's fit recomputed from y and w as the forward
+ * formed it, and mask the forward's clamp (flags, y_min, y_max as given to ti_fwd_ragged): the
+ * short-row backward's arithmetic (reference grad.cuh:200-290) for rows of their own lengths.
+ * One thread per row, a workgroup's rows staged through LDS. Rows longer than max_len are not
+ * written (their backward is ti_bwd or ti_grad over their own forward). gy or gw may be null
+ * (not wanted); gw needs w and y, the clamp needs y. No reference counterpart: the reference has
+ * no ragged rows. */
+int ti_bwd_ragged(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy, void* gw,
+                  const int64_t* offsets, int64_t nrows, int64_t total, int64_t max_len, int dtype,
+                  unsigned flags, double y_min, double y_max, void* stream);
 
 /*
  * The plan of a ragged set, one pass over its offsets (device int64, nrows + 1 values), into

@@ -230,6 +230,30 @@ def test_grad_argument_errors() -> None:
     assert grad(None, None, None, None, None, None, None, 0, 16) == 0
 
 
+def test_ragged_backward_argument_errors() -> None:
+    lib = _ext.load()
+
+    def bwd(starts, g, w, y, gy, gw, nrows=10, max_len=16, dtype=_ext.F32, flags=0):
+        return lib.ti_bwd_ragged(starts, g, w, y, gy, gw, 64, nrows, 100, max_len, dtype, flags, 0.0, 0.0, None)
+
+    assert bwd(8, 16, None, None, 24, None, dtype=5) == 2
+    assert bwd(8, 16, None, None, 24, None, nrows=-1) == 1
+    assert bwd(8, 16, None, None, 24, None, max_len=0) == 3
+    assert bwd(8, 16, None, None, 24, None, max_len=33) == 3
+    # gw needs w and y; the clamp needs y
+    assert bwd(8, 16, None, 40, 24, 32) == 1 and b"gw needs" in lib.ti_last_error()
+    assert bwd(8, 16, 48, None, 24, 32) == 1
+    assert bwd(8, 16, None, None, 24, None, flags=_ext.CLIP_MIN) == 1
+    # missing inputs, no output, aliased outputs
+    assert bwd(None, 16, None, None, 24, None) == 1
+    assert bwd(8, None, None, None, 24, None) == 1
+    assert bwd(8, 16, None, None, None, None) == 1
+    assert bwd(8, 16, None, None, 16, None) == 1 and b"alias" in lib.ti_last_error()
+    assert bwd(8, 16, 48, 40, 24, 24) == 1
+    # no rows: nothing to do
+    assert bwd(None, None, None, None, None, None, nrows=0) == 0
+
+
 def test_interp_index_sizes_and_argument_errors() -> None:
     lib = _ext.load()
     size = ctypes.c_size_t(0)

@@ -1,6 +1,7 @@
 """Ragged rows (packed end to end with offsets) on the GPU against the oracle's per-row fits:
 short rows in one launch and longer rows through the regular kernels, with block starts, the
-backward (the stateless gradient over the packed array), the clamp, and C2's padded variant
+backward (one launch for the short rows, from the forward's flat start bits; the longer rows
+from their own forwards), the clamp, and C2's padded variant
 (lengths U{4..16}: a padded row's first len_b fitted values equal the ragged row's fit;
 reference README.md:100-103)."""
 
@@ -147,6 +148,87 @@ def test_backward_matches_block_gradient(dtype: type, weighted: bool) -> None:
         np.testing.assert_allclose(got.double().cpu().numpy(), exp, rtol=tol, atol=tol * scale)
 
 
+def _ragged_abi(y: np.ndarray, w: np.ndarray | None, off: np.ndarray, g: np.ndarray, flags: int, lo: float,
+                hi: float, want_w: bool, shift: int = 0):
+    # ti_fwd_ragged then ti_bwd_ragged through the C ABI; `shift` puts every array one element
+    # past a 16-byte boundary (the element-by-element staging)
+    lib = _ext.load()
+    n, nrows = len(y), len(off) - 1
+    dt = torch.float32 if y.dtype == np.float32 else torch.float64
+    code = _ext.F32 if y.dtype == np.float32 else _ext.F64
+
+    def dev(a: np.ndarray) -> torch.Tensor:
+        t = torch.zeros(n + shift, dtype=dt, device="cuda")
+        t[shift:] = torch.from_numpy(a).cuda()
+        return t[shift:]
+
+    yt, gt = dev(y), dev(g)
+    wt = None if w is None else dev(w)
+    out, gy = dev(np.zeros_like(y)), dev(np.zeros_like(y))
+    gw = dev(np.zeros_like(y)) if want_w else None
+    offt = torch.from_numpy(off).cuda()
+    bits = torch.zeros((n + 31) // 32 + 1, dtype=torch.int32, device="cuda")
+    max_len = int(max(1, min(32, (off[1:] - off[:-1]).max())))
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.ti_fwd_ragged(yt.data_ptr(), _ext._ptr(wt), out.data_ptr(), bits.data_ptr(), None, offt.data_ptr(),
+                             nrows, n, max_len, code, flags, lo, hi, s) == 0
+    assert lib.ti_bwd_ragged(bits.data_ptr(), gt.data_ptr(), _ext._ptr(wt), yt.data_ptr(), gy.data_ptr(),
+                             _ext._ptr(gw), offt.data_ptr(), nrows, n, max_len, code, flags, lo, hi, s) == 0
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), gy.cpu().numpy(), None if gw is None else gw.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("shift", [0, 1])
+def test_backward_abi_with_the_forward_clamp(dtype: type, weighted: bool, shift: int) -> None:
+    # ti_bwd_ragged after a clamped ti_fwd_ragged: the block gradient, zero in blocks whose fit
+    # the clamp moved (torch.clamp's mask on the block mean), rows of 0 to 32 elements
+    say(f"ragged backward, C ABI, clamp: {np.dtype(dtype).name} weighted={weighted} shift={shift}")
+    rng = np.random.default_rng(21 + shift)
+    ln = rng.integers(0, 33, 30_000).astype(np.int64)
+    y, w, off = ragged_set(ln, dtype, 22)
+    g = rng.standard_normal(len(y)).astype(dtype)
+    lo, hi = -0.3, 1.2
+    flags = _ext.INCREASING | _ext.EXACT | _ext.CLIP_MIN | _ext.CLIP_MAX
+    out, gy, gw = _ragged_abi(y, w if weighted else None, off, g, flags, lo, hi, weighted, shift)
+    fit, starts = oracle.pava_ragged(y, off, w if weighted else None, acc="f64")
+    np.testing.assert_allclose(out.astype(np.float64), np.clip(fit, lo, hi), rtol=0, atol=tolerance(y))
+    ey, ew = oracle.block_grad(starts, g.astype(np.float64), w.astype(np.float64) if weighted else None,
+                               y.astype(np.float64) if weighted else None, fit, want_w=weighted)
+    mask = (fit >= lo) & (fit <= hi)
+    # (a block mean within rounding of a bound may fall either side of it in the kernel's dtype:
+    # those elements are left out, the rest compared)
+    clear = (np.abs(fit - lo) > 1e-5) & (np.abs(fit - hi) > 1e-5)
+    assert clear.mean() > 0.99 and (~mask & clear).any() and (mask & clear).any()
+    tol = 1e-11 if dtype == np.float64 else 1e-5
+    for got, exp in ((gy, ey), (gw, ew)):
+        if exp is None:
+            continue
+        exp = exp * mask
+        scale = max(float(np.abs(exp).max()), 1e-300)
+        np.testing.assert_allclose(got.astype(np.float64)[clear], exp[clear], rtol=tol, atol=tol * scale)
+
+
+def test_backward_c2_rows_at_full_size() -> None:
+    # C2's rows at their own lengths (1e6 rows, len ~ U{4..16}, seed 2), decreasing, float32:
+    # the one-launch backward against the oracle's block gradient
+    say("ragged backward, C2 rows at full size")
+    b, n = 1_000_000, 16
+    rng = np.random.default_rng(0)
+    y2 = (-0.1 * np.arange(n) + rng.standard_normal((b, n))).astype(np.float32)
+    lens = np.random.default_rng(2).integers(4, n + 1, b)
+    packed = y2[np.arange(n)[None, :] < lens[:, None]]
+    off = np.r_[0, np.cumsum(lens)].astype(np.int64)
+    g = np.random.default_rng(3).standard_normal(len(packed)).astype(np.float32)
+    yt = torch.from_numpy(packed).cuda().requires_grad_()
+    out = isotonic_ragged(yt, torch.from_numpy(off).cuda(), increasing=False)
+    (gy,) = torch.autograd.grad(out, [yt], torch.from_numpy(g).cuda())
+    fit, starts = oracle.pava_ragged(packed, off, increasing=False, acc="f64")
+    ey, _ = oracle.block_grad(starts, g.astype(np.float64))
+    np.testing.assert_allclose(gy.double().cpu().numpy(), ey, rtol=1e-5, atol=1e-5 * float(np.abs(ey).max()))
+
+
 def test_lengths_clamp_and_gradcheck() -> None:
     gen = torch.Generator().manual_seed(4)
     ln = torch.tensor([3, 0, 7, 1, 40, 12])
@@ -158,6 +240,42 @@ def test_lengths_clamp_and_gradcheck() -> None:
     yy = y.clone().requires_grad_()
     ww = (torch.rand(len(y), generator=gen, dtype=torch.float64) + 0.5).cuda().requires_grad_()
     assert torch.autograd.gradcheck(lambda t, u: isotonic_ragged(t, lengths=ln, weight=u, increasing=False), (yy, ww))
+
+
+@pytest.mark.parametrize("max_len", [0, 4, 16, 32, 1000])
+def test_max_len_bound(max_len: int) -> None:
+    # a bound on the row lengths lets the short rows' launch start before the plan is read: the
+    # same fits, starts and gradients whether the bound is right (16), too small (4: a second
+    # launch), loose (32, 1000) or absent (0), with rows past 32 and empty rows present
+    say(f"ragged max_len={max_len}")
+    rng = np.random.default_rng(31)
+    ln = np.r_[rng.integers(0, 17, 20_000), [40, 0, 300], rng.integers(1, 17, 500)].astype(np.int64)
+    y, w, off = ragged_set(ln, np.float32, 32)
+    g = rng.standard_normal(len(y)).astype(np.float32)
+    yt = torch.from_numpy(y).cuda().requires_grad_()
+    wt = torch.from_numpy(w).cuda().requires_grad_()
+    out = isotonic_ragged(yt, torch.from_numpy(off).cuda(), weight=wt, increasing=False, max_len=max_len)
+    gy, gw = torch.autograd.grad(out, [yt, wt], torch.from_numpy(g).cuda())
+    fit, starts = oracle.pava_ragged(y, off, w, increasing=False, acc="f64")
+    assert float(np.abs(out.detach().double().cpu().numpy() - fit).max()) <= tolerance(y)
+    ey, ew = oracle.block_grad(starts, g.astype(np.float64), w.astype(np.float64), y.astype(np.float64), fit,
+                               want_w=True)
+    for got, exp in ((gy, ey), (gw, ew)):
+        np.testing.assert_allclose(got.double().cpu().numpy(), exp, rtol=1e-5, atol=1e-5 * float(np.abs(exp).max()))
+
+
+def test_max_len_with_bad_offsets_raises() -> None:
+    # with a bound, the short rows' kernel runs on offsets not yet checked (it clamps every one
+    # into the packed array and each row into its workgroup's range); the plan then raises
+    y = torch.randn(100, device="cuda")
+    for off, msg in (([0, 40, 20, 100], "decrease"), ([0, 50, 150], "offsets must run"), ([5, 50, 100], "offsets must run")):
+        with pytest.raises(ValueError, match=msg):
+            isotonic_ragged(y, torch.tensor(off), max_len=16)
+    good = isotonic_ragged(y, torch.tensor([0, 40, 60, 100]), max_len=16)
+    want, _ = oracle.pava_ragged(y.cpu().numpy(), np.array([0, 40, 60, 100]), acc="f64")
+    assert float(np.abs(good.cpu().numpy() - want).max()) <= tolerance(y.cpu().numpy())
+    with pytest.raises(ValueError, match="max_len"):
+        isotonic_ragged(y, torch.tensor([0, 100]), max_len=-1)
 
 
 def test_argument_errors() -> None:

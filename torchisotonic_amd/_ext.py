@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -42,6 +42,7 @@ SYMBOLS = (
     "ti_fwd_ev",
     "ti_fwd_noalloc",
     "ti_fwd_ragged",
+    "ti_bwd_ragged",
     "ti_ragged_plan",
     "ti_bwd_workspace",
     "ti_bwd",
@@ -89,7 +90,9 @@ def load() -> ctypes.CDLL:
     lib.ti_fwd_noalloc.restype = _int
     lib.ti_fwd_noalloc.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp]
     lib.ti_fwd_ragged.restype = _int
-    lib.ti_fwd_ragged.argtypes = [_vp] * 6 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp]
+    lib.ti_fwd_ragged.argtypes = [_vp] * 6 + [_i64, _i64, _i64, _int, _uint, _dbl, _dbl, _vp]
+    lib.ti_bwd_ragged.restype = _int
+    lib.ti_bwd_ragged.argtypes = [_vp] * 7 + [_i64, _i64, _i64, _int, _uint, _dbl, _dbl, _vp]
     lib.ti_ragged_plan.restype = _int
     lib.ti_ragged_plan.argtypes = [_vp, _i64, _i64, _vp, _vp]
     lib.ti_bwd.restype = _int

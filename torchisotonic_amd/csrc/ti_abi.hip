@@ -374,19 +374,41 @@ int ti_grad(const void* out, const uint32_t* starts, const void* g, const void* 
 }
 
 int ti_fwd_ragged(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
-                  const int64_t* offsets, int64_t nrows, int64_t max_len, int dtype, unsigned flags, double y_min,
-                  double y_max, void* stream) {
+                  const int64_t* offsets, int64_t nrows, int64_t total, int64_t max_len, int dtype, unsigned flags,
+                  double y_min, double y_max, void* stream) {
   if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
-  if (nrows < 0) return fail(TI_EINVAL, "need nrows >= 0, got %lld", (long long)nrows);
+  if (nrows < 0 || total < 0) return fail(TI_EINVAL, "need nrows >= 0 and total >= 0");
   if (max_len < 1 || max_len > ti::kShortMax)
     return fail(TI_ESIZE, "max_len must be in [1, %lld], got %lld", (long long)ti::kShortMax, (long long)max_len);
   if (nrows == 0) return ok();
   if (y == nullptr || out == nullptr || offsets == nullptr) return fail(TI_EINVAL, "y, out and offsets must not be null");
   if (out == y || (w != nullptr && out == w)) return fail(TI_EINVAL, "out must not alias y or w");
   if (ti::ragged_grid(nrows, max_len, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "too many rows");
-  ti::RaggedArgs a{y, w, out, starts, bad_weight, offsets, nrows, max_len, dtype, flags, y_min, y_max,
+  ti::RaggedArgs a{y, w, out, starts, bad_weight, offsets, nrows, total, max_len, dtype, flags, y_min, y_max,
                    static_cast<hipStream_t>(stream)};
   return launched(ti::ragged_fit(a), "ragged fit");
+}
+
+int ti_bwd_ragged(const uint32_t* starts, const void* g, const void* w, const void* y, void* gy, void* gw,
+                  const int64_t* offsets, int64_t nrows, int64_t total, int64_t max_len, int dtype, unsigned flags,
+                  double y_min, double y_max, void* stream) {
+  if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
+  if (nrows < 0 || total < 0) return fail(TI_EINVAL, "need nrows >= 0 and total >= 0");
+  if (max_len < 1 || max_len > ti::kShortMax)
+    return fail(TI_ESIZE, "max_len must be in [1, %lld], got %lld", (long long)ti::kShortMax, (long long)max_len);
+  if (gw != nullptr && (w == nullptr || y == nullptr)) return fail(TI_EINVAL, "gw needs w and y");
+  if ((flags & (TI_CLIP_MIN | TI_CLIP_MAX)) != 0 && y == nullptr) return fail(TI_EINVAL, "the clamp mask needs y");
+  if (nrows == 0) return ok();
+  if (starts == nullptr || g == nullptr || offsets == nullptr) return fail(TI_EINVAL, "starts, g and offsets must not be null");
+  if (gy == nullptr && gw == nullptr) return fail(TI_EINVAL, "gy and gw must not both be null");
+  for (const void* o : {static_cast<const void*>(gy), static_cast<const void*>(gw)}) {
+    if (o != nullptr && (o == g || o == w || o == y)) return fail(TI_EINVAL, "gy and gw must not alias g, w or y");
+  }
+  if (gy != nullptr && gy == gw) return fail(TI_EINVAL, "gy and gw must not alias each other");
+  if (ti::ragged_grid(nrows, max_len, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "too many rows");
+  ti::RaggedGradArgs a{starts, g,     w,     y,     gy,    gw, offsets, nrows, total, max_len, dtype, flags,
+                       y_min,  y_max, static_cast<hipStream_t>(stream)};
+  return launched(ti::ragged_grad(a), "ragged backward");
 }
 
 int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, void* stream) {

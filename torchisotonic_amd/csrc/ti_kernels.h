@@ -56,7 +56,7 @@ struct RaggedArgs {
   uint32_t* starts;      // flat bits of the packed array (zeroed by the caller), or null
   uint32_t* bad_weight;  // null: not checked
   const int64_t* offsets;
-  int64_t nrows, max_len;
+  int64_t nrows, total, max_len;  // total: the packed array's elements (offsets are clamped to it)
   int dtype;
   unsigned flags;
   double lo, hi;
@@ -64,6 +64,23 @@ struct RaggedArgs {
 };
 int64_t ragged_grid(int64_t nrows, int64_t max_len, bool weighted);
 hipError_t ragged_fit(const RaggedArgs& a);
+// The backward of the ragged rows of at most max_len (<= kShortMax) elements, from the
+// forward's flat start bits; longer rows' elements are not written.
+struct RaggedGradArgs {
+  const uint32_t* starts;  // the forward's flat bits
+  const void* g;
+  const void* w;  // null: unweighted
+  const void* y;  // needed for gw and for the clamp mask
+  void* gy;       // null: not wanted
+  void* gw;       // null: not wanted
+  const int64_t* offsets;
+  int64_t nrows, total, max_len;
+  int dtype;
+  unsigned flags;  // the forward's (its clamp)
+  double lo, hi;
+  hipStream_t stream;
+};
+hipError_t ragged_grad(const RaggedGradArgs& a);
 // plan: four zeroed device words (see ragged_plan_kernel)
 hipError_t ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, unsigned long long* plan,
                        hipStream_t stream);

@@ -447,6 +447,8 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
   stage_out<T, THREADS>(out + row0 * n, stg, count, div);
 }
 
+__device__ __forceinline__ int64_t clamp64(int64_t v, int64_t lo, int64_t hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
 // Ragged rows: row r is y[offsets[r], offsets[r + 1]) of a packed array, one thread per row as
 // above. A workgroup whose rows lie within THREADS * NMAX elements stages them through LDS:
 // 16-byte loads and stores of the aligned chunks that cover its range (element by element in
@@ -461,7 +463,8 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void short_fit_kernel(
 template <typename T, int NMAX, bool W, bool INC>
 __global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_fit_kernel(
     const T* __restrict__ y, const T* __restrict__ w, T* __restrict__ out, uint32_t* __restrict__ starts,
-    uint32_t* __restrict__ bad_weight, const int64_t* __restrict__ offsets, int64_t nrows, unsigned flags, T lo,
+    uint32_t* __restrict__ bad_weight, const int64_t* __restrict__ offsets, int64_t nrows, int64_t n_all,
+    unsigned flags, T lo,
     T hi) {
   constexpr int THREADS = short_threads<NMAX, W>();
   constexpr int CAP = THREADS * NMAX;        // elements a workgroup stages
@@ -484,9 +487,11 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_fit_kernel(
   if constexpr (!W) {
     if (tid < kRcpN) rcp[tid] = kRcp.v[tid];
   }
-  const int64_t e0 = offsets[row0], e1 = offsets[row0 + rows];
-  const int64_t my0 = active ? offsets[row0 + tid] : e1;
-  const int64_t my1 = active ? offsets[row0 + tid + 1] : e1;
+  // (every offset clamped: to [0, n_all], a row's to its workgroup's range, a row's end to at
+  // least its start, so that no access leaves the buffers even on offsets not yet validated)
+  const int64_t e0 = clamp64(offsets[row0], 0, n_all), e1 = clamp64(offsets[row0 + rows], e0, n_all);
+  const int64_t my0 = active ? clamp64(offsets[row0 + tid], e0, e1) : e1;
+  const int64_t my1 = active ? clamp64(offsets[row0 + tid + 1], my0, e1) : e1;
   const bool fits = active && my1 > my0 && my1 - my0 <= NMAX;  // (empty rows: nothing to fit)
   const int len = fits ? static_cast<int>(my1 - my0) : 0;
   const int64_t total = e1 - e0;
@@ -635,9 +640,13 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_fit_kernel(
 // The plan of a ragged set, one pass over its offsets: plan[0] bit 0 set if offsets[0] != 0,
 // bit 1 if offsets[nrows] != total, bit 2 if some row has a negative length; plan[1] the longest
 // row of at most kShortMax elements, plan[2] the number of longer rows, plan[3] the longest
-// row. plan: four zeroed words. Each workgroup reduces its rows through its waves and LDS, then
-// one thread folds the result into plan (the grid is kept small, so few atomics meet there).
+// row. plan: four zeroed words. Each thread reads kPlanRows rows at a time (their loads in
+// flight together), each workgroup reduces its rows through its waves and LDS, then one thread
+// folds the result into plan. The grid stays at kPlanBlocks: the folds are atomics on the same
+// four words, about 12 ns each on MI355X, so 256 workgroups take 10.7 us at 1e6 rows where 977
+// take 25 us (their partial results written apart would take 4.9 us before a fold of their own).
 constexpr int kPlanThreads = 256;
+constexpr int kPlanRows = 4;
 constexpr int kPlanBlocks = 256;
 
 __device__ __forceinline__ void plan_fold(unsigned long long v[4], unsigned long long o[4]) {
@@ -653,15 +662,24 @@ __global__ __launch_bounds__(kPlanThreads) void ragged_plan_kernel(const int64_t
   __shared__ unsigned long long part[kPlanThreads / 64][4];
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
   unsigned long long v[4] = {0, 0, 0, 0};  // errors, longest short row, long rows, longest row
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; r < nrows; r += stride) {
-    const int64_t len = offsets[r + 1] - offsets[r];
-    if (len < 0) {
-      v[0] |= 4u;
-    } else {
-      const unsigned long long l = static_cast<unsigned long long>(len);
-      if (len <= kShortMax) v[1] = l > v[1] ? l : v[1];
-      else v[2] += 1;
-      v[3] = l > v[3] ? l : v[3];
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; r0 < nrows;
+       r0 += kPlanRows * stride) {
+    int64_t len[kPlanRows];
+#pragma unroll
+    for (int u = 0; u < kPlanRows; ++u) {
+      const int64_t r = r0 + u * stride;
+      len[u] = r < nrows ? offsets[r + 1] - offsets[r] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPlanRows; ++u) {
+      if (len[u] < 0) {
+        v[0] |= 4u;
+      } else {
+        const unsigned long long l = static_cast<unsigned long long>(len[u]);
+        if (len[u] <= kShortMax) v[1] = l > v[1] ? l : v[1];
+        else v[2] += 1;
+        v[3] = l > v[3] ? l : v[3];
+      }
     }
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -772,6 +790,191 @@ __device__ __forceinline__ void row_grad(const T (&gv)[NMAX], const T (&wv)[W ? 
         if (need_mean) {
           ow[i] = static_cast<T>((static_cast<double>(yv[i]) - static_cast<double>(cf)) * cq);
         }
+      }
+    }
+  }
+}
+
+// Ragged rows' backward: row r is [offsets[r], offsets[r + 1]) of the packed array, one thread
+// per row of at most NMAX elements, a workgroup's rows staged through LDS as in
+// ragged_fit_kernel (or read and written by each thread where their range is longer than
+// THREADS * NMAX); each row's start bits come from the forward's flat bits. gy = w * mask * G / W
+// and gw = (y - fit) * mask * G / W over each block (row_grad, with the forward's clamp). A row
+// longer than NMAX is left alone (its elements of gy and gw are not written: its backward is its
+// own forward's), and so are elements outside every row's range.
+template <typename T, int NMAX, bool W>
+__global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_grad_kernel(
+    const uint32_t* __restrict__ starts, const T* __restrict__ g, const T* __restrict__ w, const T* __restrict__ y,
+    T* __restrict__ gy, T* __restrict__ gw, const int64_t* __restrict__ offsets, int64_t nrows, int64_t n_all,
+    unsigned flags,
+    T lo, T hi) {
+  constexpr int THREADS = short_threads<NMAX, W>();
+  constexpr int CAP = THREADS * NMAX;
+  constexpr int V = Vec16<T>::kN;
+  using VT = typename Vec16<T>::type;
+  constexpr int KI = (CAP / V + 2 + THREADS - 1) / THREADS;
+  constexpr int WORDS = CAP / 32 + 2;
+  __shared__ __align__(16) T stg[CAP + 2 * V];
+  __shared__ uint32_t own[WORDS];  // staged elements that belong to a row of at most NMAX
+  const int tid = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
+  const int rows = static_cast<int>(min<int64_t>(THREADS, nrows - row0));
+  const bool active = tid < rows;
+  // (every offset clamped: to [0, n_all], a row's to its workgroup's range, a row's end to at
+  // least its start, so that no access leaves the buffers even on offsets not yet validated)
+  const int64_t e0 = clamp64(offsets[row0], 0, n_all), e1 = clamp64(offsets[row0 + rows], e0, n_all);
+  const int64_t my0 = active ? clamp64(offsets[row0 + tid], e0, e1) : e1;
+  const int64_t my1 = active ? clamp64(offsets[row0 + tid + 1], my0, e1) : e1;
+  const bool fits = active && my1 > my0 && my1 - my0 <= NMAX;
+  const int len = fits ? static_cast<int>(my1 - my0) : 0;
+  const int64_t total = e1 - e0;
+  const bool staged = total <= CAP;  // (the same in every thread)
+  const int b0 = static_cast<int>(e0 & 31);
+  const int rel = static_cast<int>(my0 - e0);
+  const int64_t a0 = e0 - e0 % V;
+  const int sh = static_cast<int>(e0 - a0);
+  const int nch = staged ? static_cast<int>((e1 - a0 + V - 1) / V) : 0;
+  const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
+  const bool need_mean = gw != nullptr || use_lo || use_hi;
+  const uintptr_t bases = reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(gy) |
+                          reinterpret_cast<uintptr_t>(gw) | (W ? reinterpret_cast<uintptr_t>(w) : uintptr_t{0}) |
+                          reinterpret_cast<uintptr_t>(y);
+  const bool vec = (bases & 15) == 0;
+  // the row's start bits (bit my0 + c of the flat array is bit c), its first always set
+  uint32_t bits = 1u;
+  if (len > 0) {
+    const int64_t wd = my0 >> 5;
+    const int sb = static_cast<int>(my0 & 31);
+    uint32_t b = starts[wd] >> sb;
+    if (sb != 0 && sb + len > 32) b |= starts[wd + 1] << (32 - sb);
+    bits |= b & (len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u));
+  }
+
+  auto stage_in = [&](const T* __restrict__ src) {
+    VT buf[KI];
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+      const int k = tid + j * THREADS;
+      const int64_t q = a0 + static_cast<int64_t>(k) * V;
+      buf[j] = VT{};
+      if (k < nch) {
+        if (vec && q >= e0 && q + V <= e1) {
+          buf[j] = *reinterpret_cast<const VT*>(src + q);
+        } else {
+#pragma unroll
+          for (int t = 0; t < V; ++t) {
+            if (q + t >= e0 && q + t < e1) buf[j][t] = src[q + t];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+      const int k = tid + j * THREADS;
+      if (k < nch) *reinterpret_cast<VT*>(stg + k * V) = buf[j];
+    }
+  };
+  // the staged range out to dst: whole where every element is a fitted row's, else by ownership
+  auto stage_out_range = [&](T* __restrict__ dst, bool has_long) {
+    if (!has_long) {
+#pragma unroll
+      for (int j = 0; j < KI; ++j) {
+        const int k = tid + j * THREADS;
+        const int64_t q = a0 + static_cast<int64_t>(k) * V;
+        if (k < nch) {
+          if (vec && q >= e0 && q + V <= e1) {
+            *reinterpret_cast<VT*>(dst + q) = *reinterpret_cast<const VT*>(stg + k * V);
+          } else {
+#pragma unroll
+            for (int t = 0; t < V; ++t) {
+              if (q + t >= e0 && q + t < e1) dst[q + t] = stg[k * V + t];
+            }
+          }
+        }
+      }
+    } else {
+      for (int e = tid; e < total; e += THREADS) {
+        const int bit = e + b0;
+        if ((own[bit >> 5] >> (bit & 31)) & 1u) dst[e0 + e] = stg[sh + e];
+      }
+    }
+  };
+
+  T gv[NMAX];
+  T wv[W ? NMAX : 1];
+  T yv[NMAX];
+  bool has_long = false;
+  if (staged) {
+    has_long = __syncthreads_or(active && my1 - my0 > NMAX);
+    for (int k = tid; k < WORDS; k += THREADS) own[k] = 0u;
+    stage_in(g);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) gv[c] = stg[sh + rel + c];
+    }
+    if (has_long && len > 0) {  // mark this row's elements (at most two words)
+      const uint32_t mask = len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u);
+      const int bit = rel + b0;
+      atomicOr(&own[bit >> 5], mask << (bit & 31));
+      if ((bit & 31) + len > 32) atomicOr(&own[(bit >> 5) + 1], mask >> (32 - (bit & 31)));
+    }
+    if constexpr (W) {
+      __syncthreads();
+      stage_in(w);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < len) wv[c] = stg[sh + rel + c];
+      }
+    }
+    if (need_mean) {
+      __syncthreads();
+      stage_in(y);
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < len) yv[c] = stg[sh + rel + c];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) {
+        gv[c] = g[my0 + c];
+        if constexpr (W) wv[c] = w[my0 + c];
+        if (need_mean) yv[c] = y[my0 + c];
+      }
+    }
+  }
+
+  T oy[NMAX], ow[NMAX];
+  row_grad<T, NMAX, W>(gv, wv, yv, bits, len, need_mean, use_lo, lo, use_hi, hi, oy, ow);
+  if (staged) {
+    if (gy != nullptr) {
+      __syncthreads();  // every thread has read its values
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < len) stg[sh + rel + c] = oy[c];
+      }
+      __syncthreads();
+      stage_out_range(gy, has_long);
+    }
+    if (gw != nullptr) {
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) {
+        if (c < len) stg[sh + rel + c] = ow[c];
+      }
+      __syncthreads();
+      stage_out_range(gw, has_long);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NMAX; ++c) {
+      if (c < len) {
+        if (gy != nullptr) gy[my0 + c] = oy[c];
+        if (gw != nullptr) gw[my0 + c] = ow[c];
       }
     }
   }
@@ -1172,10 +1375,28 @@ hipError_t ragged_by_len(const RaggedArgs& a) {
     T* out = static_cast<T*>(a.out);
     if (inc)
       ragged_fit_kernel<T, NMAX, W, true><<<grid, dim3(TH), 0, a.stream>>>(y, w, out, a.starts, a.bad_weight, a.offsets,
-                                                                          a.nrows, a.flags, lo, hi);
+                                                                          a.nrows, a.total, a.flags, lo, hi);
     else
       ragged_fit_kernel<T, NMAX, W, false><<<grid, dim3(TH), 0, a.stream>>>(y, w, out, a.starts, a.bad_weight, a.offsets,
-                                                                           a.nrows, a.flags, lo, hi);
+                                                                           a.nrows, a.total, a.flags, lo, hi);
+    return hipGetLastError();
+  };
+  if (a.max_len <= 4) return go(std::integral_constant<int, 4>{});
+  if (a.max_len <= 8) return go(std::integral_constant<int, 8>{});
+  if (a.max_len <= 16) return go(std::integral_constant<int, 16>{});
+  return go(std::integral_constant<int, 32>{});
+}
+
+template <typename T, bool W>
+hipError_t ragged_grad_by_len(const RaggedGradArgs& a) {
+  auto go = [&](auto nmax) -> hipError_t {
+    constexpr int NMAX = decltype(nmax)::value;
+    constexpr int TH = short_threads<NMAX, W>();
+    const dim3 grid(static_cast<unsigned>((a.nrows + TH - 1) / TH));
+    ragged_grad_kernel<T, NMAX, W><<<grid, dim3(TH), 0, a.stream>>>(
+        a.starts, static_cast<const T*>(a.g), static_cast<const T*>(a.w), static_cast<const T*>(a.y),
+        static_cast<T*>(a.gy), static_cast<T*>(a.gw), a.offsets, a.nrows, a.total, a.flags, static_cast<T>(a.lo),
+        static_cast<T>(a.hi));
     return hipGetLastError();
   };
   if (a.max_len <= 4) return go(std::integral_constant<int, 4>{});
@@ -1186,9 +1407,16 @@ hipError_t ragged_by_len(const RaggedArgs& a) {
 
 int64_t ragged_grid(int64_t nrows, int64_t max_len, bool weighted) { return short_grid(nrows, max_len, weighted); }
 
+hipError_t ragged_grad(const RaggedGradArgs& a) {
+  const bool weighted = a.w != nullptr;
+  if (a.dtype == TI_F32) return weighted ? ragged_grad_by_len<float, true>(a) : ragged_grad_by_len<float, false>(a);
+  return weighted ? ragged_grad_by_len<double, true>(a) : ragged_grad_by_len<double, false>(a);
+}
+
 hipError_t ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, unsigned long long* plan,
                        hipStream_t stream) {
-  const int64_t blocks = std::min<int64_t>(std::max<int64_t>((nrows + kPlanThreads - 1) / kPlanThreads, 1), kPlanBlocks);
+  const int64_t per_block = int64_t{kPlanThreads} * kPlanRows;
+  const int64_t blocks = std::min<int64_t>(std::max<int64_t>((nrows + per_block - 1) / per_block, 1), kPlanBlocks);
   ragged_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPlanThreads), 0, stream>>>(offsets, nrows, total,
                                                                                             plan);
   return hipGetLastError();

@@ -8,11 +8,14 @@ decreasing one) or lay them end to end with offsets
 and the row offsets (CSR layout) go to the GPU as they are:
 
 - rows of 1 to 32 elements, the short-row regime, are fitted together in one HIP launch
-  (``ti_fwd_ragged``: one thread per row, a workgroup's rows staged through LDS);
+  (``ti_fwd_ragged``: one thread per row, a workgroup's rows staged through LDS), after one
+  kernel has checked the offsets and sized the rows and its four words have reached the host
+  (the call's one wait); with ``max_len``, a bound on the row lengths, that launch goes before
+  the wait and runs during it;
 - longer rows are fitted row by row by the regular kernels (``ti_fwd`` on each row in place);
-- the backward is ``ti_grad`` (the stateless gradient operator) over the whole packed array as
-  one sequence: the forward's flat start bits separate the rows, since every row starts a
-  block; longer rows then take their gradients from their own forward's hulls (``ti_bwd``).
+- the backward of the rows of 1 to 32 elements is one HIP launch too (``ti_bwd_ragged``: one
+  thread per row, the blocks read from the forward's flat start bits); longer rows take their
+  gradients from their own forward's hulls (``ti_bwd``).
 
 The clamp to [y_min, y_max] is torch.clamp after the fit, as in the reference (_api.py:68-69).
 """
@@ -32,22 +35,22 @@ _SHORT = 32  # the longest rows the one-launch kernel fits
 _local = threading.local()
 
 
-def _host_words(device: torch.device) -> Tensor:
-    """Per thread and device: four pinned host words the plan is copied into."""
+def _host_words(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
+    """Per thread and device: four pinned host words the plan is copied into, and the event
+    recorded once they are there."""
     cache = getattr(_local, "plan", None)
     if cache is None:
         cache = _local.plan = {}
     if device.index not in cache:
-        cache[device.index] = torch.empty(4, dtype=torch.int64, pin_memory=True)
+        cache[device.index] = (torch.empty(4, dtype=torch.int64, pin_memory=True), torch.cuda.Event())
     return cache[device.index]
 
 
-def _offsets(offsets, lengths, values: Tensor, weighted: bool):
-    """The row offsets as a device int64 tensor, validated; the longest row of at most 32
-    elements (0 if none); the (start, end) of every longer row; and zeroed device words for the
-    fit: the flat start bits and the weight flag. One kernel (ti_ragged_plan) checks the offsets
-    and sizes the rows, and four words come back to the host: the offsets themselves are never
-    copied whole."""
+def _plan(offsets, lengths, values: Tensor, weighted: bool):
+    """The row offsets as a device int64 tensor; zeroed device words for the fit (the flat
+    start bits and the weight flag); and the plan of the offsets under way: one kernel
+    (ti_ragged_plan) checks them and sizes the rows, and four words are on their way to the host
+    (the offsets themselves are never copied whole). ``_plan_wait`` reads them."""
     if (offsets is None) == (lengths is None):
         raise ValueError("give exactly one of offsets and lengths")
     dev = values.device
@@ -67,15 +70,24 @@ def _offsets(offsets, lengths, values: Tensor, weighted: bool):
     # one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
     zeros = torch.zeros(10 + (total + 31) // 32, dtype=torch.int32, device=dev)
     plan, bad, bits = zeros[:8].view(torch.int64), zeros[8:9], zeros[10:]
-    host = _host_words(dev)
+    host, ready = _host_words(dev)
     with _ext._on_device(dev):
         _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), _ext._stream(values)),
                     "isotonic_ragged")
         host.copy_(plan, non_blocking=True)
-        torch.cuda.current_stream(dev).synchronize()
+        ready.record(torch.cuda.current_stream(dev))
+    return off, bits, (bad if weighted else None), (host, ready, offsets is None, total)
+
+
+def _plan_wait(off: Tensor, pending) -> tuple[int, list[tuple[int, int]]]:
+    """The plan's words, once they are on the host (the stream's later work keeps running): the
+    offsets' errors raised, the longest row of at most 32 elements (0 if none), and the (start,
+    end) of every longer row."""
+    host, ready, from_lengths, total = pending
+    ready.synchronize()
     err, short_max, n_long, _ = host.tolist()
     if err & 4:
-        raise ValueError("lengths must be non-negative" if offsets is None else "offsets must not decrease")
+        raise ValueError("lengths must be non-negative" if from_lengths else "offsets must not decrease")
     if err & 3:
         raise ValueError(f"offsets must run from 0 to values.numel() = {total}")
     long_rows: list[tuple[int, int]] = []
@@ -83,7 +95,41 @@ def _offsets(offsets, lengths, values: Tensor, weighted: bool):
         ln = off[1:] - off[:-1]
         r = torch.nonzero(ln > _SHORT).view(-1)
         long_rows = [(int(x), int(y)) for x, y in torch.stack([off[r], off[r + 1]], 1).tolist()]
-    return off, int(short_max), long_rows, bits, (bad if weighted else None)
+    return int(short_max), long_rows
+
+
+def _offsets(offsets, lengths, values: Tensor, weighted: bool):
+    """``_plan`` and ``_plan_wait`` in a row: the offsets, validated, the longest short row, the
+    longer rows, and the zeroed bits and weight flag."""
+    off, bits, bad, pending = _plan(offsets, lengths, values, weighted)
+    short_max, long_rows = _plan_wait(off, pending)
+    return off, short_max, long_rows, bits, bad
+
+
+def _fit_short(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, nmax: int, bits: Tensor,
+               bad: Tensor | None, increasing: bool) -> None:
+    """One launch (ti_fwd_ragged) over every row of at most nmax elements; longer rows are left
+    alone. Every offset is clamped in the kernel, so this may run before the plan is read."""
+    flags = (_ext.INCREASING if increasing else 0) | _ext.EXACT
+    with _ext._on_device(values.device):
+        rc = _ext.load().ti_fwd_ragged(
+            values.data_ptr(), _ext._ptr(w), out.data_ptr(), bits.data_ptr(), _ext._ptr(bad),
+            off.data_ptr(), off.numel() - 1, values.numel(), nmax, _ext._dtype_code(values), flags,
+            0.0, 0.0, _ext._stream(values),
+        )
+    _ext._check(rc, "isotonic_ragged")
+
+
+def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, long_spans: list[tuple[int, int]], increasing: bool) -> list:
+    long_rows = []
+    for a, b in long_spans:
+        wr = None if w is None else w[a:b].view(1, b - a)
+        _, starts, bad_r, ws = _ext.fit(values[a:b].view(1, b - a), wr, increasing, True, True,
+                                        out=out[a:b].view(1, b - a))
+        if bad_r:
+            raise ValueError("weight must be strictly positive")
+        long_rows.append((a, b, starts, ws))
+    return long_rows
 
 
 def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spans: list[tuple[int, int]],
@@ -93,22 +139,8 @@ def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spa
     packed starts, its forward workspace)."""
     out = torch.empty_like(values)
     if short_max > 0:
-        flags = (_ext.INCREASING if increasing else 0) | _ext.EXACT
-        with _ext._on_device(values.device):
-            rc = _ext.load().ti_fwd_ragged(
-                values.data_ptr(), _ext._ptr(w), out.data_ptr(), bits.data_ptr(), _ext._ptr(bad),
-                off.data_ptr(), off.numel() - 1, short_max, _ext._dtype_code(values), flags,
-                0.0, 0.0, _ext._stream(values),
-            )
-        _ext._check(rc, "isotonic_ragged")
-    long_rows = []
-    for a, b in long_spans:
-        wr = None if w is None else w[a:b].view(1, b - a)
-        _, starts, bad_r, ws = _ext.fit(values[a:b].view(1, b - a), wr, increasing, True, True,
-                                        out=out[a:b].view(1, b - a))
-        if bad_r:
-            raise ValueError("weight must be strictly positive")
-        long_rows.append((a, b, starts, ws))
+        _fit_short(values, w, out, off, short_max, bits, bad, increasing)
+    long_rows = _fit_long(values, w, out, long_spans, increasing)
     if bad is not None and short_max > 0 and bool(bad.item()):
         raise ValueError("weight must be strictly positive")
     return out, long_rows
@@ -116,31 +148,50 @@ def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spa
 
 class _RaggedFit(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, values: Tensor, w: Tensor | None, off: Tensor, short_max: int,  # type: ignore[override]
-                long_spans: list, bits: Tensor, bad: Tensor | None, increasing: bool) -> Tensor:
-        out, long_rows = _fit(values, w, off, short_max, long_spans, bits, bad, increasing)
+    def forward(ctx, values: Tensor, w: Tensor | None, off: Tensor, bits: Tensor,  # type: ignore[override]
+                bad: Tensor | None, pending: tuple, hint: int, increasing: bool) -> Tensor:
+        # Given a bound on the rows' lengths, the short rows' launch goes first (the kernel clamps
+        # every offset, so it may run on offsets not yet checked) and runs while the host waits
+        # for the plan; rows past the bound (and at most 32 long) take a second launch over every
+        # short row, which writes the same values and bits again.
+        out = torch.empty_like(values)
+        nmax = min(hint, _SHORT)
+        if nmax > 0:
+            _fit_short(values, w, out, off, nmax, bits, bad, increasing)
+        short_max, long_spans = _plan_wait(off, pending)
+        if short_max > nmax:
+            _fit_short(values, w, out, off, short_max, bits, bad, increasing)
+        long_rows = _fit_long(values, w, out, long_spans, increasing)
+        if bad is not None and short_max > 0 and bool(bad.item()):
+            raise ValueError("weight must be strictly positive")
         ctx.increasing = increasing
         ctx.long_rows = long_rows
+        ctx.short_max = short_max
         ctx.has_w = w is not None
-        ctx.save_for_backward(values, w if w is not None else torch.empty(0, device=values.device), out, bits)
+        ctx.save_for_backward(values, w if w is not None else torch.empty(0, device=values.device), off, bits)
         return out
 
     @staticmethod
     def backward(ctx, g: Tensor):  # type: ignore[override]
-        values, w, out, bits = ctx.saved_tensors
+        values, w, off, bits = ctx.saved_tensors
         w = w if ctx.has_w else None
         want_y = ctx.needs_input_grad[0]
         want_w = ctx.has_w and ctx.needs_input_grad[1]
         if not want_y and not want_w:
             return (None,) * 8
-        g = g.contiguous()
-        total = values.numel()
-        # the whole packed array as one sequence: rows are apart, each starting a block
-        gy, gw = _ext.isotonic_grad(out.view(1, total), bits, g.view(1, total),
-                                    None if w is None else w.view(1, total),
-                                    values.view(1, total) if want_w else None)
-        gy = gy.view(total)
-        gw = gw.view(total) if want_w else None
+        g = g.contiguous().to(values.dtype)
+        # (every element belongs to a row: the short rows' elements are written by one launch,
+        # the longer rows' by their own backward below)
+        gy = torch.empty_like(g)
+        gw = torch.empty_like(g) if want_w else None
+        if ctx.short_max > 0:
+            with _ext._on_device(values.device):
+                rc = _ext.load().ti_bwd_ragged(
+                    bits.data_ptr(), g.data_ptr(), _ext._ptr(w), values.data_ptr() if want_w else None,
+                    gy.data_ptr(), _ext._ptr(gw), off.data_ptr(), off.numel() - 1, values.numel(),
+                    ctx.short_max, _ext._dtype_code(values), 0, 0.0, 0.0, _ext._stream(values),
+                )
+            _ext._check(rc, "isotonic_ragged backward")
         for a, b, starts, ws in ctx.long_rows:
             ry, rw = _ext.grad(starts, ws, g[a:b].view(1, b - a), None if w is None else w[a:b].view(1, b - a),
                                values[a:b].view(1, b - a), True, want_w, increasing=ctx.increasing)
@@ -159,12 +210,17 @@ def isotonic_ragged(
     increasing: bool = True,
     y_min: float | None = None,
     y_max: float | None = None,
+    max_len: int | None = None,
 ) -> Tensor:
     """Isotonic regression of every row of a ragged set: row r is ``values[offsets[r]:
     offsets[r + 1]]`` (or give ``lengths``, its row lengths). ``values`` (and ``weight``, shaped
     like it, positive) is 1-D on a ROCm device; offsets run from 0 to ``values.numel()``. Returns
     the fits packed like ``values``, clamped to [y_min, y_max] where given; differentiable in
-    ``values`` and ``weight``. Dtype rules as ``isotonic``."""
+    ``values`` and ``weight``. Dtype rules as ``isotonic``.
+
+    ``max_len``: a bound on the rows' lengths, where the caller knows one (the length rows
+    would be padded to). The fit then starts without waiting for the offsets' plan to reach the
+    host; a wrong bound costs a second launch, never a wrong result."""
     if not isinstance(values, Tensor):
         raise TypeError(f"values must be a torch.Tensor, got {type(values).__name__}")
     if values.ndim != 1:
@@ -178,10 +234,13 @@ def isotonic_ragged(
         if not isinstance(weight, Tensor) or weight.shape != values.shape:
             raise ValueError("weight must be a tensor shaped like values")
         w = weight.to(device=values.device, dtype=acc).contiguous()
-    off, short_max, long_spans, bits, bad = _offsets(offsets, lengths, values, w is not None)
+    if max_len is not None and (isinstance(max_len, bool) or not isinstance(max_len, int) or max_len < 0):
+        raise ValueError("max_len must be a non-negative int")
+    off, bits, bad, pending = _plan(offsets, lengths, values, w is not None)
     if values.numel() == 0:
+        _plan_wait(off, pending)  # (the offsets' errors)
         return values.to(out_dtype, copy=True)
-    fit = _RaggedFit.apply(v, w, off, short_max, long_spans, bits, bad, increasing)
+    fit = _RaggedFit.apply(v, w, off, bits, bad, pending, max_len or 0, increasing)
     if y_min is not None or y_max is not None:
         fit = fit.clamp(min=y_min, max=y_max)
     return fit.to(out_dtype)
