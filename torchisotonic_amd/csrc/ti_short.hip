@@ -795,186 +795,144 @@ __device__ __forceinline__ void row_grad(const T (&gv)[NMAX], const T (&wv)[W ? 
   }
 }
 
-// Ragged rows' backward: row r is [offsets[r], offsets[r + 1]) of the packed array, one thread
-// per row of at most NMAX elements, a workgroup's rows staged through LDS as in
-// ragged_fit_kernel (or read and written by each thread where their range is longer than
-// THREADS * NMAX); each row's start bits come from the forward's flat bits. gy = w * mask * G / W
-// and gw = (y - fit) * mask * G / W over each block (row_grad, with the forward's clamp). A row
-// longer than NMAX is left alone (its elements of gy and gw are not written: its backward is its
-// own forward's), and so are elements outside every row's range.
+// Ragged rows' backward: row r is [offsets[r], offsets[r + 1]) of the packed array. One wave per
+// 64 consecutive rows, one lane per row of at most NMAX elements (no workgroup barriers: each
+// wave has its own LDS slice). Where the packed arrays are 16-byte aligned and none of the wave's
+// rows is longer than NMAX, the wave's range moves through its slice: 16-byte loads of the
+// chunks covering it (from the range's start rounded down to a chunk; past the array's end a
+// buffer load reads zeros), each lane then reading its row; the results go back the same way,
+// whole chunks inside the range as 16-byte stores and the at most two partial chunks at its ends
+// element by element, so no store touches a neighbouring wave's elements. Otherwise each lane
+// reads and writes its own row. Each row's start bits come from the forward's flat bits.
+// gy = w * mask * G / W and gw = (y - fit) * mask * G / W over each block (row_grad, with the
+// forward's clamp). A row longer than NMAX is left alone (its elements of gy and gw are not
+// written: its backward is its own forward's). Every offset is clamped into [0, n_all].
 template <typename T, int NMAX, bool W>
-__global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_grad_kernel(
+__global__ __launch_bounds__(256) void ragged_grad_kernel(
     const uint32_t* __restrict__ starts, const T* __restrict__ g, const T* __restrict__ w, const T* __restrict__ y,
     T* __restrict__ gy, T* __restrict__ gw, const int64_t* __restrict__ offsets, int64_t nrows, int64_t n_all,
-    unsigned flags,
-    T lo, T hi) {
-  constexpr int THREADS = short_threads<NMAX, W>();
-  constexpr int CAP = THREADS * NMAX;
+    unsigned flags, T lo, T hi) {
   constexpr int V = Vec16<T>::kN;
-  using VT = typename Vec16<T>::type;
-  constexpr int KI = (CAP / V + 2 + THREADS - 1) / THREADS;
-  constexpr int WORDS = CAP / 32 + 2;
-  __shared__ __align__(16) T stg[CAP + 2 * V];
-  __shared__ uint32_t own[WORDS];  // staged elements that belong to a row of at most NMAX
-  const int tid = threadIdx.x;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * THREADS;
-  const int rows = static_cast<int>(min<int64_t>(THREADS, nrows - row0));
-  const bool active = tid < rows;
-  // (every offset clamped: to [0, n_all], a row's to its workgroup's range, a row's end to at
-  // least its start, so that no access leaves the buffers even on offsets not yet validated)
-  const int64_t e0 = clamp64(offsets[row0], 0, n_all), e1 = clamp64(offsets[row0 + rows], e0, n_all);
-  const int64_t my0 = active ? clamp64(offsets[row0 + tid], e0, e1) : e1;
-  const int64_t my1 = active ? clamp64(offsets[row0 + tid + 1], my0, e1) : e1;
-  const bool fits = active && my1 > my0 && my1 - my0 <= NMAX;
-  const int len = fits ? static_cast<int>(my1 - my0) : 0;
-  const int64_t total = e1 - e0;
-  const bool staged = total <= CAP;  // (the same in every thread)
-  const int b0 = static_cast<int>(e0 & 31);
-  const int rel = static_cast<int>(my0 - e0);
-  const int64_t a0 = e0 - e0 % V;
-  const int sh = static_cast<int>(e0 - a0);
-  const int nch = staged ? static_cast<int>((e1 - a0 + V - 1) / V) : 0;
+  constexpr int CH = NMAX / V + 1;                          // chunks a lane moves (the range + a partial one)
+  constexpr int SLICE = (kWave * NMAX + V) * sizeof(T);     // bytes of a wave's slice
+  static_assert((NMAX * sizeof(T)) % 16 == 0, "rows of whole chunks bound the range");
+  using IT = unsigned __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) char stg[4][SLICE];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kWave;
+  if (r0 >= nrows) return;  // (the whole wave)
+  char* const sl = stg[wave];
+  const int rows = static_cast<int>(min<int64_t>(kWave, nrows - r0));
+  const bool active = lane < rows;
+  const int64_t e0 = wave_uniform(clamp64(offsets[r0], 0, n_all));
+  const int64_t e1 = wave_uniform(clamp64(offsets[r0 + rows], e0, n_all));
+  const int64_t my0 = active ? clamp64(offsets[r0 + lane], e0, e1) : e1;
+  const int64_t my1 = active ? clamp64(offsets[r0 + lane + 1], my0, e1) : e1;
+  const int64_t raw = my1 - my0;
+  const bool fits = raw > 0 && raw <= NMAX;
+  const int len = fits ? static_cast<int>(raw) : 0;
   const bool use_lo = flags & TI_CLIP_MIN, use_hi = flags & TI_CLIP_MAX;
   const bool need_mean = gw != nullptr || use_lo || use_hi;
   const uintptr_t bases = reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(gy) |
                           reinterpret_cast<uintptr_t>(gw) | (W ? reinterpret_cast<uintptr_t>(w) : uintptr_t{0}) |
                           reinterpret_cast<uintptr_t>(y);
-  const bool vec = (bases & 15) == 0;
-  // the row's start bits (bit my0 + c of the flat array is bit c), its first always set
+  // (the range's length is checked as well as its rows': clamped offsets that do not increase
+  // can leave short rows in a longer range, which the slice would not hold)
+  const bool staged = (bases & 15) == 0 && !__any(raw > NMAX) && e1 - e0 <= int64_t{kWave} * NMAX;
+  const int64_t a0 = e0 - e0 % V;                // the range's first chunk
+  const int sh = static_cast<int>(e0 - a0);       // elements of that chunk before the range
+  const int rel = static_cast<int>(my0 - e0);     // this row's first element within the range
+  const int nch = static_cast<int>((e1 - a0 + V - 1) / V);
   uint32_t bits = 1u;
   if (len > 0) {
     const int64_t wd = my0 >> 5;
     const int sb = static_cast<int>(my0 & 31);
-    uint32_t b = starts[wd] >> sb;
-    if (sb != 0 && sb + len > 32) b |= starts[wd + 1] << (32 - sb);
-    bits |= b & (len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u));
+    uint32_t bw = starts[wd] >> sb;
+    if (sb != 0 && sb + len > 32) bw |= starts[wd + 1] << (32 - sb);
+    bits |= bw & (len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u));
   }
-
-  auto stage_in = [&](const T* __restrict__ src) {
-    VT buf[KI];
-#pragma unroll
-    for (int j = 0; j < KI; ++j) {
-      const int k = tid + j * THREADS;
-      const int64_t q = a0 + static_cast<int64_t>(k) * V;
-      buf[j] = VT{};
-      if (k < nch) {
-        if (vec && q >= e0 && q + V <= e1) {
-          buf[j] = *reinterpret_cast<const VT*>(src + q);
-        } else {
-#pragma unroll
-          for (int t = 0; t < V; ++t) {
-            if (q + t >= e0 && q + t < e1) buf[j][t] = src[q + t];
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < KI; ++j) {
-      const int k = tid + j * THREADS;
-      if (k < nch) *reinterpret_cast<VT*>(stg + k * V) = buf[j];
-    }
+  auto sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
-  // the staged range out to dst: whole where every element is a fitted row's, else by ownership
-  auto stage_out_range = [&](T* __restrict__ dst, bool has_long) {
-    if (!has_long) {
+  // the range of src into the slice (element a0 + x at byte x * sizeof(T)), then this lane's row
+  auto row_in = [&](const T* __restrict__ src, T (&v)[NMAX]) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src + a0, (n_all - a0) * static_cast<int64_t>(sizeof(T)));
+    IT c[CH];
 #pragma unroll
-      for (int j = 0; j < KI; ++j) {
-        const int k = tid + j * THREADS;
-        const int64_t q = a0 + static_cast<int64_t>(k) * V;
-        if (k < nch) {
-          if (vec && q >= e0 && q + V <= e1) {
-            *reinterpret_cast<VT*>(dst + q) = *reinterpret_cast<const VT*>(stg + k * V);
-          } else {
+    for (int j = 0; j < CH; ++j) c[j] = __builtin_amdgcn_raw_buffer_load_b128(r, (lane + j * kWave) * 16, 0, 0);
 #pragma unroll
-            for (int t = 0; t < V; ++t) {
-              if (q + t >= e0 && q + t < e1) dst[q + t] = stg[k * V + t];
-            }
-          }
-        }
-      }
-    } else {
-      for (int e = tid; e < total; e += THREADS) {
-        const int bit = e + b0;
-        if ((own[bit >> 5] >> (bit & 31)) & 1u) dst[e0 + e] = stg[sh + e];
-      }
+    for (int j = 0; j < CH; ++j) {
+      const int k = lane + j * kWave;
+      if (k < nch) *reinterpret_cast<IT*>(sl + k * 16) = c[j];
     }
+    sync();
+    const T* sv = reinterpret_cast<const T*>(sl) + sh + rel;
+#pragma unroll
+    for (int c2 = 0; c2 < NMAX; ++c2) {
+      if (c2 < len) v[c2] = sv[c2];
+    }
+    sync();
+  };
+  // this lane's row into the slice, then the range out to dst
+  auto row_out = [&](T* __restrict__ dst, const T (&v)[NMAX]) {
+    T* sv = reinterpret_cast<T*>(sl) + sh + rel;
+#pragma unroll
+    for (int c2 = 0; c2 < NMAX; ++c2) {
+      if (c2 < len) sv[c2] = v[c2];
+    }
+    sync();
+    // whole chunks [kf, kl) inside [e0, e1); the partial ones element by element
+    const int kf = sh == 0 ? 0 : 1;
+    const int kl = max(kf, static_cast<int>((e1 - a0) / V));
+    const int64_t fs = min(a0 + static_cast<int64_t>(kf) * V, e1);
+    const int64_t fe = max(a0 + static_cast<int64_t>((e1 - a0) / V) * V, fs);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(dst + a0, (e1 - a0) * static_cast<int64_t>(sizeof(T)));
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int k = lane + j * kWave;
+      if (k >= kf && k < kl) __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const IT*>(sl + k * 16), r, k * 16, 0, 0);
+    }
+    const T* sr = reinterpret_cast<const T*>(sl);
+    if (lane < V) {
+      const int64_t e = e0 + lane;  // the head [e0, fs)
+      if (e < fs) dst[e] = sr[e - a0];
+    } else if (lane < 2 * V) {
+      const int64_t e = fe + (lane - V);  // the tail [fe, e1)
+      if (e < e1) dst[e] = sr[e - a0];
+    }
+    sync();
   };
 
   T gv[NMAX];
   T wv[W ? NMAX : 1];
   T yv[NMAX];
-  bool has_long = false;
   if (staged) {
-    has_long = __syncthreads_or(active && my1 - my0 > NMAX);
-    for (int k = tid; k < WORDS; k += THREADS) own[k] = 0u;
-    stage_in(g);
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < NMAX; ++c) {
-      if (c < len) gv[c] = stg[sh + rel + c];
-    }
-    if (has_long && len > 0) {  // mark this row's elements (at most two words)
-      const uint32_t mask = len >= 32 ? 0xFFFFFFFFu : ((1u << len) - 1u);
-      const int bit = rel + b0;
-      atomicOr(&own[bit >> 5], mask << (bit & 31));
-      if ((bit & 31) + len > 32) atomicOr(&own[(bit >> 5) + 1], mask >> (32 - (bit & 31)));
-    }
-    if constexpr (W) {
-      __syncthreads();
-      stage_in(w);
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < len) wv[c] = stg[sh + rel + c];
-      }
-    }
-    if (need_mean) {
-      __syncthreads();
-      stage_in(y);
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < len) yv[c] = stg[sh + rel + c];
-      }
-    }
+    row_in(g, gv);
+    if constexpr (W) row_in(w, wv);
+    if (need_mean) row_in(y, yv);
   } else {
 #pragma unroll
-    for (int c = 0; c < NMAX; ++c) {
-      if (c < len) {
-        gv[c] = g[my0 + c];
-        if constexpr (W) wv[c] = w[my0 + c];
-        if (need_mean) yv[c] = y[my0 + c];
+    for (int c2 = 0; c2 < NMAX; ++c2) {
+      if (c2 < len) {
+        gv[c2] = g[my0 + c2];
+        if constexpr (W) wv[c2] = w[my0 + c2];
+        if (need_mean) yv[c2] = y[my0 + c2];
       }
     }
   }
-
   T oy[NMAX], ow[NMAX];
   row_grad<T, NMAX, W>(gv, wv, yv, bits, len, need_mean, use_lo, lo, use_hi, hi, oy, ow);
   if (staged) {
-    if (gy != nullptr) {
-      __syncthreads();  // every thread has read its values
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < len) stg[sh + rel + c] = oy[c];
-      }
-      __syncthreads();
-      stage_out_range(gy, has_long);
-    }
-    if (gw != nullptr) {
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NMAX; ++c) {
-        if (c < len) stg[sh + rel + c] = ow[c];
-      }
-      __syncthreads();
-      stage_out_range(gw, has_long);
-    }
+    if (gy != nullptr) row_out(gy, oy);
+    if (gw != nullptr) row_out(gw, ow);
   } else {
 #pragma unroll
-    for (int c = 0; c < NMAX; ++c) {
-      if (c < len) {
-        if (gy != nullptr) gy[my0 + c] = oy[c];
-        if (gw != nullptr) gw[my0 + c] = ow[c];
+    for (int c2 = 0; c2 < NMAX; ++c2) {
+      if (c2 < len) {
+        if (gy != nullptr) gy[my0 + c2] = oy[c2];
+        if (gw != nullptr) gw[my0 + c2] = ow[c2];
       }
     }
   }
@@ -1391,9 +1349,8 @@ template <typename T, bool W>
 hipError_t ragged_grad_by_len(const RaggedGradArgs& a) {
   auto go = [&](auto nmax) -> hipError_t {
     constexpr int NMAX = decltype(nmax)::value;
-    constexpr int TH = short_threads<NMAX, W>();
-    const dim3 grid(static_cast<unsigned>((a.nrows + TH - 1) / TH));
-    ragged_grad_kernel<T, NMAX, W><<<grid, dim3(TH), 0, a.stream>>>(
+    const dim3 grid(static_cast<unsigned>((a.nrows + 4 * kWave - 1) / (4 * kWave)));
+    ragged_grad_kernel<T, NMAX, W><<<grid, dim3(4 * kWave), 0, a.stream>>>(
         a.starts, static_cast<const T*>(a.g), static_cast<const T*>(a.w), static_cast<const T*>(a.y),
         static_cast<T*>(a.gy), static_cast<T*>(a.gw), a.offsets, a.nrows, a.total, a.flags, static_cast<T>(a.lo),
         static_cast<T>(a.hi));

@@ -46,11 +46,13 @@ def _host_words(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
     return cache[device.index]
 
 
-def _plan(offsets, lengths, values: Tensor, weighted: bool):
+def _plan(offsets, lengths, values: Tensor, w: Tensor | None, hint: int = 0, increasing: bool = True):
     """The row offsets as a device int64 tensor; zeroed device words for the fit (the flat
-    start bits and the weight flag); and the plan of the offsets under way: one kernel
+    start bits and the weight flag); the plan of the offsets under way: one kernel
     (ti_ragged_plan) checks them and sizes the rows, and four words are on their way to the host
-    (the offsets themselves are never copied whole). ``_plan_wait`` reads them."""
+    (the offsets themselves are never copied whole; ``_plan_wait`` reads them); and, given a
+    bound ``hint`` on the row lengths, the fits of the rows within it, launched right behind the
+    copy of those words so that they run while the host goes on (else None)."""
     if (offsets is None) == (lengths is None):
         raise ValueError("give exactly one of offsets and lengths")
     dev = values.device
@@ -70,13 +72,20 @@ def _plan(offsets, lengths, values: Tensor, weighted: bool):
     # one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
     zeros = torch.zeros(10 + (total + 31) // 32, dtype=torch.int32, device=dev)
     plan, bad, bits = zeros[:8].view(torch.int64), zeros[8:9], zeros[10:]
+    bad = bad if w is not None else None
     host, ready = _host_words(dev)
+    out = None
     with _ext._on_device(dev):
-        _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), _ext._stream(values)),
+        stream = torch.cuda.current_stream(dev)
+        _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), stream.cuda_stream),
                     "isotonic_ragged")
         host.copy_(plan, non_blocking=True)
-        ready.record(torch.cuda.current_stream(dev))
-    return off, bits, (bad if weighted else None), (host, ready, offsets is None, total)
+        ready.record(stream)
+        # (after the copy in the stream: the host's wait for the words does not wait for the fit)
+        if hint > 0 and total > 0:
+            out = torch.empty_like(values)
+            _fit_short(values, w, out, off, min(hint, _SHORT), bits, bad, increasing)
+    return off, bits, bad, (host, ready, offsets is None, total), out
 
 
 def _plan_wait(off: Tensor, pending) -> tuple[int, list[tuple[int, int]]]:
@@ -101,7 +110,8 @@ def _plan_wait(off: Tensor, pending) -> tuple[int, list[tuple[int, int]]]:
 def _offsets(offsets, lengths, values: Tensor, weighted: bool):
     """``_plan`` and ``_plan_wait`` in a row: the offsets, validated, the longest short row, the
     longer rows, and the zeroed bits and weight flag."""
-    off, bits, bad, pending = _plan(offsets, lengths, values, weighted)
+    # (with no bound, _plan reads nothing of w but whether there is one)
+    off, bits, bad, pending, _ = _plan(offsets, lengths, values, values if weighted else None)
     short_max, long_rows = _plan_wait(off, pending)
     return off, short_max, long_rows, bits, bad
 
@@ -146,24 +156,30 @@ def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spa
     return out, long_rows
 
 
+def _finish(values: Tensor, w: Tensor | None, off: Tensor, bits: Tensor, bad: Tensor | None, pending: tuple,
+            hint: int, increasing: bool) -> tuple[Tensor, int, list]:
+    """The fit after ``_plan``: the plan's words read (its errors raised), the short rows fitted
+    (where ``_plan`` did not already, within the bound ``hint``, fit them all: rows past the bound
+    and at most 32 long take a second launch over every short row, which writes the same values
+    and bits again), the longer rows fitted one by one, the weight flag checked."""
+    plan, out = pending
+    nmax = min(hint, _SHORT) if out is not None else 0
+    if out is None:
+        out = torch.empty_like(values)
+    short_max, long_spans = _plan_wait(off, plan)
+    if short_max > nmax:
+        _fit_short(values, w, out, off, short_max, bits, bad, increasing)
+    long_rows = _fit_long(values, w, out, long_spans, increasing)
+    if bad is not None and short_max > 0 and bool(bad.item()):
+        raise ValueError("weight must be strictly positive")
+    return out, short_max, long_rows
+
+
 class _RaggedFit(torch.autograd.Function):
     @staticmethod
     def forward(ctx, values: Tensor, w: Tensor | None, off: Tensor, bits: Tensor,  # type: ignore[override]
                 bad: Tensor | None, pending: tuple, hint: int, increasing: bool) -> Tensor:
-        # Given a bound on the rows' lengths, the short rows' launch goes first (the kernel clamps
-        # every offset, so it may run on offsets not yet checked) and runs while the host waits
-        # for the plan; rows past the bound (and at most 32 long) take a second launch over every
-        # short row, which writes the same values and bits again.
-        out = torch.empty_like(values)
-        nmax = min(hint, _SHORT)
-        if nmax > 0:
-            _fit_short(values, w, out, off, nmax, bits, bad, increasing)
-        short_max, long_spans = _plan_wait(off, pending)
-        if short_max > nmax:
-            _fit_short(values, w, out, off, short_max, bits, bad, increasing)
-        long_rows = _fit_long(values, w, out, long_spans, increasing)
-        if bad is not None and short_max > 0 and bool(bad.item()):
-            raise ValueError("weight must be strictly positive")
+        out, short_max, long_rows = _finish(values, w, off, bits, bad, pending, hint, increasing)
         ctx.increasing = increasing
         ctx.long_rows = long_rows
         ctx.short_max = short_max
@@ -236,11 +252,15 @@ def isotonic_ragged(
         w = weight.to(device=values.device, dtype=acc).contiguous()
     if max_len is not None and (isinstance(max_len, bool) or not isinstance(max_len, int) or max_len < 0):
         raise ValueError("max_len must be a non-negative int")
-    off, bits, bad, pending = _plan(offsets, lengths, values, w is not None)
+    hint = max_len or 0
+    off, bits, bad, pending, out = _plan(offsets, lengths, v, w, hint, increasing)
     if values.numel() == 0:
         _plan_wait(off, pending)  # (the offsets' errors)
         return values.to(out_dtype, copy=True)
-    fit = _RaggedFit.apply(v, w, off, bits, bad, pending, max_len or 0, increasing)
+    if torch.is_grad_enabled() and (v.requires_grad or (w is not None and w.requires_grad)):
+        fit = _RaggedFit.apply(v, w, off, bits, bad, (pending, out), hint, increasing)
+    else:
+        fit = _finish(v, w, off, bits, bad, (pending, out), hint, increasing)[0]
     if y_min is not None or y_max is not None:
         fit = fit.clamp(min=y_min, max=y_max)
     return fit.to(out_dtype)
