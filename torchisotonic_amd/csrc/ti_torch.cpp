@@ -19,7 +19,9 @@
 #include <torch/csrc/autograd/custom_function.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <optional>
+#include <vector>
 
 #include "torchisotonic_amd.h"
 
@@ -217,8 +219,177 @@ at::Tensor isotonic_fit(const at::Tensor& y, const std::optional<at::Tensor>& w,
   return IsotonicFn::apply(y, w, increasing, y_min, y_max);
 }
 
+// Per thread and device: the pinned host words a ragged set's plan is copied into, and the event
+// recorded once they are there. (Kept until the process ends.)
+struct RaggedHost {
+  hipEvent_t ready = nullptr;
+  int64_t* words = nullptr;
+};
+
+RaggedHost& ragged_host(c10::DeviceIndex dev) {
+  thread_local RaggedHost per_device[64];
+  TORCH_CHECK(dev >= 0 && dev < 64, "torchisotonic_amd: device index ", static_cast<int>(dev), " out of range");
+  RaggedHost& rh = per_device[dev];
+  if (rh.ready == nullptr) {
+    check_hip(hipEventCreateWithFlags(&rh.ready, hipEventDisableTiming), "hipEventCreateWithFlags");
+    void* p = nullptr;
+    check_hip(hipHostMalloc(&p, 4 * sizeof(int64_t), hipHostMallocDefault), "hipHostMalloc");
+    rh.words = static_cast<int64_t*>(p);
+  }
+  return rh;
+}
+
+constexpr int64_t kRaggedShort = 32;  // the longest rows ti_fwd_ragged fits
+
+// Ragged rows (rows packed end to end, offsets on the device) with their backward in C++, the
+// calls of ragged.py's steps in one operator: the offsets' plan (ti_ragged_plan) and the copy of
+// its four words to the host; given a bound max_len on the row lengths, the short rows' fit
+// (ti_fwd_ragged, which clamps every offset it reads) launched right behind that copy, so that
+// it runs while the host waits for the words; the wait and the offsets' errors; a second launch
+// over every short row where rows past the bound are at most 32 long; the longer rows one by one
+// (ti_fwd, each with its own workspace, kept for its backward). The backward is one launch for
+// the short rows (ti_bwd_ragged) and ti_bwd for each longer row.
+struct RaggedFn : public torch::autograd::Function<RaggedFn> {
+  static at::Tensor forward(AutogradContext* ctx, const at::Tensor& values, const std::optional<at::Tensor>& w_opt,
+                            const at::Tensor& offsets, bool increasing, int64_t max_len, bool from_lengths) {
+    TORCH_CHECK(values.is_cuda() && values.dim() == 1 && values.is_contiguous(),
+                "torchisotonic_amd.isotonic_ragged_fit: values must be 1-D, contiguous, on a ROCm device");
+    TORCH_CHECK(offsets.dim() == 1 && offsets.numel() >= 1 && offsets.scalar_type() == at::kLong &&
+                    offsets.is_contiguous() && offsets.device() == values.device(),
+                "torchisotonic_amd.isotonic_ragged_fit: offsets must be 1-D int64, contiguous, on values' device");
+    const at::Tensor w = w_opt.has_value() ? *w_opt : at::Tensor();
+    if (w.defined()) {
+      TORCH_CHECK(w.sizes() == values.sizes() && w.scalar_type() == values.scalar_type() &&
+                      w.device() == values.device() && w.is_contiguous(),
+                  "torchisotonic_amd.isotonic_ragged_fit: weight must match values");
+    }
+    const int dtype = dtype_code(values);
+    const int64_t nrows = offsets.numel() - 1, total = values.numel();
+    const int64_t esize = values.element_size();
+    const c10::DeviceGuard guard(values.device());
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(values.device().index()).stream();
+    const unsigned flags = (increasing ? TI_INCREASING : 0u) | TI_EXACT;
+
+    // one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
+    at::Tensor zeros = at::zeros({10 + (total + 31) / 32}, values.options().dtype(at::kInt));
+    int32_t* zp = zeros.data_ptr<int32_t>();
+    int64_t* plan = reinterpret_cast<int64_t*>(zp);
+    uint32_t* bad = w.defined() ? reinterpret_cast<uint32_t*>(zp + 8) : nullptr;
+    uint32_t* bits = reinterpret_cast<uint32_t*>(zp + 10);
+    RaggedHost& rh = ragged_host(values.device().index());
+    check(ti_ragged_plan(offsets.data_ptr<int64_t>(), nrows, total, plan, stream), "isotonic_ragged");
+    check_hip(hipMemcpyAsync(rh.words, plan, 4 * sizeof(int64_t), hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+    check_hip(hipEventRecord(rh.ready, stream), "hipEventRecord");
+    at::Tensor out = at::empty_like(values);
+    const int64_t nmax = max_len > 0 ? std::min(max_len, kRaggedShort) : 0;
+    auto fit_short = [&](int64_t m) {
+      check(ti_fwd_ragged(ptr(values), ptr(w), ptr(out), bits, bad, offsets.data_ptr<int64_t>(), nrows, total, m,
+                          dtype, flags, 0.0, 0.0, stream),
+            "isotonic_ragged");
+    };
+    if (nmax > 0 && total > 0 && nrows > 0) fit_short(nmax);
+    check_hip(hipEventSynchronize(rh.ready), "hipEventSynchronize");
+    const int64_t err = rh.words[0], short_max = rh.words[1], n_long = rh.words[2];
+    TORCH_CHECK_VALUE((err & 4) == 0, from_lengths ? "lengths must be non-negative" : "offsets must not decrease");
+    TORCH_CHECK_VALUE((err & 3) == 0, "offsets must run from 0 to values.numel() = ", total);
+    if (short_max > nmax) fit_short(short_max);
+    // the longer rows, each by the regular path on its slice of the packed arrays
+    std::vector<int64_t> spans;
+    std::vector<at::Tensor> keep;  // each longer row's starts and forward workspace
+    if (n_long > 0) {
+      const at::Tensor len = offsets.slice(0, 1) - offsets.slice(0, 0, nrows);
+      const at::Tensor r = at::nonzero(len > kRaggedShort).view(-1);
+      const at::Tensor se = at::stack({offsets.index_select(0, r), offsets.index_select(0, r + 1)}, 1).cpu();
+      const int64_t* sp = se.data_ptr<int64_t>();
+      for (int64_t i = 0; i < se.size(0); ++i) {
+        const int64_t a = sp[2 * i], n = sp[2 * i + 1] - a;
+        at::Tensor starts = at::empty({ti_starts_words(1, n)}, values.options().dtype(at::kInt));
+        at::Tensor ws = workspace(true, 1, n, dtype, w.defined(), values.device());
+        char* yb = static_cast<char*>(values.data_ptr()) + a * esize;
+        char* wb = w.defined() ? static_cast<char*>(w.data_ptr()) + a * esize : nullptr;
+        check(ti_fwd(yb, wb, static_cast<char*>(out.data_ptr()) + a * esize, static_cast<uint32_t*>(starts.data_ptr()),
+                     bad, 1, n, dtype, flags, 0.0, 0.0, ptr(ws), ws.defined() ? static_cast<size_t>(ws.numel()) : 0,
+                     stream),
+              "isotonic_ragged");
+        spans.push_back(a);
+        spans.push_back(n);
+        keep.push_back(starts);
+        keep.push_back(ws);
+      }
+    }
+    if (bad != nullptr && (short_max > 0 || n_long > 0)) {
+      TORCH_CHECK_VALUE(zeros.slice(0, 8, 9).item<int32_t>() == 0, "weight must be strictly positive");
+    }
+    if (values.requires_grad() || (w.defined() && w.requires_grad())) {
+      std::vector<at::Tensor> saved = {values, w, offsets, zeros};
+      saved.insert(saved.end(), keep.begin(), keep.end());
+      ctx->save_for_backward(saved);
+      ctx->saved_data["spans"] = c10::List<int64_t>(spans);
+      ctx->saved_data["p"] = c10::List<int64_t>({short_max, increasing ? 1 : 0, w.defined() ? 1 : 0});
+    }
+    return out;
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const c10::List<int64_t> prm = ctx->saved_data["p"].toIntList();
+    const int64_t short_max = prm.get(0);
+    const unsigned flags = (prm.get(1) != 0 ? TI_INCREASING : 0u) | TI_EXACT;
+    const bool has_w = prm.get(2) != 0;
+    const c10::List<int64_t> spans = ctx->saved_data["spans"].toIntList();
+    const bool want_y = ctx->needs_input_grad(0), want_w = has_w && ctx->needs_input_grad(1);
+    variable_list none(6);
+    if (!want_y && !want_w) return none;
+    const variable_list saved = ctx->get_saved_variables();
+    const at::Tensor& values = saved[0];
+    const at::Tensor& w = saved[1];
+    const at::Tensor& offsets = saved[2];
+    const at::Tensor& zeros = saved[3];
+    const at::Tensor g = grads[0].contiguous().to(values.scalar_type());
+    const int dtype = dtype_code(values);
+    const int64_t nrows = offsets.numel() - 1, total = values.numel();
+    const int64_t esize = values.element_size();
+    const c10::DeviceGuard guard(values.device());
+    const hipStream_t stream = c10::hip::getCurrentHIPStream(values.device().index()).stream();
+    // (every element belongs to a row: the short rows' elements are written by one launch, the
+    // longer rows' by their own backward)
+    at::Tensor gy = at::empty_like(g);
+    at::Tensor gw = want_w ? at::empty_like(g) : at::Tensor();
+    const uint32_t* bits = reinterpret_cast<const uint32_t*>(zeros.data_ptr<int32_t>() + 10);
+    if (short_max > 0) {
+      check(ti_bwd_ragged(bits, ptr(g), ptr(w), want_w ? ptr(values) : nullptr, ptr(gy), ptr(gw),
+                          offsets.data_ptr<int64_t>(), nrows, total, short_max, dtype, 0u, 0.0, 0.0, stream),
+            "isotonic_ragged backward");
+    }
+    auto at_ = [&](const at::Tensor& t, int64_t a) -> char* {
+      return t.defined() ? static_cast<char*>(t.data_ptr()) + a * esize : nullptr;
+    };
+    for (size_t i = 0; i * 2 < spans.size(); ++i) {
+      const int64_t a = spans.get(2 * i), n = spans.get(2 * i + 1);
+      const at::Tensor& starts = saved[4 + 2 * i];
+      const at::Tensor& ws = saved[5 + 2 * i];
+      at::Tensor bws = workspace(false, 1, n, dtype, w.defined(), values.device());
+      check(ti_bwd(static_cast<const uint32_t*>(starts.data_ptr()), ptr(ws),
+                   ws.defined() ? static_cast<size_t>(ws.numel()) : 0, at_(g, a), at_(w, a),
+                   want_w ? at_(values, a) : nullptr, at_(gy, a), want_w ? at_(gw, a) : nullptr, 1, n, dtype, flags,
+                   0.0, 0.0, ptr(bws), bws.defined() ? static_cast<size_t>(bws.numel()) : 0, stream),
+            "isotonic_ragged backward");
+    }
+    none[0] = want_y ? gy : at::Tensor();
+    none[1] = gw;
+    return none;
+  }
+};
+
+at::Tensor isotonic_ragged_fit(const at::Tensor& values, const std::optional<at::Tensor>& w, const at::Tensor& offsets,
+                               bool increasing, int64_t max_len, bool from_lengths) {
+  return RaggedFn::apply(values, w, offsets, increasing, max_len, from_lengths);
+}
+
 }  // namespace
 
 TORCH_LIBRARY(torchisotonic_amd, m) {
   m.def("isotonic_fit(Tensor y, Tensor? w, bool increasing, float? y_min, float? y_max) -> Tensor", &isotonic_fit);
+  m.def("isotonic_ragged_fit(Tensor values, Tensor? w, Tensor offsets, bool increasing, int max_len, "
+        "bool from_lengths) -> Tensor",
+        &isotonic_ragged_fit);
 }

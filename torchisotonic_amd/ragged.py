@@ -18,6 +18,11 @@ and the row offsets (CSR layout) go to the GPU as they are:
   gradients from their own forward's hulls (``ti_bwd``).
 
 The clamp to [y_min, y_max] is torch.clamp after the fit, as in the reference (_api.py:68-69).
+These steps, and the backward, run in one C++ operator with its autograd node
+(``torch.ops.torchisotonic_amd.isotonic_ragged_fit``, csrc/ti_torch.cpp): a call costs a few
+microseconds of host time, where the same steps in Python and a Python autograd node cost more
+than the kernels. The functions below compose the same C ABI calls step by step; the tests use
+them to read the start bits.
 """
 
 from __future__ import annotations
@@ -46,46 +51,43 @@ def _host_words(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
     return cache[device.index]
 
 
-def _plan(offsets, lengths, values: Tensor, w: Tensor | None, hint: int = 0, increasing: bool = True):
+def _plan(offsets, lengths, values: Tensor, weighted: bool):
     """The row offsets as a device int64 tensor; zeroed device words for the fit (the flat
-    start bits and the weight flag); the plan of the offsets under way: one kernel
+    start bits and the weight flag); and the plan of the offsets under way: one kernel
     (ti_ragged_plan) checks them and sizes the rows, and four words are on their way to the host
-    (the offsets themselves are never copied whole; ``_plan_wait`` reads them); and, given a
-    bound ``hint`` on the row lengths, the fits of the rows within it, launched right behind the
-    copy of those words so that they run while the host goes on (else None)."""
-    if (offsets is None) == (lengths is None):
-        raise ValueError("give exactly one of offsets and lengths")
-    dev = values.device
-    src = offsets if offsets is not None else lengths
-    t = src if isinstance(src, Tensor) else torch.as_tensor(src)
-    if t.ndim != 1 or t.is_floating_point() or t.is_complex() or t.dtype == torch.bool:
-        raise ValueError("offsets / lengths must be a 1-D integer sequence")
-    t = t.to(device=dev, dtype=torch.int64)
-    if offsets is None:
-        off = torch.zeros(t.numel() + 1, dtype=torch.int64, device=dev)
-        torch.cumsum(t, 0, out=off[1:])
-    else:
-        if t.numel() < 1:
-            raise ValueError("offsets must hold at least one value")
-        off = t.contiguous()
+    (the offsets themselves are never copied whole; ``_plan_wait`` reads them)."""
+    off = _offsets_tensor(offsets, lengths, values.device)
     nrows, total = off.numel() - 1, values.numel()
     # one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
-    zeros = torch.zeros(10 + (total + 31) // 32, dtype=torch.int32, device=dev)
+    zeros = torch.zeros(10 + (total + 31) // 32, dtype=torch.int32, device=values.device)
     plan, bad, bits = zeros[:8].view(torch.int64), zeros[8:9], zeros[10:]
-    bad = bad if w is not None else None
-    host, ready = _host_words(dev)
-    out = None
-    with _ext._on_device(dev):
-        stream = torch.cuda.current_stream(dev)
+    host, ready = _host_words(values.device)
+    with _ext._on_device(values.device):
+        stream = torch.cuda.current_stream(values.device)
         _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), stream.cuda_stream),
                     "isotonic_ragged")
         host.copy_(plan, non_blocking=True)
         ready.record(stream)
-        # (after the copy in the stream: the host's wait for the words does not wait for the fit)
-        if hint > 0 and total > 0:
-            out = torch.empty_like(values)
-            _fit_short(values, w, out, off, min(hint, _SHORT), bits, bad, increasing)
-    return off, bits, bad, (host, ready, offsets is None, total), out
+    return off, bits, (bad if weighted else None), (host, ready, offsets is None, total)
+
+
+def _offsets_tensor(offsets, lengths, device: torch.device) -> Tensor:
+    """The row offsets as a contiguous device int64 tensor (from ``lengths`` by a cumulative
+    sum); type errors raised, the values checked by the plan."""
+    if (offsets is None) == (lengths is None):
+        raise ValueError("give exactly one of offsets and lengths")
+    src = offsets if offsets is not None else lengths
+    t = src if isinstance(src, Tensor) else torch.as_tensor(src)
+    if t.ndim != 1 or t.is_floating_point() or t.is_complex() or t.dtype == torch.bool:
+        raise ValueError("offsets / lengths must be a 1-D integer sequence")
+    t = t.to(device=device, dtype=torch.int64)
+    if offsets is None:
+        off = torch.zeros(t.numel() + 1, dtype=torch.int64, device=device)
+        torch.cumsum(t, 0, out=off[1:])
+        return off
+    if t.numel() < 1:
+        raise ValueError("offsets must hold at least one value")
+    return t.contiguous()
 
 
 def _plan_wait(off: Tensor, pending) -> tuple[int, list[tuple[int, int]]]:
@@ -110,8 +112,7 @@ def _plan_wait(off: Tensor, pending) -> tuple[int, list[tuple[int, int]]]:
 def _offsets(offsets, lengths, values: Tensor, weighted: bool):
     """``_plan`` and ``_plan_wait`` in a row: the offsets, validated, the longest short row, the
     longer rows, and the zeroed bits and weight flag."""
-    # (with no bound, _plan reads nothing of w but whether there is one)
-    off, bits, bad, pending, _ = _plan(offsets, lengths, values, values if weighted else None)
+    off, bits, bad, pending = _plan(offsets, lengths, values, weighted)
     short_max, long_rows = _plan_wait(off, pending)
     return off, short_max, long_rows, bits, bad
 
@@ -156,67 +157,6 @@ def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spa
     return out, long_rows
 
 
-def _finish(values: Tensor, w: Tensor | None, off: Tensor, bits: Tensor, bad: Tensor | None, pending: tuple,
-            hint: int, increasing: bool) -> tuple[Tensor, int, list]:
-    """The fit after ``_plan``: the plan's words read (its errors raised), the short rows fitted
-    (where ``_plan`` did not already, within the bound ``hint``, fit them all: rows past the bound
-    and at most 32 long take a second launch over every short row, which writes the same values
-    and bits again), the longer rows fitted one by one, the weight flag checked."""
-    plan, out = pending
-    nmax = min(hint, _SHORT) if out is not None else 0
-    if out is None:
-        out = torch.empty_like(values)
-    short_max, long_spans = _plan_wait(off, plan)
-    if short_max > nmax:
-        _fit_short(values, w, out, off, short_max, bits, bad, increasing)
-    long_rows = _fit_long(values, w, out, long_spans, increasing)
-    if bad is not None and short_max > 0 and bool(bad.item()):
-        raise ValueError("weight must be strictly positive")
-    return out, short_max, long_rows
-
-
-class _RaggedFit(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, values: Tensor, w: Tensor | None, off: Tensor, bits: Tensor,  # type: ignore[override]
-                bad: Tensor | None, pending: tuple, hint: int, increasing: bool) -> Tensor:
-        out, short_max, long_rows = _finish(values, w, off, bits, bad, pending, hint, increasing)
-        ctx.increasing = increasing
-        ctx.long_rows = long_rows
-        ctx.short_max = short_max
-        ctx.has_w = w is not None
-        ctx.save_for_backward(values, w if w is not None else torch.empty(0, device=values.device), off, bits)
-        return out
-
-    @staticmethod
-    def backward(ctx, g: Tensor):  # type: ignore[override]
-        values, w, off, bits = ctx.saved_tensors
-        w = w if ctx.has_w else None
-        want_y = ctx.needs_input_grad[0]
-        want_w = ctx.has_w and ctx.needs_input_grad[1]
-        if not want_y and not want_w:
-            return (None,) * 8
-        g = g.contiguous().to(values.dtype)
-        # (every element belongs to a row: the short rows' elements are written by one launch,
-        # the longer rows' by their own backward below)
-        gy = torch.empty_like(g)
-        gw = torch.empty_like(g) if want_w else None
-        if ctx.short_max > 0:
-            with _ext._on_device(values.device):
-                rc = _ext.load().ti_bwd_ragged(
-                    bits.data_ptr(), g.data_ptr(), _ext._ptr(w), values.data_ptr() if want_w else None,
-                    gy.data_ptr(), _ext._ptr(gw), off.data_ptr(), off.numel() - 1, values.numel(),
-                    ctx.short_max, _ext._dtype_code(values), 0, 0.0, 0.0, _ext._stream(values),
-                )
-            _ext._check(rc, "isotonic_ragged backward")
-        for a, b, starts, ws in ctx.long_rows:
-            ry, rw = _ext.grad(starts, ws, g[a:b].view(1, b - a), None if w is None else w[a:b].view(1, b - a),
-                               values[a:b].view(1, b - a), True, want_w, increasing=ctx.increasing)
-            gy[a:b] = ry.view(b - a)
-            if want_w:
-                gw[a:b] = rw.view(b - a)
-        return (gy if want_y else None), gw, None, None, None, None, None, None
-
-
 def isotonic_ragged(
     values: Tensor,
     offsets: Tensor | None = None,
@@ -252,15 +192,10 @@ def isotonic_ragged(
         w = weight.to(device=values.device, dtype=acc).contiguous()
     if max_len is not None and (isinstance(max_len, bool) or not isinstance(max_len, int) or max_len < 0):
         raise ValueError("max_len must be a non-negative int")
-    hint = max_len or 0
-    off, bits, bad, pending, out = _plan(offsets, lengths, v, w, hint, increasing)
+    off = _offsets_tensor(offsets, lengths, values.device)
+    fit = _ext.ops().isotonic_ragged_fit(v, w, off, increasing, max_len or 0, offsets is None)
     if values.numel() == 0:
-        _plan_wait(off, pending)  # (the offsets' errors)
         return values.to(out_dtype, copy=True)
-    if torch.is_grad_enabled() and (v.requires_grad or (w is not None and w.requires_grad)):
-        fit = _RaggedFit.apply(v, w, off, bits, bad, (pending, out), hint, increasing)
-    else:
-        fit = _finish(v, w, off, bits, bad, (pending, out), hint, increasing)[0]
     if y_min is not None or y_max is not None:
         fit = fit.clamp(min=y_min, max=y_max)
     return fit.to(out_dtype)
