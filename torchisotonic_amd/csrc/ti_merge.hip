@@ -73,22 +73,24 @@ __device__ __forceinline__ bool vpools(const VPt& a, const VPt& b, const VPt& c)
   return pools<true>(dS1, dW1, dS2, dW2);
 }
 
-// The vertex of B[1 .. cB) touched by the lower tangent from p (the last of equal slopes).
-template <bool W>
-__device__ int vtangent(const VArr& v, const VPt& p, int bb, int cB) {
+// The vertex of B[1 .. cB) touched by the lower tangent from p (the last of equal slopes);
+// getB(j) is B's vertex j.
+template <bool W, class GB>
+__device__ int vtangent(const VPt& p, GB getB, int cB) {
   int lo = 1, hi = cB - 1;
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    if (!vpools<W>(p, vload<W>(v, bb + mid), vload<W>(v, bb + mid + 1))) hi = mid;
+    if (!vpools<W>(p, getB(mid), getB(mid + 1))) hi = mid;
     else lo = mid + 1;
   }
   return lo;
 }
 
-// Bridge of hulls A = [ba, ba + cA) and B = [bb, bb + cB) sharing their boundary point; the
-// merged hull is A[0 .. keep) ++ B[from .. cB). (Same method as the tile kernel's.)
-template <bool W>
-__device__ void vbridge(const VArr& v, int ba, int cA, int bb, int cB, int& keep, int& from) {
+// Bridge of hulls A (cA vertices, getA(i) its vertex i) and B (cB, getB(j)) sharing their
+// boundary point (A's last is B's first); the merged hull is A[0 .. keep) ++ B[from .. cB).
+// (Same method as the tile kernel's.)
+template <bool W, class GA, class GB>
+__device__ void vbridge(GA getA, int cA, GB getB, int cB, int& keep, int& from) {
   if (cB <= 1) {
     keep = cA;
     from = cB;
@@ -99,9 +101,9 @@ __device__ void vbridge(const VArr& v, int ba, int cA, int bb, int cB, int& keep
     from = 0;
     return;
   }
-  VPt a = vload<W>(v, ba + cA - 2);
-  const VPt x = vload<W>(v, ba + cA - 1);
-  VPt b = vload<W>(v, bb + 1);
+  VPt a = getA(cA - 2);
+  const VPt x = getA(cA - 1);
+  VPt b = getB(1);
   if (!vpools<W>(a, x, b)) {
     keep = cA;
     from = 1;
@@ -109,17 +111,17 @@ __device__ void vbridge(const VArr& v, int ba, int cA, int bb, int cB, int& keep
   }
   int i = cA - 2, j = 1;
   bool done = false;
-  VPt ap = i > 0 ? vload<W>(v, ba + i - 1) : a;
-  VPt bn = j + 1 < cB ? vload<W>(v, bb + j + 1) : b;
+  VPt ap = i > 0 ? getA(i - 1) : a;
+  VPt bn = j + 1 < cB ? getB(j + 1) : b;
   for (int steps = 0; steps < 24; ++steps) {
     if (i > 0 && vpools<W>(ap, a, b)) {
       --i;
       a = ap;
-      if (i > 0) ap = vload<W>(v, ba + i - 1);
+      if (i > 0) ap = getA(i - 1);
     } else if (j + 1 < cB && vpools<W>(a, b, bn)) {
       ++j;
       b = bn;
-      if (j + 1 < cB) bn = vload<W>(v, bb + j + 1);
+      if (j + 1 < cB) bn = getB(j + 1);
     } else {
       done = true;
       break;
@@ -129,13 +131,13 @@ __device__ void vbridge(const VArr& v, int ba, int cA, int bb, int cB, int& keep
     int lo = 0, hi = cA - 2;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      const VPt am = vload<W>(v, ba + mid);
-      const int t = vtangent<W>(v, am, bb, cB);
-      if (vpools<W>(am, vload<W>(v, ba + mid + 1), vload<W>(v, bb + t))) hi = mid;
+      const VPt am = getA(mid);
+      const int t = vtangent<W>(am, getB, cB);
+      if (vpools<W>(am, getA(mid + 1), getB(t))) hi = mid;
       else lo = mid + 1;
     }
     i = lo;
-    j = vtangent<W>(v, vload<W>(v, ba + lo), bb, cB);
+    j = vtangent<W>(getA(lo), getB, cB);
   }
   keep = i + 1;
   from = j;
@@ -314,97 +316,140 @@ __device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, MergeRounds&
 }
 
 // The merge in the parent's global array, for children with more vertices than LDS holds
-// (hulls of trend-like data, where few vertices drop): children laid end to end, then pairwise
-// rounds of bridges (one lane per pair) and moves of each right part's surviving suffix.
+// (hulls of trend-like data, where few vertices drop), by reference to the children's own
+// vertices: child c keeps a range [rlo[c], rhi[c]) of its vertices (without its first for
+// c > 0: that is child c - 1's last), pairwise rounds find each bridge (one lane a pair) on the
+// concatenations of those ranges and only shorten the ranges, and one pass then writes the
+// survivors into the parent's array. A merge of segments A and B (runs of children) bridges A
+// with its first point in front (for a segment after the first: the previous segment keeps
+// that point) and B with A's last point in front, so both are whole convex chains. The pass
+// writes in increasing slot order, a chunk read before any of it is written: child c lies at
+// a fixed offset in the parent's range, c times a child's capacity, and the survivors laid
+// end to end never take a slot above their vertex's own, so no write lands on a vertex still
+// to be read. (Copying the children end to end and moving each right part's survivors down,
+// round after round, moved every vertex several times through one workgroup.)
 template <bool W, bool PR, int NT>
 __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int64_t row, int64_t c0, int nch,
                              const NodeOut& pout) {
+  __shared__ int rlo[kGroup], rhi[kGroup], pre[kGroup];
   const int tid = threadIdx.x;
-  const int total = sm.total;
   const VArr v = dvarr_of(pout);
-  // The children end to end, in the parent's frame, where they lie (the parent's vertices take
-  // the place of its children's): slot s comes from its child's vertex at or after s, so NT slots
-  // at a time, read before any is written, in increasing order, never overwrite a vertex still to
-  // be read.
-  // (B slots a thread, their loads in flight together: near-monotone data leaves hulls of
-  // millions of vertices, and a slot at a time made this loop a chain of round trips to memory)
-  constexpr int B = 4;
-  for (int s0 = 0; s0 < total; s0 += NT * B) {
-    VPt p[B];
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const int s = s0 + u * NT + tid;
-      if (s < total) {
-        const int c = child_of_slot(sm, nch, s);
-        const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, s - sm.off[c]);
-        p[u].i = h.i;
-        p[u].s = DD{h.s, h.sl};
-        p[u].w = DD{h.w, h.wl};
+  for (int c = tid; c < nch; c += NT) {
+    rlo[c] = c == 0 ? 0 : 1;
+    rhi[c] = sm.cnt[c];
+  }
+  __syncthreads();
+  auto vertex = [&](int c, int k) -> VPt {
+    const HPt h = child_vertex<W, PR>(a, sm, row, c0, c, k);
+    VPt p;
+    p.i = h.i;
+    p.s = DD{h.s, h.sl};
+    p.w = W ? DD{h.w, h.wl} : DD{static_cast<double>(h.i), 0.0};
+    return p;
+  };
+  // vertex i of the concatenation of children [c_lo, c_hi)'s ranges (pre[]: the kept vertices
+  // before each child within it): the last child whose count before it is at most i
+  auto kept = [&](int c_lo, int c_hi, int i) -> VPt {
+    int lo = c_lo, hi = c_hi - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    return vertex(lo, rlo[lo] + (i - pre[lo]));
+  };
+#pragma unroll 1
+  for (int span = 1; span < nch; span <<= 1) {
+    const int nm = (nch + 2 * span - 1) / (2 * span);  // merges this round
+    for (int m = tid; m < nm; m += NT) {
+      const int pa = m * 2 * span, pb = pa + span;
+      if (pb >= nch) continue;
+      const int pe = min(pb + span, nch);
+      int nA = 0, nB = 0;
+      for (int c = pa; c < pb; ++c) {
+        pre[c] = nA;
+        nA += rhi[c] - rlo[c];
+      }
+      for (int c = pb; c < pe; ++c) {
+        pre[c] = nB;
+        nB += rhi[c] - rlo[c];
+      }
+      const int s0 = pa > 0 ? 1 : 0;  // A's first point in front
+      const VPt first = vertex(pa, 0);
+      const int cA = s0 + nA, cB = 1 + nB;
+      auto getA = [&](int i) -> VPt { return (s0 != 0 && i == 0) ? first : kept(pa, pb, i - s0); };
+      auto getB = [&](int j) -> VPt { return j == 0 ? getA(cA - 1) : kept(pb, pe, j - 1); };
+      int keep = cA, from = 1;
+      vbridge<W>(getA, cA, getB, cB, keep, from);
+      // A keeps its first a_keep kept vertices, B drops its first b_drop
+      int left = from == 0 ? nA : keep - s0;
+      for (int c = pa; c < pb; ++c) {
+        const int k = rhi[c] - rlo[c];
+        if (left >= k) {
+          left -= k;
+        } else {
+          rhi[c] = rlo[c] + max(left, 0);
+          left = 0;
+        }
+      }
+      int drop = from > 1 ? from - 1 : 0;
+      for (int c = pb; c < pe; ++c) {
+        const int k = rhi[c] - rlo[c];
+        if (drop >= k) {
+          rlo[c] = rhi[c];
+          drop -= k;
+        } else {
+          rlo[c] += drop;
+          drop = 0;
+        }
       }
     }
     __syncthreads();
+  }
+  // the survivors, in slot order
+  if (tid == 0) {
+    int t = 0;
+    for (int c = 0; c < nch; ++c) {
+      pre[c] = t;
+      t += rhi[c] - rlo[c];
+    }
+    sm.total = t;
+  }
+  __syncthreads();
+  // Batches of NT * B slots: batch k's slots lie below every source of batch k + 1 (a survivor's
+  // slot is never above its vertex's own), so batch k + 1 is read while batch k is written; a
+  // batch is read by every thread (the barrier) before any of its slots is written.
+  const int total = sm.total;
+  constexpr int B = (W || PR) ? 4 : 8;
+  auto load = [&](int s0, VPt (&p)[B]) {
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int s = s0 + u * NT + tid;
+      if (s < total) p[u] = kept(0, nch, s);
+    }
+  };
+  auto store = [&](int s0, const VPt (&p)[B]) {
 #pragma unroll
     for (int u = 0; u < B; ++u) {
       const int s = s0 + u * NT + tid;
       if (s < total) vstore<W>(v, s, p[u]);
     }
+  };
+  VPt pa[B], pb[B];
+  load(0, pa);
+  __syncthreads();
+  for (int s0 = 0; s0 < total;) {
+    load(s0 + NT * B, pb);
+    store(s0, pa);
     __syncthreads();
+    s0 += NT * B;
+    if (s0 >= total) break;
+    load(s0 + NT * B, pa);
+    store(s0, pb);
+    __syncthreads();
+    s0 += NT * B;
   }
-#pragma unroll 1
-  for (int span = 1; span < nch; span <<= 1) {
-    const int nm = (nch + 2 * span - 1) / (2 * span);  // merges this round
-    if (tid < nm) {
-      const int pa = tid * 2 * span, pb = pa + span;
-      int keep = sm.cnt[pa], from = 0;
-      if (pb < nch) vbridge<W>(v, sm.off[pa], sm.cnt[pa], sm.off[pb], sm.cnt[pb], keep, from);
-      sm.keep[tid] = keep;
-      sm.from[tid] = from;
-    }
-    __syncthreads();
-    // Move each right part's kept suffix next to its left part's kept prefix (every thread: NT / nm
-    // a merge).
-    const int gsz = NT / nm >= 1 ? NT / nm : 1;
-    const int m = tid / gsz;
-    const int r = tid - m * gsz;
-    int len = 0, src = 0, dst = 0;
-    if (m < nm) {
-      const int pa = m * 2 * span, pb = pa + span;
-      if (pb < nch) {
-        len = sm.cnt[pb] - sm.from[m];
-        src = sm.off[pb] + sm.from[m];
-        dst = sm.off[pa] + sm.keep[m];
-        if (src == dst) len = 0;
-      }
-    }
-    if (tid == 0) sm.rounds_max = 0;
-    __syncthreads();
-    constexpr int R = 4;
-    const int my_rounds = (len + gsz * R - 1) / (gsz * R);
-    if (my_rounds > 0) atomicMax(&sm.rounds_max, my_rounds);
-    __syncthreads();
-    const int rounds = sm.rounds_max;
-    for (int rd = 0; rd < rounds; ++rd) {  // reads, then writes: src is never below dst
-      VPt buf[R];
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int jj = rd * gsz * R + q * gsz + r;
-        if (jj < len) buf[q] = vload<W>(v, src + jj);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int jj = rd * gsz * R + q * gsz + r;
-        if (jj < len) vstore<W>(v, dst + jj, buf[q]);
-      }
-      __syncthreads();
-    }
-    if (tid < nm) {
-      const int pa = tid * 2 * span, pb = pa + span;
-      if (pb < nch) sm.cnt[pa] = sm.keep[tid] + (sm.cnt[pb] - sm.from[tid]);
-    }
-    __syncthreads();
-  }
-  if (tid == 0) *pout.count = sm.cnt[0];
+  if (tid == 0) *pout.count = total;
 }
 
 // One workgroup of NT threads per parent node: G = 64 children (fewer at a row's end) -> the
