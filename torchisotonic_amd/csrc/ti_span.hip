@@ -24,6 +24,7 @@
 //
 // Output: the span hulls as the first node array of the cross-span merge (ti_merge.hip).
 #include "ti_common.h"
+#include "ti_gmerge.h"
 #include "ti_kernels.h"
 #include "ti_slots.h"
 #include "ti_tile.h"
@@ -393,8 +394,49 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
   static_assert(!(W && !PR) || sizeof(SpanLds<T, W, 2 * C, R>) == 20480, "weighted float32: 20 KB a wave");
   if (nslots > kCap) {
-    // too many vertices: the span's hull goes to the span array, for the merge kernel
+    // Too many vertices for the wave's LDS: the spans' hulls go to the span array, and (one row
+    // a wave) the group merges them there by reference to them (merge_global, its round state in
+    // the wave's LDS, free now), so that no merge launch is needed for the first level; a
+    // multi-row wave's spans are merged by the merge kernel.
     write_span_hull();
+    if (multi) return;
+    const DD pw{__shfl_up(iw.hi, 1, kSpanLanes), __shfl_up(iw.lo, 1, kSpanLanes)};
+    const DD ps{__shfl_up(is.hi, 1, kSpanLanes), __shfl_up(is.lo, 1, kSpanLanes)};
+    const bool gbad = __any(active && bad);
+    __syncthreads();  // (every lane's hull written, and its ring read, before the LDS is reused)
+    char* const gm = reinterpret_cast<char*>(&L);
+    MergeSmall& sm = *reinterpret_cast<MergeSmall*>(gm);
+    MergeRanges& mr = *reinterpret_cast<MergeRanges*>(gm + ((sizeof(MergeSmall) + 63) & ~size_t(63)));
+    static_assert(((sizeof(MergeSmall) + 63) & ~size_t(63)) + sizeof(MergeRanges) <= sizeof(SpanLds<T, W, 2 * C, R>),
+                  "the global merge's round state fits the wave's LDS");
+    if (lane < nch) {
+      sm.cnt[lane] = depth;
+      sm.tot[0][lane] = lane == 0 ? 0.0 : pw.hi;
+      sm.tot[1][lane] = lane == 0 ? 0.0 : pw.lo;
+      sm.tot[2][lane] = lane == 0 ? 0.0 : ps.hi;
+      sm.tot[3][lane] = lane == 0 ? 0.0 : ps.lo;
+    }
+    if (lane == nch - 1) {
+      sm.tot[0][nch] = iw.hi;
+      sm.tot[1][nch] = iw.lo;
+      sm.tot[2][nch] = is.hi;
+      sm.tot[3][nch] = is.lo;
+    }
+    __syncthreads();
+    MergeArgs ma;
+    ma.in = a.hulls;
+    ma.out = a.hulls1;
+    ma.child_elems = a.span0;
+    const NodeOut gout = node_out(a.hulls1, W, blockIdx.x);
+    merge_global<W, true, kSpanLanes>(ma, sm, mr.rlo, mr.rhi, mr.pre, row, grp * kSpanLanes, nch, gout);
+    if (lane == 0) {
+      *gout.bad = gbad ? 1 : 0;
+      gout.tot[0] = sm.tot[0][nch];
+      gout.tot[1] = sm.tot[1][nch];
+      gout.tot[2] = sm.tot[2][nch];
+      gout.tot[3] = sm.tot[3][nch];
+      *o.count = -1;  // (the group is merged: its first span's count says so to the merge kernel)
+    }
     return;
   }
   // offsets of this lane's span within the group
