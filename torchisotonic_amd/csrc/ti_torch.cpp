@@ -143,8 +143,9 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
       check_hip(hipEventSynchronize(keep ? wc.hulls : wc.event), "hipEventSynchronize");
       TORCH_CHECK_VALUE(!w.defined() || *static_cast<volatile uint32_t*>(wc.host) == 0u,
                         "weight must be strictly positive");
-      if (keep) {
-        const int64_t mv = *static_cast<volatile int64_t*>(wc.maxv_host);
+      const int64_t mv = keep ? *static_cast<volatile int64_t*>(wc.maxv_host) : 0;
+      // (a bound not written, which the event's system-scope release rules out: keep the workspace)
+      if (mv >= 1) {
         size_t kbytes = 0;
         check(ti_keep_bytes(batch, n, dtype, w.defined() ? 1 : 0, mv, &kbytes), "keep_bytes");
         // (hulls nearly as large as the workspace: keep the workspace itself)
