@@ -190,6 +190,23 @@ def test_float32_store_rounding_keeps_the_fit_monotone() -> None:
     close_grad(gw, ew, 1e-5)
 
 
+@pytest.mark.parametrize(("batch", "n"), [(80, 100_000), (300, 40_000), (1100, 20_000)])
+def test_float32_store_rounding_many_rows(batch: int, n: int) -> None:
+    # The same near-collinear data over many rows: with 256 rows or more the last merge launch's
+    # workgroups (256 and 64 threads here, one a row) make their rows' hulls convex in the stored
+    # values themselves; with fewer, the check and repair launches do.
+    say(f"float32 store rounding: {batch} weighted near-collinear rows of {n}")
+    rng = np.random.default_rng(11)
+    i = np.arange(n, dtype=np.float64)
+    y = (1e3 + 1e-3 * i + 1e-7 * rng.standard_normal((batch, n))).astype(np.float32)
+    w = np.exp(8 * rng.random((batch, n))).astype(np.float32)
+    assert _ext.geometry(batch, n, True)["levels"] == 2
+    got, starts = gpu_fit(y, w)
+    assert (np.diff(got, axis=1) >= 0).all()
+    want, _ = oracle.pava(y.astype(np.float64), w.astype(np.float64))
+    assert float(np.abs(got - want).max()) <= tolerance(y)
+
+
 # --- exact ties with inexact cross products ------------------------------------------------------
 
 # (batch, n): short rows, one row a lane ("packed"), several rows a wave, one row a wave, and rows

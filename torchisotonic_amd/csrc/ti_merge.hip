@@ -35,7 +35,9 @@ namespace {
 // Float32 data keeps its hull sums rounded to float64 in the vertex store (NodeOut). Rounded one
 // by one, a hull that the double-double merges found convex can turn slightly non-convex in the
 // stored values where points are nearly collinear, and the fit (its slopes) would step down
-// there. Each final hull is made convex in the stored values, in two launches:
+// there. Each final hull is made convex in the stored values: by the workgroup that merged it
+// (repair_row, at the end of the last merge launch) where rows end two or more merge levels up
+// and are many, else in two launches after the merges:
 //
 //   convex_check_kernel  `chunks` workgroups a row test every vertex against its neighbours; a
 //                        vertex on or above the chord between them marks its row (flag = the
@@ -63,36 +65,56 @@ __global__ __launch_bounds__(kRepairThreads) void convex_check_kernel(NodeLevel 
   if (found) flag[row] = epoch;
 }
 
+// (field by field, and without the weights of unweighted rows, which vpools takes from the
+// indices: whole-struct copies between LDS and registers went through scratch memory)
 template <bool W>
-__global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, unsigned epoch,
-                                                                const unsigned* __restrict__ flag) {
-  __shared__ int any;
-  __shared__ int wcount[kRepairThreads / kWave];
-  __shared__ VPt tile[kRepairThreads + 2];
-  __shared__ VPt prev;  // the original vertex before the chunk
+__device__ __forceinline__ void vput(VPt& d, const VPt& x) {
+  d.i = x.i;
+  d.s.hi = x.s.hi;
+  d.s.lo = x.s.lo;
+  if constexpr (W) {
+    d.w.hi = x.w.hi;
+    d.w.lo = x.w.lo;
+  }
+}
+
+// A workgroup of NT threads removes, pass after pass, every vertex of the row's hull `o` on or
+// above the chord between its neighbours, until none is (the first pass is the check). LDS:
+// tile[NT + 2], wcount[NT / 64], any.
+template <bool W, int NT>
+__device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int64_t row = blockIdx.x;
-  if (flag[row] != epoch) return;  // (convex already)
-  const NodeOut o = node_out(fin, W, row);
-  if (*o.bad != 0) return;
   const VArr v = dvarr_of(o);
   int cnt = *o.count;
   for (int pass = 0; pass < 64; ++pass) {
     if (tid == 0) any = 0;
     __syncthreads();
+    // (four vertices a thread at a time, all their reads in flight together: a row's hull can
+    // have as many vertices as elements)
     bool found = false;
-    for (int i = 1 + tid; i < cnt - 1; i += kRepairThreads)
-      found |= vpools<W>(vload<W>(v, i - 1), vload<W>(v, i), vload<W>(v, i + 1));
+    for (int i0 = 1 + tid; i0 < cnt - 1; i0 += 4 * NT) {
+      VPt a[4], b[4], c[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * NT, cnt - 2);
+        a[u] = vload<W>(v, i - 1);
+        b[u] = vload<W>(v, i);
+        c[u] = vload<W>(v, i + 1);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) found |= vpools<W>(a[u], b[u], c[u]);
+    }
     if (__any(found) && lane == 0) any = 1;
     __syncthreads();
     if (any == 0) break;
     int base = 0;
-    for (int c0 = 0; c0 < cnt; c0 += kRepairThreads) {
+    VPt last;  // (thread NT - 1: the previous chunk's last original vertex)
+    for (int c0 = 0; c0 < cnt; c0 += NT) {
       const int i = c0 + tid;
-      if (i < cnt) tile[tid + 1] = vload<W>(v, i);
-      if (tid == 0) {
-        if (c0 > 0) tile[0] = prev;
-        if (c0 + kRepairThreads < cnt) tile[kRepairThreads + 1] = vload<W>(v, c0 + kRepairThreads);
+      if (i < cnt) vput<W>(tile[tid + 1], vload<W>(v, i));
+      if (tid == NT - 1) {
+        if (c0 > 0) vput<W>(tile[0], last);
+        if (c0 + NT < cnt) vput<W>(tile[NT + 1], vload<W>(v, c0 + NT));
       }
       __syncthreads();
       const bool keep = i < cnt && (i == 0 || i == cnt - 1 || !vpools<W>(tile[tid], tile[tid + 1], tile[tid + 2]));
@@ -100,12 +122,13 @@ __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, u
       if (lane == 0) wcount[wave] = __popcll(m);
       __syncthreads();
       int before = base, all = 0;
-      for (int k = 0; k < kRepairThreads / kWave; ++k) {
+      for (int k = 0; k < NT / kWave; ++k) {
         before += k < wave ? wcount[k] : 0;
         all += wcount[k];
       }
-      const VPt x = tile[tid + 1];
-      if (tid == kRepairThreads - 1) prev = x;  // (read in the next chunk, after its barrier)
+      VPt x;
+      vput<W>(x, tile[tid + 1]);
+      if (tid == NT - 1) vput<W>(last, x);
       __syncthreads();  // every read of this chunk's slots is done
       if (keep) vstore<W>(v, before + __popcll(m & ((uint64_t{1} << lane) - 1)), x);
       base += all;
@@ -114,6 +137,19 @@ __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, u
     __syncthreads();
   }
   if (tid == 0) *o.count = cnt;
+}
+
+template <bool W>
+__global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, unsigned epoch,
+                                                                const unsigned* __restrict__ flag) {
+  __shared__ int any;
+  __shared__ int wcount[kRepairThreads / kWave];
+  __shared__ VPt tile[kRepairThreads + 2];
+  const int64_t row = blockIdx.x;
+  if (flag[row] != epoch) return;  // (convex already)
+  const NodeOut o = node_out(fin, W, row);
+  if (*o.bad != 0) return;
+  repair_row<W, kRepairThreads>(o, tile, wcount, any);
 }
 
 // Per merge: the children (vertex counts, first slots, offsets within the parent) and the
@@ -162,8 +198,16 @@ __device__ void merge_lds(const MergeArgs& a, const MergeSmall& sm, MergeRounds&
 // One workgroup of NT threads per parent node: G = 64 children (fewer at a row's end) -> the
 // parent's hull. NT grows where few parents share the GPU (the upper levels), so that their
 // larger hulls still take few slots per thread.
+// Rows enough for their final merge workgroups to read their hulls at the GPU's bandwidth.
+constexpr bool batch_fills_gpu(int64_t batch) { return batch >= 256; }
+
+// LDS repair_row takes with NT threads (carved from a merge kernel's slots once they are free).
+constexpr size_t repair_lds_bytes(int nt) { return (nt + 2) * sizeof(VPt) + (nt / kWave + 1) * sizeof(int); }
+
+// fix: the launch makes the final hulls of float32 data, which the workgroup then makes convex in
+// their stored values (repair_row), so no check launch follows.
 template <bool W, bool PR, int NT, int G>
-__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
+__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int fix) {
   __shared__ MergeSmall sm;
   __shared__ MergeRounds rs;
   extern __shared__ __align__(16) char lds_dyn[];
@@ -237,6 +281,12 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds) {
     pout.tot[1] = sm.tot[1][nch];
     pout.tot[2] = sm.tot[2][nch];
     pout.tot[3] = sm.tot[3][nch];
+  }
+  if (fix != 0 && sm.bad == 0) {
+    __syncthreads();  // the hull written by every thread, the slots read
+    VPt* tile = reinterpret_cast<VPt*>(lds_dyn);
+    int* wcount = reinterpret_cast<int*>(tile + NT + 2);
+    repair_row<W, NT>(pout, tile, wcount, wcount[NT / kWave]);
   }
 }
 
@@ -816,6 +866,11 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     return t.hulls_ready != nullptr ? hipEventRecord(t.hulls_ready, t.stream) : hipSuccess;
   };
   if ((e = report(0)) != hipSuccess) return e;
+  // Float32 data: the final hulls made convex in their stored values. A final level of two or more
+  // launches up has a merge workgroup for every row, which does it at its end (fold) where rows
+  // are enough to spread those workgroups over the GPU (one workgroup reading a hull of millions
+  // of vertices would take milliseconds); otherwise two launches after the merges do.
+  const bool fold = !p.lo && p.levels >= 2 && batch_fills_gpu(t.batch);
   for (int l = 1; l <= p.levels; ++l) {
     // (one row a wave: the span kernel merged every group, in LDS or, where its hulls do not
     // fit, in the group's global array; a multi-row wave's overflowing spans wait for a launch)
@@ -831,14 +886,16 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     // Workgroup size and LDS slots by how many merges share the GPU: one wave and 768 slots
     // (64 noisy span hulls take 300-500) where there are thousands, else 256 or 1024 threads
     // and up to 56 KB of slots for the fewer, larger hulls of the upper levels.
+    // (the final level of float32 data repairs its hulls in the merge launch: fold)
+    const int fix = fold && l == p.levels ? 1 : 0;
     auto launch = [&](auto k64, auto k256, auto k1024, size_t vb) {
       const int big = static_cast<int>((56 * 1024 / vb) & ~size_t(63));
       if (grid >= 1024) {
-        k64<<<dim3(grid), dim3(64), 768 * vb, t.stream>>>(m, 768);
+        k64<<<dim3(grid), dim3(64), std::max(768 * vb, repair_lds_bytes(64)), t.stream>>>(m, 768, fix);
       } else if (grid >= 64) {
-        k256<<<dim3(grid), dim3(256), big * vb, t.stream>>>(m, big);
+        k256<<<dim3(grid), dim3(256), std::max(big * vb, repair_lds_bytes(256)), t.stream>>>(m, big, fix);
       } else {
-        k1024<<<dim3(grid), dim3(1024), big * vb, t.stream>>>(m, big);
+        k1024<<<dim3(grid), dim3(1024), std::max(big * vb, repair_lds_bytes(1024)), t.stream>>>(m, big, fix);
       }
     };
 #define TI_MERGE_LAUNCH(Wv, PRv)                                                                 \
@@ -852,7 +909,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     if (e != hipSuccess) return e;
     if ((e = report(l)) != hipSuccess) return e;
   }
-  if (!p.lo && p.levels >= 1) {
+  if (!p.lo && p.levels >= 1 && !fold) {
     // (float32 data: the final hulls convex in their stored values; span hulls, the final hulls
     // of rows of one span, are exact and convex already). Enough check workgroups a row for a
     // hull of every element (4096 vertices each), at most 256.
