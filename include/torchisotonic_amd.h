@@ -46,6 +46,11 @@ extern "C" {
 #define TI_EXACT 2u      /* reference's exact= flag; this library is always exact (see ti_fwd) */
 #define TI_CLIP_MIN 4u   /* clamp the fit from below at y_min */
 #define TI_CLIP_MAX 8u   /* clamp the fit from above at y_max */
+/* A hint for rows over one tile (ti_fwd and its variants; ignored elsewhere): the fit is written
+   with non-temporal stores, its cache lines leaving for memory as they are written, for a caller
+   whose next kernels read other data (a backward): they then do not wait behind its write-back.
+   The results are the same with or without it. */
+#define TI_STREAM_OUT 16u
 
 /* The ABI version this library was built with (TI_ABI_VERSION). */
 int ti_abi_version(void);

@@ -341,7 +341,9 @@ __global__ __launch_bounds__(256) void rank_kernel(NodeLevel hulls, int64_t batc
 constexpr int kExpandTiles = 4;
 
 // Per tile: the fit from the row's final hull.
-template <typename T, bool W>
+// NTS: the fit written with non-temporal stores (TI_STREAM_OUT), its lines leaving the caches
+// as they are written instead of draining under the next kernel's reads.
+template <typename T, bool W, bool NTS>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       // fewer vertices than tiles): the edge's slope from the record, no LDS, no barriers. The
       // only possible start is the tile's first element.
       const T val = row_bad ? quiet_nan<T>() : tsgn * static_cast<T>(rec[u].slope);
-      fill_elems<T, E, NT>(out, len, tid, clip(val, use_lo, lo, use_hi, hi));
+      fill_elems<T, E, NT, NTS>(out, len, tid, clip(val, use_lo, lo, use_hi, hi));
       write_starts((t0 == 0 && (rec[u].flags & kTileHead)) ? 1u : 0u);
       continue;
     }
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       const T val = row_bad ? quiet_nan<T>() : sl[jj];
       fit[k] = clip(val, use_lo, lo, use_hi, hi);
     }
-    store_elems_any<T, E>(out + t0, ecount, fit);
+    store_elems_any<T, E, NTS>(out + t0, ecount, fit);
     write_starts(row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits);
     __syncthreads();  // sl, bits and rank_scan are reused by the next tile
   }
@@ -981,12 +983,14 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   x.lo = t.lo;
   x.hi = t.hi;
   const unsigned grid = static_cast<unsigned>((t.batch * p.tiles_per_row + kExpandTiles - 1) / kExpandTiles);
+  auto go = [&](auto k) { k<<<dim3(grid), dim3(256), 0, t.stream>>>(x); };
+  const bool nts = (t.flags & TI_STREAM_OUT) != 0;
   if (t.dtype == TI_F32) {
-    if (W) expand_kernel<float, true><<<dim3(grid), dim3(256), 0, t.stream>>>(x);
-    else expand_kernel<float, false><<<dim3(grid), dim3(256), 0, t.stream>>>(x);
+    if (W) nts ? go(expand_kernel<float, true, true>) : go(expand_kernel<float, true, false>);
+    else nts ? go(expand_kernel<float, false, true>) : go(expand_kernel<float, false, false>);
   } else {
-    if (W) expand_kernel<double, true><<<dim3(grid), dim3(256), 0, t.stream>>>(x);
-    else expand_kernel<double, false><<<dim3(grid), dim3(256), 0, t.stream>>>(x);
+    if (W) nts ? go(expand_kernel<double, true, true>) : go(expand_kernel<double, true, false>);
+    else nts ? go(expand_kernel<double, false, true>) : go(expand_kernel<double, false, false>);
   }
   return hipGetLastError();
 }

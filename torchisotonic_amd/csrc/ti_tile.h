@@ -166,7 +166,8 @@ __device__ __forceinline__ void load_elems_any(const T* __restrict__ p, int coun
   }
 }
 
-template <typename T, int E>
+// (NTS: non-temporal 16-byte stores, whose lines leave the caches as they are written)
+template <typename T, int E, bool NTS = false>
 __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, const T (&v)[E]) {
   constexpr int V = 16 / sizeof(T);
   using VT = T __attribute__((ext_vector_type(V)));
@@ -177,7 +178,8 @@ __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, co
       VT x;
 #pragma unroll
       for (int t = 0; t < V; ++t) x[t] = v[j * V + t];
-      q[j] = x;
+      if constexpr (NTS) __builtin_nontemporal_store(x, q + j);
+      else q[j] = x;
     }
   } else {
 #pragma unroll
@@ -190,7 +192,7 @@ __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, co
 // Fills p[0, len) with f from the NT threads of a workgroup, each store instruction of a wave on
 // one contiguous run of 16-byte pieces (len <= NT * E). The elements before the first 16-byte
 // boundary are written singly.
-template <typename T, int E, int NT>
+template <typename T, int E, int NT, bool NTS = false>
 __device__ __forceinline__ void fill_elems(T* __restrict__ p, int len, int tid, T f) {
   constexpr int V = 16 / sizeof(T);
   using VT = T __attribute__((ext_vector_type(V)));
@@ -205,7 +207,8 @@ __device__ __forceinline__ void fill_elems(T* __restrict__ p, int len, int tid, 
   for (int j = 0; j < E / V; ++j) {
     const int k = (j * NT + tid) * V;
     if (k + V <= rest) {
-      *reinterpret_cast<VT*>(q + k) = x;
+      if constexpr (NTS) __builtin_nontemporal_store(x, reinterpret_cast<VT*>(q + k));
+      else *reinterpret_cast<VT*>(q + k) = x;
     } else {
 #pragma unroll
       for (int t = 0; t < V; ++t)

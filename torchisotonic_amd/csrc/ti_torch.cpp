@@ -115,6 +115,9 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
     const hipStream_t stream = c10::hip::getCurrentHIPStream(yc.device().index()).stream();
     const bool want = y.requires_grad() || (w.defined() && w_opt->requires_grad());
     const unsigned flags = flags_of(increasing, y_min, y_max);
+    // (a backward is expected: the fit streams out, so the backward's first reads do not wait
+    // behind its write-back)
+    const unsigned fit_flags = flags | (want ? TI_STREAM_OUT : 0u);
 
     at::Tensor out = at::empty_like(yc);
     at::Tensor starts;
@@ -127,7 +130,7 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
     at::Tensor kept;
     if (!w.defined() && !keep) {
       check(ti_fwd(ptr(yc), nullptr, ptr(out), static_cast<uint32_t*>(ptr(starts)), nullptr, batch, n, dtype,
-                   flags, lo, hi, ptr(ws), ws_bytes, stream),
+                   fit_flags, lo, hi, ptr(ws), ws_bytes, stream),
             "fit");
     } else {
       WeightCheck& wc = weight_check(yc.device().index());
@@ -137,7 +140,7 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
       *static_cast<volatile int64_t*>(wc.maxv_host) = 0;
       // keeping the hulls: one wait, for the hulls (the weights were read before them)
       check(ti_fwd_ev_hulls(ptr(yc), ptr(w), ptr(out), static_cast<uint32_t*>(ptr(starts)),
-                            w.defined() ? wc.dev : nullptr, batch, n, dtype, flags, lo, hi, ptr(ws), ws_bytes, stream,
+                            w.defined() ? wc.dev : nullptr, batch, n, dtype, fit_flags, lo, hi, ptr(ws), ws_bytes, stream,
                             keep ? nullptr : wc.event, keep ? wc.hulls : nullptr, keep ? wc.maxv_dev : nullptr),
             "fit");
       check_hip(hipEventSynchronize(keep ? wc.hulls : wc.event), "hipEventSynchronize");
