@@ -139,17 +139,60 @@ __device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any) {
   if (tid == 0) *o.count = cnt;
 }
 
+// (repair_row's removal, written out for one 256-thread workgroup a marked row: through
+// repair_row, whose check keeps four vertices a thread in flight, C3's float32 forward took 5 us
+// longer)
 template <bool W>
 __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, unsigned epoch,
                                                                 const unsigned* __restrict__ flag) {
   __shared__ int any;
   __shared__ int wcount[kRepairThreads / kWave];
   __shared__ VPt tile[kRepairThreads + 2];
+  __shared__ VPt prev;  // the original vertex before the chunk
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int64_t row = blockIdx.x;
   if (flag[row] != epoch) return;  // (convex already)
   const NodeOut o = node_out(fin, W, row);
   if (*o.bad != 0) return;
-  repair_row<W, kRepairThreads>(o, tile, wcount, any);
+  const VArr v = dvarr_of(o);
+  int cnt = *o.count;
+  for (int pass = 0; pass < 64; ++pass) {
+    if (tid == 0) any = 0;
+    __syncthreads();
+    bool found = false;
+    for (int i = 1 + tid; i < cnt - 1; i += kRepairThreads)
+      found |= vpools<W>(vload<W>(v, i - 1), vload<W>(v, i), vload<W>(v, i + 1));
+    if (__any(found) && lane == 0) any = 1;
+    __syncthreads();
+    if (any == 0) break;
+    int base = 0;
+    for (int c0 = 0; c0 < cnt; c0 += kRepairThreads) {
+      const int i = c0 + tid;
+      if (i < cnt) tile[tid + 1] = vload<W>(v, i);
+      if (tid == 0) {
+        if (c0 > 0) tile[0] = prev;
+        if (c0 + kRepairThreads < cnt) tile[kRepairThreads + 1] = vload<W>(v, c0 + kRepairThreads);
+      }
+      __syncthreads();
+      const bool keep = i < cnt && (i == 0 || i == cnt - 1 || !vpools<W>(tile[tid], tile[tid + 1], tile[tid + 2]));
+      const uint64_t m = __ballot(keep);
+      if (lane == 0) wcount[wave] = __popcll(m);
+      __syncthreads();
+      int before = base, all = 0;
+      for (int k = 0; k < kRepairThreads / kWave; ++k) {
+        before += k < wave ? wcount[k] : 0;
+        all += wcount[k];
+      }
+      const VPt x = tile[tid + 1];
+      if (tid == kRepairThreads - 1) prev = x;  // (read in the next chunk, after its barrier)
+      __syncthreads();  // every read of this chunk's slots is done
+      if (keep) vstore<W>(v, before + __popcll(m & ((uint64_t{1} << lane) - 1)), x);
+      base += all;
+    }
+    cnt = base;
+    __syncthreads();
+  }
+  if (tid == 0) *o.count = cnt;
 }
 
 // Per merge: the children (vertex counts, first slots, offsets within the parent) and the
