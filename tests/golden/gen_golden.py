@@ -15,7 +15,7 @@ concatenated with an offsets array. Everything is float64 and loads with
 - sklearn_clip.npz: ``sklearn.isotonic.isotonic_regression`` with ``y_min``/``y_max`` (a NaN
   bound means "not given").
 - scipy_long.npz: long structured rows of the reference's tests/test_isotonic.py:103-117
-  patterns (at n = 20000) and their scipy fits.
+  patterns (at n = 20000), inputs ``y`` and their scipy fits ``x``.
 - sklearn_calib.npz: ``sklearn.isotonic.IsotonicRegression`` fit on keys with ties (pooled
   into their weighted mean, as the reference's calibration example does,
   examples/ctr_calibration/calibrate.py:171-187) and its predictions (``out_of_bounds="clip"``,
@@ -152,6 +152,7 @@ def scipy_long() -> None:
     np.savez_compressed(
         HERE / "scipy_long.npz",
         names=np.array(["increasing", "decreasing", "alternating", "constant", "sawtooth"]),
+        y=ys,
         x=xs,
     )
 

@@ -136,6 +136,19 @@ def test_empty_batch_is_a_no_op() -> None:
     assert _ext.load().ti_last_error() == b""
 
 
+def test_noalloc_refuses_sets_beyond_its_scratch() -> None:
+    # ti_fwd_noalloc refuses on the sizes alone, before any device call: here, with no GPU and
+    # null buffers, a missing check would end in a device error instead of TI_EWORKSPACE.
+    lib = _ext.load()
+    size = ctypes.c_size_t(0)
+    batch, n = 1000, 65536
+    assert lib.ti_fwd_workspace(batch, n, _ext.F32, 1, ctypes.byref(size)) == 0
+    assert size.value > 64 << 20
+    rc = lib.ti_fwd_noalloc(None, None, None, None, None, batch, n, _ext.F32, 1, 0.0, 0.0, None)
+    assert rc == 4  # TI_EWORKSPACE
+    assert b"scratch holds" in lib.ti_last_error()
+
+
 def test_bwd_argument_errors() -> None:
     lib = _ext.load()
     def bwd(starts, g, w, y, gy, gw, batch, n, flags, fws=None, fwsb=0, ws=None, wsb=0):

@@ -1,8 +1,8 @@
 """ti_fwd_noalloc (the forward whose workspace is the library's own device scratch array) against
 ti_fwd with a torch-allocated workspace, through the C ABI: bit-identical fits and partitions on
 calls in a row, each later one smaller than the one before (the scratch keeps the previous
-call's contents), and a clear refusal, before any launch, of a set whose workspace exceeds the
-scratch."""
+call's contents). The refusal of a set whose workspace exceeds the scratch is checked without a
+GPU, in tests/test_abi.py: it comes before any device call."""
 
 from __future__ import annotations
 
@@ -74,13 +74,3 @@ def test_noalloc_short_rows_need_no_scratch() -> None:
     assert lib.ti_fwd_noalloc(y.data_ptr(), None, b.data_ptr(), None, None, 1000, 16, 0, 1, 0.0, 0.0, s) == 0
     torch.cuda.synchronize()
     assert torch.equal(a, b)
-
-
-def test_noalloc_refuses_sets_beyond_its_scratch() -> None:
-    lib = _ext.load()
-    batch, n = 1000, 65536
-    assert workspace_bytes(batch, n, _ext.F32, True) > SCRATCH
-    # refused on the sizes alone, before any pointer is used or kernel launched
-    rc = lib.ti_fwd_noalloc(1, 2, 3, None, None, batch, n, _ext.F32, 1, 0.0, 0.0, None)
-    assert rc == 4  # TI_EWORKSPACE
-    assert b"scratch holds" in lib.ti_last_error()
