@@ -51,6 +51,12 @@ extern "C" {
    whose next kernels read other data (a backward): they then do not wait behind its write-back.
    The results are the same with or without it. */
 #define TI_STREAM_OUT 16u
+/* A test hook (ti_fwd and its variants, float32 rows over 32 elements): the repair that makes
+   each final hull convex in its stored float64 values skips its parallel removal passes and
+   finishes every row it repairs with its one-pass sequential monotone chain, the form it
+   otherwise takes only after a cascade of removals longer than its pass limit. The results are
+   the same with or without it. */
+#define TI_REPAIR_CHAIN 32u
 
 /* The ABI version this library was built with (TI_ABI_VERSION). */
 int ti_abi_version(void);
@@ -88,7 +94,8 @@ int ti_fwd_geometry(int64_t batch, int64_t n, int weighted, int64_t* span0, int*
  *           value (and never clear it) if some weight is not > 0, NaN included. This fuses
  *           the reference's separate check bool((w > 0).all()) (reference _api.py:60-61)
  *           into the one read of w; the caller zeroes the word first and reads it afterwards.
- *   flags   TI_INCREASING | TI_EXACT | TI_CLIP_MIN | TI_CLIP_MAX.
+ *   flags   TI_INCREASING | TI_EXACT | TI_CLIP_MIN | TI_CLIP_MAX, and the hints
+ *           TI_STREAM_OUT and TI_REPAIR_CHAIN.
  *   workspace / workspace_bytes: at least ti_fwd_workspace() bytes, 256-byte aligned
  *           (may be NULL when that is 0).
  *   stream  hipStream_t.
@@ -313,8 +320,10 @@ int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t 
  *
  * ti_interp_index_bytes: the index's size for m knots (m < 2^32).
  * ti_interp_index: build it from xp (m knots, ascending) into `index` (256-byte aligned).
- * ti_interp_indexed: ti_interp through an index built from the same xp. An index of other knots
- *   gives wrong values but reads nothing outside x, xp, fp and the index's index_bytes. */
+ * ti_interp_indexed: ti_interp through an index built from the same xp. An index built from
+ *   another knot count or dtype is not used (every query searches all m knots, as ti_interp);
+ *   one of other knots of the same count and dtype gives wrong values but reads nothing outside
+ *   x, xp, fp and the index's index_bytes. */
 int ti_interp_index_bytes(int64_t m, int dtype, size_t* bytes);
 int ti_interp_index(const void* xp, int64_t m, int dtype, void* index, size_t index_bytes,
                     void* stream);

@@ -211,6 +211,35 @@ def test_interp_index_gives_the_full_search_bit_for_bit(dtype: torch.dtype) -> N
         assert torch.equal(_ext.interp(x, xp, fp, index), _plain_interp(x, xp, fp))
 
 
+def test_interp_ignores_an_index_of_other_knots() -> None:
+    # An index built from float64 knots, used with float32 queries and knots (the calibrator's
+    # index with float32 scores), or built from more knots: the kernel must not narrow by it,
+    # so the result is the full search's.
+    say("interp index of another dtype or knot count")
+    rng = np.random.default_rng(23)
+    xp64 = torch.from_numpy(np.unique(rng.random(200_000).astype(np.float32)).astype(np.float64)).cuda()
+    # knots that round onto each other in float32, so float64 buckets misplace float32 values
+    xp64 = torch.sort(torch.cat([xp64, xp64 + 1e-9])).values
+    m = xp64.numel()
+    fp64 = torch.cumsum(torch.rand(m, dtype=torch.float64, device="cuda"), 0)
+    x32 = torch.from_numpy(np.r_[rng.random(100_000), xp64[::7].cpu().numpy()]).float().cuda()
+    xp32, fp32 = xp64.float(), fp64.float()
+    want = _plain_interp(x32, xp32, fp32)
+    lib = _ext.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    # (an index of fewer knots is refused outright: its buffer is smaller than m knots need)
+    with pytest.raises(RuntimeError):
+        _ext.interp(x32, xp32, fp32, _ext.interp_index(xp32[: m // 2]))
+    for idx in (_ext.interp_index(xp64), _ext.interp_index(torch.cat([xp32, xp32 + 2]))):
+        out = torch.empty_like(x32)
+        rc = lib.ti_interp_indexed(x32.data_ptr(), xp32.data_ptr(), fp32.data_ptr(), idx.data_ptr(), idx.numel(),
+                                   out.data_ptr(), x32.numel(), m, _ext.F32, stream)
+        assert rc == 0
+        assert torch.equal(out, want)
+    # through the wrapper, a float64 index with float32 queries is built again in float32
+    assert torch.equal(_ext.interp(x32, xp64, fp64, _ext.interp_index(xp64)), want)
+
+
 def test_calibrator_keeps_its_knot_index() -> None:
     say("calibrator knot index")
     rng = np.random.default_rng(21)

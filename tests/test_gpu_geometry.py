@@ -206,6 +206,25 @@ def test_float32_store_rounding_many_rows(batch: int, n: int) -> None:
     assert float(np.abs(got - want).max()) <= tolerance(y)
 
 
+@pytest.mark.parametrize(("batch", "n"), [(1, 4_000_000), (300, 40_000)])
+def test_float32_repair_chain_gives_the_same_hulls(batch: int, n: int) -> None:
+    # The repair finishes a row with a sequential monotone chain after a cascade of removals
+    # longer than its pass limit; the REPAIR_CHAIN hint takes that form at once (through the
+    # check and repair launches for one row, in the last merge launch for 300). Both keep the
+    # lower hull of the stored points, so fit and partition are the passes' bit for bit.
+    say(f"float32 repair chain: {batch} weighted near-collinear rows of {n}")
+    rng = np.random.default_rng(13)
+    i = np.arange(n, dtype=np.float64)
+    y = torch.from_numpy((1e3 + 1e-3 * i + 1e-7 * rng.standard_normal((batch, n))).astype(np.float32)).cuda()
+    w = torch.from_numpy(np.exp(8 * rng.random((batch, n))).astype(np.float32)).cuda()
+    a, sa, bad_a, _ = _ext.fit(y, w, True, True, True)
+    b, sb, bad_b, _ = _ext.fit(y, w, True, True, True, hints=_ext.REPAIR_CHAIN)
+    assert bad_a is False and bad_b is False
+    assert torch.equal(a, b)
+    assert torch.equal(_ext.starts_to_bool(sa, batch, n), _ext.starts_to_bool(sb, batch, n))
+    assert bool((b[:, 1:] >= b[:, :-1]).all())
+
+
 # --- exact ties with inexact cross products ------------------------------------------------------
 
 # (batch, n): short rows, one row a lane ("packed"), several rows a wave, one row a wave, and rows

@@ -27,6 +27,7 @@ ABI_VERSION = 6
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
+STREAM_OUT, REPAIR_CHAIN = 16, 32  # hints: the results are the same with or without them
 
 _vp, _i64, _int, _uint, _dbl, _sz = (
     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint, ctypes.c_double, ctypes.c_size_t,
@@ -263,6 +264,7 @@ def fit(
     y_min: float | None = None,
     y_max: float | None = None,
     out: Tensor | None = None,
+    hints: int = 0,
 ) -> tuple[Tensor, Tensor, Tensor | None, Tensor | None]:
     """The fit of every row of ``y`` ([batch, n], float32/float64, on the GPU; into ``out`` when
     given, a contiguous tensor of y's shape and dtype), clamped to
@@ -270,7 +272,7 @@ def fit(
     empty tensor); for weighted fits, whether some weight was not positive (the caller raises;
     known once the kernels have read w, which for long rows is before the fit has finished),
     else None; and the workspace, which the backward of rows longer than 32 elements reads (None
-    when the fit needed none)."""
+    when the fit needed none). ``hints``: STREAM_OUT and REPAIR_CHAIN bits passed through."""
     _on_gpu(y, "y")
     dtype = _dtype_code(y)
     if y.dim() != 2:
@@ -291,7 +293,7 @@ def fit(
     )
     bad = torch.zeros(1, dtype=torch.int32, device=y.device) if w is not None else None
     args = (
-        batch, n, dtype, _flags(increasing, exact, y_min, y_max),
+        batch, n, dtype, _flags(increasing, exact, y_min, y_max) | (hints & (STREAM_OUT | REPAIR_CHAIN)),
         float(y_min) if y_min is not None else 0.0,
         float(y_max) if y_max is not None else 0.0,
     )
@@ -376,7 +378,8 @@ def interp(x: Tensor, xp: Tensor, fp: Tensor, index: Tensor | None = None) -> Te
     example's interp (reference examples/ctr_calibration/calibrate.py:163-168) bit for bit.
     x of any shape; xp, fp 1-D of one length, xp ascending. Runs through a knot index
     (``interp_index(xp)``, built here when not given; ti_interp_indexed), whose output is
-    ti_interp's bit for bit."""
+    ti_interp's bit for bit. An index built from ``xp`` in another dtype than ``x``'s is not
+    used: the knots are searched in x's dtype, so the index is built again from those."""
     _on_gpu(x, "x")
     if xp.dim() != 1 or fp.shape != xp.shape or xp.numel() == 0:
         raise RuntimeError("torchisotonic_amd.interp: xp and fp must be 1-D, non-empty and of one length")
@@ -384,7 +387,7 @@ def interp(x: Tensor, xp: Tensor, fp: Tensor, index: Tensor | None = None) -> Te
     xc = x.contiguous()
     xpc = xp.to(device=x.device, dtype=x.dtype).contiguous()
     fpc = fp.to(device=x.device, dtype=x.dtype).contiguous()
-    if index is None:
+    if index is None or xp.dtype != x.dtype:
         index = interp_index(xpc)
     elif index.dtype != torch.uint8 or index.dim() != 1 or index.device != x.device:
         raise RuntimeError("torchisotonic_amd.interp: index must be interp_index's uint8 tensor on x's device")

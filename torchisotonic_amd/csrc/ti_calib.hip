@@ -76,11 +76,17 @@ __global__ __launch_bounds__(256) void interp_kernel(const T* __restrict__ x, co
   }
 }
 
-// The index's header, then first[0..B] (uint32).
+// The index's header, then first[0..B] (uint32). m and dtype name the knots it was built from:
+// a search through an index of another knot count or dtype would narrow to the wrong buckets.
 struct InterpIndex {
   double lo, scale;
-  int64_t buckets, m;
+  int64_t buckets, m, dtype;
 };
+
+template <typename T>
+constexpr int64_t dtype_code() {
+  return sizeof(T) == 4 ? TI_F32 : TI_F64;
+}
 constexpr size_t kIndexHead = 256;
 constexpr int64_t kKnotsPerBucket = 4;
 constexpr int kCountMax = 8;  // buckets of at most this many knots are counted, not searched
@@ -109,6 +115,7 @@ __global__ __launch_bounds__(256) void interp_index_kernel(const T* __restrict__
     head->scale = scale;
     head->buckets = buckets;
     head->m = m;
+    head->dtype = dtype_code<T>();
   }
   if (b > buckets) return;
   int64_t l = 0, h = b == 0 ? 0 : m;
@@ -122,7 +129,8 @@ __global__ __launch_bounds__(256) void interp_index_kernel(const T* __restrict__
 
 // interp_kernel through the index: the bucket's knots [a, c) are counted (at most kCountMax) or
 // searched. The header is read as stored, with the bucket count capped at what the buffer holds
-// (cap) and the bounds clamped to [0, m], so every read stays in the buffers whatever they hold.
+// (cap) and the bounds clamped to [0, m], so every read stays in the buffers whatever they hold;
+// an index built from another knot count or dtype is not used (every query searches all knots).
 template <typename T>
 __global__ __launch_bounds__(256) void interp_indexed_kernel(const T* __restrict__ x, const T* __restrict__ xp,
                                                              const T* __restrict__ fp,
@@ -132,7 +140,7 @@ __global__ __launch_bounds__(256) void interp_indexed_kernel(const T* __restrict
   const double lo = head->lo, scale = head->scale;
   int64_t buckets = head->buckets;
   buckets = buckets < cap ? buckets : cap;
-  const bool indexed = scale > 0.0 && buckets >= 1;
+  const bool indexed = scale > 0.0 && buckets >= 1 && head->m == m && head->dtype == dtype_code<T>();
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
     const T v = x[e];

@@ -78,15 +78,58 @@ __device__ __forceinline__ void vput(VPt& d, const VPt& x) {
   }
 }
 
-// A workgroup of NT threads removes, pass after pass, every vertex of the row's hull `o` on or
-// above the chord between its neighbours, until none is (the first pass is the check). LDS:
-// tile[NT + 2], wcount[NT / 64], any.
+// Parallel removal passes before the repair finishes a row with chain_row instead. Each pass
+// removes every vertex then on or above the chord between its neighbours, so it removes one at
+// least, but a removal can expose its neighbours in turn: a long near-collinear run can need a
+// cascade of passes, each a read of the whole hull.
+constexpr int kRepairPasses = 64;
+
+// The lower hull of the row's `cnt` stored vertices by one monotone chain (the same predicate
+// as the passes, so the same hull: a vertex on or above a chord between two others is on no
+// lower hull, and a convex chain through every lower-hull vertex holds no other). Thread 0
+// pushes and pops in place, writing a vertex at or below its own position, while the workgroup
+// stages the next NT vertices into `tile` (NT + 2 slots); returns the count (in thread 0).
 template <bool W, int NT>
-__device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any) {
+__device__ int chain_row(const VArr& v, int cnt, VPt* tile) {
+  const int tid = threadIdx.x;
+  int top = 0;  // stack entries, at v[0, top); a and b the two at its top
+  VPt a, b;
+  for (int c0 = 0; c0 < cnt; c0 += NT) {
+    const int i = c0 + tid;
+    if (i < cnt) vput<W>(tile[tid], vload<W>(v, i));
+    __syncthreads();
+    if (tid == 0) {
+      const int e = min(NT, cnt - c0);
+      for (int k = 0; k < e; ++k) {
+        VPt p;
+        vput<W>(p, tile[k]);
+        while (top >= 2 && vpools<W>(a, b, p)) {
+          --top;
+          vput<W>(b, a);
+          if (top >= 2) vput<W>(a, vload<W>(v, top - 2));  // (written by this thread before)
+        }
+        vstore<W>(v, top, p);
+        ++top;
+        vput<W>(a, b);
+        vput<W>(b, p);
+      }
+    }
+    __syncthreads();  // (the tile read before it is filled again)
+  }
+  return top;
+}
+
+// A workgroup of NT threads removes, pass after pass, every vertex of the row's hull `o` on or
+// above the chord between its neighbours, until none is (the first pass is the check); after
+// `passes` removal passes the row is finished by chain_row. LDS: tile[NT + 2], wcount[NT / 64],
+// any.
+template <bool W, int NT>
+__device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any, int passes) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const VArr v = dvarr_of(o);
   int cnt = *o.count;
-  for (int pass = 0; pass < 64; ++pass) {
+  bool convex = false;
+  for (int pass = 0; pass <= passes; ++pass) {
     if (tid == 0) any = 0;
     __syncthreads();
     // (four vertices a thread at a time, all their reads in flight together: a row's hull can
@@ -106,7 +149,11 @@ __device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any) {
     }
     if (__any(found) && lane == 0) any = 1;
     __syncthreads();
-    if (any == 0) break;
+    if (any == 0) {
+      convex = true;
+      break;
+    }
+    if (pass == passes) break;  // (still not convex: chain_row below)
     int base = 0;
     VPt last;  // (thread NT - 1: the previous chunk's last original vertex)
     for (int c0 = 0; c0 < cnt; c0 += NT) {
@@ -136,6 +183,7 @@ __device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any) {
     cnt = base;
     __syncthreads();
   }
+  if (!convex) cnt = chain_row<W, NT>(v, cnt, tile);
   if (tid == 0) *o.count = cnt;
 }
 
@@ -144,7 +192,7 @@ __device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any) {
 // longer)
 template <bool W>
 __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, unsigned epoch,
-                                                                const unsigned* __restrict__ flag) {
+                                                                const unsigned* __restrict__ flag, int passes) {
   __shared__ int any;
   __shared__ int wcount[kRepairThreads / kWave];
   __shared__ VPt tile[kRepairThreads + 2];
@@ -156,7 +204,8 @@ __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, u
   if (*o.bad != 0) return;
   const VArr v = dvarr_of(o);
   int cnt = *o.count;
-  for (int pass = 0; pass < 64; ++pass) {
+  bool convex = false;
+  for (int pass = 0; pass <= passes; ++pass) {
     if (tid == 0) any = 0;
     __syncthreads();
     bool found = false;
@@ -164,7 +213,11 @@ __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, u
       found |= vpools<W>(vload<W>(v, i - 1), vload<W>(v, i), vload<W>(v, i + 1));
     if (__any(found) && lane == 0) any = 1;
     __syncthreads();
-    if (any == 0) break;
+    if (any == 0) {
+      convex = true;
+      break;
+    }
+    if (pass == passes) break;  // (still not convex: chain_row below)
     int base = 0;
     for (int c0 = 0; c0 < cnt; c0 += kRepairThreads) {
       const int i = c0 + tid;
@@ -192,6 +245,7 @@ __global__ __launch_bounds__(kRepairThreads) void repair_kernel(NodeLevel fin, u
     cnt = base;
     __syncthreads();
   }
+  if (!convex) cnt = chain_row<W, kRepairThreads>(v, cnt, tile);
   if (tid == 0) *o.count = cnt;
 }
 
@@ -247,8 +301,9 @@ constexpr bool batch_fills_gpu(int64_t batch) { return batch >= 256; }
 // LDS repair_row takes with NT threads (carved from a merge kernel's slots once they are free).
 constexpr size_t repair_lds_bytes(int nt) { return (nt + 2) * sizeof(VPt) + (nt / kWave + 1) * sizeof(int); }
 
-// fix: the launch makes the final hulls of float32 data, which the workgroup then makes convex in
-// their stored values (repair_row), so no check launch follows.
+// fix > 0: the launch makes the final hulls of float32 data, which the workgroup then makes convex
+// in their stored values (repair_row, with fix - 1 removal passes before its chain), so no check
+// launch follows.
 template <bool W, bool PR, int NT, int G>
 __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int fix) {
   __shared__ MergeSmall sm;
@@ -329,7 +384,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int
     __syncthreads();  // the hull written by every thread, the slots read
     VPt* tile = reinterpret_cast<VPt*>(lds_dyn);
     int* wcount = reinterpret_cast<int*>(tile + NT + 2);
-    repair_row<W, NT>(pout, tile, wcount, wcount[NT / kWave]);
+    repair_row<W, NT>(pout, tile, wcount, wcount[NT / kWave], fix - 1);
   }
 }
 
@@ -916,6 +971,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   // are enough to spread those workgroups over the GPU (one workgroup reading a hull of millions
   // of vertices would take milliseconds); otherwise two launches after the merges do.
   const bool fold = !p.lo && p.levels >= 2 && batch_fills_gpu(t.batch);
+  const int repair_passes = (t.flags & TI_REPAIR_CHAIN) != 0 ? 0 : kRepairPasses;
   for (int l = 1; l <= p.levels; ++l) {
     // (one row a wave: the span kernel merged every group, in LDS or, where its hulls do not
     // fit, in the group's global array; a multi-row wave's overflowing spans wait for a launch)
@@ -932,7 +988,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     // (64 noisy span hulls take 300-500) where there are thousands, else 256 or 1024 threads
     // and up to 56 KB of slots for the fewer, larger hulls of the upper levels.
     // (the final level of float32 data repairs its hulls in the merge launch: fold)
-    const int fix = fold && l == p.levels ? 1 : 0;
+    const int fix = fold && l == p.levels ? 1 + repair_passes : 0;
     auto launch = [&](auto k64, auto k256, auto k1024, size_t vb) {
       const int big = static_cast<int>((56 * 1024 / vb) & ~size_t(63));
       if (grid >= 1024) {
@@ -965,10 +1021,10 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     const dim3 cgrid(static_cast<unsigned>(t.batch * chunks)), rgrid(static_cast<unsigned>(t.batch));
     if (W) {
       convex_check_kernel<true><<<cgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, chunks, epoch, flag);
-      repair_kernel<true><<<rgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, epoch, flag);
+      repair_kernel<true><<<rgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, epoch, flag, repair_passes);
     } else {
       convex_check_kernel<false><<<cgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, chunks, epoch, flag);
-      repair_kernel<false><<<rgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, epoch, flag);
+      repair_kernel<false><<<rgrid, dim3(kRepairThreads), 0, t.stream>>>(fin, epoch, flag, repair_passes);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
