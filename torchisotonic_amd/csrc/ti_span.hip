@@ -4,16 +4,16 @@
 // tiles.cuh:665-913, chunk_kernel, which builds small lane hulls and merges them across the
 // block in rounds). A lane instead runs the monotone chain over its whole span by itself: no
 // block-wide scans, no merge rounds, no barriers. The span streams through registers C elements
-// at a time (the next chunk loading meanwhile), in two phases per chunk:
+// at a time (the next block of LC loading meanwhile), in two phases:
 //
-//   1. uniform work: the cumulative sums (float64, relative to the span start; float64 data
-//      also carries their rounding errors, two-sum) at every point of the chunk go to the lane's
-//      LDS chunk buffer, and the candidate points to a bit mask;
-//   2. an event loop in which every lane does one stack operation per iteration on its own
-//      candidates - pop the top vertex, or push the next candidate - reading the top two
-//      vertices and the candidate from LDS. Lanes advance independently, so one lane's run of
-//      pops does not hold the others at a data-dependent loop (a loop per candidate would make
-//      the whole wave wait, at every point, for the lane with the most pops).
+//   1. uniform work per chunk: the cumulative sums (float64, relative to the span start;
+//      float64 data also carries their rounding errors, two-sum) at every point, and the
+//      candidate points appended to the lane's queue of Q slots in LDS;
+//   2. before each chunk, an event loop in which every lane with queued candidates does one
+//      stack operation per iteration - pop the top vertex, or push its next candidate - until
+//      every queue has room for the chunk. Lanes advance independently, so one lane's run of
+//      pops does not hold the others at a data-dependent loop, and a lane's queue lets it fall
+//      behind by up to Q candidates before the wave waits for it.
 //
 // The stack lives in a ring of R LDS slots per lane; positions that fall out of it go to the
 // span's hull array in global memory, where the finished hull ends anyway (noisy data seldom
@@ -48,16 +48,17 @@ struct SpanArgs {
   NodeLevel hulls1;       // the groups' (the first merge level; with rpw > 1, the rows')
 };
 
-// Per lane (columns [slot][lane], so lanes never share a bank row): the chunk buffer (sums at
-// each point of the chunk) and the stack ring. Arrays a configuration does not use have no rows
-// (a zero-length array, which only code under a false `if constexpr` or condition names).
-template <typename T, bool W, int C, int R>
+// Per lane (columns [slot][lane], so lanes never share a bank row): the candidate queue (index
+// and sums of each queued point) and the stack ring. Arrays a configuration does not use have
+// no rows (a zero-length array, which only code under a false `if constexpr` or condition names).
+template <typename T, bool W, int Q, int R>
 struct SpanLds {
   static constexpr bool PR = sizeof(T) == 8;
-  double cs[C][kSpanLanes];
-  double csl[PR ? C : 0][kSpanLanes];
-  double cw[W ? C : 0][kSpanLanes];
-  double cwl[W && PR ? C : 0][kSpanLanes];
+  int qi[Q][kSpanLanes];
+  double qs[Q][kSpanLanes];
+  double qsl[PR ? Q : 0][kSpanLanes];
+  double qw[W ? Q : 0][kSpanLanes];
+  double qwl[W && PR ? Q : 0][kSpanLanes];
   int ri[R][kSpanLanes];
   double rs[R][kSpanLanes];
   double rsl[PR ? R : 0][kSpanLanes];
@@ -66,7 +67,7 @@ struct SpanLds {
   // Weighted float32 runs two waves a SIMD (its registers allow no more), so eight waves share
   // a CU's 160 KB of LDS: the rest of a wave's 20 KB becomes merge slots for the group's merge
   // (C4's groups need up to about 420 slots).
-  char pad[(W && !PR) ? 20480 - (C * 8 * 2 + R * (4 + 8 * 2)) * kSpanLanes : 0];
+  char pad[(W && !PR) ? 20480 - (Q + R) * (4 + 8 * 2) * kSpanLanes : 0];
 };
 
 // N consecutive values at byte offset `off` of a buffer resource, 16 bytes per load. Reads past
@@ -86,10 +87,11 @@ __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t of
   }
 }
 
-template <typename T, bool W, int C, int R, int LC, bool INC>
+template <typename T, bool W, int C, int Q, int R, int LC, bool INC>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
-  static_assert((R & (R - 1)) == 0 && 2 * C <= 32, "ring slots: a power of two; two chunks: a 32-bit mask");
-  static_assert(LC % (2 * C) == 0, "a load block is a whole number of chunk pairs");
+  static_assert((R & (R - 1)) == 0 && (Q & (Q - 1)) == 0 && R >= 4, "ring and queue slots: powers of two");
+  static_assert(C < Q, "a chunk's candidates fit the queue");
+  static_assert(LC % C == 0, "a load block is a whole number of chunks");
   // PR: the span's own sums carry their rounding errors (float64 data). Within a span every
   // test and every later slope uses the same span-relative coordinates, so float32 data needs
   // none there; but a span's vertices moved into a larger frame (the group's, the row's) keep
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // sums cancel, and the fit would step down.
   constexpr bool PR = sizeof(T) == 8;
   static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
-  __shared__ SpanLds<T, W, 2 * C, R> L;  // the chunk buffer holds two chunks
+  __shared__ SpanLds<T, W, Q, R> L;
   const int lane = threadIdx.x;
   // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle);
   // where a row is one span (spr == 1), one row per lane and 64 rows a wave ("packed"): each
@@ -172,35 +174,47 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     return p;
   };
 
+  auto q_put = [&](int q, const HPt& p) {
+    const int r = q & (Q - 1);
+    L.qi[r][lane] = p.i;
+    L.qs[r][lane] = p.s;
+    if constexpr (PR) L.qsl[r][lane] = p.sl;
+    if constexpr (W) L.qw[r][lane] = p.w;
+    if constexpr (W && PR) L.qwl[r][lane] = p.wl;
+  };
+  auto q_get = [&](int q) -> HPt {
+    const int r = q & (Q - 1);
+    HPt p;
+    p.i = L.qi[r][lane];
+    p.s = L.qs[r][lane];
+    p.sl = PR ? L.qsl[PR ? r : 0][lane] : 0.0;
+    p.w = W ? L.qw[W ? r : 0][lane] : 0.0;
+    p.wl = (W && PR) ? L.qwl[(W && PR) ? r : 0][lane] : 0.0;
+    return p;
+  };
+
   // The stack holds positions [0, depth): [r0, depth) in the ring (1 <= depth - r0 <= R), [0, r0)
-  // in the node array.
+  // in the node array. The queue holds the candidates [qh, qt).
   int depth = 1, r0 = 0;
   ring_put(0, HPt{0, 0.0, 0.0, 0.0, 0.0});
+  int qh = 0, qt = 0;
 
   double S = 0.0, SL = 0.0, P = 0.0, PL = 0.0;
   bool bad = false, wbad = false;
-  // Candidates pending in the two chunks in LDS: bits [0, C) the older chunk, [C, 2C) the newer.
-  uint32_t pend = 0;
-  // 2. one stack operation per lane and iteration, until no lane has a candidate left among
-  // `need`; a lane done with those goes on with its later candidates. hk: the ring half (of the
-  // chunk buffer) of the older chunk, ck0 its first element. The loop touches LDS only (and
-  // stores spills), so the next loads stay in flight; a lane whose second vertex went to the
-  // node array makes the wave leave it, refill that lane's ring from the node array, and come
-  // back (rare).
-  auto run = [&](int hk, int ck0, uint32_t need) {
+  // 2. one stack operation per lane and iteration - pop the top vertex B, or push the first
+  // queued candidate c - until every lane holds at most `limit` queued candidates. An iteration's
+  // reads depend on the previous iteration's depth and queue position only, and its one ring
+  // write needs no branch: a push writes c above B, any other lane writes B back into its own
+  // slot (a pop frees it next). The loop touches LDS only (and stores spills), so the next loads
+  // stay in flight; a lane whose second vertex went to the node array makes the wave leave it,
+  // refill that lane's ring from the node array, and come back (rare).
+  auto run = [&](int limit) {
     for (;;) {
-      while (__any((pend & need) != 0)) {
-        const bool act = pend != 0;
+      while (__any(qt - qh > limit)) {
+        const bool act = qt != qh;
         const bool two = act && depth >= 2;
         if (__any(two && depth - 2 < r0)) break;
-        const int j = act ? __builtin_ctz(pend) : 0;
-        const int slot = (hk * C + j) & (2 * C - 1);
-        HPt c;
-        c.i = ck0 + j + 1;
-        c.s = L.cs[slot][lane];
-        c.sl = PR ? L.csl[PR ? slot : 0][lane] : 0.0;
-        c.w = W ? L.cw[W ? slot : 0][lane] : 0.0;
-        c.wl = (W && PR) ? L.cwl[(W && PR) ? slot : 0][lane] : 0.0;
+        const HPt c = q_get(qh);
         const HPt A = ring_get(depth - 2), B = ring_get(depth - 1);
         // pools(A, B, c): a filtered fma test, exact where it cannot decide (see pools<true>)
         double dS1 = B.s - A.s, dS2 = c.s - B.s, dW1, dW2;
@@ -230,19 +244,20 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
           if (two && close) pop = cross_sign(dS1, dW2, dS2, dW1) >= 0;
         }
         const bool push = act && !pop;
-        if (push) {
-          const int q = depth;
-          if (q - r0 == R) {  // the ring is full: its oldest position leaves for the node array
+        if (__any(push && depth - r0 == R)) {
+          // a full ring: its oldest position leaves for the node array
+          asm volatile("");
+          if (push && depth - r0 == R) {
             node_put(r0, ring_get(r0));
             ++r0;
           }
-          ring_put(q, c);
-          pend &= pend - 1;
         }
+        ring_put(push ? depth : depth - 1, hsel(push, c, B));
         depth += push ? 1 : (pop ? -1 : 0);
+        qh += push ? 1 : 0;
       }
-      if (!__any((pend & need) != 0)) break;
-      if (pend != 0 && depth >= 2 && depth - 2 < r0) {
+      if (!__any(qt - qh > limit)) break;
+      if (qt != qh && depth >= 2 && depth - 2 < r0) {
         // only the top is in the ring (depth - 1 == r0): bring back up to R / 2 positions below
         const int lo = r0 > R / 2 ? r0 - R / 2 : 0;
         for (int q = lo; q < r0; ++q) ring_put(q, node_get(q));
@@ -252,11 +267,10 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   };
 
   // loads come in blocks of LC elements (the next block in flight while this one is processed),
-  // processed in chunks of C: the sums of chunk k + 1 go to LDS while chunk k's candidates
-  // remain, so lanes with few candidates in chunk k do not wait idle for the others
+  // processed in chunks of C: before a chunk, the loop makes room in every queue for its
+  // candidates
   T yc[LC], yn[LC];
   T wc[W ? LC : 1], wn[W ? LC : 1];
-  int ck_last = 0;  // the chunk whose candidates stay pending after the loop
   load_block<T, LC>(ry, loff, yc);
   if constexpr (W) load_block<T, LC>(rw, loff, wc);
   for (int b0 = 0; b0 < len; b0 += LC) {
@@ -266,10 +280,10 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 #pragma unroll
     for (int sub = 0; sub < LC; sub += C) {
       const int c0 = b0 + sub;
-      const int h = (sub / C) & 1;  // this chunk's half of the chunk buffer
-      // 1. sums at every point of the chunk, and the candidates
-      uint32_t mask = 0;
-      auto element = [&](int k) {  // sums through element c0 + k, stored for the point after it
+      run(Q - C);
+      // 1. sums at every point of the chunk; each point goes to the queue's next free slot,
+      // which it keeps if it is a candidate (so the stores need no branch)
+      auto element = [&](int k, bool cand) {  // sums through element c0 + k, for the point after it
         const double ye = sgn * static_cast<double>(yc[sub + k]);
         bad |= ye != ye;
         double term = ye;
@@ -292,10 +306,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         } else {
           S += term;
         }
-        L.cs[h * C + k][lane] = S;
-        if constexpr (PR) L.csl[h * C + k][lane] = SL;
-        if constexpr (W) L.cw[h * C + k][lane] = P;
-        if constexpr (W && PR) L.cwl[h * C + k][lane] = PL;
+        q_put(qt, HPt{c0 + k + 1, S, PR ? SL : 0.0, W ? P : 0.0, (W && PR) ? PL : 0.0});
+        qt += cand ? 1 : 0;
       };
       // the point after element e is a candidate where y rises into e + 1, or at the span's end
       auto rises = [&](T u, T v) { return INC ? u < v : v < u; };
@@ -303,35 +315,22 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         // whole chunks (all but a row's last span): no per-element bounds
 #pragma unroll
         for (int k = 0; k < C; ++k) {
-          element(k);
           const int kk = sub + k;
           const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
           // (the span can end only after a chunk's last element here)
-          const bool cand = k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext));
-          mask |= static_cast<uint32_t>(cand) << k;
+          element(k, k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext)));
         }
       } else {
 #pragma unroll
         for (int k = 0; k < C; ++k) {
           const int e = c0 + k;
           if (e < len) {
-            element(k);
             const int kk = sub + k;
             const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
-            const bool cand = (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext));
-            mask |= static_cast<uint32_t>(cand) << k;
+            element(k, (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext)));
           }
         }
       }
-      // 2. the previous chunk's candidates (with this one's to go on with)
-      if (c0 == 0) {
-        pend = mask;
-      } else {
-        pend |= mask << C;
-        run(h ^ 1, c0 - C, (1u << C) - 1u);
-        pend >>= C;
-      }
-      ck_last = c0;
     }
 #pragma unroll
     for (int k = 0; k < LC; ++k) {
@@ -339,8 +338,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
       if constexpr (W) wc[W ? k : 0] = wn[W ? k : 0];
     }
   }
-  // the last chunk's candidates
-  run((ck_last / C) & 1, ck_last, ~0u);
+  // the last candidates
+  run(0);
   if (W && wbad && a.bad_weight != nullptr) *a.bad_weight = 1u;
 
   // The span's hull, whole, to the span array (for the merge kernel, or as the row's final hull)
@@ -390,9 +389,9 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // (the round state first, then the slots, in the wave's LDS)
   constexpr size_t kRoundBytes = (sizeof(MergeRounds) + 63) & ~size_t(63);
   constexpr int kCap =
-      static_cast<int>((sizeof(SpanLds<T, W, 2 * C, R>) - kRoundBytes) / slot_bytes<W, true>());
+      static_cast<int>((sizeof(SpanLds<T, W, Q, R>) - kRoundBytes) / slot_bytes<W, true>());
   static_assert(kCap >= 256, "the wave's LDS holds a group's noisy hulls");
-  static_assert(!(W && !PR) || sizeof(SpanLds<T, W, 2 * C, R>) == 20480, "weighted float32: 20 KB a wave");
+  static_assert(!(W && !PR) || sizeof(SpanLds<T, W, Q, R>) == 20480, "weighted float32: 20 KB a wave");
   if (nslots > kCap) {
     // Too many vertices for the wave's LDS: the spans' hulls go to the span array, and (one row
     // a wave) the group merges them there by reference to them (merge_global, its round state in
@@ -407,7 +406,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     char* const gm = reinterpret_cast<char*>(&L);
     MergeSmall& sm = *reinterpret_cast<MergeSmall*>(gm);
     MergeRanges& mr = *reinterpret_cast<MergeRanges*>(gm + ((sizeof(MergeSmall) + 63) & ~size_t(63)));
-    static_assert(((sizeof(MergeSmall) + 63) & ~size_t(63)) + sizeof(MergeRanges) <= sizeof(SpanLds<T, W, 2 * C, R>),
+    static_assert(((sizeof(MergeSmall) + 63) & ~size_t(63)) + sizeof(MergeRanges) <= sizeof(SpanLds<T, W, Q, R>),
                   "the global merge's round state fits the wave's LDS");
     if (lane < nch) {
       sm.cnt[lane] = depth;
@@ -581,11 +580,11 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
     else k_dec<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   };
   if (t.dtype == TI_F32) {
-    if (W) go(span_kernel<float, true, 4, 8, 32, true>, span_kernel<float, true, 4, 8, 32, false>);
-    else go(span_kernel<float, false, 4, 16, 32, true>, span_kernel<float, false, 4, 16, 32, false>);
+    if (W) go(span_kernel<float, true, 4, 8, 8, 32, true>, span_kernel<float, true, 4, 8, 8, 32, false>);
+    else go(span_kernel<float, false, 4, 8, 16, 32, true>, span_kernel<float, false, 4, 8, 16, 32, false>);
   } else {
-    if (W) go(span_kernel<double, true, 4, 8, 8, true>, span_kernel<double, true, 4, 8, 8, false>);
-    else go(span_kernel<double, false, 4, 16, 8, true>, span_kernel<double, false, 4, 16, 8, false>);
+    if (W) go(span_kernel<double, true, 4, 8, 8, 8, true>, span_kernel<double, true, 4, 8, 8, 8, false>);
+    else go(span_kernel<double, false, 4, 8, 16, 8, true>, span_kernel<double, false, 4, 8, 16, 8, false>);
   }
   return hipGetLastError();
 }
