@@ -61,9 +61,36 @@ def sync() -> None:
     torch.cuda.synchronize()
 
 
+SLEEP_CYCLES = 100_000  # torch.cuda._sleep: about 40 us at this part's shader clock (longer spins let it clock down)
+
+
 def timed_calls(fn, steps: int, warmup: int) -> float:
-    """Seconds per call over `steps` back-to-back calls, bracketed by synchronisations (after a
-    short clock-raising load and `warmup` untimed calls)."""
+    """Seconds per call over exactly `steps` back-to-back calls, bracketed by synchronisations:
+    after a short clock-raising load and `warmup` untimed calls, a spin kernel that touches no
+    memory (torch.cuda._sleep, about 40 us) holds the stream while the host queues the calls,
+    and one HIP event pair on the stream around them times them on the GPU. The window holds
+    the calls and every gap between them (a host slower than the GPU shows as idle time in it),
+    but not the first launch's latency nor the final synchronisation's, which a wall clock
+    around 20 calls of 30 us spreads over them as a few per cent (wall_calls)."""
+    warm_gpu(0.05)
+    for _ in range(warmup):
+        fn()
+    sync()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SLEEP_CYCLES)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    sync()
+    return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def wall_calls(fn, steps: int, warmup: int) -> float:
+    """Seconds per call by the host's clock over `steps` back-to-back calls between two
+    synchronisations: the GPU time plus the first launch's and the last synchronisation's
+    latency, divided by `steps`."""
     warm_gpu(0.05)
     for _ in range(warmup):
         fn()
@@ -78,17 +105,17 @@ def timed_calls(fn, steps: int, warmup: int) -> float:
 def kernel_ms(launch, reps: int, repeats: int = 3) -> float:
     """Device time of `launch` per launch: one HIP event pair recorded on the launch stream
     around `reps` back-to-back launches, divided by reps; the best of `repeats` such intervals,
-    each after a short clock-raising load. The launches queue behind that load, so the GPU
-    never waits for the host between them and the interval holds kernel time only (an event
-    pair per launch would add its own overhead to every interval)."""
+    each after a short clock-raising load. The launches queue behind a spin kernel that touches
+    no memory, so the GPU never waits for the host between them, no earlier kernel's write-back
+    is timed, and the interval holds kernel time only (an event pair per launch would add its
+    own overhead to every interval)."""
     stream = torch.cuda.current_stream()
     best = float("inf")
     launch()  # (first-call set-up outside the intervals)
     for _ in range(repeats):
         warm_gpu(0.03)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for _ in range(6):
-            _BUSY.mul_(1.0)
+        torch.cuda._sleep(SLEEP_CYCLES)
         e0.record(stream)
         for _ in range(reps):
             launch()
@@ -153,6 +180,8 @@ def bench_c2(steps: int, warmup: int) -> dict:
     elems = b * n
     t_fwd = timed_calls(lambda: torchisotonic_amd.isotonic(y, increasing=False), steps, warmup)
     t_fb = timed_calls(fwd_bwd_fn(y, None, g, False, increasing=False), steps, warmup)
+    t_fwd_wall = wall_calls(lambda: torchisotonic_amd.isotonic(y, increasing=False), steps, warmup)
+    t_fb_wall = wall_calls(fwd_bwd_fn(y, None, g, False, increasing=False), steps, warmup)
     lib = _ext.load()
     out = torch.empty_like(y)
     starts = torch.empty(_ext.starts_words(b, n), dtype=torch.int32, device="cuda")
@@ -168,6 +197,8 @@ def bench_c2(steps: int, warmup: int) -> dict:
         "elems": elems,
         "fwd": rate(elems, t_fwd, 8),
         "fwd_bwd": rate(elems, t_fb, 16),
+        "fwd_wall_clock": rate(elems, t_fwd_wall, 8),
+        "fwd_bwd_wall_clock": rate(elems, t_fb_wall, 16),
         "kernel_ms": {
             "short_rows_kernel<float,16,unweighted> (no starts)": kernel_ms(fwd, 100),
             "short_rows_kernel<float,16,unweighted> (with starts)": kernel_ms(fwd_s, 100),

@@ -185,7 +185,7 @@ __device__ __forceinline__ void row_fit(const T (&yv)[NMAX], const T (&wv)[W ? N
   for (int c = 0; c < NMAX; ++c) {
     if (c < nn) {
       const double yc = sgn * static_cast<double>(yv[c]);
-      bad |= yc != yc;
+      if (nn != NMAX) bad |= yc != yc;
       if constexpr (W) {
         const double wc = static_cast<double>(wv[c]);
         wbad |= !(wc > 0.0);
@@ -194,6 +194,16 @@ __device__ __forceinline__ void row_fit(const T (&yv)[NMAX], const T (&wv)[W ? N
       } else {
         S[c + 1] = S[c] + yc;
       }
+    }
+  }
+  if (nn == NMAX) {
+    // (whole rows: a NaN anywhere makes the row's total NaN; so do +inf and -inf together, so a
+    // NaN total sends the wave to the elements themselves)
+    bad = S[NMAX] != S[NMAX];
+    if (__any(bad)) {
+      bad = false;
+#pragma unroll
+      for (int c = 0; c < NMAX; ++c) bad |= yv[c] != yv[c];
     }
   }
   if constexpr (W) {
@@ -262,8 +272,10 @@ __device__ __forceinline__ void row_fit(const T (&yv)[NMAX], const T (&wv)[W ? N
         const double sA = colS[t2 * THREADS + tid];
         const double sB = colS[t1 * THREADS + tid];
         const double sk = colS[k * THREADS + tid];
+        // (t1 > 0 means something lies below the top, point 0 at least: the test of both, not a
+        // short circuit, which would put the test behind a branch)
         const bool pop =
-            below != 0 && pools<EXACT>(sB - sA, static_cast<double>(t1 - t2), sk - sB, static_cast<double>(k - t1));
+            (t1 != 0) & pools<EXACT>(sB - sA, static_cast<double>(t1 - t2), sk - sB, static_cast<double>(k - t1));
         // (selects, not branches: a wave whose lanes differ would run both)
         m = pop ? below : (m | (Mask(1) << k));
         t1 = pop ? t2 : k;
