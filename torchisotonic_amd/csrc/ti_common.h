@@ -165,6 +165,65 @@ __device__ __forceinline__ bool clip_passes(T v, bool use_lo, T lo, bool use_hi,
   return ok;
 }
 
+// Wavefront scans through DPP: every cross-lane step is a VALU move with a lane-shift modifier,
+// not an LDS permute, so a scan's steps wait on no memory pipe. Inclusive scans run row_shr 1,
+// 2, 4, 8 within each 16-lane row, then row_bcast:15 (the last lane of rows 0 and 2 into rows 1
+// and 3) and row_bcast:31 (lane 31 into rows 2 and 3); lanes without a source keep the
+// identity (zero). Controls as in the GFX9 DPP encoding: row_shr:k 0x110 + k, wave_shr:1 0x138,
+// row_bcast:15 0x142, row_bcast:31 0x143.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i32(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xF, false);
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = static_cast<uint32_t>(dpp_i32<CTRL, ROWS>(static_cast<int>(static_cast<uint32_t>(b))));
+  const uint32_t hi = static_cast<uint32_t>(dpp_i32<CTRL, ROWS>(static_cast<int>(static_cast<uint32_t>(b >> 32))));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ DD dpp_dd(DD x) {
+  return DD{dpp_f64<CTRL, ROWS>(x.hi), dpp_f64<CTRL, ROWS>(x.lo)};
+}
+
+// Inclusive sum over lanes 0..lane of the wave (all 64 lanes active).
+__device__ __forceinline__ int wave_incl_i32(int v) {
+  v += dpp_i32<0x111, 0xF>(v);
+  v += dpp_i32<0x112, 0xF>(v);
+  v += dpp_i32<0x114, 0xF>(v);
+  v += dpp_i32<0x118, 0xF>(v);
+  v += dpp_i32<0x142, 0xA>(v);
+  v += dpp_i32<0x143, 0xC>(v);
+  return v;
+}
+
+// The same in double-double, each step adding the lower lanes' part on the left.
+__device__ __forceinline__ DD wave_incl_dd(DD v) {
+  v = dd_add(dpp_dd<0x111, 0xF>(v), v);
+  v = dd_add(dpp_dd<0x112, 0xF>(v), v);
+  v = dd_add(dpp_dd<0x114, 0xF>(v), v);
+  v = dd_add(dpp_dd<0x118, 0xF>(v), v);
+  v = dd_add(dpp_dd<0x142, 0xA>(v), v);
+  v = dd_add(dpp_dd<0x143, 0xC>(v), v);
+  return v;
+}
+
+// Lane - 1's value (zero in lane 0): an inclusive scan made exclusive.
+__device__ __forceinline__ int wave_shr1_i32(int v) { return dpp_i32<0x138, 0xF>(v); }
+__device__ __forceinline__ DD wave_shr1_dd(DD v) { return dpp_dd<0x138, 0xF>(v); }
+
+// Lane 63's value, in every lane.
+__device__ __forceinline__ double wave_last_f64(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), 63));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), 63));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ DD wave_last_dd(DD v) { return DD{wave_last_f64(v.hi), wave_last_f64(v.lo)}; }
+
 // floor(e / n) for e * n < 2^32 (e >= 0, n >= 1): the high word of e * ceil(2^32 / n), exact
 // there since e * (ceil(2^32/n) - 2^32/n) < e < 2^32 / n. n = 1 has no 32-bit multiplier and is
 // passed through.

@@ -331,23 +331,10 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int
       ts = DD{ci.tot[2], ci.tot[3]};
     }
     // inclusive scans: totals (dd) and slots (count - 1, the shared point stored once)
-    DD iw = tw, is = ts;
-    int islot = max(cnt - 1, 0);
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const DD ow{__shfl_up(iw.hi, d, kWave), __shfl_up(iw.lo, d, kWave)};
-      const DD os{__shfl_up(is.hi, d, kWave), __shfl_up(is.lo, d, kWave)};
-      const int oslot = __shfl_up(islot, d, kWave);
-      if (lane >= d) {
-        iw = dd_add(ow, iw);
-        is = dd_add(os, is);
-        islot += oslot;
-      }
-    }
+    const DD iw = wave_incl_dd(tw), is = wave_incl_dd(ts);
+    const int islot = wave_incl_i32(max(cnt - 1, 0));
     const int anybad = __any(bad != 0);
-    DD ew{__shfl_up(iw.hi, 1, kWave), __shfl_up(iw.lo, 1, kWave)};
-    DD es{__shfl_up(is.hi, 1, kWave), __shfl_up(is.lo, 1, kWave)};
-    if (lane == 0) ew = es = DD{0.0, 0.0};
+    const DD ew = wave_shr1_dd(iw), es = wave_shr1_dd(is);
     if (lane < nch) {
       sm.cnt[lane] = cnt;
       sm.off[lane] = islot - max(cnt - 1, 0);
@@ -534,12 +521,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     if constexpr (E == 16) mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFFFu;
     else mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFu;
     const int pc = __builtin_popcount(mybits);
-    int incl = pc;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int o = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_i32(pc);
     if (lane == kWave - 1) rank_scan[wave] = incl;
     __syncthreads();
     int before = incl - pc;
@@ -612,12 +594,7 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
       ne = bad ? 1 : count - 1;
       rbad[tid] = bad ? 1 : 0;
     }
-    int inc = ne;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int o = __shfl_up(inc, d, kWave);
-      if (tid >= d) inc += o;
-    }
+    const int inc = wave_incl_i32(ne);
     if (tid < rows) roff[tid] = inc - ne;
     if (tid == rows - 1) roff[rows] = inc;
   }

@@ -81,22 +81,13 @@ struct GradKArgs {
   double* lv;            // [batch * cap_final][2]: prefix of g within its tile at each vertex
 };
 
-__device__ __forceinline__ DD wave_scan_dd2(DD v, int lane) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    DD o{__shfl_up(v.hi, d, kWave), __shfl_up(v.lo, d, kWave)};
-    if (lane >= d) v = dd_add(o, v);
-  }
-  return v;
-}
 
 // Exclusive double-double scan over a 256-thread workgroup; returns the exclusive prefix and
 // sets `total`.
 __device__ DD block_scan_dd(DD v, DD* wave_tot, DD& total) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const DD inc = wave_scan_dd2(v, lane);
-  DD exc{__shfl_up(inc.hi, 1, kWave), __shfl_up(inc.lo, 1, kWave)};
-  if (lane == 0) exc = DD{0.0, 0.0};
+  const DD inc = wave_incl_dd(v);
+  const DD exc = wave_shr1_dd(inc);
   if (lane == kWave - 1) wave_tot[wave] = inc;
   __syncthreads();
   DD pre{0.0, 0.0};
@@ -115,8 +106,7 @@ __device__ __forceinline__ uint32_t tile_bits(const uint32_t* srow, int x, int E
 // Sum over a 256-thread workgroup (double-double), for every thread.
 __device__ DD block_sum_dd(DD v, DD* wave_tot) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-#pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) v = dd_add(v, DD{__shfl_xor(v.hi, d, kWave), __shfl_xor(v.lo, d, kWave)});
+  v = wave_last_dd(wave_incl_dd(v));
   if (lane == 0) wave_tot[wave] = v;
   __syncthreads();
   DD t = wave_tot[0];
@@ -244,12 +234,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
     if (first + t0 == 0) mybits |= 1u;
     const int pc = __builtin_popcount(mybits);
-    int incl = pc;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int o = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_i32(pc);
     if (lane == kWave - 1) rank_scan[wave] = incl;
     __syncthreads();
     int before = incl - pc;
@@ -395,12 +380,7 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   if (first + t0 == 0) mybits |= 1u;
   if (bad) mybits = 0u;
   const int pc = __builtin_popcount(mybits);
-  int incl = pc;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int o = __shfl_up(incl, d, kWave);
-    if (lane >= d) incl += o;
-  }
+  const int incl = wave_incl_i32(pc);
   if (lane == kWave - 1) rank_scan[wave] = incl;
   __syncthreads();
   int before = incl - pc;
@@ -507,22 +487,20 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
       s += static_cast<double>(gv[k]);
     }
   }
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const double os = __shfl_up(s, d, kWave);
-    const int oc = __shfl_up(c, d, kWave);
-    if (lane >= d) seg_combine(os, oc, s, c);
-  }
+  // (DPP steps: a lane without a source gets (0, 0), which seg_combine passes through)
+  auto step = [&](double os, int oc) { seg_combine(os, oc, s, c); };
+  step(dpp_f64<0x111, 0xF>(s), dpp_i32<0x111, 0xF>(c));
+  step(dpp_f64<0x112, 0xF>(s), dpp_i32<0x112, 0xF>(c));
+  step(dpp_f64<0x114, 0xF>(s), dpp_i32<0x114, 0xF>(c));
+  step(dpp_f64<0x118, 0xF>(s), dpp_i32<0x118, 0xF>(c));
+  step(dpp_f64<0x142, 0xA>(s), dpp_i32<0x142, 0xA>(c));
+  step(dpp_f64<0x143, 0xC>(s), dpp_i32<0x143, 0xC>(c));
   if (lane == kWave - 1) {
     wave_s[wave] = s;
     wave_c[wave] = c;
   }
-  double xs = __shfl_up(s, 1, kWave);
-  int xc = __shfl_up(c, 1, kWave);
-  if (lane == 0) {
-    xs = 0.0;
-    xc = 0;
-  }
+  double xs = dpp_f64<0x138, 0xF>(s);
+  int xc = wave_shr1_i32(c);
   __syncthreads();
   double ps = 0.0;
   int pc = 0, nb = 0;

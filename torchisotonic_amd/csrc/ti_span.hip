@@ -371,21 +371,10 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     const uint64_t kmask = kl == 64 ? ~uint64_t{0} : ((uint64_t{1} << kl) - 1);
     zero_s = ((bm >> ((lane / kl) * kl)) & kmask) != 0;
   }
-  DD iw = active ? DD{W ? P : static_cast<double>(len), W ? PL : 0.0} : DD{0.0, 0.0};
-  DD is = active && !zero_s ? DD{S, SL} : DD{0.0, 0.0};
-  int islot = own;
-#pragma unroll
-  for (int d = 1; d < kSpanLanes; d <<= 1) {
-    const DD ow{__shfl_up(iw.hi, d, kSpanLanes), __shfl_up(iw.lo, d, kSpanLanes)};
-    const DD os{__shfl_up(is.hi, d, kSpanLanes), __shfl_up(is.lo, d, kSpanLanes)};
-    const int oslot = __shfl_up(islot, d, kSpanLanes);
-    if (lane >= d) {
-      iw = dd_add(ow, iw);
-      is = dd_add(os, is);
-      islot += oslot;
-    }
-  }
-  const int nslots = __shfl(islot, kSpanLanes - 1, kSpanLanes);
+  const DD iw = wave_incl_dd(active ? DD{W ? P : static_cast<double>(len), W ? PL : 0.0} : DD{0.0, 0.0});
+  const DD is = wave_incl_dd(active && !zero_s ? DD{S, SL} : DD{0.0, 0.0});
+  const int islot = wave_incl_i32(own);
+  const int nslots = __builtin_amdgcn_readlane(islot, kSpanLanes - 1);
   // (the round state first, then the slots, in the wave's LDS)
   constexpr size_t kRoundBytes = (sizeof(MergeRounds) + 63) & ~size_t(63);
   constexpr int kCap =
@@ -399,8 +388,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     // multi-row wave's spans are merged by the merge kernel.
     write_span_hull();
     if (multi) return;
-    const DD pw{__shfl_up(iw.hi, 1, kSpanLanes), __shfl_up(iw.lo, 1, kSpanLanes)};
-    const DD ps{__shfl_up(is.hi, 1, kSpanLanes), __shfl_up(is.lo, 1, kSpanLanes)};
+    const DD pw = wave_shr1_dd(iw), ps = wave_shr1_dd(is);
     const bool gbad = __any(active && bad);
     __syncthreads();  // (every lane's hull written, and its ring read, before the LDS is reused)
     char* const gm = reinterpret_cast<char*>(&L);
@@ -439,9 +427,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     return;
   }
   // offsets of this lane's span within the group
-  DD ew{__shfl_up(iw.hi, 1, kSpanLanes), __shfl_up(iw.lo, 1, kSpanLanes)};
-  DD es{__shfl_up(is.hi, 1, kSpanLanes), __shfl_up(is.lo, 1, kSpanLanes)};
-  if (lane == 0) ew = es = DD{0.0, 0.0};
+  const DD ew = wave_shr1_dd(iw), es = wave_shr1_dd(is);
   const int off = islot - own;
   // (multi: the wave's rows are one sequence, each row's end point the next row's first point)
   const int lidx = static_cast<int>(lel);
