@@ -10,7 +10,10 @@ the sizes where they reach the merge levels, through the public API on the GPU:
   and pass the gradient unchanged (reference tests/test_grad.py:40-56, tests/test_cuda.py:213-222,
   the row of linspace(0, 1, 1e6) included);
 - blocks whose means all round to 1.0 in float32: the gradient takes its blocks from the hull,
-  not from equal fitted values (reference tests/test_cuda.py:268-294, n = 500, 3000, 100 000).
+  not from equal fitted values (reference tests/test_cuda.py:268-294, n = 500, 3000, 100 000);
+- rows of a batch are independent: rows of magnitude 1e30 beside ordinary ones, in every way
+  the kernels share a wave or a workgroup between rows (one row a lane, several rows a wave,
+  one row a wave), leave the ordinary rows' fits and gradients as they are alone.
 """
 
 from __future__ import annotations
@@ -162,3 +165,41 @@ def test_gradient_blocks_from_the_hull(n: int) -> None:
     np.testing.assert_allclose(grad.cpu().numpy(), ey, rtol=1e-5, atol=1e-6)
     got_starts = torchisotonic_amd._ext.isotonic_tiles(yy.detach(), None, True, True, True)[1]
     np.testing.assert_array_equal(got_starts.cpu().numpy().astype(np.uint8), starts)
+
+
+# (batch, n): rows of 32 one a lane (short kernel); 64 one a lane in batches of 8192 ("packed");
+# 128 in a batch of 2 (16 spans a row, 4 rows a wave), 300 in 64 (4 rows a wave), 2000 in 1000
+# (2 rows a wave); 5000 one row a wave
+INDEPENDENCE_SHAPES = [(1000, 32), (8192, 64), (2, 128), (64, 300), (1000, 2000), (4, 5000)]
+
+
+@pytest.mark.parametrize("batch,n", INDEPENDENCE_SHAPES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_rows_are_independent_of_their_neighbours_magnitude(batch: int, n: int, dtype: type,
+                                                             weighted: bool) -> None:
+    print(f"row independence [{batch}, {n}] {np.dtype(dtype).name} weighted={weighted}", flush=True)
+    rng = np.random.default_rng(batch + n)
+    y = (0.01 * np.arange(n) + rng.standard_normal((batch, n))).astype(dtype)
+    huge = np.zeros(batch, dtype=bool)
+    huge[::3] = True  # every third row, the first included: 1e30 times larger, in runs of 1e30
+    y[huge] = (y[huge].astype(np.float64) * 1e30).astype(dtype)
+    w = (rng.random((batch, n)) + 0.1).astype(dtype) if weighted else None
+    g = rng.standard_normal((batch, n)).astype(dtype)
+    yt = torch.from_numpy(y).cuda().requires_grad_()
+    wt = None if w is None else torch.from_numpy(w).cuda().requires_grad_()
+    fit = torchisotonic_amd.isotonic(yt, weight=wt)
+    grads = torch.autograd.grad(fit, [yt] + ([] if wt is None else [wt]), torch.from_numpy(g).cuda())
+    want, starts = oracle.pava(y, w, acc="f64")
+    ey, ew = oracle.block_grad(starts, g.astype(np.float64), None if w is None else w.astype(np.float64),
+                               None if w is None else y.astype(np.float64), want, want_w=w is not None)
+    got = fit.detach().cpu().numpy().astype(np.float64)
+    tol = 4 * 2.0**-23 if dtype == np.float32 else 1e-12
+    # each row within its own tolerance (its own magnitude), the ordinary rows above all
+    scale = np.abs(y.astype(np.float64)).max(axis=1, keepdims=True)
+    assert (np.abs(got - want) <= tol * scale).all(), float((np.abs(got - want) / scale).max())
+    gtol = 1e-5 if dtype == np.float32 else 1e-11
+    for gt, e in zip(grads, (ey, ew)):
+        gt = gt.cpu().numpy().astype(np.float64)
+        rscale = np.abs(e).max(axis=1, keepdims=True)
+        assert (np.abs(gt - e) <= gtol * (np.abs(e) + rscale)).all(), float((np.abs(gt - e) / rscale).max())

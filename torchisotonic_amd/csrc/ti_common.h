@@ -211,6 +211,17 @@ __device__ __forceinline__ DD wave_incl_dd(DD v) {
   return v;
 }
 
+// Inclusive scan of double-double values over aligned segments of `seg` lanes (a power of two,
+// the same in every lane), each segment on its own: lane l sums lanes l & ~(seg - 1) .. l.
+__device__ __forceinline__ DD seg_incl_dd(DD v, int seg) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int d = 1; d < seg; d <<= 1) {
+    const DD o{__shfl_up(v.hi, d, kWave), __shfl_up(v.lo, d, kWave)};
+    if ((lane & (seg - 1)) >= d) v = dd_add(o, v);
+  }
+  return v;
+}
+
 // Lane - 1's value (zero in lane 0): an inclusive scan made exclusive.
 __device__ __forceinline__ int wave_shr1_i32(int v) { return dpp_i32<0x138, 0xF>(v); }
 __device__ __forceinline__ DD wave_shr1_dd(DD v) { return dpp_dd<0x138, 0xF>(v); }

@@ -23,7 +23,9 @@ namespace ti {
 // `cap` slots: coordinates in the parent's frame (double-double for float64 data), the vertex
 // index within the parent, and the child (0..63) that owns each slot. A boundary point between
 // two children is stored once, as the last vertex of the child on its left; slot 0 is the
-// parent's first point.
+// parent's first point. Where the children are several rows (aligned groups of 2^row_lg
+// children, each row in a frame of its own from its first point), a row's first child stores
+// its first point too, in the slot after the previous row's last.
 template <bool W, bool PR>
 struct Slots {
   double *s, *sl, *w, *wl;
@@ -128,7 +130,8 @@ __device__ __forceinline__ bool hpools_nb(const HPt& a, const HPt& b, const HPt&
 
 // Merges the `nch` children in slots [0, total) into one hull in slots [0, result). On entry
 // rs.seg[0][c] holds the last slot of child c and every thread has passed a barrier since the
-// slots were written. NT >= 64 threads; the vertex tests take slots s = tid + k * NT, G of
+// slots were written. row_lg: children in aligned groups of 2^row_lg are separate rows (then
+// max_rounds <= row_lg), a row's first slot its first child's own (see Slots). NT >= 64 threads; the vertex tests take slots s = tid + k * NT, G of
 // them at a time in lockstep (their LDS reads in flight together). After max_rounds rounds it
 // stops: segment s (children [s * 2^R, (s + 1) * 2^R), R the rounds run) is then one hull, and
 // rs.seg[R & 1][s] its last slot.
@@ -146,8 +149,10 @@ __device__ __forceinline__ int lead_ones(uint64_t g, uint64_t gmask, int S) {
 }
 
 template <bool W, bool PR, int NT, int G>
-__device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, int nch, int max_rounds = 6) {
+__device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, int nch, int max_rounds = 6,
+                            int row_lg = 30) {
   constexpr int NW = NT / kWave;
+  const int row_mask = (1 << row_lg) - 1;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -173,7 +178,8 @@ __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, i
       const uint64_t gmask = S == 64 ? ~uint64_t{0} : ((uint64_t{1} << S) - 1);
       const int gshift = sub << lg_s;
       const int q = se[2 * p];
-      const int lo_l = p > 0 ? se[max(2 * p - 1, 0)] : 0;
+      // (L's first point: the previous segment's last, or its own slot after it at a row's start)
+      const int lo_l = p > 0 ? se[max(2 * p - 1, 0)] + ((((2 * p) << r) & row_mask) == 0 ? 1 : 0) : 0;
       const int hi_r = se[2 * p + 1];
       double dSl, dWl, dSr, dWr;
       {
@@ -235,7 +241,7 @@ __device__ int merge_rounds(const Slots<W, PR>& v, MergeRounds& rs, int total, i
         const int p = c >> 1;
         const int pc = p < npair ? p : 0;
         const int q = se[2 * pc];
-        const int lo_l = pc > 0 ? se[max(2 * pc - 1, 0)] : 0;
+        const int lo_l = pc > 0 ? se[max(2 * pc - 1, 0)] + ((((2 * pc) << r) & row_mask) == 0 ? 1 : 0) : 0;
         const int hi_r = se[2 * pc + 1];
         const int jd = rs.jdead[pc];
         const int wl = rs.walk[pc][0], wr = rs.walk[pc][1];

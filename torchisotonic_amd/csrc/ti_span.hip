@@ -360,19 +360,26 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   }
 
   // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
-  // lane c's hull is child c, positions [0, depth), its first point shared with lane c - 1.
-  const int own = active ? (lane == 0 ? depth : depth - 1) : 0;
-  // (multi: the wave's rows share one frame, so a row holding a NaN must not carry it into the
-  // rows after it. Its fit is NaN whatever its hull, and the backward needs only its weights:
-  // its sums are taken as 0, its weights kept.)
+  // lane c's hull is child c, positions [0, depth), its first point shared with lane c - 1 - but
+  // a row's first lane (multi: every kl-th) stores its first point itself. Each row has a frame
+  // of its own, from its first point: one shared by the wave's rows would hold a row's sums
+  // beside all earlier rows' totals, whose rounding (up to half an ulp of the largest)
+  // double-double cannot keep apart from the row's own sums where magnitudes differ by 2^50 or
+  // more.
+  const bool rfirst = (lane & (kl - 1)) == 0;
+  const int own = active ? (rfirst ? depth : depth - 1) : 0;
+  // (a row holding a NaN: its fit is NaN whatever its hull, and the backward needs only its
+  // weights; its sums are taken as 0, its weights kept)
   bool zero_s = false;
   if (multi) {
     const uint64_t bm = __ballot(active && bad);
     const uint64_t kmask = kl == 64 ? ~uint64_t{0} : ((uint64_t{1} << kl) - 1);
     zero_s = ((bm >> ((lane / kl) * kl)) & kmask) != 0;
   }
-  const DD iw = wave_incl_dd(active ? DD{W ? P : static_cast<double>(len), W ? PL : 0.0} : DD{0.0, 0.0});
-  const DD is = wave_incl_dd(active && !zero_s ? DD{S, SL} : DD{0.0, 0.0});
+  const DD vw = active ? DD{W ? P : static_cast<double>(len), W ? PL : 0.0} : DD{0.0, 0.0};
+  const DD vs = active && !zero_s ? DD{S, SL} : DD{0.0, 0.0};
+  const DD iw = multi ? seg_incl_dd(vw, kl) : wave_incl_dd(vw);
+  const DD is = multi ? seg_incl_dd(vs, kl) : wave_incl_dd(vs);
   const int islot = wave_incl_i32(own);
   const int nslots = __builtin_amdgcn_readlane(islot, kSpanLanes - 1);
   // (the round state first, then the slots, in the wave's LDS)
@@ -426,10 +433,13 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     }
     return;
   }
-  // offsets of this lane's span within the group
-  const DD ew = wave_shr1_dd(iw), es = wave_shr1_dd(is);
+  // offsets of this lane's span within its row (the group's, or multi: its row's)
+  // (the shifts in every lane first: a cross-lane read inside the select would run with the
+  // row-first lanes switched off, and their right neighbours would read nothing from them)
+  const DD zero{0.0, 0.0}, pw_all = wave_shr1_dd(iw), ps_all = wave_shr1_dd(is);
+  const DD ew = rfirst ? zero : pw_all, es = rfirst ? zero : ps_all;
   const int off = islot - own;
-  // (multi: the wave's rows are one sequence, each row's end point the next row's first point)
+  // (indices: positions in the wave's elements, each row's rebased from its first point below)
   const int lidx = static_cast<int>(lel);
   const bool anybad = __any(active && bad);
   auto to_group = [&](HPt p) {
@@ -451,7 +461,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   char* const mem = reinterpret_cast<char*>(&L);
   MergeRounds& rs = *reinterpret_cast<MergeRounds*>(mem);
   const Slots<W, true> v = slots_carve<W, true>(mem + kRoundBytes, kCap);
-  const int q0 = lane == 0 ? 0 : 1;  // the first point of a later span is its left neighbour's last
+  const int q0 = rfirst ? 0 : 1;  // the first point of a later span is its left neighbour's last
   if (active) {
     for (int q = q0; q < r0; ++q) {
       const int sl = off + q - q0;
@@ -472,15 +482,14 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   __syncthreads();
   if (multi) {
     // log2(kl) rounds merge each row's spans and no further: segment r is then row r's hull,
-    // slots [seg[r - 1], seg[r]] (the first of them shared with row r - 1), in the frame of the
-    // wave's sequence; each row's hull goes out in its own frame (from its first point)
+    // slots [seg[r - 1] + 1, seg[r]] (slot 0 for row 0), in the row's own frame
     const int lgk = __builtin_ctz(kl);
-    merge_rounds<W, true, kSpanLanes, 2>(v, rs, nslots, nch, lgk);
+    merge_rounds<W, true, kSpanLanes, 2>(v, rs, nslots, nch, lgk, lgk);
     const int* se = rs.seg[lgk & 1];
     const uint64_t badm = __ballot(active && bad);
     const uint64_t kmask = kl == 64 ? ~uint64_t{0} : ((uint64_t{1} << kl) - 1);
     for (int r = 0; r < nch / kl; ++r) {
-      const int f = r == 0 ? 0 : se[r - 1];
+      const int f = r == 0 ? 0 : se[r - 1] + 1;
       const int cnt = se[r] - f + 1;
       const NodeOut pout = node_out(a.hulls1, W, static_cast<int64_t>(blockIdx.x) * a.rpw + r);
       const HPt x0 = sget(v, f);
