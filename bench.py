@@ -285,7 +285,7 @@ def bench_next(steps: int, warmup: int) -> dict:
     """The consumers around the fit, timed like the configs above (back-to-back calls of the
     public API between synchronisations): C2's rows at their own lengths (len ~ U{4..16}, seed 2;
     the padded variant is the C2 forward above), packed with offsets, forward and forward+backward
-    (8 and 16 B per element); soft ranks at the reference's shapes and strengths (reference
+    (8 and 16 B per element); 1e5 rows of lengths U{1..2000}, packed and padded; soft ranks at the reference's shapes and strengths (reference
     paper/soft_rank.py:23-28; x, g ~ N(0, 1) float32); and calibration (fit over pooled keys,
     then interpolation) of 6.5 million float32 scores, about one day of the reference's Criteo
     example (examples/ctr_calibration/calibrate.py:171-187)."""
@@ -337,6 +337,45 @@ def bench_next(steps: int, warmup: int) -> dict:
         },
     }
     del bits, gy
+    # 1e5 rows of lengths U{1..2000} (seed 31; about 1e8 elements), increasing, float32, packed
+    # with offsets, against the same rows padded to 2000 elements (each beyond its own maximum,
+    # the reference's padding rule) and fitted dense; rates in the rows' own elements
+    rb, rl = 100_000, 2000
+    lens2 = torch.from_numpy(np.random.default_rng(31).integers(1, rl + 1, rb)).cuda()
+    off2 = torch.zeros(rb + 1, dtype=torch.int64, device="cuda")
+    off2[1:] = torch.cumsum(lens2, 0)
+    tot2 = int(off2[-1])
+    rowid = torch.repeat_interleave(torch.arange(rb, device="cuda"), lens2)
+    col = torch.arange(tot2, device="cuda") - off2[:-1][rowid]
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    packed2 = 0.001 * col.float() + torch.randn(tot2, device="cuda", generator=gen)
+    g2 = torch.randn(tot2, device="cuda", generator=gen)
+    rmax = torch.full((rb,), -float("inf"), device="cuda").scatter_reduce(0, rowid, packed2, "amax")
+    padded = (rmax + 1.0)[:, None].expand(rb, rl).contiguous()
+    padded[rowid, col] = packed2
+    gpad = torch.zeros(rb, rl, device="cuda")
+    gpad[rowid, col] = g2
+    del rowid, col, rmax
+    pr2 = packed2.detach().requires_grad_()
+    pp2 = padded.detach().requires_grad_()
+    k2 = max(3, min(steps, 10))
+
+    def rfb() -> None:
+        torch.autograd.grad(torchisotonic_amd.isotonic_ragged(pr2, off2), pr2, g2)
+
+    def pfb() -> None:
+        torch.autograd.grad(torchisotonic_amd.isotonic(pp2), pp2, gpad)
+
+    res["ragged_long"] = {
+        "rows": rb,
+        "elems": tot2,
+        "padded_elems": rb * rl,
+        "fwd": rate(tot2, timed_calls(lambda: torchisotonic_amd.isotonic_ragged(packed2, off2), k2, 2), 8),
+        "fwd_bwd": rate(tot2, timed_calls(rfb, k2, 2), 16),
+        "padded_fwd": rate(tot2, timed_calls(lambda: torchisotonic_amd.isotonic(padded), k2, 2), 8),
+        "padded_fwd_bwd": rate(tot2, timed_calls(pfb, k2, 2), 16),
+    }
+    del packed2, g2, padded, gpad, pr2, pp2
     soft = {}
     for sb, sn in ((1024, 100), (256, 1000), (64, 10_000), (8, 100_000), (1, 1_000_000)):
         torch.manual_seed(0)

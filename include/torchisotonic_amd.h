@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 6
+#define TI_ABI_VERSION 7
 
 /* dtype codes */
 #define TI_F32 0
@@ -270,6 +270,34 @@ int ti_bwd_ragged(const uint32_t* starts, const void* g, const void* w, const vo
  * size the launches. No counterpart in the reference (see ti_fwd_ragged).
  */
 int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, void* stream);
+
+/*
+ * Ragged rows longer than 32 elements, a length bucket at a time: the k rows described by `rows`
+ * (device int64 pairs: first element in the packed array of `total` elements, length) as one
+ * dense row-major [k, L] block (L at least every length), which ti_fwd and ti_bwd take as a
+ * batch. No counterpart in the reference, whose callers pad ragged rows themselves with tail
+ * values that never pool into the data (reference README.md:100-103); these apply that rule.
+ * Every kernel clamps a row to the packed array and to L, so no access leaves the buffers.
+ *
+ * ti_ragged_extreme: each row's largest value (increasing != 0) or smallest (else), NaN skipped,
+ *   as an order-preserving key into keys[r] (k device words the caller has zeroed), for the pad.
+ * ti_ragged_pack: dst[r][j] = src[first_r + j] for j < len_r, else the row's pad: m + max(1, |m|)
+ *   beyond its extreme m (with keys), or 0 (keys NULL: a gradient's block); wdst likewise from w
+ *   with weight 1 past the row (w and wdst both given or both NULL).
+ * ti_ragged_unpack: dst[first_r + j] = src[r][j] for j < len_r (dst2 from src2 likewise, both
+ *   given or both NULL). For a gradient block (gy, gw) give starts, the forward's packed starts of
+ *   the block, and w, the packed weights (NULL: unweighted): a row whose last block reached into
+ *   its pad (a NaN row, or one whose extreme is the dtype's largest finite value or infinite, which
+ *   no pad exceeds) has that block's gradients scaled by (W + L - len_r) / W, W its own weight
+ *   over the block, so that the pad's weight leaves the block's mean gradient. starts NULL: no
+ *   such scaling (a fit block).
+ */
+int ti_ragged_extreme(const void* y, int64_t total, const int64_t* rows, int64_t k, int64_t L, int dtype,
+                      int increasing, uint64_t* keys, void* stream);
+int ti_ragged_pack(const void* src, const void* w, int64_t total, const int64_t* rows, const uint64_t* keys,
+                   int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream);
+int ti_ragged_unpack(const void* src, const void* src2, const int64_t* rows, int64_t k, int64_t L, int dtype,
+                     void* dst, void* dst2, int64_t total, const uint32_t* starts, const void* w, void* stream);
 
 /* Bytes of device workspace ti_grad needs for this problem set (0 when batch * n <= 2048). */
 int ti_grad_workspace(int64_t batch, int64_t n, int dtype, size_t* bytes);

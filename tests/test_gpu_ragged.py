@@ -1,9 +1,10 @@
 """Ragged rows (packed end to end with offsets) on the GPU against the oracle's per-row fits:
-short rows in one launch and longer rows through the regular kernels, with block starts, the
-backward (one launch for the short rows, from the forward's flat start bits; the longer rows
-from their own forwards), the clamp, and C2's padded variant
-(lengths U{4..16}: a padded row's first len_b fitted values equal the ragged row's fit;
-reference README.md:100-103)."""
+short rows in one launch and longer rows a length bucket at a time through the regular kernels
+(each row padded beyond its extreme in the bucket's block), with block starts, the backward (one
+launch for the short rows, from the forward's flat start bits; each bucket from its own
+forward), rows whose pad joins their last block (NaN rows, the largest finite value), the
+clamp, and C2's padded variant (lengths U{4..16}: a padded row's first len_b fitted values equal
+the ragged row's fit; reference README.md:100-103)."""
 
 from __future__ import annotations
 
@@ -39,8 +40,11 @@ def run(y: np.ndarray, w: np.ndarray | None, off: np.ndarray, increasing: bool):
     off_t, short_max, spans, bits, bad = rg._offsets(torch.from_numpy(off).cuda(), None, yt, wt is not None)
     out, long_rows = rg._fit(yt, wt, off_t, short_max, spans, bits, bad, increasing)
     starts = _ext.starts_to_bool(bits, 1, len(y))[0].cpu().numpy().astype(np.uint8)
-    for a, b, s, _ in long_rows:  # a longer row's own partition
-        starts[a:b] = _ext.starts_to_bool(s, 1, b - a)[0].cpu().numpy()
+    for rows, L, s, *_ in long_rows:  # each longer row's partition: its row of the bucket's block
+        sb = _ext.starts_to_bool(s, len(rows), L).cpu().numpy()
+        first, ln = np.array(rows, dtype=np.int64).T
+        keep = np.arange(L)[None, :] < ln[:, None]
+        starts[(first[:, None] + np.arange(L)[None, :])[keep]] = sb[keep]
     return out.cpu().numpy(), starts
 
 
@@ -146,6 +150,72 @@ def test_backward_matches_block_gradient(dtype: type, weighted: bool) -> None:
     for got, exp in zip(grads, (ey, ew)):
         scale = max(float(np.abs(exp).max()), 1e-300)
         np.testing.assert_allclose(got.double().cpu().numpy(), exp, rtol=tol, atol=tol * scale)
+
+
+def _grads(y: np.ndarray, w: np.ndarray | None, off: np.ndarray, g: np.ndarray, increasing: bool = True):
+    yt = torch.from_numpy(y).cuda().requires_grad_()
+    wt = None if w is None else torch.from_numpy(w).cuda().requires_grad_()
+    out = isotonic_ragged(yt, torch.from_numpy(off).cuda(), weight=wt, increasing=increasing)
+    grads = torch.autograd.grad(out, [yt] + ([] if wt is None else [wt]), torch.from_numpy(g).cuda())
+    return out.detach().cpu().numpy(), [t.cpu().numpy() for t in grads]
+
+
+def _block_grads(fit, starts, y, w, g):
+    ey, ew = oracle.block_grad(starts, g.astype(np.float64), None if w is None else w.astype(np.float64),
+                               None if w is None else y.astype(np.float64), fit, want_w=w is not None)
+    return [e for e in (ey, ew) if e is not None]
+
+
+def test_long_rows_of_uniform_lengths() -> None:
+    # 1e5 rows of lengths U{1..2000} (about 1e8 elements; eleven length buckets and the short
+    # rows), weighted float32: fit, partition and both gradients against the oracle's rows
+    say("ragged 1e5 rows, lengths U{1..2000}, float32 weighted")
+    rng = np.random.default_rng(31)
+    ln = rng.integers(1, 2001, 100_000).astype(np.int64)
+    y, w, off = ragged_set(ln, np.float32, 32)
+    got, starts = run(y, w, off, True)
+    fit, want_starts = oracle.pava_ragged(y, off, w, acc="f64")
+    assert float(np.abs(got.astype(np.float64) - fit).max()) <= tolerance(y)
+    np.testing.assert_array_equal(starts, want_starts)
+    del got, starts
+    g = rng.standard_normal(len(y)).astype(np.float32)
+    out, grads = _grads(y, w, off, g)
+    assert float(np.abs(out.astype(np.float64) - fit).max()) <= tolerance(y)
+    for gt, e in zip(grads, _block_grads(fit, want_starts, y, w, g)):
+        np.testing.assert_allclose(gt.astype(np.float64), e, rtol=1e-5, atol=1e-5 * float(np.abs(e).max()))
+
+
+@pytest.mark.parametrize("increasing", [True, False])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_rows_whose_pad_joins_their_last_block(increasing: bool, weighted: bool) -> None:
+    # rows past 32 elements whose pad cannot lie beyond their extreme: NaN rows (one block over
+    # the row and its pad) and rows ending in the largest finite float32 value (a last block that
+    # pools with the pad); their fits and gradients are the row's own, the pad's weight taken out
+    say(f"ragged pad joins the last block: increasing={increasing} weighted={weighted}")
+    rng = np.random.default_rng(41)
+    # buckets: (32, 64] rows 0, 2, 3, 7 (L = 64); (64, 128] rows 5, 10; (256, 512] rows 1, 8;
+    # (512, 1024] rows 4, 9; row 6 short
+    ln = np.array([40, 300, 33, 40, 1000, 70, 5, 64, 500, 1020, 128], dtype=np.int64)
+    y, w, off = ragged_set(ln, np.float32, 42)
+    top = np.float32((1 if increasing else -1) * np.finfo(np.float32).max)
+    y[off[1] + 7] = np.nan       # a NaN row, 300 elements padded to 500
+    y[off[3] + 1] = np.nan       # a NaN row, 40 elements padded to 64
+    y[off[3] - 1] = top          # ends at the extreme: a last block of its own, padded to 64
+    y[off[5] - 3:off[5]] = top   # three of them, padded to 1020
+    y[off[6] - 10] = top         # the extreme before smaller values: no pooling with the pad
+    y[off[8] - 1] = top          # a row as long as its block: no pad
+    g = rng.standard_normal(len(y)).astype(np.float32)
+    ww = w if weighted else None
+    out, grads = _grads(y, ww, off, g, increasing)
+    fit, starts = oracle.pava_ragged(y, off, ww, increasing=increasing, acc="f64")
+    np.testing.assert_array_equal(np.isnan(out), np.isnan(fit))
+    for r in range(len(ln)):  # each row within the tolerance of its own magnitude
+        a, b = off[r], off[r + 1]
+        if not np.isnan(fit[a:b]).any():
+            assert float(np.abs(out[a:b].astype(np.float64) - fit[a:b]).max()) <= tolerance(y[a:b]), r
+    for gt, e in zip(grads, _block_grads(fit, starts, y, ww, g)):
+        scale = float(np.abs(e[np.isfinite(e)]).max())
+        np.testing.assert_allclose(gt.astype(np.float64), e, rtol=1e-5, atol=1e-5 * scale)
 
 
 def _ragged_abi(y: np.ndarray, w: np.ndarray | None, off: np.ndarray, g: np.ndarray, flags: int, lo: float,

@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -45,6 +45,9 @@ SYMBOLS = (
     "ti_fwd_ragged",
     "ti_bwd_ragged",
     "ti_ragged_plan",
+    "ti_ragged_extreme",
+    "ti_ragged_pack",
+    "ti_ragged_unpack",
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_fwd_ev_hulls",
@@ -96,6 +99,12 @@ def load() -> ctypes.CDLL:
     lib.ti_bwd_ragged.argtypes = [_vp] * 7 + [_i64, _i64, _i64, _int, _uint, _dbl, _dbl, _vp]
     lib.ti_ragged_plan.restype = _int
     lib.ti_ragged_plan.argtypes = [_vp, _i64, _i64, _vp, _vp]
+    lib.ti_ragged_extreme.restype = _int
+    lib.ti_ragged_extreme.argtypes = [_vp, _i64, _vp, _i64, _i64, _int, _int, _vp, _vp]
+    lib.ti_ragged_pack.restype = _int
+    lib.ti_ragged_pack.argtypes = [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    lib.ti_ragged_unpack.restype = _int
+    lib.ti_ragged_unpack.argtypes = [_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp, _i64, _vp, _vp, _vp]
     lib.ti_bwd.restype = _int
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_fwd_ev_hulls.restype = _int

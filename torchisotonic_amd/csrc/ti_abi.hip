@@ -420,6 +420,48 @@ int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t
                   "ragged plan");
 }
 
+// (k rows of a bucket against its block [k, L]: the descriptors' grid must fit one launch)
+int check_bucket(int64_t total, const int64_t* rows, int64_t k, int64_t L, int dtype) {
+  if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);
+  if (total < 0 || k < 0 || L < 1) return fail(TI_EINVAL, "need total >= 0, k >= 0 and L >= 1");
+  if (k > 0 && rows == nullptr) return fail(TI_EINVAL, "rows must not be null");
+  if (k * ti::ragged_chunks(L) > 0x7FFFFFFF) return fail(TI_ESIZE, "k * ceil(L / 2048) must stay below 2^31");
+  return TI_OK;
+}
+
+int ti_ragged_extreme(const void* y, int64_t total, const int64_t* rows, int64_t k, int64_t L, int dtype,
+                      int increasing, uint64_t* keys, void* stream) {
+  if (int rc = check_bucket(total, rows, k, L, dtype)) return rc;
+  if (k == 0) return ok();
+  if (y == nullptr || keys == nullptr) return fail(TI_EINVAL, "y and keys must not be null");
+  return launched(ti::ragged_extreme(y, total, rows, k, L, dtype, increasing != 0,
+                                     reinterpret_cast<unsigned long long*>(keys), static_cast<hipStream_t>(stream)),
+                  "ragged extreme");
+}
+
+int ti_ragged_pack(const void* src, const void* w, int64_t total, const int64_t* rows, const uint64_t* keys,
+                   int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream) {
+  if (int rc = check_bucket(total, rows, k, L, dtype)) return rc;
+  if (k == 0) return ok();
+  if (src == nullptr || dst == nullptr) return fail(TI_EINVAL, "src and dst must not be null");
+  if ((w == nullptr) != (wdst == nullptr)) return fail(TI_EINVAL, "w and wdst go together");
+  return launched(ti::ragged_pack(src, w, total, rows, reinterpret_cast<const unsigned long long*>(keys), k, L, dtype,
+                                  increasing != 0, dst, wdst, static_cast<hipStream_t>(stream)),
+                  "ragged pack");
+}
+
+int ti_ragged_unpack(const void* src, const void* src2, const int64_t* rows, int64_t k, int64_t L, int dtype,
+                     void* dst, void* dst2, int64_t total, const uint32_t* starts, const void* w, void* stream) {
+  if (int rc = check_bucket(total, rows, k, L, dtype)) return rc;
+  if (k == 0) return ok();
+  if (src == nullptr || dst == nullptr) return fail(TI_EINVAL, "src and dst must not be null");
+  if ((src2 == nullptr) != (dst2 == nullptr)) return fail(TI_EINVAL, "src2 and dst2 go together");
+  if (w != nullptr && starts == nullptr) return fail(TI_EINVAL, "w is read with starts only");
+  return launched(
+      ti::ragged_unpack(src, src2, rows, k, L, dtype, dst, dst2, total, starts, w, static_cast<hipStream_t>(stream)),
+      "ragged unpack");
+}
+
 int ti_interp(const void* x, const void* xp, const void* fp, void* out, int64_t n, int64_t m, int dtype,
               void* stream) {
   if (dtype != TI_F32 && dtype != TI_F64) return fail(TI_EDTYPE, "dtype must be TI_F32 or TI_F64, got %d", dtype);

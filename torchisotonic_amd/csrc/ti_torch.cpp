@@ -250,9 +250,12 @@ constexpr int64_t kRaggedShort = 32;  // the longest rows ti_fwd_ragged fits
 // its four words to the host; given a bound max_len on the row lengths, the short rows' fit
 // (ti_fwd_ragged, which clamps every offset it reads) launched right behind that copy, so that
 // it runs while the host waits for the words; the wait and the offsets' errors; a second launch
-// over every short row where rows past the bound are at most 32 long; the longer rows one by one
-// (ti_fwd, each with its own workspace, kept for its backward). The backward is one launch for
-// the short rows (ti_bwd_ragged) and ti_bwd for each longer row.
+// over every short row where rows past the bound are at most 32 long; the longer rows a length
+// bucket at a time (lengths in (2^(b-1), 2^b]): the bucket's rows gathered into one dense block,
+// each padded beyond its own extreme (ti_ragged_extreme, ti_ragged_pack), one ti_fwd over the
+// block, and its fits scattered back (ti_ragged_unpack). The backward is one launch for the
+// short rows (ti_bwd_ragged) and, per bucket, g gathered into a block, one ti_bwd from the
+// bucket's forward, and the gradients scattered back.
 struct RaggedFn : public torch::autograd::Function<RaggedFn> {
   static at::Tensor forward(AutogradContext* ctx, const at::Tensor& values, const std::optional<at::Tensor>& w_opt,
                             const at::Tensor& offsets, bool increasing, int64_t max_len, bool from_lengths) {
@@ -269,7 +272,6 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     }
     const int dtype = dtype_code(values);
     const int64_t nrows = offsets.numel() - 1, total = values.numel();
-    const int64_t esize = values.element_size();
     const c10::DeviceGuard guard(values.device());
     const hipStream_t stream = c10::hip::getCurrentHIPStream(values.device().index()).stream();
     const unsigned flags = (increasing ? TI_INCREASING : 0u) | TI_EXACT;
@@ -297,38 +299,76 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     TORCH_CHECK_VALUE((err & 4) == 0, from_lengths ? "lengths must be non-negative" : "offsets must not decrease");
     TORCH_CHECK_VALUE((err & 3) == 0, "offsets must run from 0 to values.numel() = ", total);
     if (short_max > nmax) fit_short(short_max);
-    // the longer rows, each by the regular path on its slice of the packed arrays
-    std::vector<int64_t> spans;
-    std::vector<at::Tensor> keep;  // each longer row's starts and forward workspace
+    // the longer rows, a length bucket at a time (their starts and lengths to the host once)
+    const bool want = values.requires_grad() || (w.defined() && w.requires_grad());
+    std::vector<int64_t> buckets;  // per bucket: its first descriptor, its rows, its block length
+    std::vector<at::Tensor> keep;  // the descriptors, then per bucket: y, w blocks, starts, workspace
     if (n_long > 0) {
       const at::Tensor len = offsets.slice(0, 1) - offsets.slice(0, 0, nrows);
       const at::Tensor r = at::nonzero(len > kRaggedShort).view(-1);
-      const at::Tensor se = at::stack({offsets.index_select(0, r), offsets.index_select(0, r + 1)}, 1).cpu();
+      const at::Tensor se = at::stack({offsets.index_select(0, r), len.index_select(0, r)}, 1).cpu();
       const int64_t* sp = se.data_ptr<int64_t>();
-      for (int64_t i = 0; i < se.size(0); ++i) {
-        const int64_t a = sp[2 * i], n = sp[2 * i + 1] - a;
-        at::Tensor starts = at::empty({ti_starts_words(1, n)}, values.options().dtype(at::kInt));
-        at::Tensor ws = workspace(true, 1, n, dtype, w.defined(), values.device());
-        char* yb = static_cast<char*>(values.data_ptr()) + a * esize;
-        char* wb = w.defined() ? static_cast<char*>(w.data_ptr()) + a * esize : nullptr;
-        check(ti_fwd(yb, wb, static_cast<char*>(out.data_ptr()) + a * esize, static_cast<uint32_t*>(starts.data_ptr()),
-                     bad, 1, n, dtype, flags, 0.0, 0.0, ptr(ws), ws.defined() ? static_cast<size_t>(ws.numel()) : 0,
-                     stream),
+      const int64_t nl = se.size(0);
+      std::vector<std::vector<int64_t>> by(64);
+      for (int64_t i = 0; i < nl; ++i) {
+        int b = 0;
+        while ((int64_t{1} << b) < sp[2 * i + 1]) ++b;
+        by[b].push_back(i);
+      }
+      std::vector<int64_t> desc;
+      desc.reserve(2 * nl);
+      for (int b = 0; b < 64; ++b) {
+        if (by[b].empty()) continue;
+        int64_t L = 0;
+        buckets.push_back(static_cast<int64_t>(desc.size() / 2));
+        for (int64_t i : by[b]) {
+          desc.push_back(sp[2 * i]);
+          desc.push_back(sp[2 * i + 1]);
+          L = std::max(L, sp[2 * i + 1]);
+        }
+        buckets.push_back(static_cast<int64_t>(by[b].size()));
+        buckets.push_back(L);
+      }
+      const at::Tensor rows =
+          at::from_blob(desc.data(), {nl, 2}, at::TensorOptions().dtype(at::kLong)).to(values.device());
+      const at::Tensor keys = at::zeros({nl}, rows.options());
+      keep.push_back(rows);
+      const int64_t* rp = rows.data_ptr<int64_t>();
+      uint64_t* kp = reinterpret_cast<uint64_t*>(keys.data_ptr<int64_t>());
+      for (size_t i = 0; i < buckets.size(); i += 3) {
+        const int64_t f = buckets[i], k = buckets[i + 1], L = buckets[i + 2];
+        check(ti_ragged_extreme(ptr(values), total, rp + 2 * f, k, L, dtype, increasing ? 1 : 0, kp + f, stream),
               "isotonic_ragged");
-        spans.push_back(a);
-        spans.push_back(n);
-        keep.push_back(starts);
-        keep.push_back(ws);
+        at::Tensor yb = at::empty({k, L}, values.options());
+        at::Tensor wb = w.defined() ? at::empty({k, L}, values.options()) : at::Tensor();
+        check(ti_ragged_pack(ptr(values), ptr(w), total, rp + 2 * f, kp + f, k, L, dtype, increasing ? 1 : 0, ptr(yb),
+                             ptr(wb), stream),
+              "isotonic_ragged");
+        at::Tensor starts = at::empty({ti_starts_words(k, L)}, values.options().dtype(at::kInt));
+        at::Tensor ws = workspace(true, k, L, dtype, w.defined(), values.device());
+        at::Tensor ob = at::empty({k, L}, values.options());
+        check(ti_fwd(ptr(yb), ptr(wb), ptr(ob), static_cast<uint32_t*>(starts.data_ptr()), bad, k, L, dtype, flags, 0.0,
+                     0.0, ptr(ws), ws.defined() ? static_cast<size_t>(ws.numel()) : 0, stream),
+              "isotonic_ragged");
+        check(ti_ragged_unpack(ptr(ob), nullptr, rp + 2 * f, k, L, dtype, ptr(out), nullptr, total, nullptr, nullptr,
+                               stream),
+              "isotonic_ragged");
+        if (want) {
+          keep.push_back(yb);
+          keep.push_back(wb);
+          keep.push_back(starts);
+          keep.push_back(ws);
+        }
       }
     }
     if (bad != nullptr && (short_max > 0 || n_long > 0)) {
       TORCH_CHECK_VALUE(zeros.slice(0, 8, 9).item<int32_t>() == 0, "weight must be strictly positive");
     }
-    if (values.requires_grad() || (w.defined() && w.requires_grad())) {
+    if (want) {
       std::vector<at::Tensor> saved = {values, w, offsets, zeros};
       saved.insert(saved.end(), keep.begin(), keep.end());
       ctx->save_for_backward(saved);
-      ctx->saved_data["spans"] = c10::List<int64_t>(spans);
+      ctx->saved_data["buckets"] = c10::List<int64_t>(buckets);
       ctx->saved_data["p"] = c10::List<int64_t>({short_max, increasing ? 1 : 0, w.defined() ? 1 : 0});
     }
     return out;
@@ -339,7 +379,7 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     const int64_t short_max = prm.get(0);
     const unsigned flags = (prm.get(1) != 0 ? TI_INCREASING : 0u) | TI_EXACT;
     const bool has_w = prm.get(2) != 0;
-    const c10::List<int64_t> spans = ctx->saved_data["spans"].toIntList();
+    const c10::List<int64_t> buckets = ctx->saved_data["buckets"].toIntList();
     const bool want_y = ctx->needs_input_grad(0), want_w = has_w && ctx->needs_input_grad(1);
     variable_list none(6);
     if (!want_y && !want_w) return none;
@@ -351,7 +391,6 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     const at::Tensor g = grads[0].contiguous().to(values.scalar_type());
     const int dtype = dtype_code(values);
     const int64_t nrows = offsets.numel() - 1, total = values.numel();
-    const int64_t esize = values.element_size();
     const c10::DeviceGuard guard(values.device());
     const hipStream_t stream = c10::hip::getCurrentHIPStream(values.device().index()).stream();
     // (every element belongs to a row: the short rows' elements are written by one launch, the
@@ -364,19 +403,32 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
                           offsets.data_ptr<int64_t>(), nrows, total, short_max, dtype, 0u, 0.0, 0.0, stream),
             "isotonic_ragged backward");
     }
-    auto at_ = [&](const at::Tensor& t, int64_t a) -> char* {
-      return t.defined() ? static_cast<char*>(t.data_ptr()) + a * esize : nullptr;
-    };
-    for (size_t i = 0; i * 2 < spans.size(); ++i) {
-      const int64_t a = spans.get(2 * i), n = spans.get(2 * i + 1);
-      const at::Tensor& starts = saved[4 + 2 * i];
-      const at::Tensor& ws = saved[5 + 2 * i];
-      at::Tensor bws = workspace(false, 1, n, dtype, w.defined(), values.device());
-      check(ti_bwd(static_cast<const uint32_t*>(starts.data_ptr()), ptr(ws),
-                   ws.defined() ? static_cast<size_t>(ws.numel()) : 0, at_(g, a), at_(w, a),
-                   want_w ? at_(values, a) : nullptr, at_(gy, a), want_w ? at_(gw, a) : nullptr, 1, n, dtype, flags,
-                   0.0, 0.0, ptr(bws), bws.defined() ? static_cast<size_t>(bws.numel()) : 0, stream),
-            "isotonic_ragged backward");
+    if (!buckets.empty()) {
+      // per bucket: g gathered into the bucket's block (0 past each row), the block's backward
+      // from its forward, and the gradients scattered back (a row whose pad joined its last block
+      // has that block's gradients scaled back to its own weight)
+      const int64_t* rp = saved[4].data_ptr<int64_t>();
+      for (size_t i = 0, j = 5; i < buckets.size(); i += 3, j += 4) {
+        const int64_t f = buckets.get(i), k = buckets.get(i + 1), L = buckets.get(i + 2);
+        const at::Tensor& yb = saved[j];
+        const at::Tensor& wb = saved[j + 1];
+        const at::Tensor& starts = saved[j + 2];
+        const at::Tensor& ws = saved[j + 3];
+        at::Tensor gb = at::empty({k, L}, g.options());
+        check(ti_ragged_pack(ptr(g), nullptr, total, rp + 2 * f, nullptr, k, L, dtype, 0, ptr(gb), nullptr, stream),
+              "isotonic_ragged backward");
+        at::Tensor gyb = at::empty({k, L}, g.options());
+        at::Tensor gwb = want_w ? at::empty({k, L}, g.options()) : at::Tensor();
+        at::Tensor bws = workspace(false, k, L, dtype, w.defined(), values.device());
+        check(ti_bwd(static_cast<const uint32_t*>(starts.data_ptr()), ptr(ws),
+                     ws.defined() ? static_cast<size_t>(ws.numel()) : 0, ptr(gb), ptr(wb), want_w ? ptr(yb) : nullptr,
+                     ptr(gyb), ptr(gwb), k, L, dtype, flags, 0.0, 0.0, ptr(bws),
+                     bws.defined() ? static_cast<size_t>(bws.numel()) : 0, stream),
+              "isotonic_ragged backward");
+        check(ti_ragged_unpack(ptr(gyb), ptr(gwb), rp + 2 * f, k, L, dtype, ptr(gy), ptr(gw), total,
+                               static_cast<const uint32_t*>(starts.data_ptr()), ptr(w), stream),
+              "isotonic_ragged backward");
+      }
     }
     none[0] = want_y ? gy : at::Tensor();
     none[1] = gw;

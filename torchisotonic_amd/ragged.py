@@ -12,10 +12,16 @@ and the row offsets (CSR layout) go to the GPU as they are:
   kernel has checked the offsets and sized the rows and its four words have reached the host
   (the call's one wait); with ``max_len``, a bound on the row lengths, that launch goes before
   the wait and runs during it;
-- longer rows are fitted row by row by the regular kernels (``ti_fwd`` on each row in place);
+- longer rows are fitted a length bucket at a time (lengths in (2^(b-1), 2^b]): the bucket's
+  rows gathered into one dense [k, L] block, each padded beyond its own extreme with the
+  reference's rule for padding (a tail above the row's maximum for an increasing fit, below its
+  minimum for a decreasing one, which pools with nothing of the row), one ``ti_fwd`` over the
+  block, and the fits scattered back (``ti_ragged_extreme``, ``ti_ragged_pack``,
+  ``ti_ragged_unpack``);
 - the backward of the rows of 1 to 32 elements is one HIP launch too (``ti_bwd_ragged``: one
-  thread per row, the blocks read from the forward's flat start bits); longer rows take their
-  gradients from their own forward's hulls (``ti_bwd``).
+  thread per row, the blocks read from the forward's flat start bits); each bucket of longer
+  rows takes its gradients from its own forward (``ti_bwd`` over the block of g, scattered
+  back).
 
 The clamp to [y_min, y_max] is torch.clamp after the fit, as in the reference (_api.py:68-69).
 These steps, and the backward, run in one C++ operator with its autograd node
@@ -131,23 +137,52 @@ def _fit_short(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, nmax:
     _ext._check(rc, "isotonic_ragged")
 
 
-def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, long_spans: list[tuple[int, int]], increasing: bool) -> list:
-    long_rows = []
+def _buckets(long_spans: list[tuple[int, int]]) -> list[tuple[list[tuple[int, int]], int]]:
+    """The longer rows (start, end) grouped by length bucket, (2^(b-1), 2^b]: per bucket its rows
+    as (start, length) and its block length (the longest of them)."""
+    by: dict[int, list[tuple[int, int]]] = {}
     for a, b in long_spans:
-        wr = None if w is None else w[a:b].view(1, b - a)
-        _, starts, bad_r, ws = _ext.fit(values[a:b].view(1, b - a), wr, increasing, True, True,
-                                        out=out[a:b].view(1, b - a))
-        if bad_r:
+        by.setdefault((b - a - 1).bit_length(), []).append((a, b - a))
+    return [(rows, max(n for _, n in rows)) for _, rows in sorted(by.items())]
+
+
+def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, long_spans: list[tuple[int, int]],
+              increasing: bool) -> list:
+    """The longer rows, a bucket at a time (ti_ragged_extreme, ti_ragged_pack, ti_fwd over the
+    block, ti_ragged_unpack); per bucket (its rows as (start, length), block length L, the block's
+    packed starts, its forward workspace, the y and w blocks)."""
+    lib = _ext.load()
+    code = _ext._dtype_code(values)
+    total = values.numel()
+    s = _ext._stream(values)
+    inc = 1 if increasing else 0
+    buckets = []
+    for rows, L in _buckets(long_spans):
+        k = len(rows)
+        desc = torch.tensor(rows, dtype=torch.int64).to(values.device)
+        keys = torch.zeros(k, dtype=torch.int64, device=values.device)
+        with _ext._on_device(values.device):
+            _ext._check(lib.ti_ragged_extreme(values.data_ptr(), total, desc.data_ptr(), k, L, code, inc,
+                                              keys.data_ptr(), s), "isotonic_ragged")
+            yb = torch.empty(k, L, dtype=values.dtype, device=values.device)
+            wb = None if w is None else torch.empty_like(yb)
+            _ext._check(lib.ti_ragged_pack(values.data_ptr(), _ext._ptr(w), total, desc.data_ptr(), keys.data_ptr(),
+                                           k, L, code, inc, yb.data_ptr(), _ext._ptr(wb), s), "isotonic_ragged")
+        ob, starts, bad_b, ws = _ext.fit(yb, wb, increasing, True, True)
+        if bad_b:
             raise ValueError("weight must be strictly positive")
-        long_rows.append((a, b, starts, ws))
-    return long_rows
+        with _ext._on_device(values.device):
+            _ext._check(lib.ti_ragged_unpack(ob.data_ptr(), None, desc.data_ptr(), k, L, code, out.data_ptr(), None,
+                                             total, None, None, s), "isotonic_ragged")
+        buckets.append((rows, L, starts, ws, yb, wb))
+    return buckets
 
 
 def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spans: list[tuple[int, int]],
          bits: Tensor, bad: Tensor | None, increasing: bool) -> tuple[Tensor, list]:
     """The fits of every row (packed like values) with the flat start bits of the short rows
-    in ``bits`` (a longer row has its first bit only), and per longer row (start, end, its own
-    packed starts, its forward workspace)."""
+    in ``bits`` (a longer row has its first bit only), and per bucket of longer rows what
+    ``_fit_long`` returns."""
     out = torch.empty_like(values)
     if short_max > 0:
         _fit_short(values, w, out, off, short_max, bits, bad, increasing)
