@@ -321,8 +321,9 @@ def bench_next(steps: int, warmup: int) -> dict:
     assert lib.ti_fwd_ragged(packed.data_ptr(), None, out.data_ptr(), bits.data_ptr(), None, off.data_ptr(), b, elems, n, _ext.F32, 0, 0.0, 0.0, s) == 0
     rawb = lambda: lib.ti_bwd_ragged(bits.data_ptr(), g.data_ptr(), None, None, gy.data_ptr(), None, off.data_ptr(), b, elems, n, _ext.F32, 0, 0.0, 0.0, s)  # noqa: E731
     assert rawb() == 0
-    plan = torch.zeros(4, dtype=torch.int64, device="cuda")  # (repeated plans fold into it: a timing only)
-    rawp = lambda: lib.ti_ragged_plan(off.data_ptr(), b, elems, plan.data_ptr(), s)  # noqa: E731
+    plan = torch.zeros(_ext.RAGGED_PLAN_WORDS, dtype=torch.int64, device="cuda")  # (plans fold into it: a timing)
+    keys = torch.empty(b, dtype=torch.uint8, device="cuda")
+    rawp = lambda: lib.ti_ragged_plan(off.data_ptr(), b, elems, plan.data_ptr(), keys.data_ptr(), s)  # noqa: E731
     assert rawp() == 0
     res["c2_ragged"] = {
         "elems": elems,

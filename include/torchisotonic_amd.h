@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 7
+#define TI_ABI_VERSION 8
 
 /* dtype codes */
 #define TI_F32 0
@@ -263,13 +263,24 @@ int ti_bwd_ragged(const uint32_t* starts, const void* g, const void* w, const vo
 
 /*
  * The plan of a ragged set, one pass over its offsets (device int64, nrows + 1 values), into
- * four device words the caller has zeroed: plan[0] bit 0 set if offsets[0] != 0, bit 1 if
- * offsets[nrows] != total, bit 2 if a row has a negative length (offsets decrease); plan[1] the
- * longest row of at most 32 elements (the max_len ti_fwd_ragged takes), plan[2] the number of
- * longer rows, plan[3] the longest row. The host reads them back to validate the offsets and
- * size the launches. No counterpart in the reference (see ti_fwd_ragged).
+ * TI_RAGGED_PLAN_WORDS device words the caller has zeroed: plan[0] bit 0 set if offsets[0] != 0,
+ * bit 1 if offsets[nrows] != total, bit 2 if a row has a negative length (offsets decrease);
+ * plan[1] the longest row of at most 32 elements (the max_len ti_fwd_ragged takes), plan[2] the
+ * number of longer rows, plan[3] the longest row; plan[4 + b] the number of rows of length
+ * bucket b (lengths in (2^(b-1), 2^b], b >= 6) and plan[68 + b] the longest of them. keys
+ * (device, one byte a row, or NULL): each row's bucket, 0 for a row of at most 32 elements; a
+ * stable sort of them puts the longer rows in bucket order. The host reads the plan back to
+ * validate the offsets and size the launches. No counterpart in the reference (see
+ * ti_fwd_ragged).
  */
-int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, void* stream);
+#define TI_RAGGED_PLAN_WORDS 132
+int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, uint8_t* keys, void* stream);
+
+/* The descriptors (first element, length) of rows order[0..n) of a ragged set, into rows (2 n
+ * device int64), for ti_ragged_extreme / _pack / _unpack; order's entries are clamped into
+ * [0, nrows). No counterpart in the reference (see ti_fwd_ragged). */
+int ti_ragged_rows(const int64_t* offsets, int64_t nrows, const int64_t* order, int64_t n, int64_t* rows,
+                   void* stream);
 
 /*
  * Ragged rows longer than 32 elements, a length bucket at a time: the k rows described by `rows`
@@ -282,20 +293,21 @@ int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t
  * ti_ragged_extreme: each row's largest value (increasing != 0) or smallest (else), NaN skipped,
  *   as an order-preserving key into keys[r] (k device words the caller has zeroed), for the pad.
  * ti_ragged_pack: dst[r][j] = src[first_r + j] for j < len_r, else the row's pad: m + max(1, |m|)
- *   beyond its extreme m (with keys), or 0 (keys NULL: a gradient's block); wdst likewise from w
- *   with weight 1 past the row (w and wdst both given or both NULL).
+ *   beyond its extreme m (with keys), or `pad` (keys NULL: 0 for a gradient's block; for float32
+ *   values, the largest finite float32, negated for a decreasing fit, which needs no extreme);
+ *   wdst likewise from w with weight 1 past the row (w and wdst both given or both NULL).
  * ti_ragged_unpack: dst[first_r + j] = src[r][j] for j < len_r (dst2 from src2 likewise, both
  *   given or both NULL). For a gradient block (gy, gw) give starts, the forward's packed starts of
  *   the block, and w, the packed weights (NULL: unweighted): a row whose last block reached into
  *   its pad (a NaN row, or one whose extreme is the dtype's largest finite value or infinite, which
- *   no pad exceeds) has that block's gradients scaled by (W + L - len_r) / W, W its own weight
- *   over the block, so that the pad's weight leaves the block's mean gradient. starts NULL: no
- *   such scaling (a fit block).
+ *   no pad exceeds) has that block's gradients scaled by (W + P) / W, W its own weight over the
+ *   block and P the pad elements in it (up to the next start bit), so that the pad's weight
+ *   leaves the block's mean gradient. starts NULL: no such scaling (a fit block).
  */
 int ti_ragged_extreme(const void* y, int64_t total, const int64_t* rows, int64_t k, int64_t L, int dtype,
                       int increasing, uint64_t* keys, void* stream);
 int ti_ragged_pack(const void* src, const void* w, int64_t total, const int64_t* rows, const uint64_t* keys,
-                   int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream);
+                   double pad, int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream);
 int ti_ragged_unpack(const void* src, const void* src2, const int64_t* rows, int64_t k, int64_t L, int dtype,
                      void* dst, void* dst2, int64_t total, const uint32_t* starts, const void* w, void* stream);
 

@@ -23,7 +23,8 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
+RAGGED_PLAN_WORDS = 132  # (ti_ragged_plan)
 
 F32, F64 = 0, 1
 INCREASING, EXACT, CLIP_MIN, CLIP_MAX = 1, 2, 4, 8
@@ -48,6 +49,7 @@ SYMBOLS = (
     "ti_ragged_extreme",
     "ti_ragged_pack",
     "ti_ragged_unpack",
+    "ti_ragged_rows",
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_fwd_ev_hulls",
@@ -98,11 +100,13 @@ def load() -> ctypes.CDLL:
     lib.ti_bwd_ragged.restype = _int
     lib.ti_bwd_ragged.argtypes = [_vp] * 7 + [_i64, _i64, _i64, _int, _uint, _dbl, _dbl, _vp]
     lib.ti_ragged_plan.restype = _int
-    lib.ti_ragged_plan.argtypes = [_vp, _i64, _i64, _vp, _vp]
+    lib.ti_ragged_plan.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp]
     lib.ti_ragged_extreme.restype = _int
     lib.ti_ragged_extreme.argtypes = [_vp, _i64, _vp, _i64, _i64, _int, _int, _vp, _vp]
     lib.ti_ragged_pack.restype = _int
-    lib.ti_ragged_pack.argtypes = [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    lib.ti_ragged_pack.argtypes = [_vp, _vp, _i64, _vp, _vp, _dbl, _i64, _i64, _int, _int, _vp, _vp, _vp]
+    lib.ti_ragged_rows.restype = _int
+    lib.ti_ragged_rows.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp]
     lib.ti_ragged_unpack.restype = _int
     lib.ti_ragged_unpack.argtypes = [_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp, _i64, _vp, _vp, _vp]
     lib.ti_bwd.restype = _int

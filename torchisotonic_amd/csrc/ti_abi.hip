@@ -411,13 +411,27 @@ int ti_bwd_ragged(const uint32_t* starts, const void* g, const void* w, const vo
   return launched(ti::ragged_grad(a), "ragged backward");
 }
 
-int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, void* stream) {
+static_assert(ti::kRaggedPlanWords == TI_RAGGED_PLAN_WORDS, "the plan's size");
+
+int ti_ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, int64_t* plan, uint8_t* keys,
+                   void* stream) {
   if (nrows < 0 || total < 0) return fail(TI_EINVAL, "need nrows >= 0 and total >= 0");
   if (offsets == nullptr || plan == nullptr) return fail(TI_EINVAL, "offsets and plan must not be null");
   if ((reinterpret_cast<uintptr_t>(plan) & 7) != 0) return fail(TI_EINVAL, "plan must be 8-byte aligned");
-  return launched(ti::ragged_plan(offsets, nrows, total, reinterpret_cast<unsigned long long*>(plan),
+  return launched(ti::ragged_plan(offsets, nrows, total, reinterpret_cast<unsigned long long*>(plan), keys,
                                   static_cast<hipStream_t>(stream)),
                   "ragged plan");
+}
+
+int ti_ragged_rows(const int64_t* offsets, int64_t nrows, const int64_t* order, int64_t n, int64_t* rows,
+                   void* stream) {
+  if (nrows < 0 || n < 0) return fail(TI_EINVAL, "need nrows >= 0 and n >= 0");
+  if (n == 0) return ok();
+  if (nrows == 0) return fail(TI_EINVAL, "no rows to describe");
+  if (offsets == nullptr || order == nullptr || rows == nullptr)
+    return fail(TI_EINVAL, "offsets, order and rows must not be null");
+  if (n > int64_t{0x7FFFFFFF} * 256) return fail(TI_ESIZE, "too many rows");
+  return launched(ti::ragged_rows(offsets, nrows, order, n, rows, static_cast<hipStream_t>(stream)), "ragged rows");
 }
 
 // (k rows of a bucket against its block [k, L]: the descriptors' grid must fit one launch)
@@ -440,13 +454,13 @@ int ti_ragged_extreme(const void* y, int64_t total, const int64_t* rows, int64_t
 }
 
 int ti_ragged_pack(const void* src, const void* w, int64_t total, const int64_t* rows, const uint64_t* keys,
-                   int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream) {
+                   double pad, int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream) {
   if (int rc = check_bucket(total, rows, k, L, dtype)) return rc;
   if (k == 0) return ok();
   if (src == nullptr || dst == nullptr) return fail(TI_EINVAL, "src and dst must not be null");
   if ((w == nullptr) != (wdst == nullptr)) return fail(TI_EINVAL, "w and wdst go together");
-  return launched(ti::ragged_pack(src, w, total, rows, reinterpret_cast<const unsigned long long*>(keys), k, L, dtype,
-                                  increasing != 0, dst, wdst, static_cast<hipStream_t>(stream)),
+  return launched(ti::ragged_pack(src, w, total, rows, reinterpret_cast<const unsigned long long*>(keys), pad, k, L,
+                                  dtype, increasing != 0, dst, wdst, static_cast<hipStream_t>(stream)),
                   "ragged pack");
 }
 

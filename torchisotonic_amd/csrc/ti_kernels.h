@@ -81,9 +81,11 @@ struct RaggedGradArgs {
   hipStream_t stream;
 };
 hipError_t ragged_grad(const RaggedGradArgs& a);
-// plan: four zeroed device words (see ragged_plan_kernel)
+// plan: kRaggedPlanWords zeroed device words; keys: one byte per row, or null (see
+// ragged_plan_kernel)
+constexpr int kRaggedPlanWords = 132;
 hipError_t ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, unsigned long long* plan,
-                       hipStream_t stream);
+                       uint8_t* keys, hipStream_t stream);
 
 // Ragged rows of a length bucket as a dense [k, L] block (ti_ragged.hip): each row's extreme
 // (keys: k zeroed device words), the block with each row's pad (or 0 without keys), and back
@@ -93,8 +95,10 @@ int64_t ragged_chunks(int64_t len);
 hipError_t ragged_extreme(const void* y, int64_t total, const int64_t* rows, int64_t k, int64_t L, int dtype,
                           bool increasing, unsigned long long* keys, hipStream_t stream);
 hipError_t ragged_pack(const void* src, const void* w, int64_t total, const int64_t* rows,
-                       const unsigned long long* keys, int64_t k, int64_t L, int dtype, bool increasing, void* dst,
-                       void* wdst, hipStream_t stream);
+                       const unsigned long long* keys, double pad, int64_t k, int64_t L, int dtype, bool increasing,
+                       void* dst, void* wdst, hipStream_t stream);
+hipError_t ragged_rows(const int64_t* offsets, int64_t nrows, const int64_t* order, int64_t n, int64_t* rows,
+                       hipStream_t stream);
 hipError_t ragged_unpack(const void* src, const void* src2, const int64_t* rows, int64_t k, int64_t L, int dtype,
                          void* dst, void* dst2, int64_t total, const uint32_t* starts, const void* w,
                          hipStream_t stream);

@@ -16,11 +16,18 @@
 // reach into the pad: the fit of the row's own elements is still the row's, since a block that
 // pools with the pad has a mean equal to the pad's, but the block's weight in the backward holds
 // the pad's weight too. The unpack of a gradient block therefore checks each row's start bit at
-// its length and, where it is clear, scales the gradients over that last block by
-// (W + pads) / W, W the row's own weight over the block, which takes the pad back out.
+// its length and, where it is clear, scales the gradients over that last block by (W + P) / W,
+// W the row's own weight over the block and P the pad elements in it (weight 1 each: up to the
+// next start bit, which need not be the row's end, since a long run of equal pads need not stay
+// one block where their sums round), which takes the pad back out.
+//
+// float32 rows may skip the extreme: their pad is the largest finite float32 (its negative for a
+// decreasing fit), beyond every finite value of any row; a row holding that value or an infinity
+// is one whose pad may join its last block, as above.
 //
 // Row descriptors: int64 pairs (first element in the packed array, length), k of them; the
-// block is row-major [k, L], L at least every length. Every kernel clamps a row to [0, total) of
+// block is row-major [k, L], L at least every length. ragged_rows gathers them from the offsets
+// in the order the caller gives (rows sorted by length bucket). Every kernel clamps a row to [0, total) of
 // the packed array and to L, so no access leaves the buffers whatever the descriptors hold.
 #include "ti_common.h"
 #include "ti_kernels.h"
@@ -109,18 +116,20 @@ __global__ __launch_bounds__(kRagThreads) void ragged_extreme_kernel(const T* __
 }
 
 // Per (row, chunk of kRagChunk of the block's L): dst[r][j] = src[first + j] for j < len, else the
-// row's pad (0 without keys); wdst likewise from w, with weight 1 past the row.
+// row's pad (from its key, or the constant pad without keys); wdst likewise from w, with weight 1
+// past the row.
 template <typename T>
 __global__ __launch_bounds__(kRagThreads) void ragged_pack_kernel(const T* __restrict__ src, const T* __restrict__ w,
                                                                   const int64_t* __restrict__ rows,
                                                                   const unsigned long long* __restrict__ keys,
-                                                                  int64_t total, int64_t L, int64_t cpr, double sgn,
-                                                                  T* __restrict__ dst, T* __restrict__ wdst) {
+                                                                  T cpad, int64_t total, int64_t L, int64_t cpr,
+                                                                  double sgn, T* __restrict__ dst,
+                                                                  T* __restrict__ wdst) {
   const int64_t b = blockIdx.x;
   const int64_t r = b / cpr, c = b - r * cpr;
   int64_t first, len;
   row_of(rows, r, total, L, first, len);
-  const T pad = keys != nullptr ? pad_of<T>(keys[r], sgn) : T(0);
+  const T pad = keys != nullptr ? pad_of<T>(keys[r], sgn) : cpad;
   const int64_t e0 = c * kRagChunk;
 #pragma unroll
   for (int u = 0; u < kRagE; ++u) {
@@ -155,8 +164,22 @@ __global__ __launch_bounds__(kRagThreads) void ragged_unpack_kernel(const T* __r
   }
 }
 
+// rows[i] = (offsets[o], offsets[o + 1] - offsets[o]) for o = order[i] (clamped into the rows).
+__global__ __launch_bounds__(kRagThreads) void ragged_rows_kernel(const int64_t* __restrict__ offsets, int64_t nrows,
+                                                                  const int64_t* __restrict__ order, int64_t n,
+                                                                  int64_t* __restrict__ rows) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kRagThreads + threadIdx.x;
+  if (i >= n) return;
+  int64_t o = order[i];
+  o = o < 0 ? 0 : (o >= nrows ? nrows - 1 : o);
+  const int64_t a = offsets[o];
+  rows[2 * i] = a;
+  rows[2 * i + 1] = offsets[o + 1] - a;
+}
+
 // One wave per row: a row whose last block reaches into its pad (start bit len clear, len < L)
-// has gy (and gw) over that block scaled by (W + L - len) / W, W its own weight over the block.
+// has gy (and gw) over that block scaled by (W + P) / W, W its own weight over the block and P
+// the pad elements in it, those before the next start bit (or L).
 template <typename T>
 __global__ __launch_bounds__(kRagThreads) void ragged_grad_fix_kernel(const uint32_t* __restrict__ starts,
                                                                       const T* __restrict__ w,
@@ -191,11 +214,32 @@ __global__ __launch_bounds__(kRagThreads) void ragged_grad_fix_kernel(const uint
     }
     s = pos;  // (word 0 holds bit 0: the loop ends there at the latest)
   }
+  // the block's end: the first start bit past len (bits at L or beyond count as L)
+  const int64_t words = (L + 31) / 32, w0 = (len + 1) >> 5;
+  int64_t e = L;
+  for (int64_t base = w0; base < words; base += kWave) {
+    const int64_t j = base + lane;
+    int64_t pos = L;
+    if (j < words) {
+      uint32_t bits = srow[j];
+      if (j == w0) bits &= ~0u << ((len + 1) & 31);
+      if (bits != 0) pos = j * 32 + __builtin_ctz(bits);
+    }
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) {
+      const int64_t o = __shfl_xor(pos, d, kWave);
+      pos = o < pos ? o : pos;
+    }
+    if (pos < L) {  // (the same in every lane)
+      e = pos;
+      break;
+    }
+  }
   double wsum = 0.0;
   for (int64_t i = s + lane; i < len; i += kWave) wsum += w != nullptr ? static_cast<double>(w[first + i]) : 1.0;
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) wsum += __shfl_xor(wsum, d, kWave);
-  const double f = (wsum + static_cast<double>(L - len)) / wsum;
+  const double f = (wsum + static_cast<double>(e - len)) / wsum;
   for (int64_t i = s + lane; i < len; i += kWave) {
     gy[first + i] = static_cast<T>(static_cast<double>(gy[first + i]) * f);
     if (gw != nullptr) gw[first + i] = static_cast<T>(static_cast<double>(gw[first + i]) * f);
@@ -221,19 +265,26 @@ hipError_t ragged_extreme(const void* y, int64_t total, const int64_t* rows, int
 }
 
 hipError_t ragged_pack(const void* src, const void* w, int64_t total, const int64_t* rows,
-                       const unsigned long long* keys, int64_t k, int64_t L, int dtype, bool increasing, void* dst,
-                       void* wdst, hipStream_t stream) {
+                       const unsigned long long* keys, double pad, int64_t k, int64_t L, int dtype, bool increasing,
+                       void* dst, void* wdst, hipStream_t stream) {
   const int64_t cpr = ragged_chunks(L);
   const dim3 grid(static_cast<unsigned>(k * cpr));
   const double sgn = increasing ? 1.0 : -1.0;
   if (dtype == TI_F32)
     ragged_pack_kernel<float><<<grid, dim3(kRagThreads), 0, stream>>>(
-        static_cast<const float*>(src), static_cast<const float*>(w), rows, keys, total, L, cpr, sgn,
-        static_cast<float*>(dst), static_cast<float*>(wdst));
+        static_cast<const float*>(src), static_cast<const float*>(w), rows, keys, static_cast<float>(pad), total, L,
+        cpr, sgn, static_cast<float*>(dst), static_cast<float*>(wdst));
   else
     ragged_pack_kernel<double><<<grid, dim3(kRagThreads), 0, stream>>>(
-        static_cast<const double*>(src), static_cast<const double*>(w), rows, keys, total, L, cpr, sgn,
+        static_cast<const double*>(src), static_cast<const double*>(w), rows, keys, pad, total, L, cpr, sgn,
         static_cast<double*>(dst), static_cast<double*>(wdst));
+  return hipGetLastError();
+}
+
+hipError_t ragged_rows(const int64_t* offsets, int64_t nrows, const int64_t* order, int64_t n, int64_t* rows,
+                       hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((n + kRagThreads - 1) / kRagThreads));
+  ragged_rows_kernel<<<grid, dim3(kRagThreads), 0, stream>>>(offsets, nrows, order, n, rows);
   return hipGetLastError();
 }
 

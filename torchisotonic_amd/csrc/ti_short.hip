@@ -652,7 +652,11 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_fit_kernel(
 // The plan of a ragged set, one pass over its offsets: plan[0] bit 0 set if offsets[0] != 0,
 // bit 1 if offsets[nrows] != total, bit 2 if some row has a negative length; plan[1] the longest
 // row of at most kShortMax elements, plan[2] the number of longer rows, plan[3] the longest
-// row. plan: four zeroed words. Each thread reads kPlanRows rows at a time (their loads in
+// row; plan[4 + b] the number of rows of length bucket b (lengths in (2^(b-1), 2^b], b >= 6:
+// the rows past kShortMax) and plan[68 + b] the longest of them. plan: kRaggedPlanWords zeroed
+// words. keys (optional): per row its bucket, 0 for a row of at most kShortMax elements. A
+// workgroup's bucket counts and longest rows gather in LDS (atomics there), then one thread per
+// nonempty bucket folds them into plan. Each thread reads kPlanRows rows at a time (their loads in
 // flight together), each workgroup reduces its rows through its waves and LDS, then one thread
 // folds the result into plan. The grid stays at kPlanBlocks: the folds are atomics on the same
 // four words, about 12 ns each on MI355X, so 256 workgroups take 10.7 us at 1e6 rows where 977
@@ -660,6 +664,9 @@ __global__ __launch_bounds__((short_threads<NMAX, W>())) void ragged_fit_kernel(
 constexpr int kPlanThreads = 256;
 constexpr int kPlanRows = 4;
 constexpr int kPlanBlocks = 256;
+
+// the length bucket of a row longer than kShortMax: ceil(log2(len))
+__device__ __forceinline__ int ragged_bucket(unsigned long long len) { return 64 - __builtin_clzll(len - 1); }
 
 __device__ __forceinline__ void plan_fold(unsigned long long v[4], unsigned long long o[4]) {
   v[0] |= o[0];
@@ -670,8 +677,15 @@ __device__ __forceinline__ void plan_fold(unsigned long long v[4], unsigned long
 
 __global__ __launch_bounds__(kPlanThreads) void ragged_plan_kernel(const int64_t* __restrict__ offsets,
                                                                   int64_t nrows, int64_t total,
-                                                                  unsigned long long* __restrict__ plan) {
+                                                                  unsigned long long* __restrict__ plan,
+                                                                  uint8_t* __restrict__ keys) {
   __shared__ unsigned long long part[kPlanThreads / 64][4];
+  __shared__ unsigned long long hcnt[64], hmax[64];
+  if (threadIdx.x < 64) {
+    hcnt[threadIdx.x] = 0;
+    hmax[threadIdx.x] = 0;
+  }
+  __syncthreads();
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
   unsigned long long v[4] = {0, 0, 0, 0};  // errors, longest short row, long rows, longest row
   for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; r0 < nrows;
@@ -684,14 +698,23 @@ __global__ __launch_bounds__(kPlanThreads) void ragged_plan_kernel(const int64_t
     }
 #pragma unroll
     for (int u = 0; u < kPlanRows; ++u) {
+      int key = 0;
       if (len[u] < 0) {
         v[0] |= 4u;
       } else {
         const unsigned long long l = static_cast<unsigned long long>(len[u]);
-        if (len[u] <= kShortMax) v[1] = l > v[1] ? l : v[1];
-        else v[2] += 1;
+        if (len[u] <= kShortMax) {
+          v[1] = l > v[1] ? l : v[1];
+        } else {
+          v[2] += 1;
+          key = ragged_bucket(l);
+          atomicAdd(&hcnt[key], 1ull);
+          atomicMax(&hmax[key], l);
+        }
         v[3] = l > v[3] ? l : v[3];
       }
+      const int64_t r = r0 + u * stride;
+      if (keys != nullptr && r < nrows) keys[r] = static_cast<uint8_t>(key);
     }
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -717,6 +740,10 @@ __global__ __launch_bounds__(kPlanThreads) void ragged_plan_kernel(const int64_t
     if (v[1] != 0) atomicMax(&plan[1], v[1]);
     if (v[2] != 0) atomicAdd(&plan[2], v[2]);
     if (v[3] != 0) atomicMax(&plan[3], v[3]);
+  }
+  if (threadIdx.x < 64 && hcnt[threadIdx.x] != 0) {  // (the barrier above ordered the LDS atomics)
+    atomicAdd(&plan[4 + threadIdx.x], hcnt[threadIdx.x]);
+    atomicMax(&plan[68 + threadIdx.x], hmax[threadIdx.x]);
   }
 }
 
@@ -1383,11 +1410,11 @@ hipError_t ragged_grad(const RaggedGradArgs& a) {
 }
 
 hipError_t ragged_plan(const int64_t* offsets, int64_t nrows, int64_t total, unsigned long long* plan,
-                       hipStream_t stream) {
+                       uint8_t* keys, hipStream_t stream) {
   const int64_t per_block = int64_t{kPlanThreads} * kPlanRows;
   const int64_t blocks = std::min<int64_t>(std::max<int64_t>((nrows + per_block - 1) / per_block, 1), kPlanBlocks);
   ragged_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPlanThreads), 0, stream>>>(offsets, nrows, total,
-                                                                                            plan);
+                                                                                            plan, keys);
   return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <limits>
 #include <optional>
 #include <vector>
 
@@ -237,23 +238,53 @@ RaggedHost& ragged_host(c10::DeviceIndex dev) {
   if (rh.ready == nullptr) {
     check_hip(hipEventCreateWithFlags(&rh.ready, hipEventDisableTiming), "hipEventCreateWithFlags");
     void* p = nullptr;
-    check_hip(hipHostMalloc(&p, 4 * sizeof(int64_t), hipHostMallocDefault), "hipHostMalloc");
+    check_hip(hipHostMalloc(&p, TI_RAGGED_PLAN_WORDS * sizeof(int64_t), hipHostMallocDefault), "hipHostMalloc");
     rh.words = static_cast<int64_t*>(p);
   }
   return rh;
 }
 
 constexpr int64_t kRaggedShort = 32;  // the longest rows ti_fwd_ragged fits
+// the op's one zeroed buffer, in int32 words: the plan, the weight flag, the flat start bits
+constexpr int64_t kPlanAt = 0, kBadAt = 2 * TI_RAGGED_PLAN_WORDS, kBitsAt = kBadAt + 2;
+
+// Length buckets of the longer rows, from the plan's counts and longest rows: (first descriptor,
+// rows, block length) triples. A bucket joins the next longer one while that pads at most
+// kBucketMerge more elements: a bucket's launches cost about as much as fitting that many (the
+// span, merge and expansion kernels of a small block run for tens of microseconds).
+constexpr int64_t kBucketMerge = int64_t{1} << 22;
+
+std::vector<int64_t> ragged_buckets(const int64_t* words, int64_t n_long) {
+  std::vector<int64_t> out;
+  int64_t first = 0, k = 0, L = 0;
+  for (int b = 6; b < 64; ++b) {
+    const int64_t kb = words[4 + b], Lb = words[68 + b];
+    if (kb <= 0) continue;
+    if (k > 0 && k * (Lb - L) > kBucketMerge) {
+      out.insert(out.end(), {first, k, L});
+      first += k;
+      k = 0;
+    }
+    k += kb;
+    L = Lb;
+  }
+  if (k > 0) out.insert(out.end(), {first, k, L});
+  TORCH_CHECK(first + k == n_long, "torchisotonic_amd: the plan's buckets hold ", first + k, " rows, not ", n_long);
+  return out;
+}
 
 // Ragged rows (rows packed end to end, offsets on the device) with their backward in C++, the
 // calls of ragged.py's steps in one operator: the offsets' plan (ti_ragged_plan) and the copy of
-// its four words to the host; given a bound max_len on the row lengths, the short rows' fit
+// its words to the host; given a bound max_len on the row lengths, the short rows' fit
 // (ti_fwd_ragged, which clamps every offset it reads) launched right behind that copy, so that
 // it runs while the host waits for the words; the wait and the offsets' errors; a second launch
 // over every short row where rows past the bound are at most 32 long; the longer rows a length
-// bucket at a time (lengths in (2^(b-1), 2^b]): the bucket's rows gathered into one dense block,
-// each padded beyond its own extreme (ti_ragged_extreme, ti_ragged_pack), one ti_fwd over the
-// block, and its fits scattered back (ti_ragged_unpack). The backward is one launch for the
+// bucket at a time (lengths in (2^(b-1), 2^b], small buckets merged into the next): the rows
+// in bucket order by a stable sort of the plan's keys on the device (ti_ragged_rows), the
+// buckets sized by the plan's counts; per bucket the rows gathered into one dense block, each
+// padded beyond its own extreme (float32: the largest finite value; float64: from
+// ti_ragged_extreme) by ti_ragged_pack, one ti_fwd over the block, and its fits scattered back
+// (ti_ragged_unpack). The backward is one launch for the
 // short rows (ti_bwd_ragged) and, per bucket, g gathered into a block, one ti_bwd from the
 // bucket's forward, and the gradients scattered back.
 struct RaggedFn : public torch::autograd::Function<RaggedFn> {
@@ -276,15 +307,21 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     const hipStream_t stream = c10::hip::getCurrentHIPStream(values.device().index()).stream();
     const unsigned flags = (increasing ? TI_INCREASING : 0u) | TI_EXACT;
 
-    // one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
-    at::Tensor zeros = at::zeros({10 + (total + 31) / 32}, values.options().dtype(at::kInt));
+    // one zeroed buffer: the plan, the weight flag, the flat start bits
+    at::Tensor zeros = at::zeros({kBitsAt + (total + 31) / 32}, values.options().dtype(at::kInt));
     int32_t* zp = zeros.data_ptr<int32_t>();
-    int64_t* plan = reinterpret_cast<int64_t*>(zp);
-    uint32_t* bad = w.defined() ? reinterpret_cast<uint32_t*>(zp + 8) : nullptr;
-    uint32_t* bits = reinterpret_cast<uint32_t*>(zp + 10);
+    int64_t* plan = reinterpret_cast<int64_t*>(zp + kPlanAt);
+    uint32_t* bad = w.defined() ? reinterpret_cast<uint32_t*>(zp + kBadAt) : nullptr;
+    uint32_t* bits = reinterpret_cast<uint32_t*>(zp + kBitsAt);
     RaggedHost& rh = ragged_host(values.device().index());
-    check(ti_ragged_plan(offsets.data_ptr<int64_t>(), nrows, total, plan, stream), "isotonic_ragged");
-    check_hip(hipMemcpyAsync(rh.words, plan, 4 * sizeof(int64_t), hipMemcpyDeviceToHost, stream), "hipMemcpyAsync");
+    // (the rows' bucket keys unless max_len rules longer rows out)
+    const bool keyed = !(max_len > 0 && max_len <= kRaggedShort);
+    at::Tensor keys = keyed ? at::empty({nrows}, offsets.options().dtype(at::kByte)) : at::Tensor();
+    check(ti_ragged_plan(offsets.data_ptr<int64_t>(), nrows, total, plan,
+                         keyed ? keys.data_ptr<uint8_t>() : nullptr, stream),
+          "isotonic_ragged");
+    check_hip(hipMemcpyAsync(rh.words, plan, TI_RAGGED_PLAN_WORDS * sizeof(int64_t), hipMemcpyDeviceToHost, stream),
+              "hipMemcpyAsync");
     check_hip(hipEventRecord(rh.ready, stream), "hipEventRecord");
     at::Tensor out = at::empty_like(values);
     const int64_t nmax = max_len > 0 ? std::min(max_len, kRaggedShort) : 0;
@@ -299,50 +336,42 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     TORCH_CHECK_VALUE((err & 4) == 0, from_lengths ? "lengths must be non-negative" : "offsets must not decrease");
     TORCH_CHECK_VALUE((err & 3) == 0, "offsets must run from 0 to values.numel() = ", total);
     if (short_max > nmax) fit_short(short_max);
-    // the longer rows, a length bucket at a time (their starts and lengths to the host once)
+    // the longer rows, a length bucket at a time
     const bool want = values.requires_grad() || (w.defined() && w.requires_grad());
     std::vector<int64_t> buckets;  // per bucket: its first descriptor, its rows, its block length
     std::vector<at::Tensor> keep;  // the descriptors, then per bucket: y, w blocks, starts, workspace
     if (n_long > 0) {
-      const at::Tensor len = offsets.slice(0, 1) - offsets.slice(0, 0, nrows);
-      const at::Tensor r = at::nonzero(len > kRaggedShort).view(-1);
-      const at::Tensor se = at::stack({offsets.index_select(0, r), len.index_select(0, r)}, 1).cpu();
-      const int64_t* sp = se.data_ptr<int64_t>();
-      const int64_t nl = se.size(0);
-      std::vector<std::vector<int64_t>> by(64);
-      for (int64_t i = 0; i < nl; ++i) {
-        int b = 0;
-        while ((int64_t{1} << b) < sp[2 * i + 1]) ++b;
-        by[b].push_back(i);
+      buckets = ragged_buckets(rh.words, n_long);
+      if (!keyed) {  // (max_len was wrong: the keys now)
+        keys = at::empty({nrows}, offsets.options().dtype(at::kByte));
+        check(ti_ragged_plan(offsets.data_ptr<int64_t>(), nrows, total,
+                             at::zeros({TI_RAGGED_PLAN_WORDS}, offsets.options()).data_ptr<int64_t>(),
+                             keys.data_ptr<uint8_t>(), stream),
+              "isotonic_ragged");
       }
-      std::vector<int64_t> desc;
-      desc.reserve(2 * nl);
-      for (int b = 0; b < 64; ++b) {
-        if (by[b].empty()) continue;
-        int64_t L = 0;
-        buckets.push_back(static_cast<int64_t>(desc.size() / 2));
-        for (int64_t i : by[b]) {
-          desc.push_back(sp[2 * i]);
-          desc.push_back(sp[2 * i + 1]);
-          L = std::max(L, sp[2 * i + 1]);
-        }
-        buckets.push_back(static_cast<int64_t>(by[b].size()));
-        buckets.push_back(L);
-      }
-      const at::Tensor rows =
-          at::from_blob(desc.data(), {nl, 2}, at::TensorOptions().dtype(at::kLong)).to(values.device());
-      const at::Tensor keys = at::zeros({nl}, rows.options());
+      // the longer rows in bucket order (the short rows, key 0, sort first)
+      const at::Tensor order = std::get<1>(at::sort(keys, /*stable=*/true, 0, false)).slice(0, nrows - n_long);
+      const at::Tensor rows = at::empty({n_long, 2}, offsets.options());
+      check(ti_ragged_rows(offsets.data_ptr<int64_t>(), nrows, order.data_ptr<int64_t>(), n_long,
+                           rows.data_ptr<int64_t>(), stream),
+            "isotonic_ragged");
       keep.push_back(rows);
       const int64_t* rp = rows.data_ptr<int64_t>();
-      uint64_t* kp = reinterpret_cast<uint64_t*>(keys.data_ptr<int64_t>());
+      // float32: every row padded with the largest finite value (no extreme needed)
+      const bool f32 = dtype == TI_F32;
+      const at::Tensor ext = f32 ? at::Tensor() : at::zeros({n_long}, offsets.options());
+      uint64_t* kp = f32 ? nullptr : reinterpret_cast<uint64_t*>(ext.data_ptr<int64_t>());
+      const double cpad = f32 ? (increasing ? 1.0 : -1.0) * static_cast<double>(std::numeric_limits<float>::max()) : 0.0;
       for (size_t i = 0; i < buckets.size(); i += 3) {
         const int64_t f = buckets[i], k = buckets[i + 1], L = buckets[i + 2];
-        check(ti_ragged_extreme(ptr(values), total, rp + 2 * f, k, L, dtype, increasing ? 1 : 0, kp + f, stream),
-              "isotonic_ragged");
+        if (!f32) {
+          check(ti_ragged_extreme(ptr(values), total, rp + 2 * f, k, L, dtype, increasing ? 1 : 0, kp + f, stream),
+                "isotonic_ragged");
+        }
         at::Tensor yb = at::empty({k, L}, values.options());
         at::Tensor wb = w.defined() ? at::empty({k, L}, values.options()) : at::Tensor();
-        check(ti_ragged_pack(ptr(values), ptr(w), total, rp + 2 * f, kp + f, k, L, dtype, increasing ? 1 : 0, ptr(yb),
-                             ptr(wb), stream),
+        check(ti_ragged_pack(ptr(values), ptr(w), total, rp + 2 * f, f32 ? nullptr : kp + f, cpad, k, L, dtype,
+                             increasing ? 1 : 0, ptr(yb), ptr(wb), stream),
               "isotonic_ragged");
         at::Tensor starts = at::empty({ti_starts_words(k, L)}, values.options().dtype(at::kInt));
         at::Tensor ws = workspace(true, k, L, dtype, w.defined(), values.device());
@@ -362,7 +391,7 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
       }
     }
     if (bad != nullptr && (short_max > 0 || n_long > 0)) {
-      TORCH_CHECK_VALUE(zeros.slice(0, 8, 9).item<int32_t>() == 0, "weight must be strictly positive");
+      TORCH_CHECK_VALUE(zeros.slice(0, kBadAt, kBadAt + 1).item<int32_t>() == 0, "weight must be strictly positive");
     }
     if (want) {
       std::vector<at::Tensor> saved = {values, w, offsets, zeros};
@@ -397,7 +426,7 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     // longer rows' by their own backward)
     at::Tensor gy = at::empty_like(g);
     at::Tensor gw = want_w ? at::empty_like(g) : at::Tensor();
-    const uint32_t* bits = reinterpret_cast<const uint32_t*>(zeros.data_ptr<int32_t>() + 10);
+    const uint32_t* bits = reinterpret_cast<const uint32_t*>(zeros.data_ptr<int32_t>() + kBitsAt);
     if (short_max > 0) {
       check(ti_bwd_ragged(bits, ptr(g), ptr(w), want_w ? ptr(values) : nullptr, ptr(gy), ptr(gw),
                           offsets.data_ptr<int64_t>(), nrows, total, short_max, dtype, 0u, 0.0, 0.0, stream),
@@ -415,7 +444,8 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
         const at::Tensor& starts = saved[j + 2];
         const at::Tensor& ws = saved[j + 3];
         at::Tensor gb = at::empty({k, L}, g.options());
-        check(ti_ragged_pack(ptr(g), nullptr, total, rp + 2 * f, nullptr, k, L, dtype, 0, ptr(gb), nullptr, stream),
+        check(ti_ragged_pack(ptr(g), nullptr, total, rp + 2 * f, nullptr, 0.0, k, L, dtype, 0, ptr(gb), nullptr,
+                             stream),
               "isotonic_ragged backward");
         at::Tensor gyb = at::empty({k, L}, g.options());
         at::Tensor gwb = want_w ? at::empty({k, L}, g.options()) : at::Tensor();

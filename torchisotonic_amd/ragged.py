@@ -12,12 +12,14 @@ and the row offsets (CSR layout) go to the GPU as they are:
   kernel has checked the offsets and sized the rows and its four words have reached the host
   (the call's one wait); with ``max_len``, a bound on the row lengths, that launch goes before
   the wait and runs during it;
-- longer rows are fitted a length bucket at a time (lengths in (2^(b-1), 2^b]): the bucket's
-  rows gathered into one dense [k, L] block, each padded beyond its own extreme with the
-  reference's rule for padding (a tail above the row's maximum for an increasing fit, below its
-  minimum for a decreasing one, which pools with nothing of the row), one ``ti_fwd`` over the
-  block, and the fits scattered back (``ti_ragged_extreme``, ``ti_ragged_pack``,
-  ``ti_ragged_unpack``);
+- longer rows are fitted a length bucket at a time (lengths in (2^(b-1), 2^b], a small bucket
+  joined to the next): the plan's kernel gives each row its bucket key and each bucket its size,
+  a stable sort of the keys on the device orders the rows (``ti_ragged_rows``), and each
+  bucket's rows are gathered into one dense [k, L] block, each padded beyond its own extreme
+  with the reference's rule for padding (a tail above the row's maximum for an increasing fit,
+  below its minimum for a decreasing one, which pools with nothing of the row; for float32 the
+  largest finite value, which needs no extreme), one ``ti_fwd`` over the block, and the fits
+  scattered back (``ti_ragged_extreme``, ``ti_ragged_pack``, ``ti_ragged_unpack``);
 - the backward of the rows of 1 to 32 elements is one HIP launch too (``ti_bwd_ragged``: one
   thread per row, the blocks read from the forward's flat start bits); each bucket of longer
   rows takes its gradients from its own forward (``ti_bwd`` over the block of g, scattered
@@ -40,41 +42,44 @@ from torch import Tensor
 
 from torchisotonic_amd import _ext
 
-_SHORT = 32  # the longest rows the one-launch kernel fits
-
-
 _local = threading.local()
 
 
 def _host_words(device: torch.device) -> tuple[Tensor, torch.cuda.Event]:
-    """Per thread and device: four pinned host words the plan is copied into, and the event
+    """Per thread and device: the pinned host words the plan is copied into, and the event
     recorded once they are there."""
     cache = getattr(_local, "plan", None)
     if cache is None:
         cache = _local.plan = {}
     if device.index not in cache:
-        cache[device.index] = (torch.empty(4, dtype=torch.int64, pin_memory=True), torch.cuda.Event())
+        cache[device.index] = (torch.empty(_ext.RAGGED_PLAN_WORDS, dtype=torch.int64, pin_memory=True),
+                               torch.cuda.Event())
     return cache[device.index]
+
+
+_PLAN_I32 = 2 * _ext.RAGGED_PLAN_WORDS  # the plan's int32 words in the zeroed buffer
 
 
 def _plan(offsets, lengths, values: Tensor, weighted: bool):
     """The row offsets as a device int64 tensor; zeroed device words for the fit (the flat
     start bits and the weight flag); and the plan of the offsets under way: one kernel
-    (ti_ragged_plan) checks them and sizes the rows, and four words are on their way to the host
-    (the offsets themselves are never copied whole; ``_plan_wait`` reads them)."""
+    (ti_ragged_plan) checks them, sizes the rows and their length buckets and writes each
+    row's bucket key, and the plan's words are on their way to the host (the offsets
+    themselves are never copied; ``_plan_wait`` reads the words)."""
     off = _offsets_tensor(offsets, lengths, values.device)
     nrows, total = off.numel() - 1, values.numel()
-    # one zeroed buffer: the plan (4 int64), the weight flag, the flat start bits
-    zeros = torch.zeros(10 + (total + 31) // 32, dtype=torch.int32, device=values.device)
-    plan, bad, bits = zeros[:8].view(torch.int64), zeros[8:9], zeros[10:]
+    # one zeroed buffer: the plan, the weight flag, the flat start bits
+    zeros = torch.zeros(_PLAN_I32 + 2 + (total + 31) // 32, dtype=torch.int32, device=values.device)
+    plan, bad, bits = zeros[:_PLAN_I32].view(torch.int64), zeros[_PLAN_I32:_PLAN_I32 + 1], zeros[_PLAN_I32 + 2:]
+    keys = torch.empty(nrows, dtype=torch.uint8, device=values.device)
     host, ready = _host_words(values.device)
     with _ext._on_device(values.device):
         stream = torch.cuda.current_stream(values.device)
-        _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), stream.cuda_stream),
-                    "isotonic_ragged")
+        _ext._check(_ext.load().ti_ragged_plan(off.data_ptr(), nrows, total, plan.data_ptr(), keys.data_ptr(),
+                                               stream.cuda_stream), "isotonic_ragged")
         host.copy_(plan, non_blocking=True)
         ready.record(stream)
-    return off, bits, (bad if weighted else None), (host, ready, offsets is None, total)
+    return off, bits, (bad if weighted else None), (host, ready, offsets is None, total, keys)
 
 
 def _offsets_tensor(offsets, lengths, device: torch.device) -> Tensor:
@@ -96,31 +101,50 @@ def _offsets_tensor(offsets, lengths, device: torch.device) -> Tensor:
     return t.contiguous()
 
 
-def _plan_wait(off: Tensor, pending) -> tuple[int, list[tuple[int, int]]]:
+_BUCKET_MERGE = 1 << 22  # a bucket joins the next while that pads at most this many elements
+
+
+def _buckets(words: list[int], n_long: int) -> list[tuple[int, int, int]]:
+    """The length buckets of the longer rows from the plan's counts and longest rows, a bucket
+    joined to the next longer one while that pads at most _BUCKET_MERGE more elements (a
+    bucket's launches cost about as much as fitting that many): (first row in bucket order,
+    rows, block length) triples."""
+    out, first, k, L = [], 0, 0, 0
+    for b in range(6, 64):
+        kb, lb = words[4 + b], words[68 + b]
+        if kb <= 0:
+            continue
+        if k > 0 and k * (lb - L) > _BUCKET_MERGE:
+            out.append((first, k, L))
+            first, k = first + k, 0
+        k, L = k + kb, lb
+    if k > 0:
+        out.append((first, k, L))
+    assert first + k == n_long, (first + k, n_long)
+    return out
+
+
+def _plan_wait(off: Tensor, pending) -> tuple[int, tuple]:
     """The plan's words, once they are on the host (the stream's later work keeps running): the
-    offsets' errors raised, the longest row of at most 32 elements (0 if none), and the (start,
-    end) of every longer row."""
-    host, ready, from_lengths, total = pending
+    offsets' errors raised, the longest row of at most 32 elements (0 if none), and the longer
+    rows' plan: their number, their buckets and the rows' bucket keys."""
+    host, ready, from_lengths, total, keys = pending
     ready.synchronize()
-    err, short_max, n_long, _ = host.tolist()
+    words = host.tolist()
+    err, short_max, n_long = words[0], words[1], words[2]
     if err & 4:
         raise ValueError("lengths must be non-negative" if from_lengths else "offsets must not decrease")
     if err & 3:
         raise ValueError(f"offsets must run from 0 to values.numel() = {total}")
-    long_rows: list[tuple[int, int]] = []
-    if n_long:
-        ln = off[1:] - off[:-1]
-        r = torch.nonzero(ln > _SHORT).view(-1)
-        long_rows = [(int(x), int(y)) for x, y in torch.stack([off[r], off[r + 1]], 1).tolist()]
-    return int(short_max), long_rows
+    return int(short_max), (int(n_long), _buckets(words, n_long) if n_long else [], keys)
 
 
 def _offsets(offsets, lengths, values: Tensor, weighted: bool):
     """``_plan`` and ``_plan_wait`` in a row: the offsets, validated, the longest short row, the
-    longer rows, and the zeroed bits and weight flag."""
+    longer rows' plan, and the zeroed bits and weight flag."""
     off, bits, bad, pending = _plan(offsets, lengths, values, weighted)
-    short_max, long_rows = _plan_wait(off, pending)
-    return off, short_max, long_rows, bits, bad
+    short_max, long_plan = _plan_wait(off, pending)
+    return off, short_max, long_plan, bits, bad
 
 
 def _fit_short(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, nmax: int, bits: Tensor,
@@ -137,48 +161,53 @@ def _fit_short(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, nmax:
     _ext._check(rc, "isotonic_ragged")
 
 
-def _buckets(long_spans: list[tuple[int, int]]) -> list[tuple[list[tuple[int, int]], int]]:
-    """The longer rows (start, end) grouped by length bucket, (2^(b-1), 2^b]: per bucket its rows
-    as (start, length) and its block length (the longest of them)."""
-    by: dict[int, list[tuple[int, int]]] = {}
-    for a, b in long_spans:
-        by.setdefault((b - a - 1).bit_length(), []).append((a, b - a))
-    return [(rows, max(n for _, n in rows)) for _, rows in sorted(by.items())]
-
-
-def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, long_spans: list[tuple[int, int]],
+def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, long_plan: tuple,
               increasing: bool) -> list:
-    """The longer rows, a bucket at a time (ti_ragged_extreme, ti_ragged_pack, ti_fwd over the
-    block, ti_ragged_unpack); per bucket (its rows as (start, length), block length L, the block's
-    packed starts, its forward workspace, the y and w blocks)."""
+    """The longer rows, a bucket at a time: the rows in bucket order (a stable sort of the plan's
+    keys, ti_ragged_rows), then per bucket the block of its rows, each padded beyond its extreme
+    (float32: the largest finite value; float64: ti_ragged_extreme), ti_fwd over it, and the fits
+    scattered back (ti_ragged_pack, ti_ragged_unpack). Per bucket: its rows' (first, length) on
+    the host, the block length L, the block's packed starts, its forward workspace, the y and w
+    blocks."""
+    n_long, buckets, keys = long_plan
+    if n_long == 0:
+        return []
     lib = _ext.load()
     code = _ext._dtype_code(values)
-    total = values.numel()
+    nrows, total = off.numel() - 1, values.numel()
     s = _ext._stream(values)
     inc = 1 if increasing else 0
-    buckets = []
-    for rows, L in _buckets(long_spans):
-        k = len(rows)
-        desc = torch.tensor(rows, dtype=torch.int64).to(values.device)
-        keys = torch.zeros(k, dtype=torch.int64, device=values.device)
+    f32 = values.dtype == torch.float32
+    pad = (1.0 if increasing else -1.0) * float(torch.finfo(torch.float32).max) if f32 else 0.0
+    order = torch.sort(keys, stable=True).indices[nrows - n_long:].contiguous()
+    rows = torch.empty(n_long, 2, dtype=torch.int64, device=values.device)
+    ext = None if f32 else torch.zeros(n_long, dtype=torch.int64, device=values.device)
+    with _ext._on_device(values.device):
+        _ext._check(lib.ti_ragged_rows(off.data_ptr(), nrows, order.data_ptr(), n_long, rows.data_ptr(), s),
+                    "isotonic_ragged")
+    done = []
+    for f, k, L in buckets:
+        desc = rows[f:f + k]
+        kp = None if ext is None else ext[f:f + k].data_ptr()
         with _ext._on_device(values.device):
-            _ext._check(lib.ti_ragged_extreme(values.data_ptr(), total, desc.data_ptr(), k, L, code, inc,
-                                              keys.data_ptr(), s), "isotonic_ragged")
+            if ext is not None:
+                _ext._check(lib.ti_ragged_extreme(values.data_ptr(), total, desc.data_ptr(), k, L, code, inc, kp, s),
+                            "isotonic_ragged")
             yb = torch.empty(k, L, dtype=values.dtype, device=values.device)
             wb = None if w is None else torch.empty_like(yb)
-            _ext._check(lib.ti_ragged_pack(values.data_ptr(), _ext._ptr(w), total, desc.data_ptr(), keys.data_ptr(),
-                                           k, L, code, inc, yb.data_ptr(), _ext._ptr(wb), s), "isotonic_ragged")
+            _ext._check(lib.ti_ragged_pack(values.data_ptr(), _ext._ptr(w), total, desc.data_ptr(), kp, pad, k, L,
+                                           code, inc, yb.data_ptr(), _ext._ptr(wb), s), "isotonic_ragged")
         ob, starts, bad_b, ws = _ext.fit(yb, wb, increasing, True, True)
         if bad_b:
             raise ValueError("weight must be strictly positive")
         with _ext._on_device(values.device):
             _ext._check(lib.ti_ragged_unpack(ob.data_ptr(), None, desc.data_ptr(), k, L, code, out.data_ptr(), None,
                                              total, None, None, s), "isotonic_ragged")
-        buckets.append((rows, L, starts, ws, yb, wb))
-    return buckets
+        done.append((desc.cpu().numpy(), L, starts, ws, yb, wb))
+    return done
 
 
-def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spans: list[tuple[int, int]],
+def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_plan: tuple,
          bits: Tensor, bad: Tensor | None, increasing: bool) -> tuple[Tensor, list]:
     """The fits of every row (packed like values) with the flat start bits of the short rows
     in ``bits`` (a longer row has its first bit only), and per bucket of longer rows what
@@ -186,7 +215,7 @@ def _fit(values: Tensor, w: Tensor | None, off: Tensor, short_max: int, long_spa
     out = torch.empty_like(values)
     if short_max > 0:
         _fit_short(values, w, out, off, short_max, bits, bad, increasing)
-    long_rows = _fit_long(values, w, out, long_spans, increasing)
+    long_rows = _fit_long(values, w, out, off, long_plan, increasing)
     if bad is not None and short_max > 0 and bool(bad.item()):
         raise ValueError("weight must be strictly positive")
     return out, long_rows
