@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 8
+#define TI_ABI_VERSION 9
 
 /* dtype codes */
 #define TI_F32 0
@@ -310,6 +310,29 @@ int ti_ragged_pack(const void* src, const void* w, int64_t total, const int64_t*
                    double pad, int64_t k, int64_t L, int dtype, int increasing, void* dst, void* wdst, void* stream);
 int ti_ragged_unpack(const void* src, const void* src2, const int64_t* rows, int64_t k, int64_t L, int dtype,
                      void* dst, void* dst2, int64_t total, const uint32_t* starts, const void* w, void* stream);
+
+/*
+ * ti_fwd and ti_bwd for the k rows of a length bucket read and written in place in the packed
+ * arrays (`total` elements; rows as for ti_ragged_pack), without a block: row r is taken as the
+ * r-th row of a [k, L] block (L > 32, at least every length) whose elements past the row's
+ * length are `pad` with weight 1 (g = 0 in the backward), made in registers and never read;
+ * y, w, out, g, gy and gw are the packed arrays, and only the rows' own elements are written.
+ * starts, the workspaces and the flags are those of ti_fwd / ti_bwd for batch = k and n = L (the
+ * starts in the block's layout). Float32 only (TI_EDTYPE otherwise: ti_ragged_pack serves
+ * float64). The pad must lie beyond every value of its row, as for ti_ragged_pack: the largest
+ * finite float32, negated for a decreasing fit.
+ * ti_bwd_rows also applies ti_ragged_unpack's correction to rows whose pad joined their last
+ * block. The packed arrays must stay below 0x7FFF0000 bytes (one buffer resource addresses
+ * them; TI_ESIZE otherwise: ti_ragged_pack serves larger ones). No counterpart in the reference
+ * (see ti_ragged_pack).
+ */
+int ti_fwd_rows(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight, const int64_t* rows,
+                int64_t k, int64_t L, int64_t total, double pad, int dtype, unsigned flags, double y_min,
+                double y_max, void* workspace, size_t workspace_bytes, void* stream);
+int ti_bwd_rows(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspace_bytes, const void* g,
+                const void* w, const void* y, void* gy, void* gw, const int64_t* rows, int64_t k, int64_t L,
+                int64_t total, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
+                size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace ti_grad needs for this problem set (0 when batch * n <= 2048). */
 int ti_grad_workspace(int64_t batch, int64_t n, int dtype, size_t* bytes);

@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 RAGGED_PLAN_WORDS = 132  # (ti_ragged_plan)
 
 F32, F64 = 0, 1
@@ -50,6 +50,8 @@ SYMBOLS = (
     "ti_ragged_pack",
     "ti_ragged_unpack",
     "ti_ragged_rows",
+    "ti_fwd_rows",
+    "ti_bwd_rows",
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_fwd_ev_hulls",
@@ -107,6 +109,10 @@ def load() -> ctypes.CDLL:
     lib.ti_ragged_pack.argtypes = [_vp, _vp, _i64, _vp, _vp, _dbl, _i64, _i64, _int, _int, _vp, _vp, _vp]
     lib.ti_ragged_rows.restype = _int
     lib.ti_ragged_rows.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp]
+    lib.ti_fwd_rows.restype = _int
+    lib.ti_fwd_rows.argtypes = [_vp] * 6 + [_i64, _i64, _i64, _dbl, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
+    lib.ti_bwd_rows.restype = _int
+    lib.ti_bwd_rows.argtypes = [_vp, _vp, _sz] + [_vp] * 6 + [_i64, _i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_ragged_unpack.restype = _int
     lib.ti_ragged_unpack.argtypes = [_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp, _i64, _vp, _vp, _vp]
     lib.ti_bwd.restype = _int

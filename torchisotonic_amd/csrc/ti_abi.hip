@@ -152,7 +152,7 @@ namespace {
 int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
              int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
              void* workspace, size_t workspace_bytes, void* stream, hipEvent_t weights_read,
-             hipEvent_t hulls_ready = nullptr, int64_t* max_vertices = nullptr) {
+             hipEvent_t hulls_ready = nullptr, int64_t* max_vertices = nullptr, const ti::RowMap* map = nullptr) {
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   // the one-kernel paths read the weights in their only kernel (and have no hulls to keep)
   auto then_record = [&](int rc) -> int {
@@ -177,6 +177,7 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
     weights_read = nullptr;
   }
   if (n <= ti::kShortMax) {
+    if (map != nullptr) return fail(TI_EINVAL, "ragged rows of a block need a block longer than 32");
     if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
     ti::ShortArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
     return then_record(launched(ti::short_fit(a), "short-row fit"));
@@ -190,6 +191,7 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
   a.weights_read = weights_read;  // after the span kernel, the first of several
   a.hulls_ready = hulls_ready;    // after the merges
   a.max_vertices = max_vertices;
+  if (map != nullptr) a.map = *map;
   return launched(ti::long_fit(a, plan, workspace), "multi-tile fit");
 }
 
@@ -197,7 +199,7 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
 int bwd_impl(const uint32_t* starts, const void* fwd_ws, size_t fwd_ws_bytes, const void* kept,
              size_t kept_bytes, int64_t kept_maxc, const void* g, const void* w, const void* y, void* gy,
              void* gw, int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
-             void* workspace, size_t workspace_bytes, void* stream) {
+             void* workspace, size_t workspace_bytes, void* stream, const ti::RowMap* map = nullptr) {
   if (int rc = check_shape(batch, n, dtype)) return rc;
   if (batch == 0) return ok();
   if (starts == nullptr || g == nullptr) return fail(TI_EINVAL, "starts and g must not be null");
@@ -206,6 +208,7 @@ int bwd_impl(const uint32_t* starts, const void* fwd_ws, size_t fwd_ws_bytes, co
     return fail(TI_EINVAL, "y is needed for the weight gradient and for the clamp's mask");
   if (gy == nullptr && gw == nullptr) return ok();
   if (n <= ti::kShortMax) {
+    if (map != nullptr) return fail(TI_EINVAL, "ragged rows of a block need a block longer than 32");
     if (ti::short_grid(batch, n, w != nullptr) > 0x7FFFFFFF) return fail(TI_ESIZE, "batch too large");
     ti::ShortGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
                         static_cast<hipStream_t>(stream)};
@@ -235,7 +238,24 @@ int bwd_impl(const uint32_t* starts, const void* fwd_ws, size_t fwd_ws_bytes, co
   ti::LongGradArgs a{starts, g, w, y, gy, gw, batch, n, dtype, flags, y_min, y_max,
                      kept != nullptr ? nullptr : fwd_ws, kept, kept != nullptr ? kept_maxc : 0,
                      static_cast<hipStream_t>(stream)};
+  if (map != nullptr) a.map = *map;
   return launched(ti::long_grad(a, plan, workspace), "multi-tile gradient");
+}
+
+// The row map of a bucket of ragged rows (ti_fwd_rows, ti_bwd_rows): rows given, a block longer
+// than 32, and packed arrays one buffer resource addresses.
+int check_rows(const int64_t* rows, int64_t k, int64_t L, int64_t total, int dtype) {
+  if (dtype != TI_F32)
+    return fail(TI_EDTYPE, "ragged rows of a block are float32 only, got dtype %d (ti_ragged_pack serves float64)",
+                dtype);
+  if (k < 0 || total < 0) return fail(TI_EINVAL, "need k >= 0 and total >= 0");
+  if (L <= ti::kShortMax) return fail(TI_EINVAL, "ragged rows of a block need a block longer than 32, got %lld",
+                                      (long long)L);
+  if (k > 0 && rows == nullptr) return fail(TI_EINVAL, "rows must not be null");
+  if (total > ti::kRowMapBytes / 4)
+    return fail(TI_ESIZE, "the packed arrays must stay below %lld bytes (ti_ragged_pack serves larger ones)",
+                (long long)ti::kRowMapBytes);
+  return TI_OK;
 }
 
 }  // namespace
@@ -287,6 +307,29 @@ int ti_bwd(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspa
            size_t workspace_bytes, void* stream) {
   return bwd_impl(starts, fwd_workspace, fwd_workspace_bytes, nullptr, 0, 0, g, w, y, gy, gw, batch, n, dtype,
                   flags, y_min, y_max, workspace, workspace_bytes, stream);
+}
+
+int ti_fwd_rows(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight, const int64_t* rows,
+                int64_t k, int64_t L, int64_t total, double pad, int dtype, unsigned flags, double y_min,
+                double y_max, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_rows(rows, k, L, total, dtype)) return rc;
+  const ti::RowMap m{rows, total, pad};
+  return fwd_impl(y, w, out, starts, bad_weight, k, L, dtype, flags, y_min, y_max, workspace, workspace_bytes, stream,
+                  nullptr, nullptr, nullptr, &m);
+}
+
+int ti_bwd_rows(const uint32_t* starts, const void* fwd_workspace, size_t fwd_workspace_bytes, const void* g,
+                const void* w, const void* y, void* gy, void* gw, const int64_t* rows, int64_t k, int64_t L,
+                int64_t total, int dtype, unsigned flags, double y_min, double y_max, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (int rc = check_rows(rows, k, L, total, dtype)) return rc;
+  const ti::RowMap m{rows, total, 0.0};
+  if (int rc = bwd_impl(starts, fwd_workspace, fwd_workspace_bytes, nullptr, 0, 0, g, w, y, gy, gw, k, L, dtype,
+                        flags, y_min, y_max, workspace, workspace_bytes, stream, &m))
+    return rc;
+  if (k == 0 || (gy == nullptr && gw == nullptr)) return ok();
+  return launched(ti::ragged_grad_fix(starts, w, rows, k, L, dtype, gy, gw, total, static_cast<hipStream_t>(stream)),
+                  "ragged gradient correction");
 }
 
 int ti_fwd_ev_hulls(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,

@@ -99,6 +99,9 @@ hipError_t ragged_pack(const void* src, const void* w, int64_t total, const int6
                        void* dst, void* wdst, hipStream_t stream);
 hipError_t ragged_rows(const int64_t* offsets, int64_t nrows, const int64_t* order, int64_t n, int64_t* rows,
                        hipStream_t stream);
+// the gradients of rows whose pad joined their last block scaled back to the row's own weight
+hipError_t ragged_grad_fix(const uint32_t* starts, const void* w, const int64_t* rows, int64_t k, int64_t L, int dtype,
+                           void* gy, void* gw, int64_t total, hipStream_t stream);
 hipError_t ragged_unpack(const void* src, const void* src2, const int64_t* rows, int64_t k, int64_t L, int dtype,
                          void* dst, void* dst2, int64_t total, const uint32_t* starts, const void* w,
                          hipStream_t stream);

@@ -428,7 +428,7 @@ constexpr int kExpandTiles = 4;
 // Per tile: the fit from the row's final hull.
 // NTS: the fit written with non-temporal stores (TI_STREAM_OUT), its lines leaving the caches
 // as they are written instead of draining under the next kernel's reads.
-template <typename T, bool W, bool NTS>
+template <typename T, bool W, bool NTS, bool MAP = false>
 __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
@@ -480,7 +480,13 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     const int ta = static_cast<int>(first);
     const int rA = rec[u].ra;
     const int ecount = max(0, min(E, len - t0));
-    T* out = static_cast<T*>(a.out) + row * a.n + first;
+    // (ragged rows: the row's place in the packed output, and slen, the tile's elements that are
+    // the row's own: the pad's are not stored)
+    int64_t rfirst = row * a.n, rlen = a.n;
+    if constexpr (MAP) map_row(a.map, row, a.n, rfirst, rlen);
+    const int slen = MAP ? static_cast<int>(max<int64_t>(0, min<int64_t>(len, rlen - first))) : len;
+    const int scount = MAP ? max(0, min(ecount, slen - t0)) : ecount;
+    T* out = static_cast<T*>(a.out) + rfirst + first;
     auto write_starts = [&](uint32_t sb) {
       if (a.starts == nullptr || ecount <= 0) return;
       if (ecount < E) sb &= (1u << ecount) - 1u;
@@ -498,7 +504,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       // fewer vertices than tiles): the edge's slope from the record, no LDS, no barriers. The
       // only possible start is the tile's first element.
       const T val = row_bad ? quiet_nan<T>() : tsgn * static_cast<T>(rec[u].slope);
-      fill_elems<T, E, NT, NTS>(out, len, tid, clip(val, use_lo, lo, use_hi, hi));
+      fill_elems<T, E, NT, NTS>(out, slen, tid, clip(val, use_lo, lo, use_hi, hi));
       write_starts((t0 == 0 && (rec[u].flags & kTileHead)) ? 1u : 0u);
       continue;
     }
@@ -535,7 +541,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       const T val = row_bad ? quiet_nan<T>() : sl[jj];
       fit[k] = clip(val, use_lo, lo, use_hi, hi);
     }
-    store_elems_any<T, E, NTS>(out + t0, ecount, fit);
+    store_elems_any<T, E, NTS>(out + t0, scount, fit);
     write_starts(row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits);
     __syncthreads();  // sl, bits and rank_scan are reused by the next tile
   }
@@ -551,7 +557,7 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
 // element). A NaN row is one edge, fit NaN.
 constexpr int kXpackMaxN = 2048;
 
-template <typename T, bool W, int E>
+template <typename T, bool W, int E, bool MAP = false>
 __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles, int rows_per_wg) {
   constexpr int NE = 256 * E;                  // elements a workgroup
   constexpr int NR = NE / (kShortMax + 1);     // rows a workgroup (n > 32)
@@ -561,7 +567,10 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
   __shared__ int roff[NR + 1];                 // per row: its first edge; [rows]: the edges in all
   __shared__ uint8_t rbad[NR];
   __shared__ uint32_t sbits[NE / 32 + NR];     // the rows' start-bit words, in order
+  __shared__ int64_t rmf[NR];                  // (ragged rows) per row: its first packed element
+  __shared__ int rml[NR];                      // and its length
   const int tid = threadIdx.x;
+  constexpr bool mapped = MAP;
   const int n = static_cast<int>(a.n);
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
   const int rows = static_cast<int>(min<int64_t>(rows_per_wg, a.batch - row0));
@@ -593,6 +602,12 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
       tiles[row] = r;
       ne = bad ? 1 : count - 1;
       rbad[tid] = bad ? 1 : 0;
+      if constexpr (MAP) {
+        int64_t f, l;
+        map_row(a.map, row, a.n, f, l);
+        rmf[tid] = f;
+        rml[tid] = static_cast<int>(l);
+      }
     }
     const int inc = wave_incl_i32(ne);
     if (tid < rows) roff[tid] = inc - ne;
@@ -655,10 +670,12 @@ __global__ __launch_bounds__(256) void xpack_kernel(ExpandArgs a, TileRec* tiles
           }
         }
         fit[k] = sl[jj];
+        // (ragged rows: the row's own elements to their packed places)
+        if (mapped && i < rml[r]) static_cast<T*>(a.out)[rmf[r] + i] = fit[k];
       }
     }
   }
-  store_elems_any<T, E>(static_cast<T*>(a.out) + row0 * a.n + e0, ecount, fit);
+  if (!mapped) store_elems_any<T, E>(static_cast<T*>(a.out) + row0 * a.n + e0, ecount, fit);
   if (a.starts != nullptr) {
     for (int wd = tid; wd < rows * wpr; wd += 256) a.starts[row0 * wpr + wd] = sbits[wd];
   }
@@ -1019,14 +1036,22 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     x.flags = t.flags;
     x.lo = t.lo;
     x.hi = t.hi;
+    x.map = t.map;
     TileRec* recs = reinterpret_cast<TileRec*>(base + p.off_rank);
     auto go = [&](auto E_) {
       constexpr int E = decltype(E_)::value;
       const int rpw = 256 * E / static_cast<int>(t.n);
       const dim3 grid(static_cast<unsigned>((t.batch + rpw - 1) / rpw));
       if (t.dtype == TI_F32) {
-        if (W) xpack_kernel<float, true, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
-        else xpack_kernel<float, false, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+        // (ragged rows of a block: float32 only)
+        if (t.map.rows != nullptr) {
+          if (W) xpack_kernel<float, true, E, true><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+          else xpack_kernel<float, false, E, true><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+        } else if (W) {
+          xpack_kernel<float, true, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+        } else {
+          xpack_kernel<float, false, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
+        }
       } else {
         if (W) xpack_kernel<double, true, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
         else xpack_kernel<double, false, E><<<grid, dim3(256), 0, t.stream>>>(x, recs, rpw);
@@ -1058,12 +1083,19 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   x.flags = t.flags;
   x.lo = t.lo;
   x.hi = t.hi;
+  x.map = t.map;
   const unsigned grid = static_cast<unsigned>((t.batch * p.tiles_per_row + kExpandTiles - 1) / kExpandTiles);
   auto go = [&](auto k) { k<<<dim3(grid), dim3(256), 0, t.stream>>>(x); };
   const bool nts = (t.flags & TI_STREAM_OUT) != 0;
   if (t.dtype == TI_F32) {
-    if (W) nts ? go(expand_kernel<float, true, true>) : go(expand_kernel<float, true, false>);
-    else nts ? go(expand_kernel<float, false, true>) : go(expand_kernel<float, false, false>);
+    if (t.map.rows != nullptr) {  // (ragged rows of a block: float32 only)
+      if (W) go(expand_kernel<float, true, false, true>);
+      else go(expand_kernel<float, false, false, true>);
+    } else if (W) {
+      nts ? go(expand_kernel<float, true, true>) : go(expand_kernel<float, true, false>);
+    } else {
+      nts ? go(expand_kernel<float, false, true>) : go(expand_kernel<float, false, false>);
+    }
   } else {
     if (W) nts ? go(expand_kernel<double, true, true>) : go(expand_kernel<double, true, false>);
     else nts ? go(expand_kernel<double, false, true>) : go(expand_kernel<double, false, false>);

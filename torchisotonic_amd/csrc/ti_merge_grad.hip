@@ -79,6 +79,7 @@ struct GradKArgs {
   double* gt;            // [batch * ngroups][2]: group totals
   double* gp;            // [batch * (ngroups + 1)][2]: exclusive prefix of groups, then total
   double* lv;            // [batch * cap_final][2]: prefix of g within its tile at each vertex
+  RowMap map;            // ragged rows of one block: g, w, y, gy, gw in the packed layout
 };
 
 
@@ -134,7 +135,7 @@ __device__ __forceinline__ void put_tile_total(const GradKArgs& a, int64_t gt, D
 // Tiles per gsum workgroup: their loads are all in flight before the first tile is summed.
 constexpr int kGsumTiles = 2;
 
-template <typename T, bool W>
+template <typename T, bool W, bool MAP = false>
 __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
@@ -174,7 +175,17 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     const int64_t tile = tileu[u];
     const int64_t first = tile * C::kN;
     const int len = static_cast<int>(min<int64_t>(C::kN, a.n - first));
-    load_elems_any<T, E>(static_cast<const T*>(a.g) + row * a.n + first + t0, max(0, min(E, len - t0)), gv[u]);
+    // (ragged rows: the row's own elements from its packed place, g = 0 for the pad's)
+    int64_t rfirst = row * a.n, rlen = a.n;
+    if constexpr (MAP) map_row(a.map, row, a.n, rfirst, rlen);
+    const int lc = static_cast<int>(max<int64_t>(0, min<int64_t>(E, min<int64_t>(len, rlen - first) - t0)));
+    load_elems_any<T, E>(static_cast<const T*>(a.g) + rfirst + first + t0, lc, gv[u]);
+    if constexpr (MAP) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        if (k >= lc) gv[u][k] = T(0);
+      }
+    }
     const TileRec rec = a.tiles[gt];
     rA[u] = rec.ra;
     rB[u] = rec.rb;
@@ -317,7 +328,7 @@ __device__ __forceinline__ DD vertex_w(const NodeOut& f, int r) {
   else return DD{static_cast<double>(f.idx[r]), 0.0};
 }
 
-template <typename T, bool W>
+template <typename T, bool W, bool MAP = false>
 __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   using C = TileCfg<W>;
   constexpr int E = C::kE;
@@ -389,8 +400,14 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
   int jj = bad ? 0 : before + static_cast<int>(mybits & 1u) - at_start;
   T wv[W ? E : 1], yv[E];
   const bool need_y = a.gw != nullptr;
-  if constexpr (W) load_elems_any<T, E>(static_cast<const T*>(a.w) + row * a.n + first + t0, ecount, wv);
-  if (need_y) load_elems_any<T, E>(static_cast<const T*>(a.y) + row * a.n + first + t0, ecount, yv);
+  // (ragged rows: the row's own elements from and to their packed places; the pad's gradients
+  // are not stored, nor their w and y read)
+  int64_t rfirst = row * a.n, rlen = a.n;
+  if constexpr (MAP) map_row(a.map, row, a.n, rfirst, rlen);
+  const int lc = MAP ? static_cast<int>(max<int64_t>(0, min<int64_t>(ecount, min<int64_t>(len, rlen - first) - t0)))
+                     : ecount;
+  if constexpr (W) load_elems_any<T, E>(static_cast<const T*>(a.w) + rfirst + first + t0, lc, wv);
+  if (need_y) load_elems_any<T, E>(static_cast<const T*>(a.y) + rfirst + first + t0, lc, yv);
   T oy[E], ow[E];
 #pragma unroll
   for (int k = 0; k < E; ++k) {
@@ -400,8 +417,8 @@ __global__ __launch_bounds__(256) void gfill_kernel(GradKArgs a) {
     oy[k] = static_cast<T>(wk * q);
     if (need_y) ow[k] = static_cast<T>((static_cast<double>(yv[k]) - static_cast<double>(mv[jj])) * q);
   }
-  if (a.gy != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gy) + row * a.n + first + t0, ecount, oy);
-  if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + row * a.n + first + t0, ecount, ow);
+  if (a.gy != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gy) + rfirst + first + t0, lc, oy);
+  if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + rfirst + first + t0, lc, ow);
 }
 
 // Rows of at most 2048 elements: whole rows packed into a workgroup of 256 threads, E
@@ -427,7 +444,7 @@ __device__ __forceinline__ void seg_combine(double as, int ac, double& bs, int& 
 // G at its last element; a pass over the workgroup's blocks then takes each block's weight and
 // fit from the forward's hull vertices (as gfill_kernel does) and forms q = mask * G / W; each
 // element writes gy = w * q and gw = (y - fit) * q. A NaN row is one block (fit NaN).
-template <typename T, bool W, int E>
+template <typename T, bool W, int E, bool MAP = false>
 __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg) {
   using C = PackCfg<E>;
   __shared__ double qv[C::kElems];       // per block of the workgroup: G, then mask * G / W
@@ -451,9 +468,42 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
   const bool need_y = a.gw != nullptr;
 
   T gv[E], wv[W ? E : 1], yv[E];
-  load_elems_any<T, E>(static_cast<const T*>(a.g) + base + e0, ecount, gv);
-  if constexpr (W) load_elems_any<T, E>(static_cast<const T*>(a.w) + base + e0, ecount, wv);
-  if (need_y) load_elems_any<T, E>(static_cast<const T*>(a.y) + base + e0, ecount, yv);
+  // Ragged rows: element e0 + k is element i_k of the workgroup's row r_k, at its packed place
+  // for i_k below the row's length, else the pad's (g = 0; w and y unused: its gradients are not
+  // stored). Rows are longer than 32 elements and a thread holds at most 8, so a thread's
+  // elements lie in at most two rows, whose descriptors it reads once.
+  constexpr bool mapped = MAP;
+  int64_t mf[2] = {0, 0}, ml[2] = {0, 0};
+  int ra = 0;
+  if (mapped) {
+    ra = ecount > 0 ? static_cast<int>(div(static_cast<uint32_t>(e0))) : 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (ra + h < rows) map_row(a.map, row0 + ra + h, a.n, mf[h], ml[h]);
+    }
+  }
+  // (the packed index of element k, or -1 for the pad's and past the workgroup's elements)
+  auto mapped_at = [&](int k) -> int64_t {
+    const int e = e0 + k;
+    if (k >= ecount) return -1;
+    const int i = e - ra * n;
+    const int h = i >= n ? 1 : 0;
+    const int ih = i - h * n;
+    return ih < ml[h] ? mf[h] + ih : int64_t{-1};
+  };
+  if (mapped) {
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      const int64_t p = mapped_at(k);
+      gv[k] = p >= 0 ? static_cast<const T*>(a.g)[p] : T(0);
+      if constexpr (W) wv[W ? k : 0] = p >= 0 ? static_cast<const T*>(a.w)[p] : T(1);
+      if (need_y) yv[k] = p >= 0 ? static_cast<const T*>(a.y)[p] : T(0);
+    }
+  } else {
+    load_elems_any<T, E>(static_cast<const T*>(a.g) + base + e0, ecount, gv);
+    if constexpr (W) load_elems_any<T, E>(static_cast<const T*>(a.w) + base + e0, ecount, wv);
+    if (need_y) load_elems_any<T, E>(static_cast<const T*>(a.y) + base + e0, ecount, yv);
+  }
   if (tid < rows) rowbad[tid] = (a.tiles[row0 + tid].flags & kTileBad) ? 1 : 0;
   __syncthreads();
 
@@ -574,6 +624,17 @@ __global__ __launch_bounds__(256) void gpack_kernel(GradKArgs a, int rows_per_wg
     oy[k] = static_cast<T>(wk * q);
     if (need_y) ow[k] = static_cast<T>((static_cast<double>(yv[k]) - static_cast<double>(mv[eb[k]])) * q);
   }
+  if (mapped) {
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      const int64_t p = mapped_at(k);
+      if (p >= 0) {
+        if (a.gy != nullptr) static_cast<T*>(a.gy)[p] = oy[k];
+        if (a.gw != nullptr) static_cast<T*>(a.gw)[p] = ow[k];
+      }
+    }
+    return;
+  }
   if (a.gy != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gy) + base + e0, ecount, oy);
   if (a.gw != nullptr) store_elems_any<T, E>(static_cast<T*>(a.gw) + base + e0, ecount, ow);
 }
@@ -600,6 +661,7 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   a.gw = in.gw;
   a.batch = in.batch;
   a.n = in.n;
+  a.map = in.map;
   a.tpr = gpn.tpr;
   a.ngroups = gpn.ngroups;
   a.cap_final = gpn.cap_final;
@@ -625,8 +687,15 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
       const int rpw = PackCfg<E>::kElems / static_cast<int>(in.n);
       const unsigned blocks = static_cast<unsigned>((in.batch + rpw - 1) / rpw);
       if (in.dtype == TI_F32) {
-        if (W) gpack_kernel<float, true, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
-        else gpack_kernel<float, false, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+        // (ragged rows of a block: float32 only)
+        if (in.map.rows != nullptr) {
+          if (W) gpack_kernel<float, true, E, true><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+          else gpack_kernel<float, false, E, true><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+        } else if (W) {
+          gpack_kernel<float, true, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+        } else {
+          gpack_kernel<float, false, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
+        }
       } else {
         if (W) gpack_kernel<double, true, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
         else gpack_kernel<double, false, E><<<dim3(blocks), dim3(256), 0, in.stream>>>(a, rpw);
@@ -639,8 +708,14 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
   const unsigned tiles = static_cast<unsigned>(in.batch * gpn.tpr);
   const unsigned gsum_blocks = (tiles + kGsumTiles - 1) / kGsumTiles;
   if (in.dtype == TI_F32) {
-    if (W) gsum_kernel<float, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
-    else gsum_kernel<float, false><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+    if (in.map.rows != nullptr) {  // (ragged rows of a block: float32 only)
+      if (W) gsum_kernel<float, true, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+      else gsum_kernel<float, false, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+    } else if (W) {
+      gsum_kernel<float, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+    } else {
+      gsum_kernel<float, false><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
+    }
   } else {
     if (W) gsum_kernel<double, true><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
     else gsum_kernel<double, false><<<dim3(gsum_blocks), dim3(256), 0, in.stream>>>(a);
@@ -658,8 +733,14 @@ hipError_t long_grad(const LongGradArgs& in, const LongPlan& p, void* ws) {
     }
   }
   if (in.dtype == TI_F32) {
-    if (W) gfill_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
-    else gfill_kernel<float, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    if (in.map.rows != nullptr) {  // (ragged rows of a block: float32 only)
+      if (W) gfill_kernel<float, true, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+      else gfill_kernel<float, false, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    } else if (W) {
+      gfill_kernel<float, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    } else {
+      gfill_kernel<float, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
+    }
   } else {
     if (W) gfill_kernel<double, true><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);
     else gfill_kernel<double, false><<<dim3(tiles), dim3(256), 0, in.stream>>>(a);

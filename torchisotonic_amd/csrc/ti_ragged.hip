@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kRagThreads) void ragged_grad_fix_kernel(const uint
   for (int d = kWave / 2; d >= 1; d >>= 1) wsum += __shfl_xor(wsum, d, kWave);
   const double f = (wsum + static_cast<double>(e - len)) / wsum;
   for (int64_t i = s + lane; i < len; i += kWave) {
-    gy[first + i] = static_cast<T>(static_cast<double>(gy[first + i]) * f);
+    if (gy != nullptr) gy[first + i] = static_cast<T>(static_cast<double>(gy[first + i]) * f);
     if (gw != nullptr) gw[first + i] = static_cast<T>(static_cast<double>(gw[first + i]) * f);
   }
 }
@@ -293,23 +293,29 @@ hipError_t ragged_unpack(const void* src, const void* src2, const int64_t* rows,
                          hipStream_t stream) {
   const int64_t cpr = ragged_chunks(L);
   const dim3 grid(static_cast<unsigned>(k * cpr));
-  const dim3 fix_grid(static_cast<unsigned>((k + kRagThreads / kWave - 1) / (kRagThreads / kWave)));
   if (dtype == TI_F32) {
     ragged_unpack_kernel<float><<<grid, dim3(kRagThreads), 0, stream>>>(
         static_cast<const float*>(src), static_cast<const float*>(src2), rows, total, L, cpr, static_cast<float*>(dst),
         static_cast<float*>(dst2));
-    if (starts != nullptr)
-      ragged_grad_fix_kernel<float><<<fix_grid, dim3(kRagThreads), 0, stream>>>(
-          starts, static_cast<const float*>(w), rows, k, total, L, static_cast<float*>(dst), static_cast<float*>(dst2));
   } else {
     ragged_unpack_kernel<double><<<grid, dim3(kRagThreads), 0, stream>>>(
         static_cast<const double*>(src), static_cast<const double*>(src2), rows, total, L, cpr,
         static_cast<double*>(dst), static_cast<double*>(dst2));
-    if (starts != nullptr)
-      ragged_grad_fix_kernel<double><<<fix_grid, dim3(kRagThreads), 0, stream>>>(
-          starts, static_cast<const double*>(w), rows, k, total, L, static_cast<double*>(dst),
-          static_cast<double*>(dst2));
   }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || starts == nullptr) return e;
+  return ragged_grad_fix(starts, w, rows, k, L, dtype, dst, dst2, total, stream);
+}
+
+hipError_t ragged_grad_fix(const uint32_t* starts, const void* w, const int64_t* rows, int64_t k, int64_t L, int dtype,
+                           void* gy, void* gw, int64_t total, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((k + kRagThreads / kWave - 1) / (kRagThreads / kWave)));
+  if (dtype == TI_F32)
+    ragged_grad_fix_kernel<float><<<grid, dim3(kRagThreads), 0, stream>>>(
+        starts, static_cast<const float*>(w), rows, k, total, L, static_cast<float*>(gy), static_cast<float*>(gw));
+  else
+    ragged_grad_fix_kernel<double><<<grid, dim3(kRagThreads), 0, stream>>>(
+        starts, static_cast<const double*>(w), rows, k, total, L, static_cast<double*>(gy), static_cast<double*>(gw));
   return hipGetLastError();
 }
 

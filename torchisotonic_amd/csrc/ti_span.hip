@@ -46,6 +46,7 @@ struct SpanArgs {
   unsigned flags;
   NodeLevel hulls;        // the spans' level
   NodeLevel hulls1;       // the groups' (the first merge level; with rpw > 1, the rows')
+  RowMap map;             // ragged rows of one block: y and w read from the packed arrays
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the candidate queue (index
@@ -87,7 +88,7 @@ __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t of
   }
 }
 
-template <typename T, bool W, int C, int Q, int R, int LC, bool INC>
+template <typename T, bool W, int C, int Q, int R, int LC, bool INC, bool MAP = false>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert((R & (R - 1)) == 0 && (Q & (Q - 1)) == 0 && R >= 4, "ring and queue slots: powers of two");
   static_assert(C < Q, "a chunk's candidates fit the queue");
@@ -123,21 +124,38 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   const int64_t first = span * a.span0;
   const int len = active ? static_cast<int>(min<int64_t>(a.span0, a.n - first)) : 0;
   constexpr double sgn = INC ? 1.0 : -1.0;
+  // Ragged rows (MAP, a.map): the lane's row in the packed arrays, and rlim, the span's elements
+  // that are the row's own; from rlim on the span holds the pad (weight 1), made in registers: a
+  // block wholly past rlim is never read (its loads take an offset past the buffer's end, which
+  // returns zeros without a memory access).
+  constexpr bool mapped = MAP;
+  int64_t mfirst = 0, mlen = a.n;
+  if constexpr (MAP) map_row(a.map, active ? row : 0, a.n, mfirst, mlen);
+  const int rlim = MAP ? static_cast<int>(max<int64_t>(mlen - first, 0)) : 0x7FFFFFFF;
+  const T tpad = static_cast<T>(a.map.pad);
   // The wave's spans are consecutive elements (of one row, or of its rows), so one buffer
   // resource based at the first of them serves every lane.
   // (from the wave's own indices only, and read from the first lane: the compiler then keeps
   // the buffer resources in scalar registers, where a per-lane value would put every load in a
   // loop over the lanes' distinct resources)
+  // (ragged rows: one resource over the whole packed arrays, under 2 GB)
   const int64_t wrow = static_cast<int64_t>(blockIdx.x) / a.gpr;  // (one row a wave: its row)
-  const int64_t base = wave_uniform(packed  ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
-                                    : multi ? static_cast<int64_t>(blockIdx.x) * a.rpw * a.n
-                                            : wrow * a.n + (blockIdx.x - wrow * a.gpr) * kSpanLanes * a.span0);
-  const int64_t total = batch * a.n;                                      // elements of the array
+  const int64_t base = wave_uniform(mapped  ? int64_t{0}
+                                    : packed ? static_cast<int64_t>(blockIdx.x) * kSpanLanes * a.n
+                                    : multi  ? static_cast<int64_t>(blockIdx.x) * a.rpw * a.n
+                                             : wrow * a.n + (blockIdx.x - wrow * a.gpr) * kSpanLanes * a.span0);
+  const int64_t total = mapped ? a.map.total : batch * a.n;  // elements of the arrays
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + base, (total - base) * sizeof(T));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(W ? static_cast<const T*>(a.w) + base : a.y, (total - base) * sizeof(T));
-  // this lane's span (packed: its row), as an element offset from base
+  // this lane's span (packed: its row) as an element index in the wave's sequence of elements,
+  // and its place in memory, an element offset from base
   const int64_t lel = packed ? lane * a.n : multi ? (lane / kl) * a.n + first : lane * a.span0;
-  const uint32_t loff = static_cast<uint32_t>(lel * static_cast<int64_t>(sizeof(T)));
+  const int64_t lmem = mapped ? mfirst + first : lel;
+  // block b's byte offset (a block wholly past rlim: past the resource, never read)
+  auto boff = [&](int b) -> uint32_t {
+    if constexpr (!MAP) return static_cast<uint32_t>((lmem + b) * static_cast<int64_t>(sizeof(T)));
+    return b < rlim ? static_cast<uint32_t>((lmem + b) * static_cast<int64_t>(sizeof(T))) : 0x80000000u;
+  };
   const NodeOut o = node_out(a.hulls, W, node);
 
   auto ring_put = [&](int q, const HPt& p) {
@@ -271,12 +289,24 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   // candidates
   T yc[LC], yn[LC];
   T wc[W ? LC : 1], wn[W ? LC : 1];
-  load_block<T, LC>(ry, loff, yc);
-  if constexpr (W) load_block<T, LC>(rw, loff, wc);
+  load_block<T, LC>(ry, boff(0), yc);
+  if constexpr (W) load_block<T, LC>(rw, boff(0), wc);
   for (int b0 = 0; b0 < len; b0 += LC) {
     // the next block, whole, whether or not the span reaches it
-    load_block<T, LC>(ry, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), yn);
-    if constexpr (W) load_block<T, LC>(rw, loff + static_cast<uint32_t>((b0 + LC) * sizeof(T)), wn);
+    load_block<T, LC>(ry, boff(b0 + LC), yn);
+    if constexpr (W) load_block<T, LC>(rw, boff(b0 + LC), wn);
+    // (ragged rows: the pad past the row's end, in the one block a lane's row ends in or after)
+    if (MAP && __any(b0 + LC > rlim)) {
+#pragma unroll
+      for (int k = 0; k < LC; ++k) {
+        if (b0 + k >= rlim) {
+          yc[k] = tpad;
+          if constexpr (W) wc[W ? k : 0] = T(1);
+        }
+      }
+    }
+    // the element after the block: the next block's first, or the pad
+    auto after_block = [&]() { return MAP && b0 + LC >= rlim ? tpad : yn[0]; };
 #pragma unroll
     for (int sub = 0; sub < LC; sub += C) {
       const int c0 = b0 + sub;
@@ -316,7 +346,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
 #pragma unroll
         for (int k = 0; k < C; ++k) {
           const int kk = sub + k;
-          const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
+          const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : after_block();
           // (the span can end only after a chunk's last element here)
           element(k, k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext)));
         }
@@ -326,7 +356,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
           const int e = c0 + k;
           if (e < len) {
             const int kk = sub + k;
-            const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : yn[0];
+            const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : after_block();
             element(k, (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext)));
           }
         }
@@ -563,6 +593,7 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
   a.gpr = (spr + kSpanLanes - 1) / kSpanLanes;
   a.rpw = rows_per_wave;
   a.hulls1 = hulls1;
+  a.map = t.map;
   // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
   // rows_per_wave of them)
   const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes
@@ -570,13 +601,19 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
                                                                   : t.batch * a.gpr);
   const bool W = t.w != nullptr;
   const bool inc = (t.flags & TI_INCREASING) != 0;
-  auto go = [&](auto k_inc, auto k_dec) {
+  auto go = [&](auto k_inc, auto k_dec) {  // (ragged rows of a block: float32 only)
     if (inc) k_inc<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
     else k_dec<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   };
   if (t.dtype == TI_F32) {
-    if (W) go(span_kernel<float, true, 4, 8, 8, 32, true>, span_kernel<float, true, 4, 8, 8, 32, false>);
-    else go(span_kernel<float, false, 4, 8, 16, 32, true>, span_kernel<float, false, 4, 8, 16, 32, false>);
+    if (t.map.rows != nullptr) {
+      if (W) go(span_kernel<float, true, 4, 8, 8, 32, true, true>, span_kernel<float, true, 4, 8, 8, 32, false, true>);
+      else go(span_kernel<float, false, 4, 8, 16, 32, true, true>, span_kernel<float, false, 4, 8, 16, 32, false, true>);
+    } else if (W) {
+      go(span_kernel<float, true, 4, 8, 8, 32, true>, span_kernel<float, true, 4, 8, 8, 32, false>);
+    } else {
+      go(span_kernel<float, false, 4, 8, 16, 32, true>, span_kernel<float, false, 4, 8, 16, 32, false>);
+    }
   } else {
     if (W) go(span_kernel<double, true, 4, 8, 8, 8, true>, span_kernel<double, true, 4, 8, 8, 8, false>);
     else go(span_kernel<double, false, 4, 8, 16, 8, true>, span_kernel<double, false, 4, 8, 16, 8, false>);

@@ -23,6 +23,35 @@ struct TileCfg {
   static constexpr int kN = kThreads * kE;
 };
 
+// Ragged rows taken as the rows of a [batch, n] block (n at least every length): row r's
+// elements are at rows[2 r] + i of the packed arrays for i < rows[2 r + 1] (clamped to the
+// packed array and to n), and past its length the row holds `pad` with weight 1 (and g = 0 in a
+// backward), made in registers, never read. Fits and gradients are stored at the packed
+// places of the row's own elements only. rows null: the dense layout, row r at r * n. The
+// kernels address the packed arrays through one buffer resource, so total * sizeof(T) stays
+// below kRowMapBytes.
+struct RowMap {
+  const int64_t* rows = nullptr;
+  int64_t total = 0;  // elements of the packed arrays
+  double pad = 0.0;
+};
+constexpr int64_t kRowMapBytes = int64_t{0x7FFF0000};
+
+// Row r's first element and length (the dense layout without a map).
+__device__ __forceinline__ void map_row(const RowMap& m, int64_t r, int64_t n, int64_t& first, int64_t& len) {
+  if (m.rows == nullptr) {
+    first = r * n;
+    len = n;
+    return;
+  }
+  first = m.rows[2 * r];
+  first = first < 0 ? 0 : (first > m.total ? m.total : first);
+  len = m.rows[2 * r + 1];
+  len = len < 0 ? 0 : len;
+  len = len > m.total - first ? m.total - first : len;
+  len = len > n ? n : len;
+}
+
 struct TileArgs {
   const void* y;
   const void* w;
@@ -40,6 +69,7 @@ struct TileArgs {
   // it is, before the last merges and the expansion run.
   int64_t* max_vertices = nullptr;
   hipEvent_t hulls_ready = nullptr;
+  RowMap map;  // ragged rows of one block (see RowMap)
 };
 
 // One node's hull: vertex indices relative to the node's first element, cumulative sums
@@ -287,6 +317,7 @@ struct ExpandArgs {
   const TileRec* tiles;  // per tile (rank_kernel's)
   unsigned flags;
   double lo, hi;
+  RowMap map;  // out in the packed layout (starts stay in the block's)
 };
 
 // Workspace of a long-row fit: the shared vertex store of every level (span0 + 1 slots per span),
@@ -352,6 +383,7 @@ struct LongGradArgs {
   const void* kept;    // what ti_keep kept of it (fwd_ws null)
   int64_t kept_maxc;   // the kept hulls' slots a row
   hipStream_t stream;
+  RowMap map;  // g, w, y, gy, gw in the packed layout (starts in the block's)
 };
 // kept_maxc > 0: the workspace of a backward from a kept state (its vertex prefixes sized for
 // hulls of that many vertices instead of a row's every slot)

@@ -246,6 +246,7 @@ RaggedHost& ragged_host(c10::DeviceIndex dev) {
 
 constexpr int64_t kRaggedShort = 32;  // the longest rows ti_fwd_ragged fits
 // the op's one zeroed buffer, in int32 words: the plan, the weight flag, the flat start bits
+constexpr int64_t kRowMapBytes = 0x7FFF0000;  // (ti_fwd_rows' limit on the packed arrays)
 constexpr int64_t kPlanAt = 0, kBadAt = 2 * TI_RAGGED_PLAN_WORDS, kBitsAt = kBadAt + 2;
 
 // Length buckets of the longer rows, from the plan's counts and longest rows: (first descriptor,
@@ -338,6 +339,8 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     if (short_max > nmax) fit_short(short_max);
     // the longer rows, a length bucket at a time
     const bool want = values.requires_grad() || (w.defined() && w.requires_grad());
+    // float32 sets under 2 GB: each bucket fitted in place (ti_fwd_rows), else through a block
+    const bool rows_mode = dtype == TI_F32 && total * 4 < kRowMapBytes;
     std::vector<int64_t> buckets;  // per bucket: its first descriptor, its rows, its block length
     std::vector<at::Tensor> keep;  // the descriptors, then per bucket: y, w blocks, starts, workspace
     if (n_long > 0) {
@@ -364,6 +367,16 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
       const double cpad = f32 ? (increasing ? 1.0 : -1.0) * static_cast<double>(std::numeric_limits<float>::max()) : 0.0;
       for (size_t i = 0; i < buckets.size(); i += 3) {
         const int64_t f = buckets[i], k = buckets[i + 1], L = buckets[i + 2];
+        at::Tensor starts = at::empty({ti_starts_words(k, L)}, values.options().dtype(at::kInt));
+        at::Tensor ws = workspace(true, k, L, dtype, w.defined(), values.device());
+        if (rows_mode) {  // read and written in place: no block
+          check(ti_fwd_rows(ptr(values), ptr(w), ptr(out), static_cast<uint32_t*>(starts.data_ptr()), bad, rp + 2 * f,
+                            k, L, total, cpad, dtype, flags, 0.0, 0.0, ptr(ws),
+                            ws.defined() ? static_cast<size_t>(ws.numel()) : 0, stream),
+                "isotonic_ragged");
+          if (want) keep.insert(keep.end(), {at::Tensor(), at::Tensor(), starts, ws});
+          continue;
+        }
         if (!f32) {
           check(ti_ragged_extreme(ptr(values), total, rp + 2 * f, k, L, dtype, increasing ? 1 : 0, kp + f, stream),
                 "isotonic_ragged");
@@ -373,8 +386,6 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
         check(ti_ragged_pack(ptr(values), ptr(w), total, rp + 2 * f, f32 ? nullptr : kp + f, cpad, k, L, dtype,
                              increasing ? 1 : 0, ptr(yb), ptr(wb), stream),
               "isotonic_ragged");
-        at::Tensor starts = at::empty({ti_starts_words(k, L)}, values.options().dtype(at::kInt));
-        at::Tensor ws = workspace(true, k, L, dtype, w.defined(), values.device());
         at::Tensor ob = at::empty({k, L}, values.options());
         check(ti_fwd(ptr(yb), ptr(wb), ptr(ob), static_cast<uint32_t*>(starts.data_ptr()), bad, k, L, dtype, flags, 0.0,
                      0.0, ptr(ws), ws.defined() ? static_cast<size_t>(ws.numel()) : 0, stream),
@@ -398,7 +409,8 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
       saved.insert(saved.end(), keep.begin(), keep.end());
       ctx->save_for_backward(saved);
       ctx->saved_data["buckets"] = c10::List<int64_t>(buckets);
-      ctx->saved_data["p"] = c10::List<int64_t>({short_max, increasing ? 1 : 0, w.defined() ? 1 : 0});
+      ctx->saved_data["p"] =
+          c10::List<int64_t>({short_max, increasing ? 1 : 0, w.defined() ? 1 : 0, rows_mode ? 1 : 0});
     }
     return out;
   }
@@ -408,6 +420,7 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
     const int64_t short_max = prm.get(0);
     const unsigned flags = (prm.get(1) != 0 ? TI_INCREASING : 0u) | TI_EXACT;
     const bool has_w = prm.get(2) != 0;
+    const bool rows_mode = prm.get(3) != 0;
     const c10::List<int64_t> buckets = ctx->saved_data["buckets"].toIntList();
     const bool want_y = ctx->needs_input_grad(0), want_w = has_w && ctx->needs_input_grad(1);
     variable_list none(6);
@@ -443,13 +456,21 @@ struct RaggedFn : public torch::autograd::Function<RaggedFn> {
         const at::Tensor& wb = saved[j + 1];
         const at::Tensor& starts = saved[j + 2];
         const at::Tensor& ws = saved[j + 3];
+        at::Tensor bws = workspace(false, k, L, dtype, w.defined(), values.device());
+        if (rows_mode) {  // in place, the correction included
+          check(ti_bwd_rows(static_cast<const uint32_t*>(starts.data_ptr()), ptr(ws),
+                            ws.defined() ? static_cast<size_t>(ws.numel()) : 0, ptr(g), ptr(w),
+                            want_w ? ptr(values) : nullptr, ptr(gy), ptr(gw), rp + 2 * f, k, L, total, dtype, flags, 0.0,
+                            0.0, ptr(bws), bws.defined() ? static_cast<size_t>(bws.numel()) : 0, stream),
+                "isotonic_ragged backward");
+          continue;
+        }
         at::Tensor gb = at::empty({k, L}, g.options());
         check(ti_ragged_pack(ptr(g), nullptr, total, rp + 2 * f, nullptr, 0.0, k, L, dtype, 0, ptr(gb), nullptr,
                              stream),
               "isotonic_ragged backward");
         at::Tensor gyb = at::empty({k, L}, g.options());
         at::Tensor gwb = want_w ? at::empty({k, L}, g.options()) : at::Tensor();
-        at::Tensor bws = workspace(false, k, L, dtype, w.defined(), values.device());
         check(ti_bwd(static_cast<const uint32_t*>(starts.data_ptr()), ptr(ws),
                      ws.defined() ? static_cast<size_t>(ws.numel()) : 0, ptr(gb), ptr(wb), want_w ? ptr(yb) : nullptr,
                      ptr(gyb), ptr(gwb), k, L, dtype, flags, 0.0, 0.0, ptr(bws),

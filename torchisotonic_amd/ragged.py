@@ -102,6 +102,7 @@ def _offsets_tensor(offsets, lengths, device: torch.device) -> Tensor:
 
 
 _BUCKET_MERGE = 1 << 22  # a bucket joins the next while that pads at most this many elements
+_ROW_MAP_BYTES = 0x7FFF0000  # ti_fwd_rows' limit on the packed arrays
 
 
 def _buckets(words: list[int], n_long: int) -> list[tuple[int, int, int]]:
@@ -164,11 +165,13 @@ def _fit_short(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, nmax:
 def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, long_plan: tuple,
               increasing: bool) -> list:
     """The longer rows, a bucket at a time: the rows in bucket order (a stable sort of the plan's
-    keys, ti_ragged_rows), then per bucket the block of its rows, each padded beyond its extreme
-    (float32: the largest finite value; float64: ti_ragged_extreme), ti_fwd over it, and the fits
-    scattered back (ti_ragged_pack, ti_ragged_unpack). Per bucket: its rows' (first, length) on
-    the host, the block length L, the block's packed starts, its forward workspace, the y and w
-    blocks."""
+    keys, ti_ragged_rows), then per bucket either (float32 sets under 2 GB) one ti_fwd_rows, which
+    reads and writes the rows in place as the rows of a block padded with the largest finite
+    value, or the block of its rows, each padded beyond its extreme (float32: the largest finite
+    value; float64: ti_ragged_extreme), ti_fwd over it, and the fits scattered back
+    (ti_ragged_pack, ti_ragged_unpack). Per bucket: its rows' (first, length) on the host, the
+    block length L, the block's packed starts, its forward workspace, the y and w blocks (None in
+    place)."""
     n_long, buckets, keys = long_plan
     if n_long == 0:
         return []
@@ -186,8 +189,23 @@ def _fit_long(values: Tensor, w: Tensor | None, out: Tensor, off: Tensor, long_p
         _ext._check(lib.ti_ragged_rows(off.data_ptr(), nrows, order.data_ptr(), n_long, rows.data_ptr(), s),
                     "isotonic_ragged")
     done = []
+    # float32 sets under 2 GB: each bucket fitted in place (ti_fwd_rows), else through a block
+    rows_mode = f32 and total * 4 < _ROW_MAP_BYTES
+    flags = (_ext.INCREASING if increasing else 0) | _ext.EXACT
     for f, k, L in buckets:
         desc = rows[f:f + k]
+        if rows_mode:
+            starts = torch.empty(_ext.starts_words(k, L), dtype=torch.int32, device=values.device)
+            bad = None if w is None else torch.zeros(1, dtype=torch.int32, device=values.device)
+            with _ext._on_device(values.device):
+                ws = _ext._workspace("fwd", k, L, code, w is not None, values.device)
+                _ext._check(lib.ti_fwd_rows(values.data_ptr(), _ext._ptr(w), out.data_ptr(), starts.data_ptr(),
+                                            _ext._ptr(bad), desc.data_ptr(), k, L, total, pad, code, flags, 0.0, 0.0,
+                                            _ext._ptr(ws), 0 if ws is None else ws.numel(), s), "isotonic_ragged")
+            if bad is not None and bool(bad.item()):
+                raise ValueError("weight must be strictly positive")
+            done.append((desc.cpu().numpy(), L, starts, ws, None, None))
+            continue
         kp = None if ext is None else ext[f:f + k].data_ptr()
         with _ext._on_device(values.device):
             if ext is not None:
