@@ -315,3 +315,26 @@ def test_operator_library_registers_the_fit() -> None:
     schema = str(ops.isotonic_fit.default._schema)
     assert schema.startswith("torchisotonic_amd::isotonic_fit(Tensor y, Tensor? w, bool increasing")
     assert "float? y_min" in schema and "float? y_max" in schema and schema.endswith("-> Tensor")
+
+
+def test_rows_entry_points_refuse_before_any_launch() -> None:
+    # ti_fwd_rows / ti_bwd_rows check dtype, block length and the packed arrays' size before any
+    # device call (null buffers here: a missing check would end in a device error)
+    lib = _ext.load()
+
+    def fwd(k, L, total, dtype):
+        return lib.ti_fwd_rows(None, None, None, None, None, None, k, L, total, 0.0, dtype, 1, 0.0, 0.0, None, 0, None)
+
+    def bwd(k, L, total, dtype):
+        return lib.ti_bwd_rows(None, None, 0, None, None, None, None, None, None, k, L, total, dtype, 1, 0.0, 0.0,
+                               None, 0, None)
+
+    for call in (fwd, bwd):
+        assert call(4, 64, 1000, _ext.F64) == 2  # TI_EDTYPE: float32 only
+        assert b"float32 only" in lib.ti_last_error()
+        assert call(4, 32, 1000, _ext.F32) == 1  # TI_EINVAL: the short-row regime has no row map
+        assert b"longer than 32" in lib.ti_last_error()
+        assert call(4, 64, 1000, _ext.F32) == 1  # rows missing
+        assert b"rows must not be null" in lib.ti_last_error()
+        assert call(4, 64, 0x7FFF0000 // 4 + 1, _ext.F32) == 3  # TI_ESIZE: one buffer resource's reach
+        assert b"2147418112 bytes" in lib.ti_last_error()

@@ -251,10 +251,10 @@ int check_rows(const int64_t* rows, int64_t k, int64_t L, int64_t total, int dty
   if (k < 0 || total < 0) return fail(TI_EINVAL, "need k >= 0 and total >= 0");
   if (L <= ti::kShortMax) return fail(TI_EINVAL, "ragged rows of a block need a block longer than 32, got %lld",
                                       (long long)L);
-  if (k > 0 && rows == nullptr) return fail(TI_EINVAL, "rows must not be null");
   if (total > ti::kRowMapBytes / 4)
     return fail(TI_ESIZE, "the packed arrays must stay below %lld bytes (ti_ragged_pack serves larger ones)",
                 (long long)ti::kRowMapBytes);
+  if (k > 0 && rows == nullptr) return fail(TI_EINVAL, "rows must not be null");
   return TI_OK;
 }
 
