@@ -135,6 +135,35 @@ __device__ __forceinline__ void put_tile_total(const GradKArgs& a, int64_t gt, D
 // Tiles per gsum workgroup: their loads are all in flight before the first tile is summed.
 constexpr int kGsumTiles = 2;
 
+// Over a 256-thread workgroup, one barrier: the exclusive scan of v (double-double) and of c
+// (an int), and v's total. wave_tot and wave_cnt are this call's own (no later call in the
+// kernel writes them, so no barrier follows).
+__device__ __forceinline__ DD block_scan2(DD v, int c, DD* wave_tot, int* wave_cnt, DD& total, int& cbefore) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const DD inc = wave_incl_dd(v);
+  const int cinc = wave_incl_i32(c);
+  const DD exc = wave_shr1_dd(inc);
+  if (lane == kWave - 1) {
+    wave_tot[wave] = inc;
+    wave_cnt[wave] = cinc;
+  }
+  __syncthreads();
+  DD pre{0.0, 0.0};
+  total = DD{0.0, 0.0};
+  int cpre = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < kWaves256; ++w2) {
+    const DD t = wave_tot[w2];
+    if (w2 < wave) {
+      pre = dd_add(pre, t);
+      cpre += wave_cnt[w2];
+    }
+    total = dd_add(total, t);
+  }
+  cbefore = cpre + cinc - c;
+  return dd_add(pre, exc);
+}
+
 template <typename T, bool W, bool MAP = false>
 __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   using C = TileCfg<W>;
@@ -142,9 +171,9 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
   // float32 g: a thread's prefix over E values is kept in float64 (its error is far below the
   // data's); float64 g carries the rounding errors (double-double)
   constexpr bool PR = sizeof(T) == 8;
-  __shared__ DD wtot[kWaves256];
-  __shared__ int rank_scan[kWaves256];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  __shared__ DD wtot[kGsumTiles][kWaves256];  // (per tile: no barrier between the tiles' scans)
+  __shared__ int wcnt[kGsumTiles][kWaves256];
+  const int tid = threadIdx.x;
   const int64_t ntiles = a.batch * a.tpr;
   const int64_t gt0 = static_cast<int64_t>(blockIdx.x) * kGsumTiles;
   const int t0 = tid * E;
@@ -218,7 +247,9 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     if (bad || rB[u] == rA[u] + 1) {
       // no vertex inside the tile (the common case on long rows): its total, a zero prefix for
       // a vertex at its first element, and on the row's last tile the row's end point
-      const DD total = block_sum_dd(acc, wtot);
+      int unused;
+      DD total;
+      block_scan2(acc, 0, wtot[u], wcnt[u], total, unused);
       if (tid == 0) {
         put_tile_total(a, gt, total);
         if (!bad) {
@@ -235,22 +266,18 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
       }
       continue;
     }
-    DD total;
-    const DD off = block_scan_dd(acc, wtot, total);
-    if (tid == 0) put_tile_total(a, gt, total);
     // the hull vertices inside the tile, by rank: rA, less one if rA is the tile's first element
+    // (the prefix of g and the vertex ranks in one scan)
     const uint32_t* srow = a.starts + row * ((a.n + 31) / 32);
     uint32_t mybits = ecount > 0 ? tile_bits(srow, static_cast<int>(first + t0), E) : 0u;
     const int at_start = head[u];
     if (ecount > 0 && ecount < E) mybits &= (1u << ecount) - 1u;
     if (first + t0 == 0) mybits |= 1u;
     const int pc = __builtin_popcount(mybits);
-    const int incl = wave_incl_i32(pc);
-    if (lane == kWave - 1) rank_scan[wave] = incl;
-    __syncthreads();
-    int before = incl - pc;
-    for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
-    __syncthreads();  // rank_scan is reused by the next tile
+    DD total;
+    int before;
+    const DD off = block_scan2(acc, pc, wtot[u], wcnt[u], total, before);
+    if (tid == 0) put_tile_total(a, gt, total);
     int rank = rA[u] - at_start + before;
     DD run{0.0, 0.0};
 #pragma unroll
