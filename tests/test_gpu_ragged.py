@@ -185,26 +185,29 @@ def test_long_rows_of_uniform_lengths() -> None:
         np.testing.assert_allclose(gt.astype(np.float64), e, rtol=1e-5, atol=1e-5 * float(np.abs(e).max()))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("increasing", [True, False])
 @pytest.mark.parametrize("weighted", [False, True])
-def test_rows_whose_pad_joins_their_last_block(increasing: bool, weighted: bool) -> None:
+def test_rows_whose_pad_joins_their_last_block(dtype: type, increasing: bool, weighted: bool) -> None:
     # rows past 32 elements whose pad cannot lie beyond their extreme: NaN rows (one block over
-    # the row and its pad) and rows ending in the largest finite float32 value (a last block that
-    # pools with the pad); their fits and gradients are the row's own, the pad's weight taken out
-    say(f"ragged pad joins the last block: increasing={increasing} weighted={weighted}")
+    # the row and its pad) and, in float32, rows ending in the largest finite value (a last block
+    # that pools with the pad); their fits and gradients are the row's own, the pad's weight taken
+    # out (float32 buckets in place, float64 ones through a block and ti_ragged_unpack)
+    say(f"ragged pad joins the last block: {np.dtype(dtype).name} increasing={increasing} weighted={weighted}")
     rng = np.random.default_rng(41)
     # buckets: (32, 64] rows 0, 2, 3, 7 (L = 64); (64, 128] rows 5, 10; (256, 512] rows 1, 8;
     # (512, 1024] rows 4, 9; row 6 short
     ln = np.array([40, 300, 33, 40, 1000, 70, 5, 64, 500, 1020, 128], dtype=np.int64)
-    y, w, off = ragged_set(ln, np.float32, 42)
-    top = np.float32((1 if increasing else -1) * np.finfo(np.float32).max)
+    y, w, off = ragged_set(ln, dtype, 42)
     y[off[1] + 7] = np.nan       # a NaN row, 300 elements padded to 500
     y[off[3] + 1] = np.nan       # a NaN row, 40 elements padded to 64
-    y[off[3] - 1] = top          # ends at the extreme: a last block of its own, padded to 64
-    y[off[5] - 3:off[5]] = top   # three of them, padded to 1020
-    y[off[6] - 10] = top         # the extreme before smaller values: no pooling with the pad
-    y[off[8] - 1] = top          # a row as long as its block: no pad
-    g = rng.standard_normal(len(y)).astype(np.float32)
+    if dtype == np.float32:      # (float64 sums of the largest float64 overflow in any fit)
+        top = np.float32((1 if increasing else -1) * np.finfo(np.float32).max)
+        y[off[3] - 1] = top          # ends at the extreme: a last block of its own, padded to 64
+        y[off[5] - 3:off[5]] = top   # three of them, padded to 1020
+        y[off[6] - 10] = top         # the extreme before smaller values: no pooling with the pad
+        y[off[8] - 1] = top          # a row as long as its block: no pad
+    g = rng.standard_normal(len(y)).astype(dtype)
     ww = w if weighted else None
     out, grads = _grads(y, ww, off, g, increasing)
     fit, starts = oracle.pava_ragged(y, off, ww, increasing=increasing, acc="f64")
@@ -213,9 +216,10 @@ def test_rows_whose_pad_joins_their_last_block(increasing: bool, weighted: bool)
         a, b = off[r], off[r + 1]
         if not np.isnan(fit[a:b]).any():
             assert float(np.abs(out[a:b].astype(np.float64) - fit[a:b]).max()) <= tolerance(y[a:b]), r
+    gtol = 1e-5 if dtype == np.float32 else 1e-11
     for gt, e in zip(grads, _block_grads(fit, starts, y, ww, g)):
         scale = float(np.abs(e[np.isfinite(e)]).max())
-        np.testing.assert_allclose(gt.astype(np.float64), e, rtol=1e-5, atol=1e-5 * scale)
+        np.testing.assert_allclose(gt.astype(np.float64), e, rtol=gtol, atol=gtol * scale)
 
 
 def _ragged_abi(y: np.ndarray, w: np.ndarray | None, off: np.ndarray, g: np.ndarray, flags: int, lo: float,
