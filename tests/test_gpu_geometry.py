@@ -189,29 +189,39 @@ def test_float32_store_rounding_keeps_the_fit_monotone() -> None:
     close_grad(gw, ew, 1e-5)
 
 
-@pytest.mark.parametrize(("batch", "n"), [(80, 100_000), (300, 40_000), (1100, 20_000)])
-def test_float32_store_rounding_many_rows(batch: int, n: int) -> None:
+# (batch, n, merge levels): rows through two merge levels, fewer or more than 256 of them, and
+# rows whose final hulls the span kernel makes, one row a wave (merged by reference to the span
+# hulls, which do not fit the wave's LDS) or two rows a wave (the overflowing waves' rows merged
+# by the first merge launch)
+STORE_ROUNDING_SHAPES = [(80, 100_000, 2), (300, 40_000, 2), (1100, 20_000, 2), (600, 10_000, 1), (3000, 1000, 1)]
+
+
+@pytest.mark.parametrize(("batch", "n", "levels"), STORE_ROUNDING_SHAPES)
+def test_float32_store_rounding_many_rows(batch: int, n: int, levels: int) -> None:
     # The same near-collinear data over many rows: with 256 rows or more the last merge launch's
     # workgroups (256 and 64 threads here, one a row) make their rows' hulls convex in the stored
-    # values themselves; with fewer, the check and repair launches do.
+    # values themselves, and so do the span kernel's waves where they make the final hulls; with
+    # fewer rows of two levels, the check and repair launches do.
     say(f"float32 store rounding: {batch} weighted near-collinear rows of {n}")
     rng = np.random.default_rng(11)
     i = np.arange(n, dtype=np.float64)
     y = (1e3 + 1e-3 * i + 1e-7 * rng.standard_normal((batch, n))).astype(np.float32)
     w = np.exp(8 * rng.random((batch, n))).astype(np.float32)
-    assert _ext.geometry(batch, n, True)["levels"] == 2
+    assert _ext.geometry(batch, n, True)["levels"] == levels
     got, starts = gpu_fit(y, w)
     assert (np.diff(got, axis=1) >= 0).all()
     want, _ = oracle.pava(y.astype(np.float64), w.astype(np.float64))
     assert float(np.abs(got - want).max()) <= tolerance(y)
 
 
-@pytest.mark.parametrize(("batch", "n"), [(1, 4_000_000), (300, 40_000)])
+@pytest.mark.parametrize(("batch", "n"), [(1, 4_000_000), (300, 40_000), (600, 10_000), (3000, 1000), (9000, 100)])
 def test_float32_repair_chain_gives_the_same_hulls(batch: int, n: int) -> None:
     # The repair finishes a row with a sequential monotone chain after a cascade of removals
     # longer than its pass limit; the REPAIR_CHAIN hint takes that form at once (through the
-    # check and repair launches for one row, in the last merge launch for 300). Both keep the
-    # lower hull of the stored points, so fit and partition are the passes' bit for bit.
+    # check and repair launches for one row, in the last merge launch for 300, in the span
+    # kernel's waves or the first merge launch for 600 x 10000 (one row a wave), 3000 x 1000 (two
+    # rows a wave) and 9000 x 100 (eight)). Both keep the lower hull of the stored points, so fit
+    # and partition are the passes' bit for bit.
     say(f"float32 repair chain: {batch} weighted near-collinear rows of {n}")
     rng = np.random.default_rng(13)
     i = np.arange(n, dtype=np.float64)

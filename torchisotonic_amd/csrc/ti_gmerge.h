@@ -124,6 +124,128 @@ __device__ void vbridge(GA getA, int cA, GB getB, int cB, int& keep, int& from) 
 
 __device__ VArr dvarr_of(const NodeOut& o) { return VArr{o.idx, o.shi, o.slo, o.whi, o.wlo}; }
 
+// (field by field, and without the weights of unweighted rows, which vpools takes from the
+// indices: whole-struct copies between LDS and registers went through scratch memory)
+template <bool W>
+__device__ __forceinline__ void vput(VPt& d, const VPt& x) {
+  d.i = x.i;
+  d.s.hi = x.s.hi;
+  d.s.lo = x.s.lo;
+  if constexpr (W) {
+    d.w.hi = x.w.hi;
+    d.w.lo = x.w.lo;
+  }
+}
+
+// Parallel removal passes before the repair finishes a row with chain_row instead. Each pass
+// removes every vertex then on or above the chord between its neighbours, so it removes one at
+// least, but a removal can expose its neighbours in turn: a long near-collinear run can need a
+// cascade of passes, each a read of the whole hull.
+constexpr int kRepairPasses = 64;
+
+// The lower hull of the row's `cnt` stored vertices by one monotone chain (the same predicate
+// as the passes, so the same hull: a vertex on or above a chord between two others is on no
+// lower hull, and a convex chain through every lower-hull vertex holds no other). Thread 0
+// pushes and pops in place, writing a vertex at or below its own position, while the workgroup
+// stages the next NT vertices into `tile` (NT + 2 slots); returns the count (in thread 0).
+template <bool W, int NT>
+__device__ int chain_row(const VArr& v, int cnt, VPt* tile) {
+  const int tid = threadIdx.x;
+  int top = 0;  // stack entries, at v[0, top); a and b the two at its top
+  VPt a, b;
+  for (int c0 = 0; c0 < cnt; c0 += NT) {
+    const int i = c0 + tid;
+    if (i < cnt) vput<W>(tile[tid], vload<W>(v, i));
+    __syncthreads();
+    if (tid == 0) {
+      const int e = min(NT, cnt - c0);
+      for (int k = 0; k < e; ++k) {
+        VPt p;
+        vput<W>(p, tile[k]);
+        while (top >= 2 && vpools<W>(a, b, p)) {
+          --top;
+          vput<W>(b, a);
+          if (top >= 2) vput<W>(a, vload<W>(v, top - 2));  // (written by this thread before)
+        }
+        vstore<W>(v, top, p);
+        ++top;
+        vput<W>(a, b);
+        vput<W>(b, p);
+      }
+    }
+    __syncthreads();  // (the tile read before it is filled again)
+  }
+  return top;
+}
+
+// A workgroup of NT threads removes, pass after pass, every vertex of the row's hull `o` on or
+// above the chord between its neighbours, until none is (the first pass is the check); after
+// `passes` removal passes the row is finished by chain_row. LDS: tile[NT + 2], wcount[NT / 64],
+// any.
+template <bool W, int NT>
+__device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any, int passes) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const VArr v = dvarr_of(o);
+  int cnt = *o.count;
+  bool convex = false;
+  for (int pass = 0; pass <= passes; ++pass) {
+    if (tid == 0) any = 0;
+    __syncthreads();
+    // (four vertices a thread at a time, all their reads in flight together: a row's hull can
+    // have as many vertices as elements)
+    bool found = false;
+    for (int i0 = 1 + tid; i0 < cnt - 1; i0 += 4 * NT) {
+      VPt a[4], b[4], c[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * NT, cnt - 2);
+        a[u] = vload<W>(v, i - 1);
+        b[u] = vload<W>(v, i);
+        c[u] = vload<W>(v, i + 1);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) found |= vpools<W>(a[u], b[u], c[u]);
+    }
+    if (__any(found) && lane == 0) any = 1;
+    __syncthreads();
+    if (any == 0) {
+      convex = true;
+      break;
+    }
+    if (pass == passes) break;  // (still not convex: chain_row below)
+    int base = 0;
+    VPt last;  // (thread NT - 1: the previous chunk's last original vertex)
+    for (int c0 = 0; c0 < cnt; c0 += NT) {
+      const int i = c0 + tid;
+      if (i < cnt) vput<W>(tile[tid + 1], vload<W>(v, i));
+      if (tid == NT - 1) {
+        if (c0 > 0) vput<W>(tile[0], last);
+        if (c0 + NT < cnt) vput<W>(tile[NT + 1], vload<W>(v, c0 + NT));
+      }
+      __syncthreads();
+      const bool keep = i < cnt && (i == 0 || i == cnt - 1 || !vpools<W>(tile[tid], tile[tid + 1], tile[tid + 2]));
+      const uint64_t m = __ballot(keep);
+      if (lane == 0) wcount[wave] = __popcll(m);
+      __syncthreads();
+      int before = base, all = 0;
+      for (int k = 0; k < NT / kWave; ++k) {
+        before += k < wave ? wcount[k] : 0;
+        all += wcount[k];
+      }
+      VPt x;
+      vput<W>(x, tile[tid + 1]);
+      if (tid == NT - 1) vput<W>(last, x);
+      __syncthreads();  // every read of this chunk's slots is done
+      if (keep) vstore<W>(v, before + __popcll(m & ((uint64_t{1} << lane) - 1)), x);
+      base += all;
+    }
+    cnt = base;
+    __syncthreads();
+  }
+  if (!convex) cnt = chain_row<W, NT>(v, cnt, tile);
+  if (tid == 0) *o.count = cnt;
+}
+
 struct MergeSmall {
   int cnt[kGroup], off[kGroup];
   double tot[4][kGroup + 1];  // child offsets (W hi, lo, S hi, lo); [nch]: the parent's total

@@ -65,128 +65,6 @@ __global__ __launch_bounds__(kRepairThreads) void convex_check_kernel(NodeLevel 
   if (found) flag[row] = epoch;
 }
 
-// (field by field, and without the weights of unweighted rows, which vpools takes from the
-// indices: whole-struct copies between LDS and registers went through scratch memory)
-template <bool W>
-__device__ __forceinline__ void vput(VPt& d, const VPt& x) {
-  d.i = x.i;
-  d.s.hi = x.s.hi;
-  d.s.lo = x.s.lo;
-  if constexpr (W) {
-    d.w.hi = x.w.hi;
-    d.w.lo = x.w.lo;
-  }
-}
-
-// Parallel removal passes before the repair finishes a row with chain_row instead. Each pass
-// removes every vertex then on or above the chord between its neighbours, so it removes one at
-// least, but a removal can expose its neighbours in turn: a long near-collinear run can need a
-// cascade of passes, each a read of the whole hull.
-constexpr int kRepairPasses = 64;
-
-// The lower hull of the row's `cnt` stored vertices by one monotone chain (the same predicate
-// as the passes, so the same hull: a vertex on or above a chord between two others is on no
-// lower hull, and a convex chain through every lower-hull vertex holds no other). Thread 0
-// pushes and pops in place, writing a vertex at or below its own position, while the workgroup
-// stages the next NT vertices into `tile` (NT + 2 slots); returns the count (in thread 0).
-template <bool W, int NT>
-__device__ int chain_row(const VArr& v, int cnt, VPt* tile) {
-  const int tid = threadIdx.x;
-  int top = 0;  // stack entries, at v[0, top); a and b the two at its top
-  VPt a, b;
-  for (int c0 = 0; c0 < cnt; c0 += NT) {
-    const int i = c0 + tid;
-    if (i < cnt) vput<W>(tile[tid], vload<W>(v, i));
-    __syncthreads();
-    if (tid == 0) {
-      const int e = min(NT, cnt - c0);
-      for (int k = 0; k < e; ++k) {
-        VPt p;
-        vput<W>(p, tile[k]);
-        while (top >= 2 && vpools<W>(a, b, p)) {
-          --top;
-          vput<W>(b, a);
-          if (top >= 2) vput<W>(a, vload<W>(v, top - 2));  // (written by this thread before)
-        }
-        vstore<W>(v, top, p);
-        ++top;
-        vput<W>(a, b);
-        vput<W>(b, p);
-      }
-    }
-    __syncthreads();  // (the tile read before it is filled again)
-  }
-  return top;
-}
-
-// A workgroup of NT threads removes, pass after pass, every vertex of the row's hull `o` on or
-// above the chord between its neighbours, until none is (the first pass is the check); after
-// `passes` removal passes the row is finished by chain_row. LDS: tile[NT + 2], wcount[NT / 64],
-// any.
-template <bool W, int NT>
-__device__ void repair_row(const NodeOut& o, VPt* tile, int* wcount, int& any, int passes) {
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const VArr v = dvarr_of(o);
-  int cnt = *o.count;
-  bool convex = false;
-  for (int pass = 0; pass <= passes; ++pass) {
-    if (tid == 0) any = 0;
-    __syncthreads();
-    // (four vertices a thread at a time, all their reads in flight together: a row's hull can
-    // have as many vertices as elements)
-    bool found = false;
-    for (int i0 = 1 + tid; i0 < cnt - 1; i0 += 4 * NT) {
-      VPt a[4], b[4], c[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = min(i0 + u * NT, cnt - 2);
-        a[u] = vload<W>(v, i - 1);
-        b[u] = vload<W>(v, i);
-        c[u] = vload<W>(v, i + 1);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) found |= vpools<W>(a[u], b[u], c[u]);
-    }
-    if (__any(found) && lane == 0) any = 1;
-    __syncthreads();
-    if (any == 0) {
-      convex = true;
-      break;
-    }
-    if (pass == passes) break;  // (still not convex: chain_row below)
-    int base = 0;
-    VPt last;  // (thread NT - 1: the previous chunk's last original vertex)
-    for (int c0 = 0; c0 < cnt; c0 += NT) {
-      const int i = c0 + tid;
-      if (i < cnt) vput<W>(tile[tid + 1], vload<W>(v, i));
-      if (tid == NT - 1) {
-        if (c0 > 0) vput<W>(tile[0], last);
-        if (c0 + NT < cnt) vput<W>(tile[NT + 1], vload<W>(v, c0 + NT));
-      }
-      __syncthreads();
-      const bool keep = i < cnt && (i == 0 || i == cnt - 1 || !vpools<W>(tile[tid], tile[tid + 1], tile[tid + 2]));
-      const uint64_t m = __ballot(keep);
-      if (lane == 0) wcount[wave] = __popcll(m);
-      __syncthreads();
-      int before = base, all = 0;
-      for (int k = 0; k < NT / kWave; ++k) {
-        before += k < wave ? wcount[k] : 0;
-        all += wcount[k];
-      }
-      VPt x;
-      vput<W>(x, tile[tid + 1]);
-      if (tid == NT - 1) vput<W>(last, x);
-      __syncthreads();  // every read of this chunk's slots is done
-      if (keep) vstore<W>(v, before + __popcll(m & ((uint64_t{1} << lane) - 1)), x);
-      base += all;
-    }
-    cnt = base;
-    __syncthreads();
-  }
-  if (!convex) cnt = chain_row<W, NT>(v, cnt, tile);
-  if (tid == 0) *o.count = cnt;
-}
-
 // (repair_row's removal, written out for one 256-thread workgroup a marked row: through
 // repair_row, whose check keeps four vertices a thread in flight, C3's float32 forward took 5 us
 // longer)
@@ -935,7 +813,17 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   char* base = static_cast<char*>(ws);
   const NodeLevel fin = p.level(ws, p.levels);
   // level 0: span hulls (and the first merge level, fused, where there is one)
-  hipError_t e = span_run(t, p.level(ws, 0), p.span0, p.level(ws, p.levels >= 1 ? 1 : 0), p.rows_per_wave);
+  // Float32 data: the final hulls made convex in their stored values. Rows of one merge level
+  // get theirs from the span kernel (or, for a multi-row wave's overflowing spans, the level-1
+  // launch), whose waves check and repair them in place (span_fold); a final level of two or
+  // more launches up has a merge workgroup for every row, which does it at its end (fold) where
+  // rows are enough to spread those workgroups over the GPU (one workgroup reading a hull of
+  // millions of vertices would take milliseconds); otherwise two launches after the merges do.
+  const int repair_passes = (t.flags & TI_REPAIR_CHAIN) != 0 ? 0 : kRepairPasses;
+  const bool span_fold = !p.lo && p.levels == 1;
+  const bool fold = !p.lo && p.levels >= 2 && batch_fills_gpu(t.batch);
+  hipError_t e = span_run(t, p.level(ws, 0), p.span0, p.level(ws, p.levels >= 1 ? 1 : 0), p.rows_per_wave,
+                          span_fold ? 1 + repair_passes : 0);
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
@@ -960,12 +848,6 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     return t.hulls_ready != nullptr ? hipEventRecord(t.hulls_ready, t.stream) : hipSuccess;
   };
   if ((e = report(0)) != hipSuccess) return e;
-  // Float32 data: the final hulls made convex in their stored values. A final level of two or more
-  // launches up has a merge workgroup for every row, which does it at its end (fold) where rows
-  // are enough to spread those workgroups over the GPU (one workgroup reading a hull of millions
-  // of vertices would take milliseconds); otherwise two launches after the merges do.
-  const bool fold = !p.lo && p.levels >= 2 && batch_fills_gpu(t.batch);
-  const int repair_passes = (t.flags & TI_REPAIR_CHAIN) != 0 ? 0 : kRepairPasses;
   for (int l = 1; l <= p.levels; ++l) {
     // (one row a wave: the span kernel merged every group, in LDS or, where its hulls do not
     // fit, in the group's global array; a multi-row wave's overflowing spans wait for a launch)
@@ -982,7 +864,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     // (64 noisy span hulls take 300-500) where there are thousands, else 256 or 1024 threads
     // and up to 56 KB of slots for the fewer, larger hulls of the upper levels.
     // (the final level of float32 data repairs its hulls in the merge launch: fold)
-    const int fix = fold && l == p.levels ? 1 + repair_passes : 0;
+    const int fix = (fold || span_fold) && l == p.levels ? 1 + repair_passes : 0;
     auto launch = [&](auto k64, auto k256, auto k1024, size_t vb) {
       const int big = static_cast<int>((56 * 1024 / vb) & ~size_t(63));
       if (grid >= 1024) {
@@ -1004,7 +886,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     if (e != hipSuccess) return e;
     if ((e = report(l)) != hipSuccess) return e;
   }
-  if (!p.lo && p.levels >= 1 && !fold) {
+  if (!p.lo && p.levels >= 1 && !fold && !span_fold) {
     // (float32 data: the final hulls convex in their stored values; span hulls, the final hulls
     // of rows of one span, are exact and convex already). Enough check workgroups a row for a
     // hull of every element (4096 vertices each), at most 256.

@@ -47,6 +47,10 @@ struct SpanArgs {
   NodeLevel hulls;        // the spans' level
   NodeLevel hulls1;       // the groups' (the first merge level; with rpw > 1, the rows')
   RowMap map;             // ragged rows of one block: y and w read from the packed arrays
+  // > 0: the hulls this kernel merges are the rows' final hulls of float32 data, which the wave
+  // then makes convex in their stored values (repair_row, fix - 1 removal passes before its
+  // chain), so that no check launch follows
+  int fix;
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the candidate queue (index
@@ -388,6 +392,19 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     write_span_hull();
     return;
   }
+  // A final hull of float32 data convex in its stored values (a.fix): once every lane has
+  // written it, the wave checks it and, where a vertex lies on or above its neighbours' chord,
+  // repairs it in place, with the wave's LDS (free by then) for the repair's staging.
+  auto fold = [&](const NodeOut& h, bool row_bad) {
+    if constexpr (!PR) {
+      if (a.fix != 0 && !row_bad) {
+        __syncthreads();  // the hull written by every lane, the LDS read
+        VPt* tile = reinterpret_cast<VPt*>(&L);
+        int* wcount = reinterpret_cast<int*>(tile + kSpanLanes + 2);
+        repair_row<W, kSpanLanes>(h, tile, wcount, wcount[kSpanLanes / kWave], a.fix - 1);
+      }
+    }
+  };
 
   // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
   // lane c's hull is child c, positions [0, depth), its first point shared with lane c - 1 - but
@@ -461,6 +478,7 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
       gout.tot[3] = sm.tot[3][nch];
       *o.count = -1;  // (the group is merged: its first span's count says so to the merge kernel)
     }
+    fold(gout, gbad);
     return;
   }
   // offsets of this lane's span within its row (the group's, or multi: its row's)
@@ -551,6 +569,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         pout.tot[3] = e.sl;
       }
     }
+    for (int r = 0; r < nch / kl; ++r)
+      fold(node_out(a.hulls1, W, static_cast<int64_t>(blockIdx.x) * a.rpw + r), ((badm >> (r * kl)) & kmask) != 0);
     // every row merged: its first span's count says so to the merge kernel
     if (active && span == 0) *o.count = -1;
     return;
@@ -573,12 +593,13 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   }
   // the group is merged: its first span's count says so to the merge kernel
   if (lane == 0) *o.count = -1;
+  fold(pout, anybad);
 }
 
 }  // namespace
 
 hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, const NodeLevel& hulls1,
-                     int rows_per_wave) {
+                     int rows_per_wave, int fix) {
   const int64_t spr = hulls.npr;
   SpanArgs a;
   a.y = t.y;
@@ -594,6 +615,7 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
   a.rpw = rows_per_wave;
   a.hulls1 = hulls1;
   a.map = t.map;
+  a.fix = fix;
   // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
   // rows_per_wave of them)
   const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes

@@ -363,9 +363,10 @@ hipError_t long_keep(const LongPlan& p, const void* ws, const KeepPlan& k, void*
 // Level 0 (span hulls) and, fused, level 1: a group whose hulls fit the wave's LDS is merged in
 // place into its level-1 node of `hulls1` and its first span's count set to -1. With
 // rows_per_wave > 1, each wave holds that many rows of spans_per_row spans (a power of two) and
-// merges each row's spans into the row's hull.
+// merges each row's spans into the row's hull. fix > 0: those hulls are the rows' final hulls of
+// float32 data, made convex in their stored values by the same waves (fix - 1 removal passes).
 hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, const NodeLevel& hulls1,
-                    int rows_per_wave);
+                    int rows_per_wave, int fix);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {
