@@ -410,3 +410,44 @@ def test_several_rows_a_wave(batch: int, n: int) -> None:
     # number of spans each, merged per row in the wave
     print(f"rows a wave batch={batch} n={n}", flush=True)
     check_many_rows(batch, n)
+
+
+# (batch, n) of one merge level, one row a wave: the wave that builds a row's final hull also
+# writes its tile records, start bits and fit. Rows with a vertex at every element have more
+# edges than the wave's table of edge values holds (about 3.5k-4.8k), so it is restaged within
+# the row; n = 2049 is one element past the packed expansion's rows.
+ONE_LEVEL_SHAPES = [(600, 10_000), (700, 5_000), (2_100, 2_049)]
+
+
+@pytest.mark.parametrize(("batch", "n"), ONE_LEVEL_SHAPES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_one_level_rows_expanded_by_their_wave(batch: int, n: int, dtype: type, weighted: bool) -> None:
+    from torchisotonic_amd import _ext
+
+    print(f"one-level rows batch={batch} n={n} dtype={np.dtype(dtype).name} weighted={weighted}", flush=True)
+    geo = _ext.geometry(batch, n, weighted)
+    assert geo["levels"] == 1 and geo["rows_per_wave"] == 1, geo
+    rng = np.random.default_rng(n + batch + weighted)
+    y = np.linspace(0, 3, n) + rng.standard_normal((batch, n))
+    mono = np.arange(0, batch, 3)
+    y[mono] = 1e-3 * np.arange(n) + rng.random((mono.size, 1))  # a vertex at every element
+    y[5, n // 2] = np.nan
+    y = y.astype(dtype)
+    w = (rng.random((batch, n)) + 0.1).astype(dtype) if weighted else None
+    got, starts = check_fit(y, w)
+    assert starts[mono].all()
+    check_fit(y, w, increasing=False, y_min=0.5, y_max=2.0)
+    # both gradients through the wave's tile records and start bits (rows without the NaN)
+    ok = ~np.isnan(y).any(axis=1)
+    c = rng.standard_normal((batch, n)).astype(dtype)
+    gs, _ = gpu_grads(y, w, c)
+    fit, st = oracle.pava(y[ok], None if w is None else w[ok], acc="f64")
+    ey, ew = oracle.block_grad(
+        st, c[ok].astype(np.float64), None if w is None else w[ok].astype(np.float64),
+        y[ok].astype(np.float64), fit, want_w=w is not None,
+    )
+    tol = 1e-12 if dtype == np.float64 else 2e-5
+    np.testing.assert_allclose(gs[0][ok], ey, rtol=tol, atol=tol)
+    if w is not None:
+        np.testing.assert_allclose(gs[1][ok], ew, rtol=tol, atol=tol * (1 + float(np.nanmax(np.abs(y)))))

@@ -822,8 +822,12 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   const int repair_passes = (t.flags & TI_REPAIR_CHAIN) != 0 ? 0 : kRepairPasses;
   const bool span_fold = !p.lo && p.levels == 1;
   const bool fold = !p.lo && p.levels >= 2 && batch_fills_gpu(t.batch);
+  // Rows of one merge level, one row a wave: the wave that builds a row's final hull also writes
+  // its tile records, start bits and fit (span_expand), so no rank or expansion launch follows.
+  const bool span_expand = p.levels == 1 && p.rows_per_wave == 1;
+  TileRec* const recs_at = reinterpret_cast<TileRec*>(base + p.off_rank);
   hipError_t e = span_run(t, p.level(ws, 0), p.span0, p.level(ws, p.levels >= 1 ? 1 : 0), p.rows_per_wave,
-                          span_fold ? 1 + repair_passes : 0);
+                          span_fold ? 1 + repair_passes : 0, span_expand ? recs_at : nullptr);
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
@@ -905,6 +909,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  if (span_expand) return hipSuccess;
   if (t.n <= kXpackMaxN) {
     // rows of one tile: records and fit together, whole rows a workgroup
     ExpandArgs x;

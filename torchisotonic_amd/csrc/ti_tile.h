@@ -365,8 +365,10 @@ hipError_t long_keep(const LongPlan& p, const void* ws, const KeepPlan& k, void*
 // rows_per_wave > 1, each wave holds that many rows of spans_per_row spans (a power of two) and
 // merges each row's spans into the row's hull. fix > 0: those hulls are the rows' final hulls of
 // float32 data, made convex in their stored values by the same waves (fix - 1 removal passes).
+// tiles given (rows of one merge level, one row a wave): each wave also writes its row's fit,
+// start bits and tile records (into tiles), in place of the rank and expansion launches.
 hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, const NodeLevel& hulls1,
-                    int rows_per_wave, int fix);
+                    int rows_per_wave, int fix, TileRec* tiles);
 
 // Backward of long rows, from the forward's final hulls and tile ranks (its workspace).
 struct LongGradArgs {
