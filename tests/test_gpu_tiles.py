@@ -451,3 +451,23 @@ def test_one_level_rows_expanded_by_their_wave(batch: int, n: int, dtype: type, 
     np.testing.assert_allclose(gs[0][ok], ey, rtol=tol, atol=tol)
     if w is not None:
         np.testing.assert_allclose(gs[1][ok], ew, rtol=tol, atol=tol * (1 + float(np.nanmax(np.abs(y)))))
+
+
+# Rows whose hulls keep most of their points as vertices (rising data with a drop every 997
+# elements) at sizes whose upper merge levels work by reference to the children's vertices
+# (more than LDS holds) and move hundreds of thousands of survivors in place, each child's by a
+# shift that grows with every drop before it.
+@pytest.mark.parametrize(("batch", "n"), [(1, 3_000_000), (3, 700_000), (20, 150_000)])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_near_monotone_rows_many_survivors(batch: int, n: int, dtype: type, weighted: bool) -> None:
+    from torchisotonic_amd import _ext
+
+    print(f"near-monotone rows batch={batch} n={n} dtype={np.dtype(dtype).name} weighted={weighted}", flush=True)
+    assert _ext.geometry(batch, n, weighted)["levels"] >= 2
+    rng = np.random.default_rng(n + batch + weighted)
+    i = np.arange(n)
+    y = 1e-3 * i + 1e-5 * rng.standard_normal((batch, n)) - 0.3 * (i % 997 == 0)
+    y = y.astype(dtype)
+    w = (rng.random((batch, n)) + 0.5).astype(dtype) if weighted else None
+    check_fit(y, w)
