@@ -312,8 +312,13 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
   constexpr int E = C::kE;
   constexpr int NT = C::kThreads;
   constexpr int K = kExpandTiles;
+  constexpr int NW = C::kN / 32;       // bitmap words a tile
+  constexpr int V = 16 / sizeof(T);    // elements a 16-byte piece
+  constexpr int G = E / V;             // pieces a thread
+  static_assert(NW <= NT, "a thread per bitmap word");
   __shared__ T sl[C::kN + 2];  // sgn * slope per edge, rounded once to T
-  __shared__ uint32_t bits[C::kN / 32];
+  __shared__ uint32_t bits[NW];
+  __shared__ int wpre[NW];
   __shared__ int rank_scan[kWaves256];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -363,7 +368,6 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
     int64_t rfirst = row * a.n, rlen = a.n;
     if constexpr (MAP) map_row(a.map, row, a.n, rfirst, rlen);
     const int slen = MAP ? static_cast<int>(max<int64_t>(0, min<int64_t>(len, rlen - first))) : len;
-    const int scount = MAP ? max(0, min(ecount, slen - t0)) : ecount;
     T* out = static_cast<T*>(a.out) + rfirst + first;
     auto write_starts = [&](uint32_t sb) {
       if (a.starts == nullptr || ecount <= 0) return;
@@ -401,27 +405,64 @@ __global__ __launch_bounds__(256) void expand_kernel(ExpandArgs a) {
       if (p.i >= ta) atomicOr(&bits[(p.i - ta) >> 5], 1u << ((p.i - ta) & 31));
     }
     __syncthreads();
-    uint32_t mybits;
-    if constexpr (E == 16) mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFFFu;
-    else mybits = (bits[t0 >> 5] >> (t0 & 31)) & 0xFFu;
-    const int pc = __builtin_popcount(mybits);
-    const int incl = wave_incl_i32(pc);
-    if (lane == kWave - 1) rank_scan[wave] = incl;
-    __syncthreads();
-    int before = incl - pc;
-    for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
-    const int at_start = (v.idx[rA] == ta) ? 1 : 0;
-    int jj = before + static_cast<int>(mybits & 1u) - at_start;
-    T fit[E];
-#pragma unroll
-    for (int k = 0; k < E; ++k) {
-      if (k > 0) jj += (mybits >> k) & 1u;
-      const T val = row_bad ? quiet_nan<T>() : sl[jj];
-      fit[k] = clip(val, use_lo, lo, use_hi, hi);
+    // per bitmap word: the tile's vertices before it (a scan of the words' counts)
+    {
+      const int c = tid < NW ? __popc(bits[tid]) : 0;
+      const int incl = wave_incl_i32(c);
+      if (lane == kWave - 1) rank_scan[wave] = incl;
+      __syncthreads();
+      int before = incl - c;
+      for (int w2 = 0; w2 < wave; ++w2) before += rank_scan[w2];
+      if (tid < NW) wpre[tid] = before;
     }
-    store_elems_any<T, E, NTS>(out + t0, scount, fit);
-    write_starts(row_bad ? ((first + t0) == 0 ? 1u : 0u) : mybits);
-    __syncthreads();  // sl, bits and rank_scan are reused by the next tile
+    __syncthreads();
+    // An element's edge (from rA) is the tile's vertices at or before it, less one if a vertex
+    // starts the tile. Each thread takes G pieces of V consecutive elements, each store
+    // instruction of a wave one contiguous run of 64 pieces (16 bytes each); every piece's word
+    // and count are read at once, then its elements' slopes.
+    const int at_start = (v.idx[rA] == ta) ? 1 : 0;
+    int g0[G], cnt[G];
+    uint32_t wb[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      g0[j] = j * NT * V + tid * V;
+      const uint32_t word = bits[g0[j] >> 5];
+      wb[j] = word >> (g0[j] & 31);
+      cnt[j] = wpre[g0[j] >> 5] + __popc(word & ((1u << (g0[j] & 31)) - 1u)) - at_start;
+    }
+    T fit[G][V];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        cnt[j] += (wb[j] >> k) & 1u;  // (zero past the row's end: the last edge again)
+        const T val = row_bad ? quiet_nan<T>() : sl[cnt[j]];
+        fit[j][k] = clip(val, use_lo, lo, use_hi, hi);
+      }
+    }
+    const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int m = slen - g0[j];
+      if (m >= V && aligned) {
+        using VT = T __attribute__((ext_vector_type(V)));
+        VT x;
+#pragma unroll
+        for (int k = 0; k < V; ++k) x[k] = fit[j][k];
+        if constexpr (NTS) __builtin_nontemporal_store(x, reinterpret_cast<VT*>(out + g0[j]));
+        else *reinterpret_cast<VT*>(out + g0[j]) = x;
+      } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k)
+          if (k < m) out[g0[j] + k] = fit[j][k];
+      }
+    }
+    // start bits: the tile's words (a NaN row: its first element only)
+    if (a.starts != nullptr) {
+      for (int wd = tid; wd < (len + 31) / 32; wd += NT)
+        a.starts[row * wpr + (first >> 5) + wd] = row_bad ? ((first == 0 && wd == 0) ? 1u : 0u) : bits[wd];
+    }
+    __syncthreads();  // sl, bits, wpre and rank_scan are reused by the next tile
   }
 }
 
