@@ -471,3 +471,42 @@ def test_near_monotone_rows_many_survivors(batch: int, n: int, dtype: type, weig
     y = y.astype(dtype)
     w = (rng.random((batch, n)) + 0.5).astype(dtype) if weighted else None
     check_fit(y, w)
+
+
+# (batch, n): rows of two merge levels in batches of 256 or more, whose final merge launch has a
+# workgroup a row: that workgroup also writes the row's tile records, start bits and fit. Rows
+# with a vertex at every element have more edges than the workgroup's table of edge values holds,
+# so it is restaged within the row.
+LAST_MERGE_SHAPES = [(256, 20_000), (300, 40_000)]
+
+
+@pytest.mark.parametrize(("batch", "n"), LAST_MERGE_SHAPES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_rows_expanded_by_their_last_merge(batch: int, n: int, dtype: type, weighted: bool) -> None:
+    from torchisotonic_amd import _ext
+
+    print(f"last-merge rows batch={batch} n={n} dtype={np.dtype(dtype).name} weighted={weighted}", flush=True)
+    assert _ext.geometry(batch, n, weighted)["levels"] == 2
+    rng = np.random.default_rng(n + batch + weighted)
+    y = np.linspace(0, 3, n) + rng.standard_normal((batch, n))
+    mono = np.arange(0, batch, 5)
+    y[mono] = 1e-3 * np.arange(n) + rng.random((mono.size, 1))  # a vertex at every element
+    y[7, n // 3] = np.nan
+    y = y.astype(dtype)
+    w = (rng.random((batch, n)) + 0.1).astype(dtype) if weighted else None
+    got, starts = check_fit(y, w)
+    assert starts[mono].all()
+    check_fit(y, w, increasing=False, y_min=0.5, y_max=2.0)
+    ok = ~np.isnan(y).any(axis=1)
+    c = rng.standard_normal((batch, n)).astype(dtype)
+    gs, _ = gpu_grads(y, w, c)
+    fit, st = oracle.pava(y[ok], None if w is None else w[ok], acc="f64")
+    ey, ew = oracle.block_grad(
+        st, c[ok].astype(np.float64), None if w is None else w[ok].astype(np.float64),
+        y[ok].astype(np.float64), fit, want_w=w is not None,
+    )
+    tol = 1e-12 if dtype == np.float64 else 2e-5
+    np.testing.assert_allclose(gs[0][ok], ey, rtol=tol, atol=tol)
+    if w is not None:
+        np.testing.assert_allclose(gs[1][ok], ew, rtol=tol, atol=tol * (1 + float(np.nanmax(np.abs(y)))))

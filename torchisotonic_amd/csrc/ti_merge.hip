@@ -21,6 +21,7 @@
 #include <type_traits>
 
 #include "ti_common.h"
+#include "ti_expand.h"
 #include "ti_kernels.h"
 #include "ti_slots.h"
 #include "ti_gmerge.h"
@@ -182,8 +183,11 @@ constexpr size_t repair_lds_bytes(int nt) { return (nt + 2) * sizeof(VPt) + (nt 
 // fix > 0: the launch makes the final hulls of float32 data, which the workgroup then makes convex
 // in their stored values (repair_row, with fix - 1 removal passes before its chain), so no check
 // launch follows.
-template <bool W, bool PR, int NT, int G>
-__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int fix) {
+// TX (float or double: the fit's type) with the final level of rows enough to fill the GPU: the
+// workgroup then expands its row's final hull too (expand_row, with x.lds_bytes of its dynamic
+// LDS), in place of the rank and expansion launches.
+template <bool W, bool PR, int NT, int G, typename TX = void>
+__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int fix, RowExpand x) {
   __shared__ MergeSmall sm;
   __shared__ MergeRounds rs;
   extern __shared__ __align__(16) char lds_dyn[];
@@ -251,6 +255,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int
     int* wcount = reinterpret_cast<int*>(tile + NT + 2);
     repair_row<W, NT>(pout, tile, wcount, wcount[NT / kWave], fix - 1);
   }
+  if constexpr (!std::is_void_v<TX>) expand_row<TX, W, false, NT>(x, pout, sm.bad != 0, row, lds_dyn);
 }
 
 // Per expansion tile of tile_n elements (one thread each): the final hull's last vertex at or
@@ -893,6 +898,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     return t.hulls_ready != nullptr ? hipEventRecord(t.hulls_ready, t.stream) : hipSuccess;
   };
   if ((e = report(0)) != hipSuccess) return e;
+  bool expanded = false;  // (the final merge launch expanded the rows)
   for (int l = 1; l <= p.levels; ++l) {
     // (one row a wave: the span kernel merged every group, in LDS or, where its hulls do not
     // fit, in the group's global array; a multi-row wave's overflowing spans wait for a launch)
@@ -910,19 +916,53 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     // and up to 56 KB of slots for the fewer, larger hulls of the upper levels.
     // (the final level of float32 data repairs its hulls in the merge launch: fold)
     const int fix = (fold || span_fold) && l == p.levels ? 1 + repair_passes : 0;
-    auto launch = [&](auto k64, auto k256, auto k1024, size_t vb) {
+    // The final level of rows enough to fill the GPU, one workgroup a row (dense rows whose
+    // bitmap, counts and a pass's edges fit the launch's LDS): the workgroup expands its row.
+    // Only from the second level on: a first-level launch merges just the rows of multi-row
+    // waves whose spans overflowed, the span kernel's waves having finished the others.
+    const bool last_fills =
+        l == p.levels && l >= 2 && batch_fills_gpu(t.batch) && grid >= 64 && t.map.rows == nullptr;
+    RowExpand x{};
+    x.n = t.n;
+    x.out = t.out;
+    x.starts = t.starts;
+    x.tiles = recs_at;
+    x.tpr = p.tiles_per_row;
+    x.tile_n = static_cast<int>(tile_elems(W));
+    x.flags = t.flags;
+    x.lo = t.lo;
+    x.hi = t.hi;
+    const int tb = t.dtype == TI_F32 ? 4 : 8;
+    auto launch = [&](auto k64, auto k256, auto k1024, auto x64f, auto x256f, auto x64d, auto x256d, size_t vb) {
       const int big = static_cast<int>((56 * 1024 / vb) & ~size_t(63));
       if (grid >= 1024) {
-        k64<<<dim3(grid), dim3(64), std::max(768 * vb, repair_lds_bytes(64)), t.stream>>>(m, 768, fix);
+        const size_t lds = std::max(768 * vb, repair_lds_bytes(64));
+        x.lds_bytes = static_cast<int>(lds);
+        if (last_fills && static_cast<int>(lds) >= expand_lds_min(t.n, 64, tb)) {
+          expanded = true;
+          if (tb == 4) x64f<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x);
+          else x64d<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x);
+        } else {
+          k64<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x);
+        }
       } else if (grid >= 64) {
-        k256<<<dim3(grid), dim3(256), std::max(big * vb, repair_lds_bytes(256)), t.stream>>>(m, big, fix);
+        const size_t lds = std::max(big * vb, repair_lds_bytes(256));
+        x.lds_bytes = static_cast<int>(lds);
+        if (last_fills && static_cast<int>(lds) >= expand_lds_min(t.n, 256, tb)) {
+          expanded = true;
+          if (tb == 4) x256f<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x);
+          else x256d<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x);
+        } else {
+          k256<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x);
+        }
       } else {
-        k1024<<<dim3(grid), dim3(1024), std::max(big * vb, repair_lds_bytes(1024)), t.stream>>>(m, big, fix);
+        k1024<<<dim3(grid), dim3(1024), std::max(big * vb, repair_lds_bytes(1024)), t.stream>>>(m, big, fix, x);
       }
     };
-#define TI_MERGE_LAUNCH(Wv, PRv)                                                                 \
-  launch(merge_kernel<Wv, PRv, 64, 4>, merge_kernel<Wv, PRv, 256, 2>, merge_kernel<Wv, PRv, 1024, 2>, \
-         slot_bytes<Wv, PRv>())
+#define TI_MERGE_LAUNCH(Wv, PRv)                                                                            \
+  launch(merge_kernel<Wv, PRv, 64, 4>, merge_kernel<Wv, PRv, 256, 2>, merge_kernel<Wv, PRv, 1024, 2>,           \
+         merge_kernel<Wv, PRv, 64, 4, float>, merge_kernel<Wv, PRv, 256, 2, float>,                            \
+         merge_kernel<Wv, PRv, 64, 4, double>, merge_kernel<Wv, PRv, 256, 2, double>, slot_bytes<Wv, PRv>())
     // (node arrays and slots are double-double for both dtypes: see child_vertex)
     if (W) TI_MERGE_LAUNCH(true, true);
     else TI_MERGE_LAUNCH(false, true);
@@ -950,7 +990,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (span_expand) return hipSuccess;
+  if (span_expand || expanded) return hipSuccess;
   if (t.n <= kXpackMaxN) {
     // rows of one tile: records and fit together, whole rows a workgroup
     ExpandArgs x;

@@ -24,6 +24,7 @@
 //
 // Output: the span hulls as the first node array of the cross-span merge (ti_merge.hip).
 #include "ti_common.h"
+#include "ti_expand.h"
 #include "ti_gmerge.h"
 #include "ti_kernels.h"
 #include "ti_slots.h"
@@ -52,15 +53,10 @@ struct SpanArgs {
   // chain), so that no check launch follows
   int fix;
   // (rows of one merge level, one row a wave) the wave expands its row's final hull itself: the
-  // fit into out, the start bits into starts (if given) and the tile records (tpr tiles of
-  // tile_n elements a row) into tiles, in place of the rank and expansion launches
+  // fit, the start bits (if asked for) and the tile records, in place of the rank and expansion
+  // launches
   bool expand;
-  void* out;
-  uint32_t* starts;
-  TileRec* tiles;
-  int64_t tpr;
-  int tile_n;
-  double lo, hi;
+  RowExpand xp;
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the candidate queue (index
@@ -416,158 +412,15 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     }
   };
   // The row's final hull h expanded by the wave (a.expand; one row a wave, the group the whole
-  // row), in place of the rank and expansion launches: the hull's vertices as a bitmap of the
-  // row's elements in LDS, and per bitmap word the vertices before it (one wave scan), from
-  // which an element's edge (the vertices at or before it, less one) and a tile's records (its
-  // first and last edges, as rank_kernel's searches find them) follow without a search; the
-  // start bits are the bitmap; the fit, 1024 elements a pass, is each edge's slope
-  // rounded once, signed and clamped as the expansion kernels form it, from a table of the
-  // edges' values in LDS, restaged where 1024 elements need edges past the table (a row's hull
-  // can have a vertex every element).
+  // row), in place of the rank and expansion launches, with the wave's LDS (free by then).
+  // (rows of one group: n <= 64 spans of kSpanMax, so the bitmap and the word counts take at
+  // most 4 KB, and the table holds thousands of edges, past the 1024 a pass can need)
+  static_assert(expand_lds_min(kGroup * kSpanMax, kSpanLanes, sizeof(T)) <= static_cast<int>(sizeof(SpanLds<T, W, Q, R>)),
+                "bitmap, counts and a pass's edges fit the wave's LDS");
   auto expand = [&](const NodeOut& h, bool row_bad) {
-    constexpr int E = 16;                   // elements a lane a pass
-    constexpr int V = 16 / sizeof(T);       // elements a 16-byte store
-    constexpr int G = E / V;                // stores a lane a pass
-    constexpr int kStep = E * kSpanLanes;  // elements a pass
-    __syncthreads();  // the hull written (and repaired) by every lane, the LDS read
-    const int n = static_cast<int>(a.n);
-    const int cnt = *h.count;
-    const VArr hv = dvarr_of(h);
-    const int words = (n + 31) / 32;
-    const int words4 = (words + 3) & ~3;
-    uint32_t* vbits = reinterpret_cast<uint32_t*>(&L);
-    int* wpre = reinterpret_cast<int*>(vbits + words4);
-    T* tab = reinterpret_cast<T*>(wpre + words4);
-    // (rows of one group: n <= 64 spans of kSpanMax, so the bitmap and the word counts take at
-    // most 4 KB, and the table holds thousands of edges, past the kStep a pass can need)
-    constexpr int kLdsBytes = static_cast<int>(sizeof(SpanLds<T, W, Q, R>));
-    static_assert(kLdsBytes >= 2 * (kGroup * kSpanMax / 8) + kStep * 8, "bitmap, counts and a pass's edges fit");
-    const int cap = (kLdsBytes - 2 * words4 * static_cast<int>(sizeof(uint32_t))) / static_cast<int>(sizeof(T));
-    // the bitmap (a NaN row's too: its records come from its hull as any row's)
-    for (int k = lane; k < words; k += kSpanLanes) vbits[k] = 0u;
-    __syncthreads();
-    for (int e = lane; e < cnt - 1; e += kSpanLanes) {
-      const int p = hv.idx[e];
-      atomicOr(&vbits[p >> 5], 1u << (p & 31));
-    }
-    __syncthreads();
-    // vertices before each word: lane l counts words [l * wl, l * wl + wl)
-    {
-      const int wl = (words + kSpanLanes - 1) / kSpanLanes;
-      const int k0 = min(lane * wl, words), k1 = min(k0 + wl, words);
-      int c = 0;
-      for (int k = k0; k < k1; ++k) c += __popc(vbits[k]);
-      int ex = wave_incl_i32(c) - c;
-      for (int k = k0; k < k1; ++k) {
-        wpre[k] = ex;
-        ex += __popc(vbits[k]);
-      }
-    }
-    __syncthreads();
-    // vertices at positions below i (i < n)
-    auto below = [&](int i) { return wpre[i >> 5] + __popc(vbits[i >> 5] & ((1u << (i & 31)) - 1u)); };
-    // the start bits (a NaN row: its first element only)
-    if (a.starts != nullptr)
-      for (int k = lane; k < words; k += kSpanLanes)
-        a.starts[row * words + k] = row_bad ? (k == 0 ? 1u : 0u) : vbits[k];
-    // tile records: ra, the last vertex at or before the tile's first element; rb, the first at
-    // or after its end (the row's end vertex, cnt - 1, for the last tile)
-    for (int64_t t = lane; t < a.tpr; t += kSpanLanes) {
-      const int ta = static_cast<int>(t * a.tile_n);
-      const int tb = min(ta + a.tile_n, n);
-      const bool at_vertex = (vbits[ta >> 5] >> (ta & 31)) & 1u;
-      TileRec r;
-      r.ra = below(ta) + (at_vertex ? 1 : 0) - 1;
-      r.rb = tb == n ? cnt - 1 : below(tb);
-      r.last = cnt - 1;
-      const bool head = row_bad ? ta == 0 : at_vertex;
-      r.flags = (row_bad ? kTileBad : 0) | (head ? kTileHead : 0);
-      r.slope = 0.0;
-      r.unused = 0.0;
-      if (!row_bad && r.rb == r.ra + 1) {
-        double dW, dS;
-        vdiff<W>(vload<W>(hv, r.ra), vload<W>(hv, r.ra + 1), dW, dS);
-        r.slope = slope_div(dS, dW);
-      }
-      a.tiles[row * a.tpr + t] = r;
-    }
-    // the fit (ragged rows: the row's own elements, at their packed place; the row's, not the
-    // lane's span's mapping, which an idle lane takes from row 0)
-    int64_t xfirst = row * a.n, xlen = a.n;
-    if constexpr (MAP) map_row(a.map, row, a.n, xfirst, xlen);
-    T* const out = static_cast<T*>(a.out) + xfirst;
-    const int lim = static_cast<int>(xlen);
-    if (row_bad) {
-      const T nanv = quiet_nan<T>();
-      for (int i = lane; i < lim; i += kSpanLanes) out[i] = nanv;
-      return;
-    }
-    const T tsgn = static_cast<T>(sgn);
-    const bool use_lo = a.flags & TI_CLIP_MIN, use_hi = a.flags & TI_CLIP_MAX;
-    const T lo = static_cast<T>(a.lo), hi = static_cast<T>(a.hi);
-    auto stage = [&](int e0) {  // edges [e0, e0 + cap) of the row's cnt - 1
-      const int e1 = min(cnt - 1, e0 + cap);
-      for (int e = e0 + lane; e < e1; e += kSpanLanes) {
-        double dW, dS;
-        vdiff<W>(vload<W>(hv, e), vload<W>(hv, e + 1), dW, dS);
-        tab[e - e0] = clip(tsgn * static_cast<T>(slope_div(dS, dW)), use_lo, lo, use_hi, hi);
-      }
-    };
-    int e0 = 0;
-    stage(0);
-    __syncthreads();
-    const bool aligned = (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-    for (int c = 0; c < n; c += kStep) {
-      if (cnt - 1 > cap) {
-        // the pass's edges: from its first element's, f, to at most f + kStep - 1 (and cnt - 2);
-        // the table restaged from f where it ends short of them
-        const int f = below(c) + static_cast<int>((vbits[c >> 5] >> (c & 31)) & 1u) - 1;
-        if (min(f + kStep, cnt - 1) > e0 + cap) {
-          __syncthreads();
-          e0 = f;
-          stage(e0);
-          __syncthreads();
-        }
-      }
-      // G stores of 16 bytes a lane, each store instruction of the wave on 64 consecutive
-      // 16-byte pieces (V elements each, of one bitmap word: c is a multiple of kStep); every
-      // group's bitmap word and count read at once, then every element's table entry (a group
-      // past n reads the pass's first element's, in the table, and stores nothing)
-      int g0[G];
-      uint32_t wb[G];
-      int cum[G];
-#pragma unroll
-      for (int j = 0; j < G; ++j) {
-        g0[j] = c + j * (kSpanLanes * V) + lane * V;
-        const int ii = g0[j] < n ? g0[j] : c;
-        wb[j] = vbits[ii >> 5] >> (ii & 31);
-        cum[j] = wpre[ii >> 5] + __popc(vbits[ii >> 5] & ((1u << (ii & 31)) - 1u));
-      }
-      T fit[G][V];
-#pragma unroll
-      for (int j = 0; j < G; ++j) {
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-          cum[j] += (wb[j] >> k) & 1u;  // (zero past n: the last edge again)
-          fit[j][k] = tab[cum[j] - 1 - e0];
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < G; ++j) {
-        const int m = lim - g0[j];
-        if (m >= V && aligned) {
-          using VT = T __attribute__((ext_vector_type(V)));
-          VT x;
-#pragma unroll
-          for (int k = 0; k < V; ++k) x[k] = fit[j][k];
-          *reinterpret_cast<VT*>(out + g0[j]) = x;
-        } else {
-#pragma unroll
-          for (int k = 0; k < V; ++k)
-            if (k < m) out[g0[j] + k] = fit[j][k];
-        }
-      }
-    }
+    RowExpand x = a.xp;
+    x.lds_bytes = static_cast<int>(sizeof(L));
+    expand_row<T, W, MAP, kSpanLanes>(x, h, row_bad, row, reinterpret_cast<char*>(&L));
   };
 
   // The group's merge (the first merge level), in the wave's own LDS when the spans' hulls fit:
@@ -783,13 +636,17 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
   a.map = t.map;
   a.fix = fix;
   a.expand = tiles != nullptr;
-  a.out = t.out;
-  a.starts = t.starts;
-  a.tiles = tiles;
-  a.tile_n = static_cast<int>(tile_elems(t.w != nullptr));
-  a.tpr = (t.n + a.tile_n - 1) / a.tile_n;
-  a.lo = t.lo;
-  a.hi = t.hi;
+  a.xp.n = t.n;
+  a.xp.out = t.out;
+  a.xp.starts = t.starts;
+  a.xp.tiles = tiles;
+  a.xp.tile_n = static_cast<int>(tile_elems(t.w != nullptr));
+  a.xp.tpr = (t.n + a.xp.tile_n - 1) / a.xp.tile_n;
+  a.xp.flags = t.flags;
+  a.xp.lo = t.lo;
+  a.xp.hi = t.hi;
+  a.xp.map = t.map;
+  a.xp.lds_bytes = 0;  // (the kernel's: its wave's LDS)
   // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
   // rows_per_wave of them)
   const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes
