@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define TI_ABI_VERSION 9
+#define TI_ABI_VERSION 10
 
 /* dtype codes */
 #define TI_F32 0
@@ -205,6 +205,21 @@ int ti_fwd_ev_hulls(const void* y, const void* w, void* out, uint32_t* starts, u
                     int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
                     void* workspace, size_t workspace_bytes, void* stream, void* weights_read,
                     void* hulls_ready, int64_t* max_vertices);
+
+/*
+ * ti_fwd_ev_hulls with no event between the fit's kernels: a kernel of one thread writes
+ * mark_value to *weights_mark (a device-visible word of host memory, or NULL) once every weight
+ * has been read and *bad_weight is final, and *max_vertices (likewise host memory, or NULL; rows of
+ * more than 32 elements only) is written once the bound is known, both with stores that reach host
+ * memory directly. A caller that sets both words to values the call will not write polls them
+ * instead of waiting on events: an event recorded between two kernels leaves the GPU idle for some
+ * microseconds. No counterpart in the reference (its weight check is a synchronous read of w
+ * before the fit, reference _api.py:60-61).
+ */
+int ti_fwd_marked(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                  int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+                  void* workspace, size_t workspace_bytes, void* stream, uint32_t* weights_mark,
+                  uint32_t mark_value, int64_t* max_vertices);
 
 /* Bytes of the kept buffer for final hulls of at most max_vertices vertices (0 for rows of at
  * most 32 elements, which keep nothing). */

@@ -23,7 +23,7 @@ from torch import Tensor
 
 LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd.so"
 OPS_LIB_PATH = Path(__file__).resolve().parent / "libtorchisotonic_amd_ops.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 RAGGED_PLAN_WORDS = 132  # (ti_ragged_plan)
 
 F32, F64 = 0, 1
@@ -55,6 +55,7 @@ SYMBOLS = (
     "ti_bwd_workspace",
     "ti_bwd",
     "ti_fwd_ev_hulls",
+    "ti_fwd_marked",
     "ti_keep_bytes",
     "ti_keep",
     "ti_bwd_kept_workspace",
@@ -119,6 +120,8 @@ def load() -> ctypes.CDLL:
     lib.ti_bwd.argtypes = [_vp, _vp, _sz] + [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp]
     lib.ti_fwd_ev_hulls.restype = _int
     lib.ti_fwd_ev_hulls.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp, _vp, _vp]
+    lib.ti_fwd_marked.restype = _int
+    lib.ti_fwd_marked.argtypes = [_vp] * 5 + [_i64, _i64, _int, _uint, _dbl, _dbl, _vp, _sz, _vp, _vp, _uint, _vp]
     lib.ti_keep_bytes.restype = _int
     lib.ti_keep_bytes.argtypes = [_i64, _i64, _int, _int, _i64, ctypes.POINTER(_sz)]
     lib.ti_keep.restype = _int

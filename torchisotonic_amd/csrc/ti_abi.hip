@@ -57,6 +57,11 @@ __global__ void starts_to_bool_kernel(const uint32_t* __restrict__ starts, uint8
   }
 }
 
+// The call's mark (see ti::mark_run): a system-scope store, which goes to host memory directly.
+__global__ __launch_bounds__(64) void mark_kernel(uint32_t* word, uint32_t v) {
+  if (threadIdx.x == 0) __hip_atomic_store(word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Sets *bad to 1 if any of w[0, count) is not positive (or is NaN). A lane that finds one
 // stores the word itself.
 template <typename T>
@@ -107,6 +112,13 @@ int scratch_ptr(void** out) {
 
 }  // namespace
 
+namespace ti {
+hipError_t mark_run(uint32_t* word, uint32_t v, hipStream_t stream) {
+  mark_kernel<<<dim3(1), dim3(64), 0, stream>>>(word, v);
+  return hipGetLastError();
+}
+}  // namespace ti
+
 extern "C" {
 
 int ti_abi_version(void) { return TI_ABI_VERSION; }
@@ -152,11 +164,13 @@ namespace {
 int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
              int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
              void* workspace, size_t workspace_bytes, void* stream, hipEvent_t weights_read,
-             hipEvent_t hulls_ready = nullptr, int64_t* max_vertices = nullptr, const ti::RowMap* map = nullptr) {
+             hipEvent_t hulls_ready = nullptr, int64_t* max_vertices = nullptr, const ti::RowMap* map = nullptr,
+             uint32_t* weights_mark = nullptr, uint32_t mark_value = 0) {
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   // the one-kernel paths read the weights in their only kernel (and have no hulls to keep)
   auto then_record = [&](int rc) -> int {
     if (rc == TI_OK && weights_read != nullptr) rc = launched(hipEventRecord(weights_read, hs), "weights-read event");
+    if (rc == TI_OK && weights_mark != nullptr) rc = launched(ti::mark_run(weights_mark, mark_value, hs), "weights mark");
     if (rc == TI_OK && hulls_ready != nullptr) rc = launched(hipEventRecord(hulls_ready, hs), "hulls-ready event");
     return rc;
   };
@@ -164,7 +178,8 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
   if (batch == 0) return then_record(ok());
   if (y == nullptr || out == nullptr) return fail(TI_EINVAL, "y and out must not be null");
   if (out == y || (w != nullptr && out == w)) return fail(TI_EINVAL, "out must not alias y or w");
-  if (weights_read != nullptr && w != nullptr && bad_weight != nullptr && batch * n <= kEarlyCheckElems) {
+  if ((weights_read != nullptr || weights_mark != nullptr) && w != nullptr && bad_weight != nullptr &&
+      batch * n <= kEarlyCheckElems) {
     const int64_t count = batch * n;
     const unsigned blocks = static_cast<unsigned>((count + 1023) / 1024 < 2048 ? (count + 1023) / 1024 : 2048);
     if (dtype == TI_F32)
@@ -172,9 +187,13 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
     else
       check_weights_kernel<double><<<dim3(blocks), dim3(256), 0, hs>>>(static_cast<const double*>(w), count, bad_weight);
     if (int rc = launched(hipGetLastError(), "weight check")) return rc;
-    if (int rc = launched(hipEventRecord(weights_read, hs), "weights-read event")) return rc;
+    if (weights_read != nullptr)
+      if (int rc = launched(hipEventRecord(weights_read, hs), "weights-read event")) return rc;
+    if (weights_mark != nullptr)
+      if (int rc = launched(ti::mark_run(weights_mark, mark_value, hs), "weights mark")) return rc;
     bad_weight = nullptr;  // (checked: the fit need not)
     weights_read = nullptr;
+    weights_mark = nullptr;
   }
   if (n <= ti::kShortMax) {
     if (map != nullptr) return fail(TI_EINVAL, "ragged rows of a block need a block longer than 32");
@@ -189,6 +208,8 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
   if (batch * plan.tiles_per_row > 0x7FFFFFFF) return fail(TI_ESIZE, "too many tiles");
   ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
   a.weights_read = weights_read;  // after the span kernel, the first of several
+  a.weights_mark = weights_mark;  // likewise
+  a.mark_value = mark_value;
   a.hulls_ready = hulls_ready;    // after the merges
   a.max_vertices = max_vertices;
   if (map != nullptr) a.map = *map;
@@ -339,6 +360,14 @@ int ti_fwd_ev_hulls(const void* y, const void* w, void* out, uint32_t* starts, u
   return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, workspace,
                   workspace_bytes, stream, static_cast<hipEvent_t>(weights_read),
                   static_cast<hipEvent_t>(hulls_ready), max_vertices);
+}
+
+int ti_fwd_marked(const void* y, const void* w, void* out, uint32_t* starts, uint32_t* bad_weight,
+                  int64_t batch, int64_t n, int dtype, unsigned flags, double y_min, double y_max,
+                  void* workspace, size_t workspace_bytes, void* stream, uint32_t* weights_mark,
+                  uint32_t mark_value, int64_t* max_vertices) {
+  return fwd_impl(y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, workspace,
+                  workspace_bytes, stream, nullptr, nullptr, max_vertices, nullptr, weights_mark, mark_value);
 }
 
 int ti_keep_bytes(int64_t batch, int64_t n, int dtype, int weighted, int64_t max_vertices, size_t* bytes) {

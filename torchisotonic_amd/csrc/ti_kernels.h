@@ -11,6 +11,11 @@ namespace ti {
 // Rows up to this length take the short-row kernels (one thread per row).
 constexpr int64_t kShortMax = 32;
 
+// v written to *word (a word of host memory the host polls) by a kernel of one thread, with a
+// store that reaches host memory directly: the stream's earlier kernels have finished by then, so
+// whatever they wrote to host memory (a weight flag) is there before it.
+hipError_t mark_run(uint32_t* word, uint32_t v, hipStream_t stream);
+
 struct ShortArgs {
   const void* y;
   const void* w;  // null: unweighted

@@ -637,8 +637,9 @@ __global__ __launch_bounds__(256) void maxc_rows_kernel(const int* __restrict__ 
   const int sub = threadIdx.x & (P - 1);
   const int64_t rows_per_wg = 256 >> lg_p;
   int64_t v = 0;
-  // (four stretches of rows at a time, their loads in flight together)
-  constexpr int U = 4;
+  // (sixteen stretches of rows at a time, their loads in flight together: a thousand rows of a
+  // few groups in one memory round trip)
+  constexpr int U = 16;
   for (int64_t r0 = blockIdx.x * rows_per_wg; r0 < batch; r0 += U * rows_per_wg * gridDim.x) {
     int64_t t[U];
 #pragma unroll
@@ -656,8 +657,9 @@ __global__ __launch_bounds__(256) void maxc_rows_kernel(const int* __restrict__ 
     }
   }
   const int64_t m = block_max_i64(v, sh);
+  // (a store that goes to host memory directly where out is there: its caller may poll it)
   if (threadIdx.x == 0) {
-    if (gridDim.x == 1) *out = m < cap ? m : cap;
+    if (gridDim.x == 1) __hip_atomic_store(out, m < cap ? m : cap, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     else partial[blockIdx.x] = m;
   }
 }
@@ -668,7 +670,7 @@ __global__ __launch_bounds__(256) void maxc_final_kernel(const int64_t* __restri
   int64_t v = 0;
   for (int k = threadIdx.x; k < parts; k += 256) v = partial[k] > v ? partial[k] : v;
   const int64_t m = block_max_i64(v, sh);
-  if (threadIdx.x == 0) *out = m < cap ? m : cap;
+  if (threadIdx.x == 0) __hip_atomic_store(out, m < cap ? m : cap, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // The first hull_blocks workgroups: cpr of them a row, 256 slots each, the row's final hull
@@ -877,6 +879,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
+  if (t.weights_mark != nullptr && (e = mark_run(t.weights_mark, t.mark_value, t.stream)) != hipSuccess) return e;
   // for a caller that keeps only the final hulls: a bound on their vertex counts, from the
   // counts of level keep_level once it is merged
   auto report = [&](int l) -> hipError_t {

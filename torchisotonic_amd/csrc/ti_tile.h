@@ -64,6 +64,10 @@ struct TileArgs {
   double lo, hi;
   hipStream_t stream;
   hipEvent_t weights_read = nullptr;  // recorded once every weight has been read, if given
+  // Where given: mark_value written to *weights_mark (a word of host memory that the host polls)
+  // once every weight has been read, by a kernel of one thread, with no event between kernels
+  uint32_t* weights_mark = nullptr;
+  uint32_t mark_value = 0;
   // Where given (rows over 32 elements): a bound on the final hulls' vertex counts (at least the
   // largest, at most n + 1) is written here (a device-visible word) and hulls_ready recorded once
   // it is, before the last merges and the expansion run.

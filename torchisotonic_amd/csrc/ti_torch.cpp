@@ -20,6 +20,8 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <chrono>
+#include <cstring>
 #include <limits>
 #include <optional>
 #include <vector>
@@ -60,35 +62,53 @@ at::Tensor workspace(bool fwd, int64_t batch, int64_t n, int dtype, bool weighte
   return at::empty({static_cast<int64_t>(bytes)}, at::TensorOptions().dtype(at::kByte).device(dev));
 }
 
-// Per thread and device: the event a weighted fit records once it has read every weight, and
-// the weight flag itself in pinned host memory, which the kernels write through the fabric. The
-// host waits for that event only (the first of a long row's kernels) and reads the flag while
-// the rest of the fit still runs on the stream. Likewise the event a long-row fit records once
-// its final hulls are merged, with their largest vertex count (a second pinned word), for a
-// node that keeps those hulls instead of the workspace. (Kept until the process ends.)
+// Per thread and device, in coherent pinned host memory (the kernels' stores reach it directly):
+// the weight flag; the mark a weighted fit writes once it has read every weight (ti_fwd_marked:
+// a kernel of one thread after the first of a long row's kernels), which the host polls before
+// it reads the flag, while the rest of the fit still runs on the stream; and the final hulls'
+// largest vertex count, which a long-row fit writes once they are merged and which the host
+// polls for a node that keeps those hulls instead of the workspace. Polled words, not events: an
+// event recorded between two kernels leaves the GPU idle for about 6 us. (Kept until the
+// process ends.)
 struct WeightCheck {
-  hipEvent_t event = nullptr;
   uint32_t* host = nullptr;  // the host's view of the flag
   uint32_t* dev = nullptr;   // the kernels' view
-  hipEvent_t hulls = nullptr;
+  uint32_t* mark_host = nullptr;
+  uint32_t* mark_dev = nullptr;
+  uint32_t mark = 0;             // the last call's mark
   int64_t* maxv_host = nullptr;  // the final hulls' largest vertex count
   int64_t* maxv_dev = nullptr;
 };
+
+// Polls until done(); where a second passes first (a fit that never writes its word), waits for
+// the stream instead.
+template <class Done>
+void poll_until(Done done, hipStream_t stream) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (unsigned it = 0;; ++it) {
+    if (done()) return;
+    if ((it & 4095) == 4095 && std::chrono::steady_clock::now() - t0 > std::chrono::seconds(1)) {
+      check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize");
+      return;
+    }
+  }
+}
 
 WeightCheck& weight_check(c10::DeviceIndex dev) {
   thread_local WeightCheck per_device[64];
   TORCH_CHECK(dev >= 0 && dev < 64, "torchisotonic_amd: device index ", static_cast<int>(dev), " out of range");
   WeightCheck& wc = per_device[dev];
-  if (wc.event == nullptr) {
-    check_hip(hipEventCreateWithFlags(&wc.event, hipEventDisableTiming), "hipEventCreateWithFlags");
-    check_hip(hipEventCreateWithFlags(&wc.hulls, hipEventDisableTiming), "hipEventCreateWithFlags");
+  if (wc.host == nullptr) {
     void* p = nullptr;
-    check_hip(hipHostMalloc(&p, 16, hipHostMallocDefault), "hipHostMalloc");
-    wc.host = static_cast<uint32_t*>(p);
-    wc.maxv_host = reinterpret_cast<int64_t*>(static_cast<char*>(p) + 8);
+    check_hip(hipHostMalloc(&p, 16, hipHostMallocCoherent), "hipHostMalloc");
+    std::memset(p, 0, 16);  // (marks start at 1)
     void* d = nullptr;
     check_hip(hipHostGetDevicePointer(&d, p, 0), "hipHostGetDevicePointer");
+    wc.host = static_cast<uint32_t*>(p);
+    wc.mark_host = static_cast<uint32_t*>(p) + 1;
+    wc.maxv_host = reinterpret_cast<int64_t*>(static_cast<char*>(p) + 8);
     wc.dev = static_cast<uint32_t*>(d);
+    wc.mark_dev = static_cast<uint32_t*>(d) + 1;
     wc.maxv_dev = reinterpret_cast<int64_t*>(static_cast<char*>(d) + 8);
   }
   return wc;
@@ -136,19 +156,22 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
     } else {
       WeightCheck& wc = weight_check(yc.device().index());
       // (the previous call on this thread had read every weight, and its hull count, before it
-      // returned, so nothing still running writes the words)
+      // returned, so nothing still running writes the flag or the count; a mark it wrote late
+      // would be its own, not this call's)
       *static_cast<volatile uint32_t*>(wc.host) = 0u;
       *static_cast<volatile int64_t*>(wc.maxv_host) = 0;
-      // keeping the hulls: one wait, for the hulls (the weights were read before them)
-      check(ti_fwd_ev_hulls(ptr(yc), ptr(w), ptr(out), static_cast<uint32_t*>(ptr(starts)),
-                            w.defined() ? wc.dev : nullptr, batch, n, dtype, fit_flags, lo, hi, ptr(ws), ws_bytes, stream,
-                            keep ? nullptr : wc.event, keep ? wc.hulls : nullptr, keep ? wc.maxv_dev : nullptr),
+      const uint32_t mark = ++wc.mark == 0 ? ++wc.mark : wc.mark;
+      // keeping the hulls: one wait, for the hull count (the weights were read before it)
+      check(ti_fwd_marked(ptr(yc), ptr(w), ptr(out), static_cast<uint32_t*>(ptr(starts)),
+                          w.defined() ? wc.dev : nullptr, batch, n, dtype, fit_flags, lo, hi, ptr(ws), ws_bytes, stream,
+                          keep ? nullptr : wc.mark_dev, mark, keep ? wc.maxv_dev : nullptr),
             "fit");
-      check_hip(hipEventSynchronize(keep ? wc.hulls : wc.event), "hipEventSynchronize");
+      if (keep) poll_until([&] { return *static_cast<volatile int64_t*>(wc.maxv_host) != 0; }, stream);
+      else poll_until([&] { return *static_cast<volatile uint32_t*>(wc.mark_host) == mark; }, stream);
       TORCH_CHECK_VALUE(!w.defined() || *static_cast<volatile uint32_t*>(wc.host) == 0u,
                         "weight must be strictly positive");
       const int64_t mv = keep ? *static_cast<volatile int64_t*>(wc.maxv_host) : 0;
-      // (a bound not written, which the event's system-scope release rules out: keep the workspace)
+      // (a bound not written, after the stream's wait: keep the workspace)
       if (mv >= 1) {
         size_t kbytes = 0;
         check(ti_keep_bytes(batch, n, dtype, w.defined() ? 1 : 0, mv, &kbytes), "keep_bytes");
