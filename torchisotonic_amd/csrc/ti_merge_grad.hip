@@ -104,18 +104,6 @@ __device__ __forceinline__ uint32_t tile_bits(const uint32_t* srow, int x, int E
   return (srow[x >> 5] >> (x & 31)) & mask;
 }
 
-// Sum over a 256-thread workgroup (double-double), for every thread.
-__device__ DD block_sum_dd(DD v, DD* wave_tot) {
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  v = wave_last_dd(wave_incl_dd(v));
-  if (lane == 0) wave_tot[wave] = v;
-  __syncthreads();
-  DD t = wave_tot[0];
-  for (int w2 = 1; w2 < kWaves256; ++w2) t = dd_add(t, wave_tot[w2]);
-  __syncthreads();  // wave_tot is reused
-  return t;
-}
-
 // A tile's total of g; for rows of one tile also the scans' results (no scan kernel runs then):
 // the tile's prefix within its group and the group's within the row are 0, the row total is
 // the tile's.
