@@ -200,6 +200,17 @@ __device__ __forceinline__ int wave_incl_i32(int v) {
   return v;
 }
 
+// The same in float64.
+__device__ __forceinline__ double wave_incl_f64(double v) {
+  v = dpp_f64<0x111, 0xF>(v) + v;
+  v = dpp_f64<0x112, 0xF>(v) + v;
+  v = dpp_f64<0x114, 0xF>(v) + v;
+  v = dpp_f64<0x118, 0xF>(v) + v;
+  v = dpp_f64<0x142, 0xA>(v) + v;
+  v = dpp_f64<0x143, 0xC>(v) + v;
+  return v;
+}
+
 // The same in double-double, each step adding the lower lanes' part on the left.
 __device__ __forceinline__ DD wave_incl_dd(DD v) {
   v = dd_add(dpp_dd<0x111, 0xF>(v), v);

@@ -126,8 +126,37 @@ constexpr int kGsumTiles = 2;
 // Over a 256-thread workgroup, one barrier: the exclusive scan of v (double-double) and of c
 // (an int), and v's total. wave_tot and wave_cnt are this call's own (no later call in the
 // kernel writes them, so no barrier follows).
+// PR false (float32 g): v.hi alone, scanned in float64, the results' lo parts zero. A tile's
+// 2048 sums then carry a relative error near 2^-42, far below float32's 2^-24 (the reference
+// sums its tiles in float64 too, grad.cuh:187-190); the scans across a row's tiles stay
+// double-double.
+template <bool PR>
 __device__ __forceinline__ DD block_scan2(DD v, int c, DD* wave_tot, int* wave_cnt, DD& total, int& cbefore) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  if constexpr (!PR) {
+    const double inc = wave_incl_f64(v.hi);
+    const int cinc = wave_incl_i32(c);
+    const double exc = dpp_f64<0x138, 0xF>(inc);
+    if (lane == kWave - 1) {
+      wave_tot[wave] = DD{inc, 0.0};
+      wave_cnt[wave] = cinc;
+    }
+    __syncthreads();
+    double pre = 0.0, tot = 0.0;
+    int cpre = 0;
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves256; ++w2) {
+      const double t = wave_tot[w2].hi;
+      if (w2 < wave) {
+        pre += t;
+        cpre += wave_cnt[w2];
+      }
+      tot += t;
+    }
+    cbefore = cpre + cinc - c;
+    total = DD{tot, 0.0};
+    return DD{pre + exc, 0.0};
+  }
   const DD inc = wave_incl_dd(v);
   const int cinc = wave_incl_i32(c);
   const DD exc = wave_shr1_dd(inc);
@@ -237,7 +266,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
       // a vertex at its first element, and on the row's last tile the row's end point
       int unused;
       DD total;
-      block_scan2(acc, 0, wtot[u], wcnt[u], total, unused);
+      block_scan2<PR>(acc, 0, wtot[u], wcnt[u], total, unused);
       if (tid == 0) {
         put_tile_total(a, gt, total);
         if (!bad) {
@@ -264,7 +293,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     const int pc = __builtin_popcount(mybits);
     DD total;
     int before;
-    const DD off = block_scan2(acc, pc, wtot[u], wcnt[u], total, before);
+    const DD off = block_scan2<PR>(acc, pc, wtot[u], wcnt[u], total, before);
     if (tid == 0) put_tile_total(a, gt, total);
     int rank = rA[u] - at_start + before;
     DD run{0.0, 0.0};
@@ -272,7 +301,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     for (int k = 0; k < E; ++k) {
       if ((mybits >> k) & 1u) {
         ++rank;
-        const DD p = dd_add(off, DD{run.hi, PR ? run.lo : 0.0});
+        const DD p = PR ? dd_add(off, run) : DD{off.hi + run.hi, 0.0};
         lv[2 * rank] = p.hi;
         lv[2 * rank + 1] = p.lo;
       }
