@@ -225,13 +225,7 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     int64_t rfirst = row * a.n, rlen = a.n;
     if constexpr (MAP) map_row(a.map, row, a.n, rfirst, rlen);
     const int lc = static_cast<int>(max<int64_t>(0, min<int64_t>(E, min<int64_t>(len, rlen - first) - t0)));
-    load_elems_any<T, E>(static_cast<const T*>(a.g) + rfirst + first + t0, lc, gv[u]);
-    if constexpr (MAP) {
-#pragma unroll
-      for (int k = 0; k < E; ++k) {
-        if (k >= lc) gv[u][k] = T(0);
-      }
-    }
+    load_elems_zero<T, E>(static_cast<const T*>(a.g) + rfirst + first + t0, lc, gv[u]);
     const TileRec rec = a.tiles[gt];
     rA[u] = rec.ra;
     rB[u] = rec.rb;
@@ -251,12 +245,11 @@ __global__ __launch_bounds__(256) void gsum_kernel(GradKArgs a) {
     const int bad = badu[u];
     double* lv = a.lv + 2 * row * a.cap_final;
     // the thread's sum; its prefixes are formed again, in the same order, where a vertex needs
-    // one (keeping them would hold E more float64 registers through the tile)
+    // one (keeping them would hold E more float64 registers through the tile); elements past
+    // the tile's or the row's end were loaded as zeros, which leave a sum as it is
     auto add = [&](DD& acc, int k) {
-      if (k < ecount) {
-        if constexpr (PR) acc = dd_add(acc, static_cast<double>(gv[u][k]));
-        else acc.hi += static_cast<double>(gv[u][k]);
-      }
+      if constexpr (PR) acc = dd_add(acc, static_cast<double>(gv[u][k]));
+      else acc.hi += static_cast<double>(gv[u][k]);
     };
     DD acc{0.0, 0.0};
 #pragma unroll

@@ -200,6 +200,27 @@ __device__ __forceinline__ void load_elems_any(const T* __restrict__ p, int coun
   }
 }
 
+// The same, the elements past count zero (so sums over all E need no per-element checks).
+template <typename T, int E>
+__device__ __forceinline__ void load_elems_zero(const T* __restrict__ p, int count, T (&v)[E]) {
+  constexpr int V = 16 / sizeof(T);
+  using VT = T __attribute__((ext_vector_type(V)));
+  if (count == E && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    const VT* q = reinterpret_cast<const VT*>(p);
+    VT buf[E / V];
+#pragma unroll
+    for (int j = 0; j < E / V; ++j) buf[j] = q[j];
+#pragma unroll
+    for (int j = 0; j < E / V; ++j) {
+#pragma unroll
+      for (int t = 0; t < V; ++t) v[j * V + t] = buf[j][t];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = k < count ? p[k] : T(0);
+  }
+}
+
 // (NTS: non-temporal 16-byte stores, whose lines leave the caches as they are written)
 template <typename T, int E, bool NTS = false>
 __device__ __forceinline__ void store_elems_any(T* __restrict__ p, int count, const T (&v)[E]) {
