@@ -191,15 +191,15 @@ def test_autograd_keeps_little_at_c4() -> None:
     assert torch.equal(gy, ry) and torch.equal(gw, rw)
 
 
-def test_autograd_keeps_the_workspace_for_monotone_rows() -> None:
-    # every element a vertex: the kept hulls would be as large as the workspace, which is kept
-    n = 10_000_000
-    say(f"autograd on a monotone weighted row of {n}")
+def _monotone_autograd(batch: int, n: int) -> tuple[int, int]:
+    # rows already increasing (every element a vertex, its own block): the fit under autograd,
+    # the memory it holds beside the fit, the workspace size, and both gradients against the
+    # oracle's
     rng = np.random.default_rng(3)
-    y = torch.from_numpy(np.cumsum(rng.random(n) + 0.01).astype(np.float64)).cuda().view(1, n)
-    w = torch.from_numpy(rng.random(n) + 0.1).cuda().view(1, n)
-    g = torch.from_numpy(rng.standard_normal(n)).cuda().view(1, n)
-    ws = _size(_ext.load().ti_fwd_workspace, 1, n, _ext.F64, 1)
+    y = torch.from_numpy(np.cumsum(rng.random((batch, n)) + 0.01, axis=1)).cuda()
+    w = torch.from_numpy(rng.random((batch, n)) + 0.1).cuda()
+    g = torch.from_numpy(rng.standard_normal((batch, n))).cuda()
+    ws = _size(_ext.load().ti_fwd_workspace, batch, n, _ext.F64, 1)
     assert ws >= 256 << 20  # (the size at which the node keeps hulls instead)
     yr, wr = y.clone().requires_grad_(), w.clone().requires_grad_()
     torch.cuda.synchronize()
@@ -207,12 +207,30 @@ def test_autograd_keeps_the_workspace_for_monotone_rows() -> None:
     fit = torchisotonic_amd.isotonic(yr, wr)
     torch.cuda.synchronize()
     held = torch.cuda.memory_allocated() - before - fit.numel() * fit.element_size()
-    assert held >= ws
     gy, gw = torch.autograd.grad(fit, (yr, wr), g)
-    # (already monotone: every element a block, its mean its own value up to rounding)
     f = fit.detach().cpu().numpy()
     assert float(np.abs(f - y.cpu().numpy()).max()) <= 1e-12 * float(y.abs().max())
-    starts = np.ones((1, n), dtype=np.uint8)
+    starts = np.ones((batch, n), dtype=np.uint8)
     ey, ew = oracle.block_grad(starts, g.cpu().numpy(), w.cpu().numpy(), y.cpu().numpy(), f, want_w=True)
     np.testing.assert_allclose(gy.cpu().numpy(), ey, rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(gw.cpu().numpy(), ew, rtol=1e-9, atol=1e-12 * float(np.abs(ey).max()))
+    return held, ws
+
+
+def test_autograd_keeps_the_workspace_for_monotone_rows() -> None:
+    # every element a vertex, in a batch whose merges fill the GPU (one vertex store): the kept
+    # hulls would be as large as the workspace, which is kept
+    say("autograd on 256 monotone weighted rows of 40000")
+    held, ws = _monotone_autograd(256, 40_000)
+    assert held >= ws
+
+
+def test_autograd_keeps_hulls_for_a_monotone_row() -> None:
+    # one row: its upper merge levels write into a second vertex store, so the hulls, every
+    # element a vertex, take half the workspace and are kept in its place
+    n = 10_000_000
+    say(f"autograd on a monotone weighted row of {n}")
+    held, ws = _monotone_autograd(1, n)
+    kb = ctypes.c_size_t(0)
+    assert _ext.load().ti_keep_bytes(1, n, _ext.F64, 1, n + 1, ctypes.byref(kb)) == 0
+    assert kb.value <= held < ws

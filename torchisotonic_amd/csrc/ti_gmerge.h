@@ -302,9 +302,11 @@ __device__ __forceinline__ HPt child_vertex(const MergeArgs& a, const MergeSmall
 // end to end never take a slot above their vertex's own, so no write lands on a vertex still
 // to be read. (Copying the children end to end and moving each right part's survivors down,
 // round after round, moved every vertex several times through one workgroup.)
-template <bool W, bool PR, int NT>
+// DF (parents whose hull lies in the other store than their children's): more than kDeferMin
+// survivors are left to survivors_kernel, their ranges and offsets in *tab.
+template <bool W, bool PR, int NT, bool DF = false>
 __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int* rlo, int* rhi, int* pre, int64_t row,
-                             int64_t c0, int nch, const NodeOut& pout) {
+                             int64_t c0, int nch, const NodeOut& pout, DeferTab* tab = nullptr) {
   const int tid = threadIdx.x;
   const VArr v = dvarr_of(pout);
   for (int c = tid; c < nch; c += NT) {
@@ -389,10 +391,24 @@ __device__ void merge_global(const MergeArgs& a, MergeSmall& sm, int* rlo, int* 
     sm.total = t;
   }
   __syncthreads();
+  const int total = sm.total;
+  if (DF && total > kDeferMin) {
+    for (int c = tid; c < nch; c += NT) {
+      tab->rlo[c] = rlo[c];
+      tab->pre[c] = pre[c];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tab->tot[q][c] = sm.tot[q][c];
+    }
+    if (tid == 0) {
+      tab->total = total;
+      tab->deferred = 1;
+      *pout.count = total;
+    }
+    return;
+  }
   // Batches of NT * B slots: batch k's slots lie below every source of batch k + 1 (a survivor's
   // slot is never above its vertex's own), so batch k + 1 is read while batch k is written; a
   // batch is read by every thread (the barrier) before any of its slots is written.
-  const int total = sm.total;
   constexpr int B = (W || PR) ? 4 : 8;
   auto load = [&](int s0, VPt (&p)[B]) {
 #pragma unroll

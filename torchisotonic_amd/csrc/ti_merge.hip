@@ -186,12 +186,14 @@ constexpr size_t repair_lds_bytes(int nt) { return (nt + 2) * sizeof(VPt) + (nt 
 // TX (float or double: the fit's type) with the final level of rows enough to fill the GPU: the
 // workgroup then expands its row's final hull too (expand_row, with x.lds_bytes of its dynamic
 // LDS), in place of the rank and expansion launches.
-template <bool W, bool PR, int NT, int G, typename TX = void>
-__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int fix, RowExpand x) {
+// DF: a deferring level, tab its parents' DeferTabs (see merge_global).
+template <bool W, bool PR, int NT, int G, typename TX = void, bool DF = false>
+__global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int fix, RowExpand x, DeferTab* tab) {
   __shared__ MergeSmall sm;
   __shared__ MergeRounds rs;
   extern __shared__ __align__(16) char lds_dyn[];
   const int tid = threadIdx.x;
+  if (DF && tid == 0) tab[blockIdx.x].deferred = 0;
   const int64_t row = blockIdx.x / a.out.npr;
   const int64_t j = blockIdx.x - row * a.out.npr;
   const int64_t c0 = j * kGroup;  // first child within the row
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int
     merge_lds<W, PR, NT, G>(a, sm, rs, slots_carve<W, PR>(lds_dyn, cap_lds), row, c0, nch, pout);
   } else {
     __shared__ MergeRanges mr;
-    merge_global<W, PR, NT>(a, sm, mr.rlo, mr.rhi, mr.pre, row, c0, nch, pout);
+    merge_global<W, PR, NT, DF>(a, sm, mr.rlo, mr.rhi, mr.pre, row, c0, nch, pout, DF ? tab + blockIdx.x : nullptr);
   }
   if (tid == 0) {
     *pout.bad = sm.bad;
@@ -256,6 +258,72 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int
     repair_row<W, NT>(pout, tile, wcount, wcount[NT / kWave], fix - 1);
   }
   if constexpr (!std::is_void_v<TX>) expand_row<TX, W, false, NT>(x, pout, sm.bad != 0, row, lds_dyn);
+}
+
+// The survivors of a deferring level's parents that merge_global left to it (their children's
+// kept ranges and offsets in each parent's DeferTab), written into the parents' arrays, which
+// lie in the other store than the children's: per_parent workgroups a parent, each a stretch of
+// its slots, in no order (no slot of the parent's array is a source). A slot's vertex is the
+// kept vertex of the last child whose survivors start at or before it, its coordinates rebased
+// into the parent's as the merge's own pass does (child_vertex); four slots a thread at a time,
+// their loads in flight together.
+constexpr int64_t kSurvivorBlocks = 2048;
+
+template <bool W, bool PR>
+__global__ __launch_bounds__(256) void survivors_kernel(MergeArgs a, const DeferTab* __restrict__ tab,
+                                                        int per_parent) {
+  constexpr int NT = 256, U = 4;
+  __shared__ MergeSmall sm;  // (its tot only: child_vertex's offsets)
+  __shared__ int rlo[kGroup], pre[kGroup];
+  const int tid = threadIdx.x;
+  const int64_t parent = blockIdx.x / per_parent;
+  const int part = static_cast<int>(blockIdx.x - parent * per_parent);
+  const DeferTab* tp = tab + parent;
+  const int64_t row = parent / a.out.npr;
+  const int64_t c0 = (parent - row * a.out.npr) * kGroup;
+  const int nch = static_cast<int>(min<int64_t>(kGroup, a.in.npr - c0));
+  // (the flag, the count and the table in one round trip: a parent the merge finished, the
+  // common case, costs its workgroups no more)
+  const int deferred = tp->deferred;
+  const int64_t total = tp->total;
+  for (int c = tid; c < nch; c += NT) {
+    rlo[c] = tp->rlo[c];
+    pre[c] = tp->pre[c];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sm.tot[q][c] = tp->tot[q][c];
+  }
+  if (deferred == 0) return;
+  __syncthreads();
+  const int64_t chunk = ((total + per_parent - 1) / per_parent + NT * U - 1) / (NT * U) * (NT * U);
+  const int s_end = static_cast<int>(min<int64_t>(total, (part + 1) * chunk));
+  const VArr v = dvarr_of(node_out(a.out, W, parent));
+  for (int s0 = static_cast<int>(min<int64_t>(total, part * chunk)); s0 < s_end; s0 += NT * U) {
+    HPt h[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u * NT + tid;
+      if (s < s_end) {
+        int lo = 0, hi = nch - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (pre[mid] <= s) lo = mid;
+          else hi = mid - 1;
+        }
+        h[u] = child_vertex<W, PR>(a, sm, row, c0, lo, rlo[lo] + (s - pre[lo]));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u * NT + tid;
+      if (s < s_end) {
+        VPt p;
+        p.i = h[u].i;
+        p.s = DD{h[u].s, h[u].sl};
+        p.w = W ? DD{h[u].w, h[u].wl} : DD{static_cast<double>(h[u].i), 0.0};
+        vstore<W>(v, s, p);
+      }
+    }
+  }
 }
 
 // Per expansion tile of tile_n elements (one thread each): the final hull's last vertex at or
@@ -812,8 +880,20 @@ LongPlan long_plan(int64_t batch, int64_t n, bool weighted, bool lo) {
   // allocation), but not level 0, whose counts the span kernel's fused merge overwrites
   p.keep_level = p.levels <= 1 ? p.levels : std::max(1, p.levels - 2);
   p.slots = batch * p.npr[0] * (span0 + 1);
+  bool any_defer = false, alt = false;
+  for (int l = 0; l <= p.levels; ++l) {
+    p.defer[l] = l >= 2 && batch * p.npr[l] < kDeferParents && p.span[l] >= kDeferSpan;
+    if (p.defer[l]) alt = !alt;
+    p.alt[l] = alt;
+    any_defer = any_defer || p.defer[l];
+  }
   p.off_store = off;
-  p.off_rank = p.off_store + align256(vertex_store_bytes(p.slots, weighted, lo));
+  off += align256(vertex_store_bytes(p.slots, weighted, lo));
+  p.off_store2 = off;
+  if (any_defer) off += align256(vertex_store_bytes(p.slots, weighted, lo));
+  p.off_defer = off;
+  if (any_defer) off += align256(static_cast<size_t>(kDeferParents) * sizeof(DeferTab));
+  p.off_rank = off;
   p.off_maxc = p.off_rank + align256(static_cast<size_t>(batch * p.tiles_per_row) * sizeof(TileRec));
   p.off_rflag = p.off_maxc + align256(kMaxcBlocks * sizeof(int64_t));
   p.bytes = p.off_rflag + align256(static_cast<size_t>(batch) * sizeof(unsigned));
@@ -936,42 +1016,60 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     x.lo = t.lo;
     x.hi = t.hi;
     const int tb = t.dtype == TI_F32 ? 4 : 8;
-    auto launch = [&](auto k64, auto k256, auto k1024, auto x64f, auto x256f, auto x64d, auto x256d, size_t vb) {
+    DeferTab* const tab_l = p.defer[l] ? reinterpret_cast<DeferTab*>(base + p.off_defer) : nullptr;
+    // (a deferring level has fewer than kDeferParents parents: a 256- or 1024-thread launch, DF)
+    static_assert(kDeferParents <= 1024, "a deferring level's launch has 256 or 1024 threads");
+    auto launch = [&](auto k64, auto k256, auto k1024, auto x64f, auto x256f, auto x64d, auto x256d, auto k256df,
+                      auto k1024df, size_t vb) {
       const int big = static_cast<int>((56 * 1024 / vb) & ~size_t(63));
       if (grid >= 1024) {
         const size_t lds = std::max(768 * vb, repair_lds_bytes(64));
         x.lds_bytes = static_cast<int>(lds);
         if (last_fills && static_cast<int>(lds) >= expand_lds_min(t.n, 64, tb)) {
           expanded = true;
-          if (tb == 4) x64f<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x);
-          else x64d<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x);
+          if (tb == 4) x64f<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x, tab_l);
+          else x64d<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x, tab_l);
         } else {
-          k64<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x);
+          k64<<<dim3(grid), dim3(64), lds, t.stream>>>(m, 768, fix, x, tab_l);
         }
       } else if (grid >= 64) {
         const size_t lds = std::max(big * vb, repair_lds_bytes(256));
         x.lds_bytes = static_cast<int>(lds);
         if (last_fills && static_cast<int>(lds) >= expand_lds_min(t.n, 256, tb)) {
           expanded = true;
-          if (tb == 4) x256f<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x);
-          else x256d<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x);
+          if (tb == 4) x256f<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x, tab_l);
+          else x256d<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x, tab_l);
+        } else if (tab_l != nullptr) {
+          k256df<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x, tab_l);
         } else {
-          k256<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x);
+          k256<<<dim3(grid), dim3(256), lds, t.stream>>>(m, big, fix, x, tab_l);
         }
       } else {
-        k1024<<<dim3(grid), dim3(1024), std::max(big * vb, repair_lds_bytes(1024)), t.stream>>>(m, big, fix, x);
+        const size_t lds = std::max(big * vb, repair_lds_bytes(1024));
+        if (tab_l != nullptr) k1024df<<<dim3(grid), dim3(1024), lds, t.stream>>>(m, big, fix, x, tab_l);
+        else k1024<<<dim3(grid), dim3(1024), lds, t.stream>>>(m, big, fix, x, tab_l);
       }
     };
 #define TI_MERGE_LAUNCH(Wv, PRv)                                                                            \
   launch(merge_kernel<Wv, PRv, 64, 4>, merge_kernel<Wv, PRv, 256, 2>, merge_kernel<Wv, PRv, 1024, 2>,           \
          merge_kernel<Wv, PRv, 64, 4, float>, merge_kernel<Wv, PRv, 256, 2, float>,                            \
-         merge_kernel<Wv, PRv, 64, 4, double>, merge_kernel<Wv, PRv, 256, 2, double>, slot_bytes<Wv, PRv>())
+         merge_kernel<Wv, PRv, 64, 4, double>, merge_kernel<Wv, PRv, 256, 2, double>,                           \
+         merge_kernel<Wv, PRv, 256, 2, void, true>, merge_kernel<Wv, PRv, 1024, 2, void, true>, slot_bytes<Wv, PRv>())
     // (node arrays and slots are double-double for both dtypes: see child_vertex)
     if (W) TI_MERGE_LAUNCH(true, true);
     else TI_MERGE_LAUNCH(false, true);
 #undef TI_MERGE_LAUNCH
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (tab_l != nullptr) {
+      // the deferred parents' survivors: about kSurvivorBlocks workgroups over the launch's parents
+      const int per = static_cast<int>(std::max<int64_t>(1, kSurvivorBlocks / grid));
+      const dim3 sgrid(static_cast<unsigned>(grid * per));
+      if (W) survivors_kernel<true, true><<<sgrid, dim3(256), 0, t.stream>>>(m, tab_l, per);
+      else survivors_kernel<false, true><<<sgrid, dim3(256), 0, t.stream>>>(m, tab_l, per);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     if ((e = report(l)) != hipSuccess) return e;
   }
   if (!p.lo && p.levels >= 1 && !fold && !span_fold) {

@@ -318,6 +318,24 @@ struct MergeArgs {
   int64_t child_elems;  // elements per child node
 };
 
+// Merge levels 2 and up with fewer than kDeferParents parents, each over kDeferSpan elements or
+// more (a small batch's upper levels), write their hulls into the other vertex store than their
+// children's, so that a parent's survivors need not move in order: a parent with more than
+// kDeferMin of them leaves its children's kept ranges in its DeferTab, and survivors_kernel's
+// workgroups, many a parent, write them (one workgroup moving the survivors in place took
+// about 1.1 ns a vertex: 11 ms for 1e7).
+constexpr int64_t kDeferParents = 256;
+constexpr int64_t kDeferSpan = int64_t{1} << 16;
+constexpr int kDeferMin = 4096;
+struct DeferTab {
+  int deferred;  // 1: survivors_kernel writes this parent's hull
+  int total;     // the parent's vertices
+  int unused[2];
+  int rlo[kGroup];       // child c keeps its vertices rlo[c] ..
+  int pre[kGroup];       // .. as the parent's vertices pre[c] .. (pre[c + 1] or total)
+  double tot[4][kGroup];  // child c's offsets in the parent (W hi, lo, S hi, lo)
+};
+
 // Per tile of a long row, written by rank_kernel once the row's final hull is known: the hull's
 // vertex ranks around the tile and, for the common case of one hull edge over the whole tile
 // (rb == ra + 1 on a row without NaN), that edge's slope, so that the expansion and the
@@ -356,13 +374,18 @@ struct LongPlan {
   int64_t batch;
   int64_t npr[kMaxLevels + 1], spn[kMaxLevels + 1], span[kMaxLevels + 1];
   int64_t slots;  // of the store: batch * npr[0] * (span0 + 1)
-  size_t off_meta[kMaxLevels + 1], off_store, off_rank, off_maxc, off_rflag, bytes;
+  // defer[l]: level l's merges may leave survivors to survivors_kernel (see DeferTab); alt[l]:
+  // level l's hulls lie in the second store (each deferring level writes the other store than
+  // its children's)
+  bool defer[kMaxLevels + 1], alt[kMaxLevels + 1];
+  size_t off_meta[kMaxLevels + 1], off_store, off_store2, off_defer, off_rank, off_maxc, off_rflag, bytes;
   bool weighted;
   bool lo;  // the vertex store keeps low parts (float64 data)
 
   NodeLevel level(void* ws, int l) const {
     char* base = static_cast<char*>(ws);
-    return NodeLevel{base + off_meta[l], base + off_store, batch * npr[l], npr[l], spn[l], npr[0], span0 + 1, slots, lo};
+    return NodeLevel{base + off_meta[l], base + (alt[l] ? off_store2 : off_store), batch * npr[l], npr[l], spn[l],
+                     npr[0], span0 + 1, slots, lo};
   }
 };
 
