@@ -58,6 +58,26 @@ def test_soft_rank_matches_oracle(batch: int, n: int, strength: str, dtype: torc
     np.testing.assert_allclose(dx.double().cpu().numpy(), want_dx, rtol=tol_g, atol=tol_g * scale)
 
 
+# A single row of 2^18 .. 2^20 elements is sorted padded with -inf to 2^20 + 1 (the size from
+# which the sort library's faster algorithm runs): rows at both ends of that range and one past
+# it, with many ties (the padded sort keeps their order, as the oracle's stable sort does; tied
+# entries pool into one block of the decreasing fit, so their ranks do not depend on it).
+@pytest.mark.parametrize("n", [1 << 18, 1 << 20, (1 << 20) + 1])
+def test_soft_rank_single_row_padded_sort(n: int) -> None:
+    say(f"soft rank 1x{n} with ties")
+    gen = torch.Generator().manual_seed(n)
+    x = torch.round(torch.randn(1, n, generator=gen, dtype=torch.float64) * 64) / 64
+    g = torch.randn(1, n, generator=gen, dtype=torch.float64)
+    xr = x.cuda().requires_grad_()
+    r = soft_rank(xr, 1.0)
+    (dx,) = torch.autograd.grad(r, xr, g.cuda())
+    want, _ = oracle.soft_rank(x.numpy(), 1.0, np.float64)
+    want_dx = oracle.soft_rank_vjp(x.numpy(), 1.0, g.numpy(), np.float64)
+    scale = max(float(np.abs(x.numpy()).max()), float(n))
+    np.testing.assert_allclose(r.detach().cpu().numpy(), want, rtol=0, atol=1e-12 * scale)
+    np.testing.assert_allclose(dx.cpu().numpy(), want_dx, rtol=1e-10, atol=1e-10 * float(np.abs(want_dx).max()))
+
+
 def test_soft_rank_limits_and_gradcheck() -> None:
     gen = torch.Generator().manual_seed(0)
     x = torch.randn(6, 50, generator=gen, dtype=torch.float64).cuda()
