@@ -1,7 +1,7 @@
 """Throughput of the isotonic hot path on one MI355X, against the HBM roofline, with the
 reference CPU solver timed beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3,next[,grid]] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c4,c5,c1,c3,next,hull[,grid]] [--no-cpu]
 
 Prints ONE JSON line. The headline ``value`` is BASELINE config C2: a forward
 ``torchisotonic_amd.isotonic`` of float32 y[1e6, 16] = -0.1 i + N(0, 1), unweighted,
@@ -10,7 +10,7 @@ synchronisations (Gelem/s = 1.6e7 K / seconds). ``extra`` holds the metric's oth
 forward+backward (dy), C4 (one row of 1e8, weighted 0/1 labels, integer counts) forward and
 forward+backward (dy, dw) - the other BASELINE configs (C5 bootstrap, C1, C3), and the rows
 either side of the path (``next``: C2's rows at their own lengths with offsets, soft ranks,
-calibration). With
+calibration), and hull-heavy rows (``hull``: one row of 1e8 rising with noise). With
 ``--configs ...,grid`` (not in the default run) ``extra.grid`` also times the reference's own
 README table: its (batch, n) grid and data, each call synchronised, median and best of ten.
 
@@ -281,6 +281,29 @@ def bench_c1_c3(steps: int, warmup: int) -> dict:
 # --- the rows either side of the path: ragged rows, soft ranks, calibration -------------------
 
 
+def bench_hull(steps: int, warmup: int) -> dict:
+    """Hull-heavy rows: one float32 row of 1e8 rising with noise, y = i / n + s N(0, 1) (float64,
+    rounded once to float32; seed 0), unweighted, increasing, forward through the public API,
+    for s = 1e-9 (about 3.8e7 blocks: nearly every point a hull vertex) and 1e-7 (about 1.6e7),
+    with the fit's block count. Their upper merge levels have one or two parents each, whose
+    survivors survivors_kernel writes."""
+    n = 100_000_000
+    res: dict = {}
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    for noise in (1e-9, 1e-7):
+        i = torch.arange(n, device="cuda", dtype=torch.float64)
+        y = (i / n + noise * torch.randn(n, device="cuda", dtype=torch.float64, generator=gen)).float().view(1, n)
+        del i
+        fit = torchisotonic_amd.isotonic(y)
+        blocks = int(torch.unique_consecutive(fit).numel())
+        del fit
+        r = rate(n, timed_calls(lambda y=y: torchisotonic_amd.isotonic(y), max(5, min(steps, 10)), 2), 8)
+        r["blocks"] = blocks
+        res[f"rising_1e8_noise_{noise:g}"] = r
+        del y
+    return res
+
+
 def bench_next(steps: int, warmup: int) -> dict:
     """The consumers around the fit, timed like the configs above (back-to-back calls of the
     public API between synchronisations): C2's rows at their own lengths (len ~ U{4..16}, seed 2;
@@ -542,7 +565,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c2,c4,c5,c1,c3,next")
+    ap.add_argument("--configs", default="c2,c4,c5,c1,c3,next,hull")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -573,6 +596,9 @@ def main() -> None:
     if "next" in configs:
         log("ragged rows, soft ranks, calibration ...")
         extra.update(bench_next(args.steps, args.warmup))
+    if "hull" in configs:
+        log("hull-heavy rows ...")
+        extra["hull_heavy"] = bench_hull(args.steps, args.warmup)
     if "grid" in configs:
         log("README grid ...")
         extra["grid"] = bench_grid()

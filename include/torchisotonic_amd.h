@@ -67,7 +67,9 @@ const char* ti_last_error(void);
 /* Number of 32-bit words of the starts bit array of a [batch, n] problem set. */
 int64_t ti_starts_words(int64_t batch, int64_t n);
 
-/* Bytes of device workspace ti_fwd needs for this problem set (0 when none). */
+/* Bytes of device workspace ti_fwd needs for this problem set (0 when none): rows of more than
+ * 32 elements take a vertex store of a slot per element and small arrays, and a batch whose upper
+ * merge levels have few parents (fewer than 256 rows of 1e6 elements, say) a second store. */
 int ti_fwd_workspace(int64_t batch, int64_t n, int dtype, int weighted, size_t* bytes);
 
 /* Diagnostic: the kernel geometry ti_fwd takes for rows of more than 32 elements - elements per
