@@ -514,3 +514,45 @@ def test_rows_expanded_by_their_last_merge(batch: int, n: int, dtype: type, weig
     np.testing.assert_allclose(gs[0][ok], ey, rtol=tol, atol=tol)
     if w is not None:
         np.testing.assert_allclose(gs[1][ok], ew, rtol=tol, atol=tol * (1 + float(np.nanmax(np.abs(y)))))
+
+
+# Six rows of 300000 elements: spans of 32, so the second merge level has three parents a row,
+# each over 131072 elements (18 in the batch), and the third one a row (6): both levels write
+# their hulls into the other vertex store than their children's, the second store and then the
+# first again. Rows with a vertex at every element (0, 3) have parents of more than 4096
+# survivors, which survivors_kernel writes; a near-monotone row with drops (2) some of either;
+# noisy rows (1, 5) only parents that write their own; row 4 holds a NaN. Fit, start bits and
+# both gradients against the oracle, increasing, and decreasing with clamps.
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_deferred_survivors_mixed_rows(dtype: type, weighted: bool) -> None:
+    from torchisotonic_amd import _ext
+
+    batch, n = 6, 300_000
+    print(f"deferred survivors batch={batch} n={n} dtype={np.dtype(dtype).name} weighted={weighted}", flush=True)
+    geo = _ext.geometry(batch, n, weighted)
+    assert geo["span0"] == 32 and geo["levels"] == 3
+    rng = np.random.default_rng(7 + weighted)
+    i = np.arange(n)
+    y = np.linspace(0, 3, n) + rng.standard_normal((batch, n))
+    for r in (0, 3):
+        y[r] = 1e-3 * i + rng.random()
+    y[2] = 1e-3 * i + 1e-5 * rng.standard_normal(n) - 0.3 * (i % 997 == 0)
+    y[4, n // 3] = np.nan
+    y = y.astype(dtype)
+    w = (rng.random((batch, n)) + 0.1).astype(dtype) if weighted else None
+    got, starts = check_fit(y, w)
+    assert starts[0].all() and starts[3].all()
+    check_fit(y, w, increasing=False, y_min=0.5, y_max=2.0)
+    ok = ~np.isnan(y).any(axis=1)
+    c = rng.standard_normal((batch, n)).astype(dtype)
+    gs, _ = gpu_grads(y, w, c)
+    fit, st = oracle.pava(y[ok], None if w is None else w[ok], acc="f64")
+    ey, ew = oracle.block_grad(
+        st, c[ok].astype(np.float64), None if w is None else w[ok].astype(np.float64),
+        y[ok].astype(np.float64), fit, want_w=w is not None,
+    )
+    tol = 1e-12 if dtype == np.float64 else 2e-5
+    np.testing.assert_allclose(gs[0][ok], ey, rtol=tol, atol=tol)
+    if w is not None:
+        np.testing.assert_allclose(gs[1][ok], ew, rtol=tol, atol=tol * (1 + float(np.nanmax(np.abs(y)))))
