@@ -25,14 +25,16 @@ def workspace_bytes(batch: int, n: int, dtype: int, weighted: bool) -> int:
     return size.value
 
 
-def run_both(batch: int, n: int, dtype: type, weighted: bool, flags: int) -> None:
+def run_both(batch: int, n: int, dtype: type, weighted: bool, flags: int, rising: bool = False) -> None:
     lib = _ext.load()
     code = _ext.F32 if dtype == np.float32 else _ext.F64
     need = workspace_bytes(batch, n, code, weighted)
     assert 0 < need <= SCRATCH
     print(f"noalloc {batch} x {n} {np.dtype(dtype).name} weighted={weighted} flags={flags} ({need} B)", flush=True)
     rng = np.random.default_rng(batch * n)
-    y = torch.from_numpy((np.linspace(0, 3, n) + rng.standard_normal((batch, n))).astype(dtype)).cuda()
+    # (rising: a vertex at every element, so every parent of an out-of-place level defers)
+    base = 1e-3 * np.arange(n) + rng.random((batch, 1)) if rising else np.linspace(0, 3, n) + rng.standard_normal((batch, n))
+    y = torch.from_numpy(base.astype(dtype)).cuda()
     w = torch.from_numpy((rng.random((batch, n)) + 0.1).astype(dtype)).cuda() if weighted else None
     words = _ext.starts_words(batch, n)
     s = torch.cuda.current_stream().cuda_stream
@@ -61,6 +63,15 @@ def test_noalloc_matches_fwd_on_calls_in_a_row() -> None:
     run_both(7, 3000, np.float32, True, _ext.INCREASING | _ext.CLIP_MIN | _ext.CLIP_MAX)
     run_both(100, 1000, np.float64, False, 0)
     run_both(3, 40, np.float32, False, _ext.INCREASING)
+
+
+def test_noalloc_with_out_of_place_levels() -> None:
+    # one row of 300000 (spans of 32): its second and third merge levels write their hulls into
+    # the scratch's second vertex store and back, every parent's survivors written by
+    # survivors_kernel from its table in the scratch; then two noisy rows of 150000 float64, whose
+    # second level is out of place too, with tables and stores left over from the first call
+    run_both(1, 300_000, np.float32, True, _ext.INCREASING, rising=True)
+    run_both(2, 150_000, np.float64, False, _ext.INCREASING)
 
 
 def test_noalloc_short_rows_need_no_scratch() -> None:
