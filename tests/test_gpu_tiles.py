@@ -521,8 +521,8 @@ def test_rows_expanded_by_their_last_merge(batch: int, n: int, dtype: type, weig
 # their hulls into the other vertex store than their children's, the second store and then the
 # first again. Rows with a vertex at every element (0, 3) have parents of more than 4096
 # survivors, which survivors_kernel writes; a near-monotone row with drops (2) some of either;
-# noisy rows (1, 5) only parents that write their own; row 4 holds a NaN. Fit, start bits and
-# both gradients against the oracle, increasing, and decreasing with clamps.
+# noisy rows (1, 5) only parents that write their own; row 4 rises too but holds a NaN. Fit,
+# start bits and both gradients against the oracle, increasing, and decreasing with clamps.
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("weighted", [False, True])
 def test_deferred_survivors_mixed_rows(dtype: type, weighted: bool) -> None:
@@ -535,10 +535,10 @@ def test_deferred_survivors_mixed_rows(dtype: type, weighted: bool) -> None:
     rng = np.random.default_rng(7 + weighted)
     i = np.arange(n)
     y = np.linspace(0, 3, n) + rng.standard_normal((batch, n))
-    for r in (0, 3):
+    for r in (0, 3, 4):
         y[r] = 1e-3 * i + rng.random()
     y[2] = 1e-3 * i + 1e-5 * rng.standard_normal(n) - 0.3 * (i % 997 == 0)
-    y[4, n // 3] = np.nan
+    y[4, n // 3] = np.nan  # (a rising row with a NaN: its parents defer as well)
     y = y.astype(dtype)
     w = (rng.random((batch, n)) + 0.1).astype(dtype) if weighted else None
     got, starts = check_fit(y, w)
