@@ -191,6 +191,9 @@ def test_autograd_keeps_little_at_c4() -> None:
     assert torch.equal(gy, ry) and torch.equal(gw, rw)
 
 
+KEEP_256MB = str(256 << 20)  # (TI_KEEP_MIN_BYTES: the node keeps hulls from 256 MB of workspace)
+
+
 def _monotone_autograd(batch: int, n: int) -> tuple[int, int]:
     # rows already increasing (every element a vertex, its own block): the fit under autograd,
     # the memory it holds beside the fit, the workspace size, and both gradients against the
@@ -217,20 +220,61 @@ def _monotone_autograd(batch: int, n: int) -> tuple[int, int]:
     return held, ws
 
 
-def test_autograd_keeps_the_workspace_for_monotone_rows() -> None:
+def test_autograd_keeps_the_workspace_for_monotone_rows(monkeypatch: pytest.MonkeyPatch) -> None:
     # every element a vertex, in a batch whose merges fill the GPU (one vertex store): the kept
     # hulls would be as large as the workspace, which is kept
+    monkeypatch.setenv("TI_KEEP_MIN_BYTES", KEEP_256MB)
     say("autograd on 256 monotone weighted rows of 40000")
     held, ws = _monotone_autograd(256, 40_000)
     assert held >= ws
 
 
-def test_autograd_keeps_hulls_for_a_monotone_row() -> None:
+def test_autograd_keeps_hulls_for_a_monotone_row(monkeypatch: pytest.MonkeyPatch) -> None:
     # one row: its upper merge levels write into a second vertex store, so the hulls, every
     # element a vertex, take half the workspace and are kept in its place
+    monkeypatch.setenv("TI_KEEP_MIN_BYTES", KEEP_256MB)
     n = 10_000_000
     say(f"autograd on a monotone weighted row of {n}")
     held, ws = _monotone_autograd(1, n)
     kb = ctypes.c_size_t(0)
     assert _ext.load().ti_keep_bytes(1, n, _ext.F64, 1, n + 1, ctypes.byref(kb)) == 0
     assert kb.value <= held < ws
+
+
+def test_autograd_holds_workspaces_under_a_share_of_the_device() -> None:
+    # C5's shape (1.33 GB of workspace): under 1/128 of the device's memory the node holds the
+    # workspace itself (no bound kernel, no copy); with TI_KEEP_MIN_BYTES at 256 MB it keeps the
+    # final hulls instead. The same gradients either way.
+    import os
+
+    b, n = 1000, 65536
+    say(f"autograd workspace held or hulls kept: {b} x {n} weighted")
+    ws = _size(_ext.load().ti_fwd_workspace, b, n, _ext.F32, 1)
+    total = torch.cuda.get_device_properties(0).total_memory
+    assert (256 << 20) <= ws <= total // 128
+    rng = np.random.default_rng(5)
+    y = torch.from_numpy((np.linspace(0, 3, n) + rng.standard_normal((b, n))).astype(np.float32)).cuda()
+    w = torch.from_numpy((rng.random((b, n)) + 0.1).astype(np.float32)).cuda()
+    g = torch.from_numpy(rng.standard_normal((b, n)).astype(np.float32)).cuda()
+    grads = []
+    for keep in (None, KEEP_256MB):
+        if keep is None:
+            os.environ.pop("TI_KEEP_MIN_BYTES", None)
+        else:
+            os.environ["TI_KEEP_MIN_BYTES"] = keep
+        try:
+            yr, wr = y.clone().requires_grad_(), w.clone().requires_grad_()
+            torch.cuda.synchronize()
+            before = torch.cuda.memory_allocated()
+            fit = torchisotonic_amd.isotonic(yr, wr)
+            torch.cuda.synchronize()
+            held = torch.cuda.memory_allocated() - before - fit.numel() * fit.element_size()
+            if keep is None:
+                assert held >= ws
+            else:
+                assert held < 64e6  # (the partition's 8 MB, the kept hulls and tile records)
+            grads.append(torch.autograd.grad(fit, (yr, wr), g))
+        finally:
+            os.environ.pop("TI_KEEP_MIN_BYTES", None)
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])

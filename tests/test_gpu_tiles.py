@@ -373,9 +373,10 @@ def check_many_rows(batch: int, n: int) -> None:
 
 
 @pytest.mark.parametrize(("batch", "n"), [(1, 2**24 + 5), (1_100_000, 16)])
-def test_weight_check_large(batch: int, n: int) -> None:
+def test_weight_check_large(batch: int, n: int, monkeypatch: pytest.MonkeyPatch) -> None:
     # past 2^24 elements the fit's own first kernel checks the weights as it reads them (smaller
     # fits check them in a kernel of their own first): a bad weight anywhere still raises
+    monkeypatch.setenv("TI_KEEP_MIN_BYTES", str(256 << 20))  # (the kept-hulls path under autograd)
     import torch
 
     import torchisotonic_amd

@@ -20,7 +20,9 @@
 #include <torch/library.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <optional>
@@ -114,10 +116,31 @@ WeightCheck& weight_check(c10::DeviceIndex dev) {
   return wc;
 }
 
-// A long-row fit under autograd whose workspace is at least this large keeps only the final hulls
-// and tile records for its backward (ti_keep): waiting for the hulls costs the host the time of the
-// merges, which smaller problems would not repay.
-constexpr size_t kKeepMinBytes = size_t{256} << 20;
+// A long-row fit under autograd whose workspace is at least keep_min_bytes() keeps only the final
+// hulls and tile records for its backward (ti_keep) and frees the workspace; a smaller one is held
+// until the backward. The copy costs a step about 20 us (the hull-count bound's kernel and the
+// copy; C5 forward + backward), the workspace costs its memory meanwhile: the threshold is 1/128 of
+// the device's memory (2.25 GB on an MI355X: C5's 1.33 GB is held, C4's 4.06 GB copied), and never
+// below 256 MB, under which waiting for the hulls costs the host the time of the merges. The
+// environment's TI_KEEP_MIN_BYTES (bytes), read at each call, replaces it.
+size_t keep_min_bytes(int dev) {
+  if (const char* e = std::getenv("TI_KEEP_MIN_BYTES")) {
+    char* end = nullptr;
+    const unsigned long long v = std::strtoull(e, &end, 10);
+    if (end != e && *end == '\0') return static_cast<size_t>(v);
+  }
+  static std::atomic<size_t> per_device[64];
+  const int d = dev >= 0 && dev < 64 ? dev : 0;
+  size_t v = per_device[d].load(std::memory_order_relaxed);
+  if (v == 0) {
+    size_t total = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess) total = prop.totalGlobalMem;
+    v = std::max<size_t>(size_t{256} << 20, total / 128);
+    per_device[d].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
 
 struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
   static at::Tensor forward(AutogradContext* ctx, const at::Tensor& y, const std::optional<at::Tensor>& w_opt,
@@ -146,7 +169,7 @@ struct IsotonicFn : public torch::autograd::Function<IsotonicFn> {
     at::Tensor ws = workspace(true, batch, n, dtype, w.defined(), yc.device());
     const size_t ws_bytes = ws.defined() ? static_cast<size_t>(ws.numel()) : 0;
     const double lo = y_min.value_or(0.0), hi = y_max.value_or(0.0);
-    const bool keep = want && ws_bytes >= kKeepMinBytes;
+    const bool keep = want && ws_bytes >= keep_min_bytes(yc.device().index());
     int64_t maxv = 0;  // > 0: the backward reads `kept`, not the workspace
     at::Tensor kept;
     if (!w.defined() && !keep) {
