@@ -178,6 +178,7 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
   if (batch == 0) return then_record(ok());
   if (y == nullptr || out == nullptr) return fail(TI_EINVAL, "y and out must not be null");
   if (out == y || (w != nullptr && out == w)) return fail(TI_EINVAL, "out must not alias y or w");
+  uint32_t* start_mark = nullptr;
   if ((weights_read != nullptr || weights_mark != nullptr) && w != nullptr && bad_weight != nullptr &&
       batch * n <= kEarlyCheckElems) {
     const int64_t count = batch * n;
@@ -189,7 +190,10 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
     if (int rc = launched(hipGetLastError(), "weight check")) return rc;
     if (weights_read != nullptr)
       if (int rc = launched(hipEventRecord(weights_read, hs), "weights-read event")) return rc;
-    if (weights_mark != nullptr)
+    // (rows over 32 elements: the span kernel's first thread stores the mark as it starts, one
+    // launch fewer)
+    if (weights_mark != nullptr && n > ti::kShortMax) start_mark = weights_mark;
+    else if (weights_mark != nullptr)
       if (int rc = launched(ti::mark_run(weights_mark, mark_value, hs), "weights mark")) return rc;
     bad_weight = nullptr;  // (checked: the fit need not)
     weights_read = nullptr;
@@ -209,6 +213,7 @@ int fwd_impl(const void* y, const void* w, void* out, uint32_t* starts, uint32_t
   ti::TileArgs a{y, w, out, starts, bad_weight, batch, n, dtype, flags, y_min, y_max, hs};
   a.weights_read = weights_read;  // after the span kernel, the first of several
   a.weights_mark = weights_mark;  // likewise
+  a.start_mark = start_mark;
   a.mark_value = mark_value;
   a.hulls_ready = hulls_ready;    // after the merges
   a.max_vertices = max_vertices;

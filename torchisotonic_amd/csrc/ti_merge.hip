@@ -194,6 +194,8 @@ __global__ __launch_bounds__(NT) void merge_kernel(MergeArgs a, int cap_lds, int
   extern __shared__ __align__(16) char lds_dyn[];
   const int tid = threadIdx.x;
   if (DF && tid == 0) tab[blockIdx.x].deferred = 0;
+  if (a.mark != nullptr && blockIdx.x == 0 && tid == 0)
+    __hip_atomic_store(a.mark, a.mark_value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   const int64_t row = blockIdx.x / a.out.npr;
   const int64_t j = blockIdx.x - row * a.out.npr;
   const int64_t c0 = j * kGroup;  // first child within the row
@@ -959,7 +961,9 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
   if (e != hipSuccess) return e;
   // the span kernel has read every weight (and set the flag if one is not positive)
   if (t.weights_read != nullptr && (e = hipEventRecord(t.weights_read, t.stream)) != hipSuccess) return e;
-  if (t.weights_mark != nullptr && (e = mark_run(t.weights_mark, t.mark_value, t.stream)) != hipSuccess) return e;
+  // (the weights' mark: stored by the first merge launch as it starts, or by a kernel of its own
+  // where no merge launch follows the span kernel)
+  uint32_t* pending_mark = t.weights_mark;
   // for a caller that keeps only the final hulls: a bound on their vertex counts, from the
   // counts of level keep_level once it is merged
   auto report = [&](int l) -> hipError_t {
@@ -993,6 +997,9 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     m.in = p.level(ws, l - 1);
     m.out = p.level(ws, l);
     m.child_elems = p.span[l - 1];
+    m.mark = pending_mark;
+    m.mark_value = t.mark_value;
+    pending_mark = nullptr;
     const unsigned grid = static_cast<unsigned>(t.batch * p.npr[l]);
     // Workgroup size and LDS slots by how many merges share the GPU: one wave and 768 slots
     // (64 noisy span hulls take 300-500) where there are thousands, else 256 or 1024 threads
@@ -1072,6 +1079,7 @@ hipError_t long_fit(const TileArgs& t, const LongPlan& p, void* ws) {
     }
     if ((e = report(l)) != hipSuccess) return e;
   }
+  if (pending_mark != nullptr && (e = mark_run(pending_mark, t.mark_value, t.stream)) != hipSuccess) return e;
   if (!p.lo && p.levels >= 1 && !fold && !span_fold) {
     // (float32 data: the final hulls convex in their stored values; span hulls, the final hulls
     // of rows of one span, are exact and convex already). Enough check workgroups a row for a

@@ -57,6 +57,10 @@ struct SpanArgs {
   // launches
   bool expand;
   RowExpand xp;
+  // (where given) mark_value stored to *mark by the kernel's first thread as it starts: the
+  // caller's mark that a kernel before this one has read every weight
+  uint32_t* mark;
+  uint32_t mark_value;
 };
 
 // Per lane (columns [slot][lane], so lanes never share a bank row): the candidate queue (index
@@ -113,6 +117,8 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert(kSpanLanes == kGroup, "a wave's spans are one group of the first merge level");
   __shared__ SpanLds<T, W, Q, R> L;
   const int lane = threadIdx.x;
+  if (a.mark != nullptr && blockIdx.x == 0 && lane == 0)
+    __hip_atomic_store(a.mark, a.mark_value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   // One wave per group of kGroup spans of one row (fewer at the row's end: the other lanes idle);
   // where a row is one span (spr == 1), one row per lane and 64 rows a wave ("packed"): each
   // span's hull is then its row's final hull, and there is nothing to merge; with rpw > 1, rpw
@@ -647,6 +653,8 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
   a.xp.hi = t.hi;
   a.xp.map = t.map;
   a.xp.lds_bytes = 0;  // (the kernel's: its wave's LDS)
+  a.mark = t.start_mark;
+  a.mark_value = t.mark_value;
   // (rows of one span: one row per lane, and no first merge level to write; several rows a wave:
   // rows_per_wave of them)
   const unsigned grid = static_cast<unsigned>(spr == 1 ? (t.batch + kSpanLanes - 1) / kSpanLanes

@@ -65,9 +65,13 @@ struct TileArgs {
   hipStream_t stream;
   hipEvent_t weights_read = nullptr;  // recorded once every weight has been read, if given
   // Where given: mark_value written to *weights_mark (a word of host memory that the host polls)
-  // once every weight has been read, by a kernel of one thread, with no event between kernels
+  // once every weight has been read, with no event between kernels: at the start of the first
+  // merge launch after the span kernel, or by a kernel of one thread where none follows it
   uint32_t* weights_mark = nullptr;
   uint32_t mark_value = 0;
+  // Where given (the weights read by a kernel before the fit): mark_value written to *start_mark
+  // by the span kernel's first thread as it starts, all of that kernel's reads being done
+  uint32_t* start_mark = nullptr;
   // Where given (rows over 32 elements): a bound on the final hulls' vertex counts (at least the
   // largest, at most n + 1) is written here (a device-visible word) and hulls_ready recorded once
   // it is, before the last merges and the expansion run.
@@ -316,6 +320,10 @@ constexpr int kMaxLevels = 8;
 struct MergeArgs {
   NodeLevel in, out;    // the children's level and the parents'
   int64_t child_elems;  // elements per child node
+  // (where given) mark_value stored to *mark by the launch's first thread as it starts: the
+  // caller's mark that the kernels before have read every weight
+  uint32_t* mark = nullptr;
+  uint32_t mark_value = 0;
 };
 
 // Merge levels 2 and up with fewer than kDeferParents parents, each over kDeferSpan elements or
