@@ -557,3 +557,53 @@ def test_deferred_survivors_mixed_rows(dtype: type, weighted: bool) -> None:
     np.testing.assert_allclose(gs[0][ok], ey, rtol=tol, atol=tol)
     if w is not None:
         np.testing.assert_allclose(gs[1][ok], ew, rtol=tol, atol=tol * (1 + float(np.nanmax(np.abs(y)))))
+
+
+def chord_rows(rows: int, n: int, dtype: type, weighted: bool, seed: int) -> tuple[np.ndarray, np.ndarray | None, np.ndarray]:
+    """Rows that put points on and near the chords of their neighbours, in four kinds by row
+    (index mod 4): small integers (exact ties, points exactly on chords), noise over 24 decades,
+    noise rounded to 1/64 plus a trace of noise (near ties), a trend with noise."""
+    rng = np.random.default_rng(seed)
+    kind = np.arange(rows) % 4
+    y = np.empty((rows, n))
+    y[kind == 0] = rng.integers(0, 4, ((kind == 0).sum(), n))
+    y[kind == 1] = rng.standard_normal(((kind == 1).sum(), n)) * 10.0 ** rng.uniform(-12, 12, ((kind == 1).sum(), n))
+    q = rng.standard_normal(((kind == 2).sum(), n))
+    y[kind == 2] = np.round(q * 64) / 64 + 1e-9 * rng.standard_normal(q.shape)
+    y[kind == 3] = np.linspace(0, 3, n) + rng.standard_normal(((kind == 3).sum(), n))
+    w = None
+    if weighted:
+        w = rng.random((rows, n)) + 0.1
+        w[kind == 0] = rng.integers(1, 5, ((kind == 0).sum(), n))
+        w = w.astype(dtype)
+    return y.astype(dtype), w, kind
+
+
+@pytest.mark.parametrize("increasing", [True, False])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_candidate_filter_same_bits(dtype: type, weighted: bool, increasing: bool) -> None:
+    # A grid of at most one wave a SIMD (600 rows of 5000: 600 waves) runs the span kernel's
+    # stronger candidate test, which drops points lying clearly above the chord of their
+    # neighbours two elements away; 2048 rows (2048 waves, the same spans of 80) run without it. The same rows through
+    # both give the same bits, and the oracle's fit (and, but for the rows over 24 decades, whose
+    # sums round differently in any order, its partition).
+    from torchisotonic_amd import _ext
+
+    n, small, big = 5000, 600, 2048
+    print(f"candidate filter dtype={np.dtype(dtype).name} weighted={weighted} increasing={increasing}", flush=True)
+    assert _ext.geometry(small, n, weighted) == _ext.geometry(big, n, weighted)
+    y, w, kind = chord_rows(small, n, dtype, weighted, 11 + weighted + 2 * increasing)
+    yb, wb, _ = chord_rows(big, n, dtype, weighted, 5)
+    yb[:small] = y
+    if w is not None:
+        wb[:small] = w
+    got, starts = gpu_fit(y, w, increasing)
+    got_b, starts_b = gpu_fit(yb, wb, increasing)
+    np.testing.assert_array_equal(got_b[:small].view(np.uint8), got.view(np.uint8))
+    np.testing.assert_array_equal(starts_b[:small], starts)
+    exact = kind != 1
+    check_fit(y[exact], None if w is None else w[exact], increasing)
+    # (rows over 24 decades: the float64 oracle's fit only; a float32 sum of them is no reference)
+    want, _ = oracle.pava(y[~exact], None if w is None else w[~exact], increasing=increasing, acc="f64")
+    assert float(np.abs(got[~exact].astype(np.float64) - want).max()) <= tolerance(y[~exact])

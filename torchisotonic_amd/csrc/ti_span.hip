@@ -20,9 +20,14 @@
 // gets that deep).
 //
 // A point is a candidate only where the data rises into it (y_{k-1} < y_k): elsewhere the slope
-// into it is at least the slope out of it, and equal slopes pool, so it is never a vertex.
+// into it is at least the slope out of it, and equal slopes pool, so it is never a vertex. Grids
+// of at most one wave a SIMD (FILT) also drop a point that lies clearly above the chord of its
+// neighbours two elements away on either side: about 0.68 loop iterations per element of noisy
+// data instead of 0.98, for some twenty more float64 operations per element.
 //
 // Output: the span hulls as the first node array of the cross-span merge (ti_merge.hip).
+#include <atomic>
+
 #include "ti_common.h"
 #include "ti_expand.h"
 #include "ti_gmerge.h"
@@ -102,7 +107,7 @@ __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t r, uint32_t of
   }
 }
 
-template <typename T, bool W, int C, int Q, int R, int LC, bool INC, bool MAP = false>
+template <typename T, bool W, int C, int Q, int R, int LC, bool INC, bool MAP = false, bool FILT = false>
 __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   static_assert((R & (R - 1)) == 0 && (Q & (Q - 1)) == 0 && R >= 4, "ring and queue slots: powers of two");
   static_assert(C < Q, "a chunk's candidates fit the queue");
@@ -307,6 +312,37 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   T wc[W ? LC : 1], wn[W ? LC : 1];
   load_block<T, LC>(ry, boff(0), yc);
   if constexpr (W) load_block<T, LC>(rw, boff(0), wc);
+  // FILT: a point is queued one element late, for the stronger test below, which needs the
+  // element after it. Carried from element to element: the last three elements' terms (t1 the
+  // newest), their weights and signed values, the running sum of |term| (the rounding margin's
+  // scale), and the sums of the point waiting to be queued.
+  double t1 = 0.0, t2 = 0.0, t3 = 0.0, w1 = 1.0, w2 = 1.0, w3 = 1.0, v1 = 0.0, v2 = 0.0, A = 0.0;
+  HPt pend{0, 0.0, 0.0, 0.0, 0.0};
+  // (FILT) Point e - 1 (between elements e - 2 and e - 1; e the element just summed, its term t0
+  // and weight w0) is a candidate where the data rises into it (v2 < v1) and it does not lie
+  // above the chord from point e - 3 to point e (b, from e >= 3) or from point e - 2 to point
+  // e + 1 (c, where e is in the span). Such a point is no vertex of the exact hull; it is dropped
+  // only where its height above the chord exceeds 2^-39 x A x the chord's width, which bounds
+  // what the rounding of the span's sums (and of this test) can move, so that near-ties stay
+  // candidates and the event loop decides them as without the test.
+  auto keep = [&](bool use_b, bool use_c, double t0, double w0) {
+    const double thr = A * 0x1p-39;
+    bool k = v2 < v1;
+    if constexpr (W) {
+      const double d3 = w3 + w2;
+      const double db = __builtin_fma(t3 + t2, w1, -(t1 * d3));
+      const double wc1 = w1 + w0;
+      const double dc = __builtin_fma(t2, wc1, -((t1 + t0) * w2));
+      k &= !(use_b && db > thr * (d3 + w1));
+      k &= !(use_c && dc > thr * (w2 + wc1));
+    } else {
+      const double db = (t3 + t2) - 2.0 * t1;
+      const double dc = 2.0 * t2 - (t1 + t0);
+      k &= !(use_b && db > 3.0 * thr);
+      k &= !(use_c && dc > 3.0 * thr);
+    }
+    return k;
+  };
   for (int b0 = 0; b0 < len; b0 += LC) {
     // the next block, whole, whether or not the span reaches it
     load_block<T, LC>(ry, boff(b0 + LC), yn);
@@ -328,15 +364,27 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
       const int c0 = b0 + sub;
       run(Q - C);
       // 1. sums at every point of the chunk; each point goes to the queue's next free slot,
-      // which it keeps if it is a candidate (so the stores need no branch)
-      auto element = [&](int k, bool cand) {  // sums through element c0 + k, for the point after it
+      // which it keeps if it is a candidate (so the stores need no branch). Without FILT, point
+      // e + 1 as element e is summed, a candidate where y rises into element e + 1 (or at the
+      // span's end); with FILT, point e - 1.
+      auto element = [&](int k, bool cand) {
+        const int e = c0 + k;
         const double ye = sgn * static_cast<double>(yc[sub + k]);
         bad |= ye != ye;
-        double term = ye;
+        double term = ye, we = 1.0;
         if constexpr (W) {
-          const double we = static_cast<double>(wc[W ? sub + k : 0]);
+          we = static_cast<double>(wc[W ? sub + k : 0]);
           wbad |= !(we > 0.0);
           term = we * ye;
+        }
+        if constexpr (FILT) {
+          A += __builtin_fabs(term);
+          const bool kept = e >= 2 && keep(e >= 3, true, term, we);
+          q_put(qt, pend);
+          qt += kept ? 1 : 0;
+          pend = HPt{e, S, PR ? SL : 0.0, W ? P : 0.0, (W && PR) ? PL : 0.0};
+        }
+        if constexpr (W) {
           if constexpr (PR) {
             const DD t = two_sum(P, we);
             P = t.hi;
@@ -352,8 +400,19 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         } else {
           S += term;
         }
-        q_put(qt, HPt{c0 + k + 1, S, PR ? SL : 0.0, W ? P : 0.0, (W && PR) ? PL : 0.0});
-        qt += cand ? 1 : 0;
+        if constexpr (FILT) {
+          t3 = t2;
+          t2 = t1;
+          t1 = term;
+          w3 = w2;
+          w2 = w1;
+          w1 = we;
+          v2 = v1;
+          v1 = ye;
+        } else {
+          q_put(qt, HPt{e + 1, S, PR ? SL : 0.0, W ? P : 0.0, (W && PR) ? PL : 0.0});
+          qt += cand ? 1 : 0;
+        }
       };
       // the point after element e is a candidate where y rises into e + 1, or at the span's end
       auto rises = [&](T u, T v) { return INC ? u < v : v < u; };
@@ -361,19 +420,27 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
         // whole chunks (all but a row's last span): no per-element bounds
 #pragma unroll
         for (int k = 0; k < C; ++k) {
-          const int kk = sub + k;
-          const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : after_block();
-          // (the span can end only after a chunk's last element here)
-          element(k, k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext)));
+          if constexpr (FILT) {
+            element(k, false);
+          } else {
+            const int kk = sub + k;
+            const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : after_block();
+            // (the span can end only after a chunk's last element here)
+            element(k, k + 1 < C ? rises(yc[kk], ynext) : ((c0 + C == len) | rises(yc[kk], ynext)));
+          }
         }
       } else {
 #pragma unroll
         for (int k = 0; k < C; ++k) {
           const int e = c0 + k;
           if (e < len) {
-            const int kk = sub + k;
-            const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : after_block();
-            element(k, (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext)));
+            if constexpr (FILT) {
+              element(k, false);
+            } else {
+              const int kk = sub + k;
+              const T ynext = kk + 1 < LC ? yc[kk + 1 < LC ? kk + 1 : 0] : after_block();
+              element(k, (e + 1 == len) | (e + 1 < len && rises(yc[kk], ynext)));
+            }
           }
         }
       }
@@ -382,6 +449,18 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
     for (int k = 0; k < LC; ++k) {
       yc[k] = yn[k];
       if constexpr (W) wc[W ? k : 0] = wn[W ? k : 0];
+    }
+  }
+  if constexpr (FILT) {
+    // the span's last two points: point len - 1 (tests a and b: there is no point len + 1), and
+    // the span's end, always a vertex
+    run(Q - 2);
+    if (len >= 1) {
+      const bool kept = len >= 2 && keep(len >= 3, false, 0.0, 1.0);
+      q_put(qt, pend);
+      qt += kept ? 1 : 0;
+      q_put(qt, HPt{len, S, PR ? SL : 0.0, W ? P : 0.0, (W && PR) ? PL : 0.0});
+      ++qt;
     }
   }
   // the last candidates
@@ -621,6 +700,21 @@ __global__ __launch_bounds__(kSpanLanes) void span_kernel(SpanArgs a) {
   if (a.expand) expand(pout, anybad);
 }
 
+// SIMDs of the current device (four a CU), read once per device
+int simd_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    v = 4 * cus;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 }  // namespace
 
 hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, const NodeLevel& hulls1,
@@ -662,22 +756,34 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
                                                                   : t.batch * a.gpr);
   const bool W = t.w != nullptr;
   const bool inc = (t.flags & TI_INCREASING) != 0;
-  auto go = [&](auto k_inc, auto k_dec) {  // (ragged rows of a block: float32 only)
+  // A grid of at most one wave a SIMD is latency-bound: each wave's event loop sets the time, and
+  // the stronger candidate test (FILT: fewer loop iterations for more arithmetic per element)
+  // pays (1000 rows of 5000: 67 -> 61.5 us); where waves share SIMDs over several rounds it costs
+  // more than it saves (C4-shaped rows 519 -> 547 us).
+  const bool filt = t.map.rows == nullptr && grid <= static_cast<unsigned>(simd_count());
+  auto go = [&](auto k_inc, auto k_dec) {
     if (inc) k_inc<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
     else k_dec<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
   };
   if (t.dtype == TI_F32) {
-    if (t.map.rows != nullptr) {
+    if (t.map.rows != nullptr) {  // (ragged rows of a block: float32 only)
       if (W) go(span_kernel<float, true, 4, 8, 8, 32, true, true>, span_kernel<float, true, 4, 8, 8, 32, false, true>);
       else go(span_kernel<float, false, 4, 8, 16, 32, true, true>, span_kernel<float, false, 4, 8, 16, 32, false, true>);
     } else if (W) {
-      go(span_kernel<float, true, 4, 8, 8, 32, true>, span_kernel<float, true, 4, 8, 8, 32, false>);
+      if (filt) go(span_kernel<float, true, 4, 8, 8, 32, true, false, true>, span_kernel<float, true, 4, 8, 8, 32, false, false, true>);
+      else go(span_kernel<float, true, 4, 8, 8, 32, true>, span_kernel<float, true, 4, 8, 8, 32, false>);
     } else {
-      go(span_kernel<float, false, 4, 8, 16, 32, true>, span_kernel<float, false, 4, 8, 16, 32, false>);
+      if (filt) go(span_kernel<float, false, 4, 8, 16, 32, true, false, true>, span_kernel<float, false, 4, 8, 16, 32, false, false, true>);
+      else go(span_kernel<float, false, 4, 8, 16, 32, true>, span_kernel<float, false, 4, 8, 16, 32, false>);
     }
   } else {
-    if (W) go(span_kernel<double, true, 4, 8, 8, 8, true>, span_kernel<double, true, 4, 8, 8, 8, false>);
-    else go(span_kernel<double, false, 4, 8, 16, 8, true>, span_kernel<double, false, 4, 8, 16, 8, false>);
+    if (W) {
+      if (filt) go(span_kernel<double, true, 4, 8, 8, 8, true, false, true>, span_kernel<double, true, 4, 8, 8, 8, false, false, true>);
+      else go(span_kernel<double, true, 4, 8, 8, 8, true>, span_kernel<double, true, 4, 8, 8, 8, false>);
+    } else {
+      if (filt) go(span_kernel<double, false, 4, 8, 16, 8, true, false, true>, span_kernel<double, false, 4, 8, 16, 8, false, false, true>);
+      else go(span_kernel<double, false, 4, 8, 16, 8, true>, span_kernel<double, false, 4, 8, 16, 8, false>);
+    }
   }
   return hipGetLastError();
 }
