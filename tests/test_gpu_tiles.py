@@ -583,14 +583,14 @@ def chord_rows(rows: int, n: int, dtype: type, weighted: bool, seed: int) -> tup
 @pytest.mark.parametrize("weighted", [False, True])
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_candidate_filter_same_bits(dtype: type, weighted: bool, increasing: bool) -> None:
-    # A grid of at most one wave a SIMD (600 rows of 5000: 600 waves) runs the span kernel's
+    # A grid of at most two waves a SIMD (600 rows of 5000: 600 waves) runs the span kernel's
     # stronger candidate test, which drops points lying clearly above the chord of their
-    # neighbours two elements away; 2048 rows (2048 waves, the same spans of 80) run without it. The same rows through
+    # neighbours two elements away; 3000 rows (3000 waves, the same spans of 80) run without it. The same rows through
     # both give the same bits, and the oracle's fit (and, but for the rows over 24 decades, whose
     # sums round differently in any order, its partition).
     from torchisotonic_amd import _ext
 
-    n, small, big = 5000, 600, 2048
+    n, small, big = 5000, 600, 3000
     print(f"candidate filter dtype={np.dtype(dtype).name} weighted={weighted} increasing={increasing}", flush=True)
     assert _ext.geometry(small, n, weighted) == _ext.geometry(big, n, weighted)
     y, w, kind = chord_rows(small, n, dtype, weighted, 11 + weighted + 2 * increasing)

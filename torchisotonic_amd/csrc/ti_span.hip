@@ -21,7 +21,7 @@
 //
 // A point is a candidate only where the data rises into it (y_{k-1} < y_k): elsewhere the slope
 // into it is at least the slope out of it, and equal slopes pool, so it is never a vertex. Grids
-// of at most one wave a SIMD (FILT) also drop a point that lies clearly above the chord of its
+// of at most two waves a SIMD (FILT) also drop a point that lies clearly above the chord of its
 // neighbours two elements away on either side: about 0.68 loop iterations per element of noisy
 // data instead of 0.98, for some twenty more float64 operations per element.
 //
@@ -756,11 +756,11 @@ hipError_t span_run(const TileArgs& t, const NodeLevel& hulls, int64_t span0, co
                                                                   : t.batch * a.gpr);
   const bool W = t.w != nullptr;
   const bool inc = (t.flags & TI_INCREASING) != 0;
-  // A grid of at most one wave a SIMD is latency-bound: each wave's event loop sets the time, and
-  // the stronger candidate test (FILT: fewer loop iterations for more arithmetic per element)
-  // pays (1000 rows of 5000: 67 -> 61.5 us); where waves share SIMDs over several rounds it costs
-  // more than it saves (C4-shaped rows 519 -> 547 us).
-  const bool filt = t.map.rows == nullptr && grid <= static_cast<unsigned>(simd_count());
+  // A grid the GPU holds in one round at two waves a SIMD or fewer is latency-bound: each wave's
+  // event loop sets the time, and the stronger candidate test (FILT: fewer loop iterations for
+  // more arithmetic per element) pays (1000 rows of 5000: 67 -> 61.5 us; 2000: 79.8 -> 75.2 us);
+  // over several rounds it costs more than it saves (C4-shaped rows 519 -> 547 us).
+  const bool filt = t.map.rows == nullptr && grid <= 2u * static_cast<unsigned>(simd_count());
   auto go = [&](auto k_inc, auto k_dec) {
     if (inc) k_inc<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
     else k_dec<<<dim3(grid), dim3(kSpanLanes), 0, t.stream>>>(a);
